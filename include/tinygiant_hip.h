@@ -1,0 +1,196 @@
+/*
+ * tinygiant_hip.h -- C ABI of libtinygiant_hip.so, the MI355X (gfx950)
+ * implementation of TinyGiant's fused quantized MoE expert path.
+ *
+ * Part 1 declares the 21 symbols that tinygiant/_lib.py:39-93 binds with
+ * ctypes, with the reference's exact C signatures (csrc/libtinygiant.c), so
+ * the library is a drop-in for libtinygiant.{so,dylib}.  Part 2 declares the
+ * device-resident extensions (tg_hip_*), which have no reference counterpart.
+ *
+ * Conventions shared with the reference:
+ *   formats   0 = Q4_K (144-byte 256-blocks), 1 = F16, 2 = Q6_K (210-byte
+ *             256-blocks), 3 = MXFP4 (17-byte 32-blocks), 4 = Q8_0 (34-byte
+ *             32-blocks)                        (csrc/libtinygiant.c:594)
+ *   act       0 = SiLU(g)*u, 1 = gpt-oss clamp/sigmoid(1.702 g)*(u+1) (:1248)
+ *   outputs of the MoE entry points are accumulated (+=), not overwritten
+ *   every call is synchronous: outputs are complete on return
+ *   all pointers in Part 1 are host pointers; a pointer inside a range given
+ *   to tg_mlock resolves to that range's copy in HBM, any other weight
+ *   pointer is staged to the device for the duration of the call
+ *   activation widths (embed_dim, inter_dim, ncols) are multiples of 32
+ */
+#ifndef TINYGIANT_HIP_H
+#define TINYGIANT_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ======================= Part 1: reference ABI ======================= */
+
+/* Fused top-k expert FFN over k rows (replaces csrc/libtinygiant.c:1386-1437,
+ * bound at tinygiant/_lib.py:74-75, called at tinygiant/engine.py:336-340).
+ * row_weights[e*k + r] == 0 excludes row r from expert e. */
+void tg_moe_forward_rows_v2(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs,
+                            const void *const *down_ptrs, int gate_fmt, const int *down_fmts,
+                            const float *const *gate_bias, const float *const *up_bias,
+                            const float *const *down_bias, int act, int n_experts,
+                            const float *row_weights, const float *inputs, float *output, int k,
+                            int embed_dim, int inter_dim);
+
+/* v2 with Q4_K gate/up, no biases, SiLU (replaces :1439-1448; _lib.py:90) */
+void tg_moe_forward_rows(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs,
+                         const void *const *down_ptrs, const int *down_fmts, int n_experts,
+                         const float *row_weights, const float *inputs, float *output, int k,
+                         int embed_dim, int inter_dim);
+
+/* Sum over experts of weight * all-Q4_K expert [gate|up|down]; zeroes output
+ * first (replaces :1452-1460; exported, not bound by _lib.py). */
+void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights, int n_experts,
+                    const float *input, float *output, int embed_dim, int inter_dim);
+
+/* output += weight * expert(input), all-Q4_K [gate|up|down] buffer
+ * (replaces :1040-1080; _lib.py:42) */
+void tg_expert_forward(const uint8_t *q4_data, const float *input, float *output, float weight,
+                       int embed_dim, int inter_dim);
+
+/* down_format 1 = f16, 2 = q6_K, else q4_K (replaces :1084-1128; _lib.py:43-44) */
+void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *up_q4, const void *down_data,
+                             int down_format, const float *input, float *output, float weight,
+                             int embed_dim, int inter_dim);
+
+/* output[r] += weights[r] * expert(inputs[r]) for k rows (replaces :1182-1231; _lib.py:89) */
+void tg_expert_forward_rows(const uint8_t *gate_q4, const uint8_t *up_q4, const void *down_data,
+                            int down_format, const float *inputs, float *output, const float *weights,
+                            int k, int embed_dim, int inter_dim);
+
+/* output[r] = dot(mat row r, q8(input)) + bias[r] (replaces :925-931; _lib.py:76,
+ * called at tinygiant/engine.py:352) */
+void tg_matmul(int fmt, const void *mat, const float *bias, const float *input, float *output,
+               int nrows, int ncols);
+void tg_matmul_q4k(const uint8_t *q4_matrix, const float *input, float *output, int nrows,
+                   int ncols);                                   /* :375-378; _lib.py:45 */
+void tg_matmul_q6k(const uint8_t *q6_matrix, const float *input, float *output, int nrows,
+                   int ncols);                                   /* :498-501; _lib.py:46 */
+size_t tg_row_bytes(int fmt, int ncols);                         /* :606; _lib.py:77-78 */
+
+/* The reference sizes its CPU pool (:85-104); here the count sizes nothing on
+ * the GPU path and is returned by tg_get_threads.  _lib.py:79-81 */
+void tg_set_threads(int n);
+int tg_get_threads(void);
+
+/* The reference mlocks host pages (:1566-1571; _lib.py:65-66, called by
+ * tinygiant/cache.py:153-162 for every pinned expert view).  Here the range
+ * is copied into HBM once and later pointers into it use the copy.
+ * Returns 0, or -1 if HBM is exhausted. */
+int tg_mlock(const void *addr, size_t len);
+
+/* Out of the hot path; served so the engine runs unchanged (tg_host_ops.cpp). */
+void tg_rms_norm(const float *x, const float *weight, float *out, int dim, float eps); /* :680; _lib.py:47 */
+void tg_f32_matvec(const float *A, const float *x, float *out, int nrows, int ncols); /* :662; _lib.py:48 */
+void tg_f16_matvec(const uint16_t *A, const float *x, float *out, int nrows, int ncols); /* :655; _lib.py:49 */
+void tg_attention_decode(const float *wq, const float *wk, const float *wv, const float *wo,
+                         const float *q_norm_w, const float *k_norm_w, float *kv_k, float *kv_v,
+                         int kv_len, int kv_max, const float *rope_cos, const float *rope_sin,
+                         const float *input, float *output, int embed_dim, int n_heads,
+                         int n_kv_heads, int head_dim, int pos);          /* :723; _lib.py:50-56 */
+void tg_attention_decode_q4(const uint8_t *wq_q4, const uint8_t *wk_q4, const uint16_t *wv_f16,
+                            const uint8_t *wo_q4, const float *q_norm_w, const float *k_norm_w,
+                            float *kv_k, float *kv_v, int kv_len, int kv_max, const float *rope_cos,
+                            const float *rope_sin, const float *input, float *output, int embed_dim,
+                            int n_heads, int n_kv_heads, int head_dim, int pos); /* :985; _lib.py:57-63 */
+void tg_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk,
+                     const void *wv, const void *wo, const float *bq, const float *bk, const float *bv,
+                     const float *bo, const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                     float *kv_k, float *kv_v, int kv_len, int kv_max, int window,
+                     const float *rope_cos, const float *rope_sin, const float *input, float *output,
+                     int embed_dim, int n_heads, int n_kv_heads, int head_dim, int pos,
+                     float eps);                                          /* :939; _lib.py:67-73 */
+void tg_transformer_layer(const float *wq, const float *wk, const float *wv, const float *wo,
+                          const float *attn_norm_w, const float *q_norm_w, const float *k_norm_w,
+                          const float *ffn_norm_w, float *kv_k, float *kv_v, int kv_len, int kv_max,
+                          const float *rope_cos, const float *rope_sin, const uint8_t **gate_ptrs,
+                          const uint8_t **up_ptrs, const void **down_ptrs, const int *down_is_f16,
+                          const float *expert_weights, int n_active, float *x, int embed_dim,
+                          int inter_dim, int n_heads, int n_kv_heads, int head_dim,
+                          int pos);                                       /* :1467; _lib.py:91-92 */
+void tg_prefetch(const void *addr, size_t len);                         /* :1550; _lib.py:64 */
+void tg_prefetch_batch(const void **addrs, const size_t *lens, int count); /* :1557; _lib.py:64 */
+
+/* ================ Part 2: device-resident extensions ================ */
+/* No reference counterpart.  Pointers named *_dev are device pointers;
+ * `stream` is a hipStream_t (NULL = the library's stream).  These only queue
+ * work (except where noted) and never allocate inside *_run/*_dev calls. */
+
+const char *tg_hip_last_error(void);           /* last argument error, "" if none */
+void tg_hip_clear_error(void);
+int tg_hip_register(const void *addr, size_t len);   /* = tg_mlock */
+int tg_hip_unregister(const void *addr);             /* frees the HBM copy; 0 or -1 */
+size_t tg_hip_registered_bytes(void);
+const void *tg_hip_device_ptr(const void *host, size_t n);  /* HBM copy of a registered range */
+void *tg_hip_stream(void);
+void *tg_hip_malloc(size_t n);
+void tg_hip_free(void *p);
+void tg_hip_memcpy_h2d(void *dst_dev, const void *src, size_t n);   /* synchronous */
+void tg_hip_memcpy_d2h(void *dst, const void *src_dev, size_t n);   /* synchronous */
+void tg_hip_memcpy_d2d(void *dst_dev, const void *src_dev, size_t n, void *stream);
+void tg_hip_synchronize(void);
+
+/* Seeded synthetic tensors: kind -1 raw bytes, 0 Q4_K, 2 Q6_K, 3 MXFP4, 4 Q8_0
+ * (block scale fields drawn as documented in tg_synth.h). */
+void tg_hip_synth_fill(int kind, uint64_t seed, void *dst_dev, uint64_t nbytes, void *stream);
+void tg_hip_synth_fill_host(int kind, uint64_t seed, void *dst, uint64_t nbytes);
+
+/* Parity probes (synchronous, host pointers). */
+void tg_hip_quantize_q8(const float *x, int ncols, int nrows, void *out_blocks /* 296 B each */);
+int tg_hip_isums(int fmt, const void *mat, int nrows, int ncols, const float *x, int32_t *out);
+
+/* tg_moe_forward_rows_v2 plus its stage outputs (stage-wise parity): the
+ * hidden rows [pairs][inter_dim] f32, pairs numbered expert-major in gather
+ * order, and their q8 blocks [pairs][ceil(inter_dim/256)] (296 B each). */
+void tg_hip_moe_forward_stages(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs,
+                               const void *const *down_ptrs, int gate_fmt, const int *down_fmts,
+                               const float *const *gate_bias, const float *const *up_bias,
+                               const float *const *down_bias, int act, int n_experts,
+                               const float *row_weights, const float *inputs, float *output, int k,
+                               int embed_dim, int inter_dim, float *hidden_out, void *hq_blocks_out);
+
+/* A MoE layer whose weights are already in HBM, planned once and replayed. */
+typedef struct tg_hip_moe_plan tg_hip_moe_plan;
+tg_hip_moe_plan *tg_hip_moe_plan_create(const void *const *gate_dev, const void *const *up_dev,
+                                        const void *const *down_dev, int gate_fmt, const int *down_fmts,
+                                        const float *const *gate_bias_dev, const float *const *up_bias_dev,
+                                        const float *const *down_bias_dev, int act, int n_experts,
+                                        const float *row_weights, int k, int embed_dim, int inter_dim);
+void tg_hip_moe_plan_run(tg_hip_moe_plan *plan, const float *inputs_dev, float *output_dev, void *stream);
+int tg_hip_moe_plan_pairs(const tg_hip_moe_plan *plan);
+void tg_hip_moe_plan_destroy(tg_hip_moe_plan *plan);
+
+/* k-row device GEMV: y[j][r] = dot(mat row r, q8(x_j)) + bias[r];
+ * scratch_dev holds tg_hip_matmul_scratch_bytes(k, ncols) bytes. */
+void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_dev, const float *inputs_dev,
+                       float *outputs_dev, int nrows, int ncols, int k, void *scratch_dev, void *stream);
+size_t tg_hip_matmul_scratch_bytes(int k, int ncols);
+void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n,
+                         float eps, void *stream);
+
+/* Device-resident decode step over L planned layers sharing one hidden
+ * state h_dev [k][embed_dim]: h <- h + MoE_l(RMSNorm_l(h)) for each layer
+ * (tinygiant/engine.py:281-282,335-341).  norm_w_dev may be NULL (weight 1).
+ * With use_graph the launch sequence is captured once into a HIP graph. */
+typedef struct tg_hip_decode tg_hip_decode;
+tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers,
+                                    const float *const *norm_w_dev, float eps, float *h_dev,
+                                    int use_graph);
+void tg_hip_decode_run(tg_hip_decode *step, void *stream);
+float tg_hip_decode_time(tg_hip_decode *step, int iters);   /* ms for iters steps, HIP events */
+void tg_hip_decode_kernel_times(tg_hip_decode *step, float *ms_out /*[6]*/, int *n_out /*[6]*/);
+void tg_hip_decode_destroy(tg_hip_decode *step);
+void tg_hip_device_name(char *buf, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,351 @@
+"""Pins the CPU oracle (oracle/tg_oracle.c) before it is trusted as the
+checker of the HIP path.
+
+The reference ships no golden vectors (its tests draw inputs from libc
+rand(), csrc/test_libtinygiant.c:94-130), and csrc/libtinygiant.c needs
+<arm_neon.h>, which this x86 image lacks, so it cannot be built here.  Each
+oracle function is therefore pinned by checks chosen so that a plausible
+mistake fails one of them:
+  * closed forms (f16 and e8m0 decode for every pattern, q8 special cases);
+  * an independent numpy restatement (q8 quantizer; format decoders in
+    tests/_formats.py written from the byte layouts, not from the oracle);
+  * integer special cases where the float path must return the exact
+    integer sum (d=1, dmin=0, unit sub-scales, x integer with amax=127);
+  * the reference test's own invariants: dequantize-then-dot (Test 2, 9),
+    x4 == x1 (Tests 5, 6), MoE == per-row expert composition (Test 7),
+    MXFP4 + gpt-oss activation + biases vs float64 (Test 10), threaded ==
+    serial (Test 8);
+  * the committed golden fixtures in tests/golden/ (regression of the above).
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+from tests import _formats as F
+
+RNG = np.random.default_rng(20261201)
+
+
+def test_f16_decode_every_pattern(orc):
+    h = np.arange(65536, dtype=np.uint16)
+    got = np.array([orc.f16_to_f32(int(v)) for v in h], np.float32)
+    finite = ((h >> 10) & 0x1F) != 31
+    ref = h.view(np.float16).astype(np.float32)
+    assert np.array_equal(got[finite].view(np.uint32), ref[finite].view(np.uint32))
+    # exponent 31: the reference's 32-bit shift yields 0xB7800000 | m << 13
+    m = (h[~finite] & 0x3FF).astype(np.uint32)
+    assert np.array_equal(got[~finite].view(np.uint32), np.uint32(0xB7800000) | (m << 13))
+
+
+def test_e8m0_half_every_exponent(orc):
+    for e in range(256):
+        assert orc.e8m0_half(e) == np.float32(np.ldexp(1.0, e - 128)), e
+
+
+def _numpy_q8(x):
+    """Independent numpy restatement of quantize_q8 (csrc/libtinygiant.c:169-208)."""
+    x = np.asarray(x, np.float32)
+    n = x.shape[0]
+    nb = (n + 255) // 256
+    xp = np.zeros(nb * 256, np.float32)
+    xp[:n] = x
+    blocks = xp.reshape(nb, 256)
+    amax = np.abs(blocks).max(axis=1).astype(np.float32)
+    scale = (amax / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", over="ignore"):
+        inv = np.where(amax > 0, np.float32(127) / amax, np.float32(0)).astype(np.float32)
+    with np.errstate(invalid="ignore", over="ignore"):
+        v = np.rint((blocks * inv[:, None]).astype(np.float32)).astype(np.float64)
+    # AArch64 FCVTNS: saturate to int32, NaN -> 0; qs keeps the low byte
+    v = np.where(np.isnan(v), 0.0, np.clip(v, -2.0 ** 31, 2.0 ** 31 - 1))
+    q = v.astype(np.int64)
+    bs = q.reshape(nb, 8, 32).sum(-1)
+    wrap = lambda a: ((a + 2 ** 31) % 2 ** 32 - 2 ** 31).astype(np.int32)
+    return scale, (q & 0xFF).astype(np.uint8).view(np.int8), wrap(bs), wrap(bs.sum(-1))
+
+
+@pytest.mark.parametrize("n", [32, 256, 768, 2048, 2880])
+def test_quantize_q8_matches_numpy(orc, n):
+    for trial in range(5):
+        x = (RNG.standard_normal(n) * 10 ** RNG.uniform(-3, 3)).astype(np.float32)
+        if trial == 1:
+            x[: n // 2] = 0.0
+        if trial == 2:
+            x = (x * np.float32(1e-42)).astype(np.float32)    # denormal blocks
+        got = orc.quantize_q8(x)
+        scale, q, bs, tot = _numpy_q8(x)
+        assert np.array_equal(got["scale"].view(np.uint32), scale.view(np.uint32))
+        assert np.array_equal(got["qs"], q)
+        assert np.array_equal(got["bsums"], bs)
+        assert np.array_equal(got["sum"], tot)
+
+
+def test_quantize_q8_closed_forms(orc):
+    z = orc.quantize_q8(np.zeros(256, np.float32))
+    assert z["scale"] == 0 and not z["qs"].any() and not z["bsums"].any()
+    # integer values with amax 127: scale 1, q == x
+    x = RNG.integers(-127, 128, 512).astype(np.float32)
+    x[3] = 127.0
+    x[300] = -127.0
+    q = orc.quantize_q8(x)
+    assert np.all(q["scale"] == 1.0)
+    assert np.array_equal(q["qs"].reshape(-1).astype(np.int64), x.astype(np.int64))
+    # +-amax map to +-127; ties round half to even (x*inv = 0.5 and 1.5 exactly)
+    y = np.zeros(256, np.float32)
+    y[0], y[1], y[2], y[3] = 127.0, 0.5, 1.5, -2.5
+    qy = orc.quantize_q8(y)["qs"].reshape(-1)
+    assert list(qy[:4]) == [127, 0, 2, -2]
+    # amax so small that 127/amax overflows: inv = inf, x*inv = +-inf saturates
+    # to +-2^31 (low byte 0xFF / 0x00), zeros give NaN -> 0
+    t = np.zeros(256, np.float32)
+    t[0], t[1] = np.float32(1e-40), np.float32(-1e-40)
+    qt = orc.quantize_q8(t)
+    assert list(qt["qs"].reshape(-1)[:3]) == [-1, 0, 0]
+    assert qt["bsums"].reshape(-1)[0] == np.int32(-1)      # INT32_MAX + INT32_MIN wraps to -1
+    # partial last block (2880 = 11*256 + 64) is zero padded
+    w = RNG.standard_normal(2880).astype(np.float32)
+    qw = orc.quantize_q8(w)
+    assert qw.shape == (12,) and not qw[11]["qs"][64:].any() and not qw[11]["bsums"][2:].any()
+
+
+FMT_SHAPES = [(O.FMT_Q4K, 2048), (O.FMT_Q4K, 768), (O.FMT_Q6K, 768), (O.FMT_Q6K, 2048),
+              (O.FMT_MXFP4, 2880), (O.FMT_Q80, 2880)]
+
+
+def _rand_row(fmt, ncols, tg_synth=True):
+    rb = O.row_bytes(fmt, ncols)
+    row = RNG.integers(0, 256, rb, dtype=np.uint8)
+    if fmt == O.FMT_Q4K:
+        b = row.reshape(-1, 144)
+        b[:, 0:2] = np.frombuffer(np.float16(RNG.uniform(1e-3, 2e-2)).tobytes(), np.uint8)
+        b[:, 2:4] = np.frombuffer(np.float16(RNG.uniform(1e-3, 2e-2)).tobytes(), np.uint8)
+    elif fmt == O.FMT_Q6K:
+        b = row.reshape(-1, 210)
+        b[:, 208:210] = np.frombuffer(np.float16(RNG.uniform(1e-3, 2e-2)).tobytes(), np.uint8)
+    elif fmt == O.FMT_MXFP4:
+        row.reshape(-1, 17)[:, 0] = RNG.integers(118, 131, ncols // 32)
+    elif fmt == O.FMT_Q80:
+        row.reshape(-1, 34)[:, 0:2] = np.frombuffer(np.float16(0.0625).tobytes(), np.uint8)
+    return row
+
+
+@pytest.mark.parametrize("fmt,ncols", FMT_SHAPES)
+def test_isums_match_bruteforce(orc, fmt, ncols):
+    for _ in range(4):
+        row = _rand_row(fmt, ncols)
+        x = RNG.standard_normal(ncols).astype(np.float32)
+        got = orc.isums(fmt, row, 1, ncols, x)[0]
+        ref = F.brute_isums(fmt, row, ncols, orc.quantize_q8(x))
+        assert np.array_equal(got.astype(np.int64), ref)
+
+
+def _unit_row(fmt, ncols):
+    """Scales that make the float path return the exact integer sum."""
+    rb = O.row_bytes(fmt, ncols)
+    row = RNG.integers(0, 256, rb, dtype=np.uint8)
+    if fmt == O.FMT_Q4K:
+        b = row.reshape(-1, 144)
+        b[:, 0:2] = [0x00, 0x3C]        # d = 1
+        b[:, 2:4] = 0                   # dmin = 0
+        b[:, 4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]   # sc = 1, m = 0 for all 8
+    elif fmt == O.FMT_Q6K:
+        b = row.reshape(-1, 210)
+        b[:, 192:208] = 1
+        b[:, 208:210] = [0x00, 0x3C]
+    elif fmt == O.FMT_MXFP4:
+        row.reshape(-1, 17)[:, 0] = 128
+    elif fmt == O.FMT_Q80:
+        row.reshape(-1, 34)[:, 0:2] = [0x00, 0x3C]
+    return row
+
+
+@pytest.mark.parametrize("fmt,ncols", FMT_SHAPES)
+def test_float_dot_exact_on_integer_cases(orc, fmt, ncols):
+    # x integer-valued with amax 127 => every q8 scale is 1 and q == x
+    row = _unit_row(fmt, ncols)
+    x = RNG.integers(-127, 128, ncols).astype(np.float32)
+    x[::256] = 127.0
+    xq = orc.quantize_q8(x)
+    exact = F.brute_isums(fmt, row, ncols, xq).sum()
+    # (MXFP4: e = 128 makes half(e) = 2^0, so the doubled table values are the weights)
+    assert abs(exact) < 2 ** 24
+    assert orc.dot(fmt, row, xq, ncols) == np.float32(exact)
+    if fmt == O.FMT_Q4K:
+        # dmin and m: dot = d*sc*isum - dmin*m*bsum, with dmin = 2, m = 3 on every sub-block
+        r2 = row.copy().reshape(-1, 144)
+        r2[:, 2:4] = [0x00, 0x40]
+        r2[:, 8:12] = 3
+        r2[:, 12:16] = 0x31
+        bs = xq["bsums"].reshape(-1).astype(np.int64)[: ncols // 32]
+        want = exact - 2.0 * 3.0 * bs.sum()
+        assert orc.dot(fmt, r2.reshape(-1), xq, ncols) == np.float32(want)
+
+
+@pytest.mark.parametrize("fmt,ncols", FMT_SHAPES)
+def test_dequant_then_dot(orc, fmt, ncols):
+    """Fused q8 dot == dequantized weights . dequantized q8 activations."""
+    for _ in range(3):
+        row = _rand_row(fmt, ncols)
+        x = RNG.standard_normal(ncols).astype(np.float32)
+        xq = orc.quantize_q8(x)
+        xd = (F.q8_ints(xq).reshape(-1, 256) * xq["scale"][:, None].astype(np.float64)).reshape(-1)[:ncols]
+        ref = float(F.dequant_row(fmt, row, ncols) @ xd)
+        got = orc.dot(fmt, row, xq, ncols)
+        scale = np.abs(F.dequant_row(fmt, row, ncols) * xd).sum()
+        assert abs(got - ref) <= 2e-6 * scale + 1e-6, (got, ref)
+
+
+@pytest.mark.parametrize("fmt,ncols", [(O.FMT_Q4K, 2048), (O.FMT_Q6K, 768), (O.FMT_MXFP4, 2880)])
+def test_x4_matches_x1(orc, fmt, ncols):
+    row = _rand_row(fmt, ncols)
+    xs = [orc.quantize_q8(RNG.standard_normal(ncols).astype(np.float32) * 0.1) for _ in range(4)]
+    o4 = orc.dot_x4(fmt, row, xs, ncols)
+    for r in range(4):
+        o1 = orc.dot(fmt, row, xs[r], ncols)
+        assert abs(o1 - o4[r]) <= 1e-5 * max(abs(o1), 1e-3)
+
+
+def test_f16_dot_vs_float64(orc):
+    ncols = 768
+    w = (RNG.standard_normal(ncols) * 0.05).astype(np.float16)
+    x = RNG.standard_normal(ncols).astype(np.float32)
+    got = orc.dot(O.FMT_F16, w.view(np.uint8), None, ncols, xf=x)
+    ref = float(w.astype(np.float64) @ x.astype(np.float64))
+    assert abs(got - ref) <= 1e-5 * np.abs(w.astype(np.float64) * x).sum()
+
+
+def test_q4k_scalar_matches_dequant(orc):
+    ncols, nrows = 512, 5
+    mat = np.concatenate([_rand_row(O.FMT_Q4K, ncols) for _ in range(nrows)])
+    x = (RNG.standard_normal(ncols) * 0.05).astype(np.float32)
+    got = orc.matmul_q4k_scalar(mat, x, nrows, ncols)
+    rb = O.row_bytes(O.FMT_Q4K, ncols)
+    for r in range(nrows):
+        w = F.dequant_row(O.FMT_Q4K, mat[r * rb:(r + 1) * rb], ncols)
+        ref = float(w @ x)
+        assert abs(got[r] - ref) <= 1e-4 * np.abs(w * x).sum()
+
+
+def test_rms_norm_vs_float64(orc):
+    x = RNG.standard_normal(2048).astype(np.float32)
+    w = RNG.uniform(0.5, 1.5, 2048).astype(np.float32)
+    got = orc.rms_norm(x, w, 1e-6)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd * xd).mean() + 1e-6) * w
+    assert np.max(np.abs(got - ref)) <= 1e-6 * np.abs(ref).max()
+
+
+def test_matmul_threaded_equals_serial(orc):
+    """Reference Test 8: the row chunking is invisible in the result."""
+    ncols, nrows = 2048, 300
+    mat = np.concatenate([_rand_row(O.FMT_Q4K, ncols) for _ in range(nrows)])
+    x = (RNG.standard_normal(ncols) * 0.02).astype(np.float32)
+    orc.set_threads(1)
+    o1 = orc.matmul(O.FMT_Q4K, mat, None, x, nrows, ncols)
+    orc.set_threads(4)
+    o4 = orc.matmul(O.FMT_Q4K, mat, None, x, nrows, ncols)
+    orc.set_threads(1)
+    assert np.array_equal(o1.view(np.uint32), o4.view(np.uint32))
+    # and each row is the single-row dot plus bias
+    bias = RNG.standard_normal(nrows).astype(np.float32)
+    ob = orc.matmul(O.FMT_Q4K, mat, bias, x, nrows, ncols)
+    xq = orc.quantize_q8(x)
+    rb = O.row_bytes(O.FMT_Q4K, ncols)
+    for r in (0, 7, 299):
+        assert ob[r] == np.float32(orc.dot(O.FMT_Q4K, mat[r * rb:(r + 1) * rb], xq, ncols) + bias[r])
+
+
+def _moe_weights(n, D, I, down_fmts, seed):
+    rng = np.random.default_rng(seed)
+    gates, ups, downs = [], [], []
+    global RNG
+    saved, RNG = RNG, rng
+    try:
+        for e in range(n):
+            gates.append(np.concatenate([_rand_row(O.FMT_Q4K, D) for _ in range(I)]))
+            ups.append(np.concatenate([_rand_row(O.FMT_Q4K, D) for _ in range(I)]))
+            downs.append(np.concatenate([_rand_row(down_fmts[e], I) for _ in range(D)]))
+    finally:
+        RNG = saved
+    return gates, ups, downs
+
+
+def test_moe_v2_equals_per_row_expert_composition(orc):
+    """Reference Test 7: tg_moe_forward_rows == per-row tg_expert_forward_mixed."""
+    D, I, k, n = 512, 256, 6, 4
+    fmts = [O.FMT_Q4K, O.FMT_Q6K, O.FMT_Q4K, O.FMT_Q6K]
+    gates, ups, downs = _moe_weights(n, D, I, fmts, 7)
+    x = (RNG.standard_normal((k, D)) * 0.5).astype(np.float32)
+    rw = np.zeros((n, k), np.float32)
+    for r in range(k):
+        for j in range(3):
+            rw[(r + 2 * j) % n, r] = 0.2 + 0.1 * j
+    ref = np.zeros((k, D), np.float32)
+    for r in range(k):
+        for e in range(n):
+            if rw[e, r] != 0:
+                code = 2 if fmts[e] == O.FMT_Q6K else 0
+                orc.expert_forward_mixed(gates[e], ups[e], downs[e], code, x[r], ref[r], rw[e, r], D, I)
+    got = orc.moe_v2(gates, ups, downs, O.FMT_Q4K, fmts, None, None, None, O.ACT_SILU, rw, x,
+                     np.zeros((k, D), np.float32), I)
+    assert np.max(np.abs(got - ref)) <= 1e-5 * np.abs(ref).max()
+    # the single-row groups take the x1 kernels: rows alone must match exactly
+    solo = orc.moe_v2(gates[:1], ups[:1], downs[:1], O.FMT_Q4K, fmts[:1], None, None, None,
+                      O.ACT_SILU, rw[:1, :1], x[:1], np.zeros((1, D), np.float32), I)
+    one = np.zeros(D, np.float32)
+    orc.expert_forward_mixed(gates[0], ups[0], downs[0], 0, x[0], one, rw[0, 0], D, I)
+    if rw[0, 0] != 0:
+        assert np.array_equal(solo[0], one)
+
+
+def test_moe_v2_mxfp4_gptoss_biases_vs_float64(orc):
+    """Reference Test 10: MXFP4 experts, gpt-oss activation and biases against a
+    float64 dequantized reference, within the q8 quantization error."""
+    D = I = 2880      # 11 full q8 blocks + a zero-padded one
+    k, n = 3, 2
+    rng = np.random.default_rng(77)
+    mats = []
+    for e in range(n):
+        trio = []
+        for (nr, nc) in ((I, D), (I, D), (D, I)):
+            m = rng.integers(0, 256, nr * nc // 32 * 17, dtype=np.uint8)
+            m.reshape(-1, 17)[:, 0] = rng.integers(112, 118, nr * nc // 32)
+            trio.append(m)
+        mats.append(trio)
+    bg = [rng.uniform(-0.5, 0.5, I).astype(np.float32) for _ in range(n)]
+    bu = [rng.uniform(-0.5, 0.5, I).astype(np.float32) for _ in range(n)]
+    bd = [rng.uniform(-0.05, 0.05, D).astype(np.float32) for _ in range(n)]
+    x = rng.uniform(-1, 1, (k, D)).astype(np.float32)
+    rw = np.array([[0.6, 0.0, 0.3], [0.4, 1.0, 0.7]], np.float32)
+    got = orc.moe_v2([m[0] for m in mats], [m[1] for m in mats], [m[2] for m in mats], O.FMT_MXFP4,
+                     [O.FMT_MXFP4] * n, bg, bu, bd, O.ACT_GPTOSS, rw, x, np.zeros((k, D), np.float32), I)
+    ref = np.zeros((k, D))
+    for e in range(n):
+        G = F.dequant_row(O.FMT_MXFP4, mats[e][0], I * D).reshape(I, D)
+        U = F.dequant_row(O.FMT_MXFP4, mats[e][1], I * D).reshape(I, D)
+        Dn = F.dequant_row(O.FMT_MXFP4, mats[e][2], D * I).reshape(D, I)
+        for r in range(k):
+            if rw[e, r] == 0:
+                continue
+            g = G @ x[r] + bg[e]
+            u = U @ x[r] + bu[e]
+            g = np.minimum(g, 7.0)
+            u = np.clip(u, -7.0, 7.0)
+            h = g / (1 + np.exp(-1.702 * g)) * (u + 1)
+            ref[r] += rw[e, r] * (Dn @ h + bd[e])
+    assert np.max(np.abs(got - ref)) <= 0.03 * np.abs(ref).max()
+
+
+def test_moe_v2_skips_exact_zero_and_accumulates(orc):
+    D, I, k, n = 512, 256, 2, 2
+    gates, ups, downs = _moe_weights(n, D, I, [O.FMT_Q6K] * n, 3)
+    x = RNG.standard_normal((k, D)).astype(np.float32)
+    base = RNG.standard_normal((k, D)).astype(np.float32)
+    rw = np.array([[0.5, 0.0], [0.0, 0.0]], np.float32)
+    out = orc.moe_v2(gates, ups, downs, O.FMT_Q4K, [O.FMT_Q6K] * n, None, None, None, O.ACT_SILU, rw, x,
+                     base.copy(), I)
+    assert np.array_equal(out[1], base[1])         # row 1 has no expert: untouched
+    only = orc.moe_v2(gates[:1], ups[:1], downs[:1], O.FMT_Q4K, [O.FMT_Q6K], None, None, None, O.ACT_SILU,
+                      rw[:1, :1], x[:1], np.zeros((1, D), np.float32), I)
+    assert np.array_equal(out[0], base[0] + only[0])

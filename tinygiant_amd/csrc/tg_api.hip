@@ -1,0 +1,1041 @@
+/*
+ * tg_api.hip -- the C ABI of libtinygiant_hip.so.
+ *
+ * The reference's ctypes loader (tinygiant/_lib.py:39-93) binds 21 symbols of
+ * csrc/libtinygiant.c.  This file implements the hot-path ones on the GPU:
+ *   tg_moe_forward_rows_v2, tg_moe_forward_rows, tg_moe_forward,
+ *   tg_expert_forward, tg_expert_forward_mixed, tg_expert_forward_rows,
+ *   tg_matmul, tg_matmul_q4k, tg_matmul_q6k, tg_row_bytes,
+ *   tg_mlock (uploads the range to HBM), tg_set_threads, tg_get_threads,
+ * and the device-resident tg_hip_* extensions (include/tinygiant_hip.h).
+ * The out-of-scope symbols (attention, norms, f32/f16 matvecs, prefetch
+ * hints, the full transformer layer) live in tg_host_ops.cpp.
+ *
+ * Calls are synchronous like the reference's: outputs are complete on
+ * return.  All work runs on one non-blocking stream of the current device
+ * under one process-wide mutex.  HIP runtime failures abort the process
+ * with a message; invalid arguments are reported on stderr and through
+ * tg_hip_last_error() and leave the outputs untouched.
+ */
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "tg_kernels.h"
+#include "tg_synth.h"
+
+#define TG_API extern "C" __attribute__((visibility("default")))
+
+using namespace tg;
+
+namespace {
+
+std::recursive_mutex g_mu;
+char g_err[1024];
+int g_threads = 1;
+
+void hip_fail(hipError_t e, const char *what, const char *file, int line) {
+    fprintf(stderr, "libtinygiant_hip: %s failed: %s (%s:%d)\n", what, hipGetErrorString(e), file, line);
+    fflush(stderr);
+    abort();
+}
+#define HIPCHECK(x)                                              \
+    do {                                                         \
+        hipError_t e_ = (x);                                     \
+        if (e_ != hipSuccess) hip_fail(e_, #x, __FILE__, __LINE__); \
+    } while (0)
+
+void set_err(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    fprintf(stderr, "libtinygiant_hip: %s\n", g_err);
+    fflush(stderr);
+}
+
+/* ---- device context ---- */
+struct Ctx {
+    bool ready = false;
+    int dev = 0;
+    hipStream_t st = nullptr;
+    /* grow-only device arena for per-call scratch, pinned host staging */
+    uint8_t *arena = nullptr;
+    size_t arena_cap = 0;
+    uint8_t *pin = nullptr;
+    size_t pin_cap = 0;
+};
+Ctx g;
+
+void ensure_init() {
+    if (g.ready) return;
+    HIPCHECK(hipGetDevice(&g.dev));
+    HIPCHECK(hipStreamCreateWithFlags(&g.st, hipStreamNonBlocking));
+    g.ready = true;
+}
+
+uint8_t *arena(size_t n) {
+    if (n > g.arena_cap) {
+        if (g.arena) {
+            HIPCHECK(hipStreamSynchronize(g.st));
+            HIPCHECK(hipFree(g.arena));
+        }
+        size_t cap = std::max(n, (size_t)64 << 20);
+        HIPCHECK(hipMalloc(&g.arena, cap));
+        g.arena_cap = cap;
+    }
+    return g.arena;
+}
+
+uint8_t *pinned(size_t n) {
+    if (n > g.pin_cap) {
+        if (g.pin) {
+            HIPCHECK(hipStreamSynchronize(g.st));
+            HIPCHECK(hipHostFree(g.pin));
+        }
+        size_t cap = std::max(n, (size_t)4 << 20);
+        HIPCHECK(hipHostMalloc(&g.pin, cap, hipHostMallocDefault));
+        g.pin_cap = cap;
+    }
+    return g.pin;
+}
+
+/* Bump allocator over a byte range, 256-byte aligned pieces. */
+struct Bump {
+    size_t off = 0;
+    size_t take(size_t n) {
+        size_t o = off;
+        off += (n + 255) & ~(size_t)255;
+        return o;
+    }
+};
+
+/* ---- HBM residency registry (tg_mlock) ---- */
+struct Region {
+    size_t len;
+    uint8_t *dev;
+};
+std::map<uintptr_t, Region> g_regs;
+
+/* device copy of [p, p+n) if that range lies inside one registered region */
+const void *lookup(const void *p, size_t n) {
+    if (!p || g_regs.empty()) return nullptr;
+    uintptr_t a = (uintptr_t)p;
+    auto it = g_regs.upper_bound(a);
+    if (it == g_regs.begin()) return nullptr;
+    --it;
+    if (a >= it->first && a + n <= it->first + it->second.len) return it->second.dev + (a - it->first);
+    return nullptr;
+}
+
+int do_register(const void *addr, size_t len) {
+    if (!addr || len == 0) return 0;
+    ensure_init();
+    if (lookup(addr, len)) return 0;
+    uintptr_t a = (uintptr_t)addr;
+    auto it = g_regs.find(a);
+    if (it != g_regs.end()) {   /* same start, longer range: replace */
+        HIPCHECK(hipStreamSynchronize(g.st));
+        HIPCHECK(hipFree(it->second.dev));
+        g_regs.erase(it);
+    }
+    uint8_t *dev = nullptr;
+    hipError_t e = hipMalloc(&dev, len);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_err("tg_mlock: cannot allocate %zu bytes of HBM (%s)", len, hipGetErrorString(e));
+        return -1;
+    }
+    HIPCHECK(hipMemcpy(dev, addr, len, hipMemcpyHostToDevice));
+    g_regs[a] = Region{len, dev};
+    return 0;
+}
+
+/* ---- per-call input resolution: registered range or staged copy ---- */
+struct Stager {
+    struct Item {
+        const void *host;
+        size_t n;
+        size_t off;
+    };
+    std::vector<Item> items;
+    Bump *bump;
+    /* returns an arena offset (for staged data) or the device address */
+    uintptr_t resolve(const void *host, size_t n, bool *staged) {
+        const void *d = lookup(host, n);
+        if (d) {
+            *staged = false;
+            return (uintptr_t)d;
+        }
+        *staged = true;
+        size_t off = bump->take(n);
+        items.push_back({host, n, off});
+        return off;
+    }
+};
+
+bool fmt_ok(int fmt) { return fmt == TG_FMT_Q4K || fmt == TG_FMT_F16 || fmt == TG_FMT_Q6K || fmt == TG_FMT_MXFP4 || fmt == TG_FMT_Q80; }
+
+size_t q8_bytes(int nrows, int ncols) {
+    size_t nb = TG_Q8_NB(ncols);
+    return (size_t)nrows * nb * (256 + 4 + 32 + 64 + 4);
+}
+
+Q8Rows q8_view(uint8_t *base, int nrows, int ncols, const float *f) {
+    Q8Rows q;
+    const size_t nb = TG_Q8_NB(ncols);
+    q.nb = (int)nb;
+    q.qs = (int8_t *)base;
+    q.d = (float *)(base + (size_t)nrows * nb * 256);
+    q.s32 = (int32_t *)((uint8_t *)q.d + (size_t)nrows * nb * 4);
+    q.s16 = (int32_t *)((uint8_t *)q.s32 + (size_t)nrows * nb * 32);
+    q.sum = (int32_t *)((uint8_t *)q.s16 + (size_t)nrows * nb * 64);
+    q.f = f;
+    q.fstride = ncols;
+    return q;
+}
+
+/* ---- MoE plan: device tables + scratch for one call shape ---- */
+struct HostPlan {
+    int n = 0, k = 0, P = 0, D = 0, I = 0, act = 0, gate_fmt = 0;
+    std::vector<uint64_t> gate, up, down, gbias, ubias, dbias;
+    std::vector<int> down_fmt, p_off, p_row, r_off, r_pair;
+    std::vector<float> p_w;
+    bool has_gb = false, has_ub = false, has_db = false;
+    std::vector<int> fmts_present;
+};
+
+bool validate_moe(int gate_fmt, const int *down_fmts, int n, int k, int D, int I, int act) {
+    if (n < 0 || k < 0 || D <= 0 || I <= 0) {
+        set_err("moe: bad sizes n=%d k=%d D=%d I=%d", n, k, D, I);
+        return false;
+    }
+    if (D % 32 || I % 32) {
+        set_err("moe: embed_dim (%d) and inter_dim (%d) must be multiples of 32", D, I);
+        return false;
+    }
+    if (!fmt_ok(gate_fmt) || gate_fmt == TG_FMT_F16) {
+        set_err("moe: unsupported gate/up format %d (F16 gate/up dereferences NULL in the reference)", gate_fmt);
+        return false;
+    }
+    if (act != TG_ACT_SILU && act != TG_ACT_GPTOSS) {
+        set_err("moe: unknown activation %d", act);
+        return false;
+    }
+    for (int e = 0; e < n; e++)
+        if (!fmt_ok(down_fmts[e])) {
+            set_err("moe: unsupported down format %d for expert %d", down_fmts[e], e);
+            return false;
+        }
+    if ((uint64_t)I * row_bytes(gate_fmt, D) >= (1ull << 32) || (uint64_t)D * row_bytes(TG_FMT_F16, I) >= (1ull << 32)) {
+        set_err("moe: expert matrices must be under 4 GiB");
+        return false;
+    }
+    return true;
+}
+
+/* pairs in the reference's gather order (csrc/libtinygiant.c:1411-1423) */
+void build_pairs(HostPlan &h, const float *row_weights) {
+    h.p_off.assign(h.n + 1, 0);
+    h.p_row.clear();
+    h.p_w.clear();
+    std::vector<std::vector<int>> per_row(h.k);
+    for (int e = 0; e < h.n; e++) {
+        h.p_off[e] = (int)h.p_row.size();
+        for (int r = 0; r < h.k; r++) {
+            float w = row_weights[(size_t)e * h.k + r];
+            if (w == 0.f) continue;
+            per_row[r].push_back((int)h.p_row.size());
+            h.p_row.push_back(r);
+            h.p_w.push_back(w);
+        }
+    }
+    h.p_off[h.n] = (int)h.p_row.size();
+    h.P = (int)h.p_row.size();
+    h.r_off.assign(h.k + 1, 0);
+    h.r_pair.clear();
+    for (int r = 0; r < h.k; r++) {
+        h.r_off[r] = (int)h.r_pair.size();
+        for (int p : per_row[r]) h.r_pair.push_back(p);
+    }
+    h.r_off[h.k] = (int)h.r_pair.size();
+    h.fmts_present.clear();
+    for (int e = 0; e < h.n; e++)
+        if (h.p_off[e + 1] > h.p_off[e] &&
+            std::find(h.fmts_present.begin(), h.fmts_present.end(), h.down_fmt[e]) == h.fmts_present.end())
+            h.fmts_present.push_back(h.down_fmt[e]);
+}
+
+/* Lays out tables + scratch in `base` (device) and the table image in `img`
+ * (host); returns MoeArgs pointing into base. */
+struct Layout {
+    size_t tables, tables_len, xin, xq, hidden, hq, part, out, total;
+};
+
+Layout plan_layout(const HostPlan &h) {
+    Layout L;
+    Bump b;
+    const int n = h.n, k = h.k, P = std::max(h.P, 1);
+    L.tables = b.take(0);
+    size_t t = 0;
+    t += 6 * (size_t)n * 8;                 /* gate, up, down, gbias, ubias, dbias */
+    t += (size_t)n * 4;                     /* down_fmt */
+    t += (size_t)(n + 1) * 4 + (size_t)P * 4 + (size_t)P * 4 + (size_t)(k + 1) * 4 + (size_t)P * 4;
+    L.tables_len = t + 64;
+    b.take(L.tables_len);
+    L.xin = b.take((size_t)k * h.D * 4);
+    L.xq = b.take(q8_bytes(std::max(k, 1), h.D));
+    L.hidden = b.take((size_t)P * h.I * 4);
+    L.hq = b.take(q8_bytes(P, h.I));
+    L.part = b.take((size_t)P * h.D * 4);
+    L.out = b.take((size_t)k * h.D * 4);
+    L.total = b.off;
+    return L;
+}
+
+/* serialises the tables into img (host, tables_len bytes) and returns the
+ * MoeArgs for a device base address */
+MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img) {
+    const int n = h.n, k = h.k, P = std::max(h.P, 1);
+    size_t o = 0;
+    auto put = [&](const void *src, size_t bytes) {
+        size_t at = o;
+        if (bytes) memcpy(img + o, src, bytes);
+        o += (bytes + 7) & ~(size_t)7;
+        return dev + L.tables + at;
+    };
+    MoeArgs a;
+    memset(&a, 0, sizeof a);
+    a.gate = (const uint64_t *)put(h.gate.data(), (size_t)n * 8);
+    a.up = (const uint64_t *)put(h.up.data(), (size_t)n * 8);
+    a.down = (const uint64_t *)put(h.down.data(), (size_t)n * 8);
+    const uint64_t *gb = (const uint64_t *)put(h.gbias.data(), (size_t)n * 8);
+    const uint64_t *ub = (const uint64_t *)put(h.ubias.data(), (size_t)n * 8);
+    const uint64_t *db = (const uint64_t *)put(h.dbias.data(), (size_t)n * 8);
+    a.gbias = h.has_gb ? gb : nullptr;
+    a.ubias = h.has_ub ? ub : nullptr;
+    a.dbias = h.has_db ? db : nullptr;
+    a.down_fmt = (const int *)put(h.down_fmt.data(), (size_t)n * 4);
+    a.p_off = (const int *)put(h.p_off.data(), (size_t)(n + 1) * 4);
+    a.p_row = (const int *)put(h.p_row.data(), (size_t)h.P * 4);
+    a.p_w = (const float *)put(h.p_w.data(), (size_t)h.P * 4);
+    a.r_off = (const int *)put(h.r_off.data(), (size_t)(k + 1) * 4);
+    a.r_pair = (const int *)put(h.r_pair.data(), (size_t)h.P * 4);
+    (void)P;
+    a.xin = (const float *)(dev + L.xin);
+    a.xq = q8_view(dev + L.xq, std::max(k, 1), h.D, a.xin);
+    a.hidden = (float *)(dev + L.hidden);
+    a.hq = q8_view(dev + L.hq, std::max(h.P, 1), h.I, a.hidden);
+    a.part = (float *)(dev + L.part);
+    a.out = (float *)(dev + L.out);
+    a.n = n;
+    a.k = k;
+    a.P = h.P;
+    a.D = h.D;
+    a.I = h.I;
+    a.act = h.act;
+    a.gate_fmt = h.gate_fmt;
+    a.gate_rb = row_bytes(h.gate_fmt, h.D);
+    return a;
+}
+
+/* The synchronous host-pointer MoE call behind every reference MoE symbol. */
+/* q8 rows on the device -> the reference's 296-byte blocks on the host */
+void q8_to_blocks(const Q8Rows &q, int nrows, void *out_blocks) {
+    const size_t nq = (size_t)nrows * q.nb;
+    std::vector<int8_t> qs(nq * 256);
+    std::vector<float> d(nq);
+    std::vector<int32_t> s32(nq * 8), sum(nq);
+    HIPCHECK(hipMemcpyAsync(qs.data(), q.qs, qs.size(), hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipMemcpyAsync(d.data(), q.d, nq * 4, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipMemcpyAsync(s32.data(), q.s32, nq * 32, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipMemcpyAsync(sum.data(), q.sum, nq * 4, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+    uint8_t *o = (uint8_t *)out_blocks;
+    for (size_t i = 0; i < nq; i++) {
+        uint8_t *blk = o + i * 296;
+        memcpy(blk, &d[i], 4);
+        memcpy(blk + 4, &sum[i], 4);
+        memcpy(blk + 8, &s32[i * 8], 32);
+        memcpy(blk + 40, &qs[i * 256], 256);
+    }
+}
+
+void moe_host(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs, const void *const *down_ptrs,
+              int gate_fmt, const int *down_fmts, const float *const *gate_bias, const float *const *up_bias,
+              const float *const *down_bias, int act, int n, const float *row_weights, const float *inputs,
+              float *output, int k, int D, int I, float *dbg_hidden = nullptr, void *dbg_hq = nullptr) {
+    if (!validate_moe(gate_fmt, down_fmts, n, k, D, I, act)) return;
+    if (n == 0 || k == 0) return;
+    ensure_init();
+    HostPlan h;
+    h.n = n;
+    h.k = k;
+    h.D = D;
+    h.I = I;
+    h.act = act;
+    h.gate_fmt = gate_fmt;
+    h.down_fmt.assign(down_fmts, down_fmts + n);
+    build_pairs(h, row_weights);
+    if (h.P == 0) return;   /* every weight is zero: output unchanged */
+
+    Layout L = plan_layout(h);
+    Bump bump;
+    bump.off = L.total;
+    Stager sg;
+    sg.bump = &bump;
+    const size_t grb = (size_t)I * row_bytes(gate_fmt, D);
+    std::vector<std::pair<uint64_t *, bool>> fix;   /* pointers that are arena offsets */
+    h.gate.resize(n);
+    h.up.resize(n);
+    h.down.resize(n);
+    h.gbias.assign(n, 0);
+    h.ubias.assign(n, 0);
+    h.dbias.assign(n, 0);
+    h.has_gb = gate_bias != nullptr;
+    h.has_ub = up_bias != nullptr;
+    h.has_db = down_bias != nullptr;
+    if (h.has_gb != h.has_ub) {
+        set_err("moe: gate and up biases must both be given or both be NULL");
+        return;
+    }
+    std::vector<char> staged_flags;
+    struct Fix {
+        std::vector<uint64_t> *vec;
+        int idx;
+    };
+    std::vector<Fix> fixes;
+    auto res = [&](std::vector<uint64_t> &vec, int e, const void *p, size_t bytes) {
+        if (!p) {
+            vec[e] = 0;
+            return;
+        }
+        bool st;
+        vec[e] = sg.resolve(p, bytes, &st);
+        if (st) fixes.push_back({&vec, e});
+    };
+    for (int e = 0; e < n; e++) {
+        if (h.p_off[e + 1] == h.p_off[e]) {   /* inactive expert: never read */
+            h.gate[e] = h.up[e] = h.down[e] = 0;
+            continue;
+        }
+        res(h.gate, e, gate_ptrs[e], grb);
+        res(h.up, e, up_ptrs[e], grb);
+        res(h.down, e, down_ptrs[e], (size_t)D * row_bytes(down_fmts[e], I));
+        if (h.has_gb) res(h.gbias, e, gate_bias[e], (size_t)I * 4);
+        if (h.has_ub) res(h.ubias, e, up_bias[e], (size_t)I * 4);
+        if (h.has_db) res(h.dbias, e, down_bias[e], (size_t)D * 4);
+    }
+    uint8_t *dev = arena(bump.off);
+    for (auto &f : fixes) (*f.vec)[f.idx] += (uint64_t)(uintptr_t)dev;
+
+    const size_t io_len = (size_t)k * D * 4;
+    uint8_t *img = pinned(L.tables_len + 2 * io_len);
+    MoeArgs a = plan_args(h, L, dev, img);
+    memcpy(img + L.tables_len, inputs, io_len);
+    memcpy(img + L.tables_len + io_len, output, io_len);
+    HIPCHECK(hipMemcpyAsync(dev + L.tables, img, L.tables_len, hipMemcpyHostToDevice, g.st));
+    HIPCHECK(hipMemcpyAsync(dev + L.xin, img + L.tables_len, io_len, hipMemcpyHostToDevice, g.st));
+    HIPCHECK(hipMemcpyAsync(dev + L.out, img + L.tables_len + io_len, io_len, hipMemcpyHostToDevice, g.st));
+    for (auto &it : sg.items) HIPCHECK(hipMemcpyAsync(dev + it.off, it.host, it.n, hipMemcpyHostToDevice, g.st));
+    launch_moe(a, h.fmts_present.data(), (int)h.fmts_present.size(), g.st);
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipMemcpyAsync(img, dev + L.out, io_len, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+    memcpy(output, img, io_len);
+    if (dbg_hidden)
+        HIPCHECK(hipMemcpy(dbg_hidden, a.hidden, (size_t)h.P * I * 4, hipMemcpyDeviceToHost));
+    if (dbg_hq) q8_to_blocks(a.hq, h.P, dbg_hq);
+}
+
+void matmul_host(int fmt, const void *mat, const float *bias, const float *input, float *output, int nrows,
+                 int ncols) {
+    if (!fmt_ok(fmt)) {
+        set_err("tg_matmul: unknown format %d", fmt);
+        return;
+    }
+    if (ncols <= 0 || ncols % 32 || nrows < 0) {
+        set_err("tg_matmul: ncols (%d) must be a positive multiple of 32", ncols);
+        return;
+    }
+    if (nrows == 0) return;
+    ensure_init();
+    const size_t rb = row_bytes(fmt, ncols);
+    Bump b;
+    const size_t o_in = b.take((size_t)ncols * 4);
+    const size_t o_q = b.take(q8_bytes(1, ncols));
+    const size_t o_out = b.take((size_t)nrows * 4);
+    Stager sg;
+    sg.bump = &b;
+    bool st_m = false, st_b = false;
+    uintptr_t m = sg.resolve(mat, (size_t)nrows * rb, &st_m);
+    uintptr_t bi = bias ? sg.resolve(bias, (size_t)nrows * 4, &st_b) : 0;
+    uint8_t *dev = arena(b.off);
+    if (st_m) m += (uintptr_t)dev;
+    if (bias && st_b) bi += (uintptr_t)dev;
+    HIPCHECK(hipMemcpyAsync(dev + o_in, input, (size_t)ncols * 4, hipMemcpyHostToDevice, g.st));
+    for (auto &it : sg.items) HIPCHECK(hipMemcpyAsync(dev + it.off, it.host, it.n, hipMemcpyHostToDevice, g.st));
+    Q8Rows q = q8_view(dev + o_q, 1, ncols, (const float *)(dev + o_in));
+    if (fmt != TG_FMT_F16) launch_quantize((const float *)(dev + o_in), ncols, 1, ncols, q, g.st);
+    launch_gemv(fmt, (const uint8_t *)m, nrows, ncols, (const float *)bi, q, 1, (float *)(dev + o_out), nrows, g.st);
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipMemcpyAsync(output, dev + o_out, (size_t)nrows * 4, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+}
+
+}  // namespace
+
+/* ===================== reference ABI (tinygiant/_lib.py) ===================== */
+
+TG_API void tg_moe_forward_rows_v2(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs,
+                                   const void *const *down_ptrs, int gate_fmt, const int *down_fmts,
+                                   const float *const *gate_bias, const float *const *up_bias,
+                                   const float *const *down_bias, int act, int n_experts, const float *row_weights,
+                                   const float *inputs, float *output, int k, int embed_dim, int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    moe_host(gate_ptrs, up_ptrs, down_ptrs, gate_fmt, down_fmts, gate_bias, up_bias, down_bias, act, n_experts,
+             row_weights, inputs, output, k, embed_dim, inter_dim);
+}
+
+/* tg_moe_forward_rows_v2 that also returns the stage outputs: the hidden
+ * rows [pairs][inter_dim] (f32, pairs expert-major in gather order) and their
+ * q8 quantization as 296-byte blocks [pairs][ceil(inter_dim/256)]. */
+TG_API void tg_hip_moe_forward_stages(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs,
+                                      const void *const *down_ptrs, int gate_fmt, const int *down_fmts,
+                                      const float *const *gate_bias, const float *const *up_bias,
+                                      const float *const *down_bias, int act, int n_experts,
+                                      const float *row_weights, const float *inputs, float *output, int k,
+                                      int embed_dim, int inter_dim, float *hidden_out, void *hq_blocks_out) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    moe_host(gate_ptrs, up_ptrs, down_ptrs, gate_fmt, down_fmts, gate_bias, up_bias, down_bias, act, n_experts,
+             row_weights, inputs, output, k, embed_dim, inter_dim, hidden_out, hq_blocks_out);
+}
+
+TG_API void tg_moe_forward_rows(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs,
+                                const void *const *down_ptrs, const int *down_fmts, int n_experts,
+                                const float *row_weights, const float *inputs, float *output, int k, int embed_dim,
+                                int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    moe_host(gate_ptrs, up_ptrs, down_ptrs, TG_FMT_Q4K, down_fmts, nullptr, nullptr, nullptr, TG_ACT_SILU,
+             n_experts, row_weights, inputs, output, k, embed_dim, inter_dim);
+}
+
+/* tg_expert_forward_mixed down codes (csrc/libtinygiant.c:1113-1124):
+ * 1 = f16, 2 = q6_K, anything else = q4_K */
+static int mixed_down_fmt(int code) { return code == 1 ? TG_FMT_F16 : code == 2 ? TG_FMT_Q6K : TG_FMT_Q4K; }
+
+TG_API void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *up_q4, const void *down_data,
+                                    int down_format, const float *input, float *output, float weight, int embed_dim,
+                                    int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const uint8_t *g1[1] = {gate_q4}, *u1[1] = {up_q4};
+    const void *d1[1] = {down_data};
+    int f1[1] = {mixed_down_fmt(down_format)};
+    float w1[1] = {weight};
+    moe_host(g1, u1, d1, TG_FMT_Q4K, f1, nullptr, nullptr, nullptr, TG_ACT_SILU, 1, w1, input, output, 1,
+             embed_dim, inter_dim);
+}
+
+TG_API void tg_expert_forward(const uint8_t *q4_data, const float *input, float *output, float weight,
+                              int embed_dim, int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    /* [gate | up | down], all Q4_K (csrc/libtinygiant.c:1040-1049) */
+    const size_t gate_bytes = (size_t)inter_dim * (embed_dim / 256) * 144;
+    const uint8_t *g1[1] = {q4_data}, *u1[1] = {q4_data + gate_bytes};
+    const void *d1[1] = {q4_data + 2 * gate_bytes};
+    int f1[1] = {TG_FMT_Q4K};
+    float w1[1] = {weight};
+    moe_host(g1, u1, d1, TG_FMT_Q4K, f1, nullptr, nullptr, nullptr, TG_ACT_SILU, 1, w1, input, output, 1,
+             embed_dim, inter_dim);
+}
+
+TG_API void tg_expert_forward_rows(const uint8_t *gate_q4, const uint8_t *up_q4, const void *down_data,
+                                   int down_format, const float *inputs, float *output, const float *weights, int k,
+                                   int embed_dim, int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const uint8_t *g1[1] = {gate_q4}, *u1[1] = {up_q4};
+    const void *d1[1] = {down_data};
+    int f1[1] = {mixed_down_fmt(down_format)};
+    moe_host(g1, u1, d1, TG_FMT_Q4K, f1, nullptr, nullptr, nullptr, TG_ACT_SILU, 1, weights, inputs, output, k,
+             embed_dim, inter_dim);
+}
+
+TG_API void tg_moe_forward(const uint8_t **expert_ptrs, const float *weights, int n_experts, const float *input,
+                           float *output, int embed_dim, int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    /* csrc/libtinygiant.c:1452-1460: zero the output, then one all-Q4_K expert each */
+    memset(output, 0, (size_t)embed_dim * sizeof(float));
+    if (n_experts <= 0) return;
+    const size_t gate_bytes = (size_t)inter_dim * (embed_dim / 256) * 144;
+    std::vector<const uint8_t *> g(n_experts), u(n_experts);
+    std::vector<const void *> d(n_experts);
+    std::vector<int> f(n_experts, TG_FMT_Q4K);
+    for (int e = 0; e < n_experts; e++) {
+        g[e] = expert_ptrs[e];
+        u[e] = expert_ptrs[e] + gate_bytes;
+        d[e] = expert_ptrs[e] + 2 * gate_bytes;
+    }
+    moe_host(g.data(), u.data(), d.data(), TG_FMT_Q4K, f.data(), nullptr, nullptr, nullptr, TG_ACT_SILU,
+             n_experts, weights, input, output, 1, embed_dim, inter_dim);
+}
+
+TG_API void tg_matmul(int fmt, const void *mat, const float *bias, const float *input, float *output, int nrows,
+                      int ncols) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    matmul_host(fmt, mat, bias, input, output, nrows, ncols);
+}
+
+TG_API void tg_matmul_q4k(const uint8_t *q4_matrix, const float *input, float *output, int nrows, int ncols) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    matmul_host(TG_FMT_Q4K, q4_matrix, nullptr, input, output, nrows, ncols);
+}
+
+TG_API void tg_matmul_q6k(const uint8_t *q6_matrix, const float *input, float *output, int nrows, int ncols) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    matmul_host(TG_FMT_Q6K, q6_matrix, nullptr, input, output, nrows, ncols);
+}
+
+TG_API size_t tg_row_bytes(int fmt, int ncols) {
+    switch (fmt) {
+        case TG_FMT_Q4K: return (size_t)(ncols / 256) * 144;
+        case TG_FMT_Q6K: return (size_t)(ncols / 256) * 210;
+        case TG_FMT_MXFP4: return (size_t)(ncols / 32) * 17;
+        case TG_FMT_Q80: return (size_t)(ncols / 32) * 34;
+        default: return (size_t)ncols * 2;
+    }
+}
+
+TG_API void tg_set_threads(int n) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    g_threads = n < 1 ? 1 : n;
+}
+
+TG_API int tg_get_threads(void) { return g_threads; }
+
+/* The reference pins host pages (csrc/libtinygiant.c:1566-1571).  Here the
+ * range is copied into HBM once; every later pointer inside it resolves to
+ * the device copy.  Returns 0 on success, -1 if HBM is exhausted. */
+TG_API int tg_mlock(const void *addr, size_t len) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return do_register(addr, len);
+}
+
+/* ===================== tg_hip_* extensions ===================== */
+
+TG_API const char *tg_hip_last_error(void) { return g_err; }
+
+TG_API void tg_hip_clear_error(void) { g_err[0] = 0; }
+
+TG_API int tg_hip_register(const void *addr, size_t len) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return do_register(addr, len);
+}
+
+TG_API int tg_hip_unregister(const void *addr) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    auto it = g_regs.find((uintptr_t)addr);
+    if (it == g_regs.end()) return -1;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipFree(it->second.dev));
+    g_regs.erase(it);
+    return 0;
+}
+
+TG_API size_t tg_hip_registered_bytes(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    size_t s = 0;
+    for (auto &kv : g_regs) s += kv.second.len;
+    return s;
+}
+
+TG_API const void *tg_hip_device_ptr(const void *host, size_t n) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return lookup(host, n);
+}
+
+TG_API void *tg_hip_stream(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    return (void *)g.st;
+}
+
+TG_API void *tg_hip_malloc(size_t n) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    void *p = nullptr;
+    hipError_t e = hipMalloc(&p, n ? n : 1);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        set_err("tg_hip_malloc(%zu): %s", n, hipGetErrorString(e));
+        return nullptr;
+    }
+    return p;
+}
+
+TG_API void tg_hip_free(void *p) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!p) return;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipFree(p));
+}
+
+TG_API void tg_hip_memcpy_h2d(void *dst, const void *src, size_t n) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    HIPCHECK(hipMemcpyAsync(dst, src, n, hipMemcpyHostToDevice, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+}
+
+TG_API void tg_hip_memcpy_d2h(void *dst, const void *src, size_t n) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    HIPCHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+}
+
+TG_API void tg_hip_memcpy_d2d(void *dst, const void *src, size_t n, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    HIPCHECK(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, stream ? (hipStream_t)stream : g.st));
+}
+
+TG_API void tg_hip_synchronize(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipDeviceSynchronize());
+}
+
+/* Seeded synthetic tensor (tg_synth.h) written on the device / on the host. */
+TG_API void tg_hip_synth_fill(int kind, uint64_t seed, void *dst_dev, uint64_t nbytes, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    if (((uintptr_t)dst_dev & 7) != 0) {
+        set_err("tg_hip_synth_fill: destination must be 8-byte aligned");
+        return;
+    }
+    launch_synth_fill(kind, seed, dst_dev, nbytes, stream ? (hipStream_t)stream : g.st);
+    HIPCHECK(hipGetLastError());
+}
+
+TG_API void tg_hip_synth_fill_host(int kind, uint64_t seed, void *dst, uint64_t nbytes) {
+    uint8_t *p = (uint8_t *)dst;
+    for (uint64_t i = 0; i < nbytes; i++) p[i] = tg_syn_byte(kind, seed, i);
+}
+
+/* q8 quantization of nrows rows of ncols floats, returned in the reference's
+ * 296-byte q8_block layout (csrc/libtinygiant.c:159-164). */
+TG_API void tg_hip_quantize_q8(const float *x, int ncols, int nrows, void *out_blocks) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (ncols <= 0 || ncols % 32 || nrows <= 0) {
+        set_err("tg_hip_quantize_q8: ncols must be a positive multiple of 32");
+        return;
+    }
+    ensure_init();
+    Bump b;
+    const size_t o_in = b.take((size_t)nrows * ncols * 4);
+    const size_t o_q = b.take(q8_bytes(nrows, ncols));
+    uint8_t *dev = arena(b.off);
+    HIPCHECK(hipMemcpyAsync(dev + o_in, x, (size_t)nrows * ncols * 4, hipMemcpyHostToDevice, g.st));
+    Q8Rows q = q8_view(dev + o_q, nrows, ncols, nullptr);
+    launch_quantize((const float *)(dev + o_in), ncols, nrows, ncols, q, g.st);
+    HIPCHECK(hipGetLastError());
+    q8_to_blocks(q, nrows, out_blocks);
+}
+
+/* Per-sub-block integer sums of every row of a weight matrix against one
+ * q8-quantized activation row, from the same decode path as the GEMV:
+ * Q4_K 8 per 256-block, Q6_K 16 per 256-block, MXFP4/Q8_0 1 per 32-block. */
+TG_API int tg_hip_isums(int fmt, const void *mat, int nrows, int ncols, const float *x, int32_t *out) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!fmt_ok(fmt) || fmt == TG_FMT_F16 || ncols <= 0 || ncols % 32 || nrows <= 0) {
+        set_err("tg_hip_isums: bad format or shape");
+        return -1;
+    }
+    ensure_init();
+    const int nsr = (fmt == TG_FMT_Q4K) ? ncols / 256 * 8 : (fmt == TG_FMT_Q6K) ? ncols / 256 * 16 : ncols / 32;
+    const size_t rb = row_bytes(fmt, ncols);
+    Bump b;
+    const size_t o_in = b.take((size_t)ncols * 4);
+    const size_t o_q = b.take(q8_bytes(1, ncols));
+    const size_t o_out = b.take((size_t)nrows * nsr * 4);
+    const size_t o_m = b.take((size_t)nrows * rb);
+    uint8_t *dev = arena(b.off);
+    HIPCHECK(hipMemcpyAsync(dev + o_in, x, (size_t)ncols * 4, hipMemcpyHostToDevice, g.st));
+    HIPCHECK(hipMemcpyAsync(dev + o_m, mat, (size_t)nrows * rb, hipMemcpyHostToDevice, g.st));
+    HIPCHECK(hipMemsetAsync(dev + o_out, 0, (size_t)nrows * nsr * 4, g.st));
+    Q8Rows q = q8_view(dev + o_q, 1, ncols, nullptr);
+    launch_quantize((const float *)(dev + o_in), ncols, 1, ncols, q, g.st);
+    launch_isums(fmt, dev + o_m, nrows, ncols, q, nsr, (int32_t *)(dev + o_out), g.st);
+    HIPCHECK(hipGetLastError());
+    HIPCHECK(hipMemcpyAsync(out, dev + o_out, (size_t)nrows * nsr * 4, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+    return nsr;
+}
+
+/* ---- device-resident MoE plans (pointers already in HBM) ---- */
+
+struct tg_hip_moe_plan {
+    HostPlan h;
+    Layout L;
+    uint8_t *dev;
+    MoeArgs a;
+};
+
+TG_API tg_hip_moe_plan *tg_hip_moe_plan_create(const void *const *gate_dev, const void *const *up_dev,
+                                               const void *const *down_dev, int gate_fmt, const int *down_fmts,
+                                               const float *const *gate_bias_dev, const float *const *up_bias_dev,
+                                               const float *const *down_bias_dev, int act, int n_experts,
+                                               const float *row_weights, int k, int embed_dim, int inter_dim) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!validate_moe(gate_fmt, down_fmts, n_experts, k, embed_dim, inter_dim, act)) return nullptr;
+    if (n_experts == 0 || k == 0) {
+        set_err("tg_hip_moe_plan_create: empty plan");
+        return nullptr;
+    }
+    ensure_init();
+    tg_hip_moe_plan *p = new tg_hip_moe_plan();
+    HostPlan &h = p->h;
+    h.n = n_experts;
+    h.k = k;
+    h.D = embed_dim;
+    h.I = inter_dim;
+    h.act = act;
+    h.gate_fmt = gate_fmt;
+    h.down_fmt.assign(down_fmts, down_fmts + n_experts);
+    build_pairs(h, row_weights);
+    h.has_gb = gate_bias_dev != nullptr;
+    h.has_ub = up_bias_dev != nullptr;
+    h.has_db = down_bias_dev != nullptr;
+    for (int e = 0; e < n_experts; e++) {
+        h.gate.push_back((uint64_t)(uintptr_t)gate_dev[e]);
+        h.up.push_back((uint64_t)(uintptr_t)up_dev[e]);
+        h.down.push_back((uint64_t)(uintptr_t)down_dev[e]);
+        h.gbias.push_back(h.has_gb ? (uint64_t)(uintptr_t)gate_bias_dev[e] : 0);
+        h.ubias.push_back(h.has_ub ? (uint64_t)(uintptr_t)up_bias_dev[e] : 0);
+        h.dbias.push_back(h.has_db ? (uint64_t)(uintptr_t)down_bias_dev[e] : 0);
+    }
+    p->L = plan_layout(h);
+    HIPCHECK(hipMalloc(&p->dev, p->L.total));
+    std::vector<uint8_t> img(p->L.tables_len);
+    p->a = plan_args(h, p->L, p->dev, img.data());
+    HIPCHECK(hipMemcpy(p->dev + p->L.tables, img.data(), img.size(), hipMemcpyHostToDevice));
+    return p;
+}
+
+/* Queues the layer on `stream` (null = the library stream): quantize inputs,
+ * gate/up + act, quantize hidden, down, combine into `output` (accumulated).
+ * Launches only kernels, so it can be captured into a HIP graph. */
+TG_API void tg_hip_moe_plan_run(tg_hip_moe_plan *p, const float *inputs_dev, float *output_dev, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!p) return;
+    if (p->h.P == 0) return;
+    MoeArgs a = p->a;
+    a.xin = inputs_dev;
+    a.xq.f = inputs_dev;
+    a.out = output_dev;
+    launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), stream ? (hipStream_t)stream : g.st);
+    HIPCHECK(hipGetLastError());
+}
+
+TG_API int tg_hip_moe_plan_pairs(const tg_hip_moe_plan *p) { return p ? p->h.P : 0; }
+
+TG_API void tg_hip_moe_plan_destroy(tg_hip_moe_plan *p) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!p) return;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipFree(p->dev));
+    delete p;
+}
+
+/* y[j][r] = dot(W[r], x_j) + bias[r] for k rows of device-resident input. */
+TG_API void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_dev, const float *inputs_dev,
+                              float *outputs_dev, int nrows, int ncols, int k, void *scratch_dev, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!fmt_ok(fmt) || ncols <= 0 || ncols % 32 || nrows <= 0 || k <= 0) {
+        set_err("tg_hip_matmul_dev: bad format or shape");
+        return;
+    }
+    ensure_init();
+    hipStream_t st = stream ? (hipStream_t)stream : g.st;
+    Q8Rows q = q8_view((uint8_t *)scratch_dev, k, ncols, inputs_dev);
+    if (fmt != TG_FMT_F16) launch_quantize(inputs_dev, ncols, k, ncols, q, st);
+    launch_gemv(fmt, (const uint8_t *)mat_dev, nrows, ncols, bias_dev, q, k, outputs_dev, nrows, st);
+    HIPCHECK(hipGetLastError());
+}
+
+TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k, ncols); }
+
+TG_API void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n, float eps,
+                                void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    launch_rms_norm(x_dev, w_dev, out_dev, nrows, n, eps, stream ? (hipStream_t)stream : g.st);
+    HIPCHECK(hipGetLastError());
+}
+
+/* ---- device-resident multi-layer decode step ----
+ * h <- h + MoE_l(RMSNorm(h)) for l = 0..L-1 on k rows of width D, the chain
+ * tinygiant/engine.py:281-282,335-341 runs per layer (RMSNorm weight 1 when
+ * norm_w is NULL).  The launch sequence is captured once into a HIP graph
+ * and replayed by tg_hip_decode_run. */
+
+struct tg_hip_decode {
+    std::vector<tg_hip_moe_plan *> plans;
+    std::vector<const float *> norm_w;
+    int L = 0, D = 0, k = 0;
+    float eps = 1e-6f;
+    float *h = nullptr;
+    float *x = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+static void decode_enqueue(tg_hip_decode *d, hipStream_t st) {
+    for (int l = 0; l < d->L; l++) {
+        launch_rms_norm(d->h, d->norm_w.empty() ? nullptr : d->norm_w[l], d->x, d->k, d->D, d->eps, st);
+        tg_hip_moe_plan *p = d->plans[l];
+        if (p->h.P == 0) continue;
+        MoeArgs a = p->a;
+        a.xin = d->x;
+        a.xq.f = d->x;
+        a.out = d->h;
+        launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), st);
+    }
+}
+
+TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers, const float *const *norm_w_dev,
+                                           float eps, float *h_dev, int use_graph) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (n_layers <= 0 || !plans || !h_dev) {
+        set_err("tg_hip_decode_create: bad arguments");
+        return nullptr;
+    }
+    ensure_init();
+    tg_hip_decode *d = new tg_hip_decode();
+    d->L = n_layers;
+    d->D = plans[0]->h.D;
+    d->k = plans[0]->h.k;
+    for (int l = 0; l < n_layers; l++) {
+        if (!plans[l] || plans[l]->h.D != d->D || plans[l]->h.k != d->k) {
+            set_err("tg_hip_decode_create: layer %d has a different shape", l);
+            delete d;
+            return nullptr;
+        }
+        d->plans.push_back(plans[l]);
+        if (norm_w_dev) d->norm_w.push_back(norm_w_dev[l]);
+    }
+    d->eps = eps;
+    d->h = h_dev;
+    HIPCHECK(hipMalloc(&d->x, (size_t)d->k * d->D * 4));
+    if (use_graph) {
+        hipStream_t cs;
+        HIPCHECK(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+        HIPCHECK(hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal));
+        decode_enqueue(d, cs);
+        HIPCHECK(hipStreamEndCapture(cs, &d->graph));
+        HIPCHECK(hipGraphInstantiate(&d->exec, d->graph, nullptr, nullptr, 0));
+        HIPCHECK(hipStreamDestroy(cs));
+    }
+    return d;
+}
+
+TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d) return;
+    hipStream_t st = stream ? (hipStream_t)stream : g.st;
+    if (d->exec)
+        HIPCHECK(hipGraphLaunch(d->exec, st));
+    else
+        decode_enqueue(d, st);
+    HIPCHECK(hipGetLastError());
+}
+
+TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d) return;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    if (d->exec) HIPCHECK(hipGraphExecDestroy(d->exec));
+    if (d->graph) HIPCHECK(hipGraphDestroy(d->graph));
+    HIPCHECK(hipFree(d->x));
+    delete d;
+}
+
+/* Runs `iters` decode steps back to back on the library stream between two
+ * HIP events and returns the elapsed milliseconds. */
+TG_API float tg_hip_decode_time(tg_hip_decode *d, int iters) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d || iters <= 0) return 0.f;
+    hipEvent_t a, b;
+    HIPCHECK(hipEventCreate(&a));
+    HIPCHECK(hipEventCreate(&b));
+    HIPCHECK(hipEventRecord(a, g.st));
+    for (int i = 0; i < iters; i++) tg_hip_decode_run(d, nullptr);
+    HIPCHECK(hipEventRecord(b, g.st));
+    HIPCHECK(hipEventSynchronize(b));
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, a, b));
+    HIPCHECK(hipEventDestroy(a));
+    HIPCHECK(hipEventDestroy(b));
+    return ms;
+}
+
+/* One eager decode step with HIP events around every kernel; returns the
+ * summed milliseconds per kernel class in ms_out[6] = {rms_norm,
+ * quantize(x), gate/up, quantize(hidden), down, combine} and their launch
+ * counts in n_out[6]. */
+TG_API void tg_hip_decode_kernel_times(tg_hip_decode *d, float *ms_out, int *n_out) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d) return;
+    for (int i = 0; i < 6; i++) {
+        ms_out[i] = 0.f;
+        n_out[i] = 0;
+    }
+    std::vector<hipEvent_t> ev;
+    std::vector<int> cls;
+    auto mark = [&](int c) {
+        hipEvent_t e;
+        HIPCHECK(hipEventCreate(&e));
+        HIPCHECK(hipEventRecord(e, g.st));
+        ev.push_back(e);
+        cls.push_back(c);
+    };
+    for (int l = 0; l < d->L; l++) {
+        mark(-1);
+        launch_rms_norm(d->h, d->norm_w.empty() ? nullptr : d->norm_w[l], d->x, d->k, d->D, d->eps, g.st);
+        mark(0);
+        tg_hip_moe_plan *p = d->plans[l];
+        if (p->h.P == 0) continue;
+        MoeArgs a = p->a;
+        a.xin = d->x;
+        a.xq.f = d->x;
+        a.out = d->h;
+        std::function<void(int)> mk = [&](int c) { mark(c); };
+        launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), g.st, &mk);
+    }
+    HIPCHECK(hipStreamSynchronize(g.st));
+    for (size_t i = 1; i < ev.size(); i++) {
+        if (cls[i] < 0) continue;
+        float ms;
+        HIPCHECK(hipEventElapsedTime(&ms, ev[i - 1], ev[i]));
+        ms_out[cls[i]] += ms;
+        n_out[cls[i]] += 1;
+    }
+    for (auto e : ev) HIPCHECK(hipEventDestroy(e));
+}
+
+TG_API void tg_hip_device_name(char *buf, int n) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    hipDeviceProp_t pr;
+    HIPCHECK(hipGetDeviceProperties(&pr, g.dev));
+    snprintf(buf, (size_t)n, "%s (%s, %d CUs)", pr.name, pr.gcnArchName, pr.multiProcessorCount);
+}

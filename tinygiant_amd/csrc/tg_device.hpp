@@ -1,0 +1,414 @@
+/*
+ * tg_device.hpp -- CDNA4 (gfx950) device building blocks for the fused
+ * quantized GEMV family: bounds-checked buffer loads, the reference's f16
+ * decode, per-format "items" (the slice of a weight row one lane decodes),
+ * and wave-segment reductions.
+ *
+ * Lane model.  A weight row of `ncols` values is cut into items:
+ *   Q4_K   4 items per 256-block  (one 32-byte quarter of qs[] + the 16-byte
+ *          block header; sub-blocks 2g and 2g+1)
+ *   Q6_K   4 items per 256-block  (half h, lanes l0..l0+15: 48 bytes of
+ *          ql/qh, 4 int8 sub-scales, d)
+ *   MXFP4  1 item per 32-block    (17 bytes)
+ *   Q8_0   1 item per 32-block    (34 bytes)
+ *   F16    1 item per 8 values    (16 bytes, f32 activations)
+ * A wave is split into 64/S segments of S lanes (S a power of two); each
+ * segment owns one weight row per step and lane s of the segment decodes
+ * items s, s+S, s+2S, ...  The integer sums of every item are exact; the
+ * float combine of an item follows the reference's formula, and the
+ * segment sum is a butterfly over the S lanes.
+ */
+#ifndef TG_DEVICE_HPP
+#define TG_DEVICE_HPP
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tg_common.h"
+
+namespace tg {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+/* ---- bounds-checked raw buffer loads (out-of-range lanes read zero) ---- */
+
+struct Buf {
+    __amdgpu_buffer_rsrc_t r;
+};
+
+__device__ inline Buf make_buf(const void *p, uint32_t nbytes) {
+    Buf b;
+    b.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)nbytes, 0x00020000);
+    return b;
+}
+__device__ inline u32x4 ld16(Buf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, 0);
+}
+__device__ inline u32x2 ld8(Buf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)off, 0, 0);
+}
+__device__ inline uint32_t ld4(Buf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)off, 0, 0);
+}
+__device__ inline uint32_t ld2(Buf b, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.r, (int)off, 0, 0);
+}
+__device__ inline uint32_t ld1(Buf b, uint32_t off) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(b.r, (int)off, 0, 0);
+}
+
+/* f16 -> f32 exactly as csrc/libtinygiant.c:128-137 decodes it: IEEE for
+ * every finite pattern; exponent 31 yields the bit pattern 0xB7800000|m<<13
+ * that the reference's 32-bit shift produces. */
+__device__ inline float ref_f16(uint32_t h) {
+    h &= 0xFFFFu;
+    float f = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    if ((h & 0x7C00u) == 0x7C00u) f = __uint_as_float(0xB7800000u | ((h & 0x3FFu) << 13));
+    return f;
+}
+
+/* e8m0_to_fp32_half (csrc/libtinygiant.c:516-519) */
+__device__ inline float e8m0_half(uint32_t e) {
+    uint32_t bits = e < 2 ? (0x00200000u << e) : ((e - 1u) << 23);
+    return __uint_as_float(bits);
+}
+
+__device__ inline int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+/* ---- segment reductions (segments of S lanes, S power of two <= 64) ---- */
+
+template <int S>
+__device__ inline float seg_sum(float v) {
+#pragma unroll
+    for (int o = S / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ inline float seg_sum_rt(float v, int S) {
+    for (int o = S / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+/* ---- q8 activation rows on the device ----
+ * Row r of an activation matrix with nb 256-blocks:
+ *   qs  int8[nb*256] (zero padded), d f32[nb] (block scale),
+ *   s32 int32[nb*8]  (32-element sums), s16 int32[nb*16] (16-element sums). */
+struct Q8Rows {
+    int8_t *qs;
+    float *d;
+    int32_t *s32;
+    int32_t *s16;
+    int32_t *sum;     /* per-block total (the reference's q8_block.sum) */
+    const float *f;   /* the unquantized f32 rows (used by F16 weights) */
+    int nb;
+    int fstride;      /* floats per f32 row */
+};
+
+struct Q8Row {
+    Buf qs, d, s32, s16, f;
+};
+
+__device__ inline Q8Row q8_row(const Q8Rows &a, int r) {
+    Q8Row x;
+    x.qs = make_buf(a.qs + (size_t)r * a.nb * 256, (uint32_t)a.nb * 256);
+    x.d = make_buf(a.d + (size_t)r * a.nb, (uint32_t)a.nb * 4);
+    x.s32 = make_buf(a.s32 + (size_t)r * a.nb * 8, (uint32_t)a.nb * 32);
+    x.s16 = make_buf(a.s16 + (size_t)r * a.nb * 16, (uint32_t)a.nb * 64);
+    x.f = make_buf(a.f + (size_t)r * a.fstride, (uint32_t)a.fstride * 4);
+    return x;
+}
+
+/* ====================== formats ====================== */
+
+/* ---- Q4_K: item = (block b, group g) ---- */
+struct FQ4K {
+    static constexpr int FMT = TG_FMT_Q4K;
+    static constexpr int ITEMS_PER_BLOCK = 4, BLOCK_VALS = 256, BLOCK_BYTES = 144;
+    static constexpr int NSUMS = 2;   /* integer sums per item */
+    struct W { u32x4 hdr, q0, q1; };
+    struct X { u32x4 a0, a1, b0, b1; int s_lo, s_hi; float d; };
+
+    __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
+        uint32_t p = row_off + (uint32_t)(item >> 2) * 144u;
+        uint32_t g = item & 3;
+        W r;
+        r.hdr = ld16(w, p);
+        r.q0 = ld16(w, p + 16 + 32 * g);
+        r.q1 = ld16(w, p + 32 + 32 * g);
+        return r;
+    }
+    __device__ static inline X load_x(const Q8Row &x, int item) {
+        uint32_t b = item >> 2, g = item & 3;
+        uint32_t o = b * 256 + 64 * g;
+        X r;
+        r.a0 = ld16(x.qs, o);
+        r.a1 = ld16(x.qs, o + 16);
+        r.b0 = ld16(x.qs, o + 32);
+        r.b1 = ld16(x.qs, o + 48);
+        u32x2 s = ld8(x.s32, (b * 8 + 2 * g) * 4);
+        r.s_lo = (int)s.x;
+        r.s_hi = (int)s.y;
+        r.d = __uint_as_float(ld4(x.d, b * 4));
+        return r;
+    }
+    __device__ static inline void isums(const W &w, const X &x, int *out) {
+        const uint32_t m = 0x0F0F0F0Fu;
+        int lo = 0, hi = 0;
+        lo = dot4(w.q0.x & m, x.a0.x, lo); lo = dot4(w.q0.y & m, x.a0.y, lo);
+        lo = dot4(w.q0.z & m, x.a0.z, lo); lo = dot4(w.q0.w & m, x.a0.w, lo);
+        lo = dot4(w.q1.x & m, x.a1.x, lo); lo = dot4(w.q1.y & m, x.a1.y, lo);
+        lo = dot4(w.q1.z & m, x.a1.z, lo); lo = dot4(w.q1.w & m, x.a1.w, lo);
+        hi = dot4((w.q0.x >> 4) & m, x.b0.x, hi); hi = dot4((w.q0.y >> 4) & m, x.b0.y, hi);
+        hi = dot4((w.q0.z >> 4) & m, x.b0.z, hi); hi = dot4((w.q0.w >> 4) & m, x.b0.w, hi);
+        hi = dot4((w.q1.x >> 4) & m, x.b1.x, hi); hi = dot4((w.q1.y >> 4) & m, x.b1.y, hi);
+        hi = dot4((w.q1.z >> 4) & m, x.b1.z, hi); hi = dot4((w.q1.w >> 4) & m, x.b1.w, hi);
+        out[0] = lo;
+        out[1] = hi;
+    }
+    /* get_scale_min_k4 (csrc/libtinygiant.c:146-155) for sub-blocks 2g, 2g+1 */
+    __device__ static inline void scales(const W &w, int g, int &sc_lo, int &m_lo, int &sc_hi, int &m_hi) {
+        uint32_t s0 = w.hdr.y, s1 = w.hdr.z, s2 = w.hdr.w;   /* scales[0..3], [4..7], [8..11] */
+        int j = 2 * g;
+        if (g < 2) {
+            sc_lo = (s0 >> (8 * j)) & 63;        m_lo = (s1 >> (8 * j)) & 63;
+            sc_hi = (s0 >> (8 * j + 8)) & 63;    m_hi = (s1 >> (8 * j + 8)) & 63;
+        } else {
+            int jl = j - 4, jh = j - 3;   /* 0..3 */
+            sc_lo = ((s2 >> (8 * jl)) & 0xF) | (((s0 >> (8 * jl + 6)) & 3) << 4);
+            m_lo = ((s2 >> (8 * jl + 4)) & 0xF) | (((s1 >> (8 * jl + 6)) & 3) << 4);
+            sc_hi = ((s2 >> (8 * jh)) & 0xF) | (((s0 >> (8 * jh + 6)) & 3) << 4);
+            m_hi = ((s2 >> (8 * jh + 4)) & 0xF) | (((s1 >> (8 * jh + 6)) & 3) << 4);
+        }
+    }
+    /* x.d * (d*(sc_lo*lo + sc_hi*hi) - dmin*(m_lo*bs_lo + m_hi*bs_hi)):
+     * both integer brackets are below 2^24, so they convert exactly. */
+    __device__ static inline float value(const W &w, const X &x, int item) {
+        int s[2];
+        isums(w, x, s);
+        int sc_lo, m_lo, sc_hi, m_hi;
+        scales(w, item & 3, sc_lo, m_lo, sc_hi, m_hi);
+        float d = ref_f16(w.hdr.x), dmin = ref_f16(w.hdr.x >> 16);
+        int A = sc_lo * s[0] + sc_hi * s[1];
+        int B = m_lo * x.s_lo + m_hi * x.s_hi;
+        return x.d * (d * (float)A - dmin * (float)B);
+    }
+    /* where this item's integer sums go in the per-row isum vector
+     * (8 sub-blocks per 256-block) */
+    __device__ static inline int isum_index(int item, int i) { return (item >> 2) * 8 + 2 * (item & 3) + i; }
+};
+
+/* ---- Q6_K: item = (block b, unit u): half h = u>>1, lanes l0 = 16*(u&1) ---- */
+struct FQ6K {
+    static constexpr int FMT = TG_FMT_Q6K;
+    static constexpr int ITEMS_PER_BLOCK = 4, BLOCK_VALS = 256, BLOCK_BYTES = 210;
+    static constexpr int NSUMS = 4;
+    struct W { u32x4 qla, qlb, qh; u32x2 sc; uint32_t d; };
+    struct X { u32x4 x0, x1, x2, x3; int s0, s1, s2, s3; float d; };
+
+    __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
+        uint32_t p = row_off + (uint32_t)(item >> 2) * 210u;
+        uint32_t u = item & 3, h = u >> 1, l0 = (u & 1) * 16;
+        W r;
+        r.qla = ld16(w, p + 64 * h + l0);
+        r.qlb = ld16(w, p + 64 * h + 32 + l0);
+        r.qh = ld16(w, p + 128 + 32 * h + l0);
+        r.sc = ld8(w, p + 192 + 8 * h);
+        r.d = ld2(w, p + 208);
+        return r;
+    }
+    __device__ static inline X load_x(const Q8Row &x, int item) {
+        uint32_t b = item >> 2, u = item & 3, h = u >> 1, l0 = (u & 1) * 16;
+        uint32_t o = b * 256 + 128 * h + l0;
+        X r;
+        r.x0 = ld16(x.qs, o);
+        r.x1 = ld16(x.qs, o + 32);
+        r.x2 = ld16(x.qs, o + 64);
+        r.x3 = ld16(x.qs, o + 96);
+        /* 16-element sums of groups 8h + (u&1) + 2q, q = 0..3 */
+        uint32_t sb = (b * 16 + 8 * h + (u & 1)) * 4;
+        r.s0 = (int)ld4(x.s16, sb);
+        r.s1 = (int)ld4(x.s16, sb + 8);
+        r.s2 = (int)ld4(x.s16, sb + 16);
+        r.s3 = (int)ld4(x.s16, sb + 24);
+        r.d = __uint_as_float(ld4(x.d, b * 4));
+        return r;
+    }
+    /* sum_i (q_i - 32) * x_i for the four 16-element groups: the unsigned
+     * 6-bit codes are dotted, then 32 * (16-element x sum) is subtracted */
+    __device__ static inline void isums(const W &w, const X &x, int *out) {
+        const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
+        int a0 = 0, a1 = 0, a2 = 0, a3 = 0;
+#define TG_Q6_COL(c)                                                         \
+        {                                                                    \
+            uint32_t la = w.qla.c, lb = w.qlb.c, hh = w.qh.c;                \
+            uint32_t q1 = (la & m4) | ((hh << 4) & m2);                      \
+            uint32_t q2 = (lb & m4) | ((hh << 2) & m2);                      \
+            uint32_t q3 = ((la >> 4) & m4) | (hh & m2);                      \
+            uint32_t q4 = ((lb >> 4) & m4) | ((hh >> 2) & m2);               \
+            a0 = dot4(q1, x.x0.c, a0);                                       \
+            a1 = dot4(q2, x.x1.c, a1);                                       \
+            a2 = dot4(q3, x.x2.c, a2);                                       \
+            a3 = dot4(q4, x.x3.c, a3);                                       \
+        }
+        TG_Q6_COL(x) TG_Q6_COL(y) TG_Q6_COL(z) TG_Q6_COL(w)
+#undef TG_Q6_COL
+        out[0] = a0 - 32 * x.s0;
+        out[1] = a1 - 32 * x.s1;
+        out[2] = a2 - 32 * x.s2;
+        out[3] = a3 - 32 * x.s3;
+    }
+    __device__ static inline float value(const W &w, const X &x, int item) {
+        int s[4];
+        isums(w, x, s);
+        int odd = item & 1;   /* sub-scale byte (u&1) + 2q of sc[8h..8h+7] */
+        int sc0 = (int)(int8_t)(w.sc.x >> (8 * odd));
+        int sc1 = (int)(int8_t)(w.sc.x >> (8 * odd + 16));
+        int sc2 = (int)(int8_t)(w.sc.y >> (8 * odd));
+        int sc3 = (int)(int8_t)(w.sc.y >> (8 * odd + 16));
+        int A = sc0 * s[0] + sc1 * s[1] + sc2 * s[2] + sc3 * s[3];
+        return ref_f16(w.d) * x.d * (float)A;
+    }
+    __device__ static inline int isum_index(int item, int i) {
+        int u = item & 3;
+        return (item >> 2) * 16 + 8 * (u >> 1) + (u & 1) + 2 * i;
+    }
+};
+
+/* ---- MXFP4: item = one 32-value block (e8m0 byte + 16 code bytes) ---- */
+struct FMXFP4 {
+    static constexpr int FMT = TG_FMT_MXFP4;
+    static constexpr int ITEMS_PER_BLOCK = 1, BLOCK_VALS = 32, BLOCK_BYTES = 17;
+    static constexpr int NSUMS = 1;
+    struct W { u32x4 c; uint32_t e; };
+    struct X { u32x4 a, b; float d; };
+
+    __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
+        uint32_t p = row_off + (uint32_t)item * 17u;
+        W r;
+        r.e = ld1(w, p);
+        r.c = ld16(w, p + 1);
+        return r;
+    }
+    __device__ static inline X load_x(const Q8Row &x, int item) {
+        uint32_t o = (uint32_t)(item >> 3) * 256 + (item & 7) * 32;
+        X r;
+        r.a = ld16(x.qs, o);
+        r.b = ld16(x.qs, o + 16);
+        r.d = __uint_as_float(ld4(x.d, (item >> 3) * 4));
+        return r;
+    }
+    /* doubled e2m1 table {0,1,2,3,4,6,8,12} by byte permute; codes 8..15 are
+     * the negatives, selected per byte from a second permute */
+    __device__ static inline uint32_t lut(uint32_t n) {
+        const uint32_t pos_lo = 0x03020100u, pos_hi = 0x0C080604u;
+        const uint32_t neg_lo = 0xFDFEFF00u, neg_hi = 0xF4F8FAFCu;
+        uint32_t idx = n & 0x07070707u;
+        uint32_t p = __builtin_amdgcn_perm(pos_hi, pos_lo, idx);
+        uint32_t q = __builtin_amdgcn_perm(neg_hi, neg_lo, idx);
+        uint32_t sel = ((n >> 3) & 0x01010101u) * 0xFFu;
+        return (p & ~sel) | (q & sel);
+    }
+    __device__ static inline void isums(const W &w, const X &x, int *out) {
+        const uint32_t m = 0x0F0F0F0Fu;
+        int acc = 0;
+        acc = dot4(lut(w.c.x & m), x.a.x, acc);
+        acc = dot4(lut(w.c.y & m), x.a.y, acc);
+        acc = dot4(lut(w.c.z & m), x.a.z, acc);
+        acc = dot4(lut(w.c.w & m), x.a.w, acc);
+        acc = dot4(lut((w.c.x >> 4) & m), x.b.x, acc);
+        acc = dot4(lut((w.c.y >> 4) & m), x.b.y, acc);
+        acc = dot4(lut((w.c.z >> 4) & m), x.b.z, acc);
+        acc = dot4(lut((w.c.w >> 4) & m), x.b.w, acc);
+        out[0] = acc;
+    }
+    __device__ static inline float value(const W &w, const X &x, int item) {
+        int s;
+        isums(w, x, &s);
+        return x.d * e8m0_half(w.e) * (float)s;
+    }
+    __device__ static inline int isum_index(int item, int) { return item; }
+};
+
+/* ---- Q8_0 weights: item = one 34-byte block (f16 d + 32 int8) ---- */
+struct FQ80 {
+    static constexpr int FMT = TG_FMT_Q80;
+    static constexpr int ITEMS_PER_BLOCK = 1, BLOCK_VALS = 32, BLOCK_BYTES = 34;
+    static constexpr int NSUMS = 1;
+    struct W { u32x4 q0, q1; uint32_t d; };
+    struct X { u32x4 a, b; float d; };
+
+    __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
+        uint32_t p = row_off + (uint32_t)item * 34u;
+        W r;
+        r.d = ld2(w, p);
+        r.q0 = ld16(w, p + 2);
+        r.q1 = ld16(w, p + 18);
+        return r;
+    }
+    __device__ static inline X load_x(const Q8Row &x, int item) {
+        FMXFP4::X t = FMXFP4::load_x(x, item);
+        X r;
+        r.a = t.a;
+        r.b = t.b;
+        r.d = t.d;
+        return r;
+    }
+    __device__ static inline void isums(const W &w, const X &x, int *out) {
+        int acc = 0;
+        acc = dot4(w.q0.x, x.a.x, acc); acc = dot4(w.q0.y, x.a.y, acc);
+        acc = dot4(w.q0.z, x.a.z, acc); acc = dot4(w.q0.w, x.a.w, acc);
+        acc = dot4(w.q1.x, x.b.x, acc); acc = dot4(w.q1.y, x.b.y, acc);
+        acc = dot4(w.q1.z, x.b.z, acc); acc = dot4(w.q1.w, x.b.w, acc);
+        out[0] = acc;
+    }
+    __device__ static inline float value(const W &w, const X &x, int) {
+        int s;
+        isums(w, x, &s);
+        return x.d * ref_f16(w.d) * (float)s;
+    }
+    __device__ static inline int isum_index(int item, int) { return item; }
+};
+
+/* ---- F16 weights: item = 8 halfs, against the unquantized f32 row ----
+ * Rows are multiples of 32 values, so every value goes through the
+ * reference's vectorised loop, whose vcvt_f32_f16 is the IEEE conversion
+ * (csrc/libtinygiant.c:641-648). */
+struct FF16 {
+    static constexpr int FMT = TG_FMT_F16;
+    static constexpr int ITEMS_PER_BLOCK = 1, BLOCK_VALS = 8, BLOCK_BYTES = 16;
+    static constexpr int NSUMS = 0;
+    struct W { u32x4 h; };
+    struct X { u32x4 a, b; };
+
+    __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
+        W r;
+        r.h = ld16(w, row_off + (uint32_t)item * 16u);
+        return r;
+    }
+    __device__ static inline X load_x(const Q8Row &x, int item) {
+        X r;
+        r.a = ld16(x.f, (uint32_t)item * 32u);
+        r.b = ld16(x.f, (uint32_t)item * 32u + 16u);
+        return r;
+    }
+    __device__ static inline float h2f(uint32_t h) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
+    }
+    __device__ static inline float value(const W &w, const X &x, int) {
+        float s = h2f(w.h.x) * __uint_as_float(x.a.x);
+        s = fmaf(h2f(w.h.x >> 16), __uint_as_float(x.a.y), s);
+        s = fmaf(h2f(w.h.y), __uint_as_float(x.a.z), s);
+        s = fmaf(h2f(w.h.y >> 16), __uint_as_float(x.a.w), s);
+        s = fmaf(h2f(w.h.z), __uint_as_float(x.b.x), s);
+        s = fmaf(h2f(w.h.z >> 16), __uint_as_float(x.b.y), s);
+        s = fmaf(h2f(w.h.w), __uint_as_float(x.b.z), s);
+        s = fmaf(h2f(w.h.w >> 16), __uint_as_float(x.b.w), s);
+        return s;
+    }
+    __device__ static inline void isums(const W &, const X &, int *) {}
+    __device__ static inline int isum_index(int, int) { return 0; }
+};
+
+}  // namespace tg
+#endif

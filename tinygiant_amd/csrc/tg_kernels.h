@@ -1,0 +1,55 @@
+/*
+ * tg_kernels.h -- launch interface between the C-ABI layer (tg_api.hip) and
+ * the kernels (tg_kernels.hip).  Internal to libtinygiant_hip.
+ */
+#ifndef TG_KERNELS_H
+#define TG_KERNELS_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <functional>
+
+#include "tg_common.h"
+#include "tg_device.hpp"
+
+namespace tg {
+
+/* Everything one MoE layer call needs, all pointers on the device.
+ * Pairs p = (expert e, active input row) are numbered expert-major, in the
+ * order the reference gathers them (csrc/libtinygiant.c:1411-1423). */
+struct MoeArgs {
+    const uint64_t *gate, *up, *down;       /* [n] weight base addresses */
+    const int *down_fmt;                    /* [n] */
+    const uint64_t *gbias, *ubias, *dbias;  /* [n] or null; entries may be 0 */
+    const int *p_off;                       /* [n+1] first pair of each expert */
+    const int *p_row;                       /* [P] input row of the pair */
+    const float *p_w;                       /* [P] router weight of the pair */
+    const int *r_off;                       /* [k+1] first entry of each output row */
+    const int *r_pair;                      /* [P] pairs of each output row, expert order */
+    const float *xin;                       /* [k][D] inputs */
+    Q8Rows xq;                              /* [k] quantized inputs */
+    float *hidden;                          /* [P][I] */
+    Q8Rows hq;                              /* [P] quantized hidden */
+    float *part;                            /* [P][D] weighted down outputs */
+    float *out;                             /* [k][D] accumulated output */
+    int n, k, P, D, I, act, gate_fmt;
+    uint32_t gate_rb;
+};
+
+int items_per_row(int fmt, int ncols);
+uint32_t row_bytes(int fmt, int ncols);
+
+void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st);
+void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *bias, const Q8Rows &x, int k,
+                 float *y, long ystride, hipStream_t st);
+void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows &x, int nsums_row, int32_t *out,
+                  hipStream_t st);
+/* `mark`, when given, is called after each kernel with its class:
+ * 1 quantize(x), 2 gate/up, 3 quantize(hidden), 4 down, 5 combine */
+void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
+                const std::function<void(int)> *mark = nullptr);
+void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st);
+void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st);
+
+}  // namespace tg
+#endif

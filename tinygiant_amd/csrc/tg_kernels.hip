@@ -1,0 +1,423 @@
+/*
+ * tg_kernels.hip -- HIP kernels of libtinygiant_hip for gfx950 and their
+ * stream-ordered launchers.
+ *
+ *   k_quantize_q8   activation rows -> q8 blocks   (quantize_q8, csrc/libtinygiant.c:169-208)
+ *   k_gemv          y[j][r] = dot(W[r], x_j) + bias[r]   (tg_matmul, :908-931)
+ *   k_moe_a         hidden = act(gate.x + bg, up.x + bu) per (expert, row)  (moe_phase_a, :1279-1327)
+ *   k_moe_b         part = w * (down.q8(hidden) + bd)                      (moe_phase_b, :1329-1384)
+ *   k_moe_combine   out[row] += part, experts in index order               (:1428-1434)
+ *   k_isums         per-sub-block integer dot sums (bit-exactness probe)
+ *   k_rms_norm      x * 1/sqrt(mean(x^2)+eps) * w                          (tg_rms_norm, :680-698)
+ *   k_synth_fill    seeded synthetic weights (tg_synth.h)
+ *
+ * Every weight and activation read goes through a raw buffer resource sized
+ * to its tensor, so an indexing slip reads zeros instead of faulting.
+ */
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <functional>
+
+#include "tg_device.hpp"
+#include "tg_kernels.h"
+#include "tg_synth.h"
+
+namespace tg {
+
+/* ======================= q8 quantization ======================= */
+
+/* One wave per 256-value block: lane l owns values 4l..4l+3. */
+__global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x, int ncols, int nrows,
+                                                     long xstride, Q8Rows out) {
+    const int lane = threadIdx.x & 63;
+    const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    const int nb = out.nb;
+    if (wave >= nrows * nb) return;   /* uniform per wave */
+    const int r = wave / nb, b = wave % nb;
+    const int n = min(256, ncols - b * 256);
+    Buf xb = make_buf(x + (size_t)r * xstride + (size_t)b * 256, (uint32_t)n * 4u);
+    u32x4 raw = ld16(xb, (uint32_t)lane * 16u);   /* zeros past n */
+    float v0 = __uint_as_float(raw.x), v1 = __uint_as_float(raw.y);
+    float v2 = __uint_as_float(raw.z), v3 = __uint_as_float(raw.w);
+    float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float sc = amax / 127.f;                  /* correctly rounded */
+    const float inv = amax > 0.f ? 127.f / amax : 0.f;
+    int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
+    int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
+    uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                      ((uint32_t)(q3 & 0xFF) << 24);
+    int8_t *qrow = out.qs + ((size_t)r * nb + b) * 256;
+    reinterpret_cast<uint32_t *>(qrow)[lane] = packed;
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);            /* 16-element sum */
+    int s32 = s + __shfl_xor(s, 4, 64);   /* 32-element sum */
+    int tot = s32;
+    tot += __shfl_xor(tot, 8, 64);
+    tot += __shfl_xor(tot, 16, 64);
+    tot += __shfl_xor(tot, 32, 64);
+    const size_t rb = (size_t)r * nb + b;
+    if ((lane & 3) == 0) out.s16[rb * 16 + (lane >> 2)] = s;
+    if ((lane & 7) == 0) out.s32[rb * 8 + (lane >> 3)] = s32;
+    if (lane == 0) {
+        out.d[rb] = sc;
+        out.sum[rb] = tot;
+    }
+}
+
+/* ======================= generic GEMV ======================= */
+
+/* W: nrows rows of rb bytes.  For each activation row j < k:
+ *   y[j*ystride + r] = dot(W[r], x_j) + bias[r]
+ * Each wave takes `rows_per_wave` consecutive rows in steps of 64/S. */
+template <class F, int S>
+__global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uint32_t rb, int nrows,
+                                              const float *__restrict__ bias, Q8Rows x, int k, float *y,
+                                              long ystride, int nitems, int T, int rows_per_wave) {
+    constexpr int G = 64 / S;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    const int row0 = wave * rows_per_wave;
+    if (row0 >= nrows) return;
+    Buf wb = make_buf(W + (size_t)row0 * rb, (uint32_t)((size_t)min(rows_per_wave, nrows - row0) * rb));
+    for (int j = 0; j < k; j++) {
+        Q8Row xr = q8_row(x, j);
+        for (int rs = 0; rs < rows_per_wave; rs += G) {
+            const int rl = rs + seg, r = row0 + rl;
+            const bool rv = rl < rows_per_wave && r < nrows;
+            float v = 0.f;
+            if (rv) {
+                for (int t = 0; t < T; t++) {
+                    const int item = sl + t * S;
+                    if (item < nitems) {
+                        typename F::W w = F::load_w(wb, (uint32_t)rl * rb, item);
+                        typename F::X xs = F::load_x(xr, item);
+                        v += F::value(w, xs, item);
+                    }
+                }
+            }
+            v = seg_sum<S>(v);
+            if (rv && sl == 0) y[(size_t)j * ystride + r] = v + (bias ? bias[r] : 0.f);
+        }
+    }
+}
+
+/* ======================= MoE phases ======================= */
+
+__device__ inline float act_fn(int act, float g, float u) {
+    if (act == TG_ACT_GPTOSS) {
+        g = fminf(g, 7.f);
+        u = fminf(fmaxf(u, -7.f), 7.f);
+        return g / (1.f + expf(-1.702f * g)) * (u + 1.f);
+    }
+    return g / (1.f + expf(-g)) * u;
+}
+
+/* Phase A: grid (x: wave groups over the I rows, y: expert).  hidden[p][r] for
+ * every pair p of the expert. */
+template <class F, int S>
+__global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int rows_per_wave) {
+    constexpr int G = 64 / S;
+    const int e = blockIdx.y;
+    const int p0 = a.p_off[e], ne = a.p_off[e + 1] - p0;
+    if (ne == 0) return;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int row0 = wave * rows_per_wave;
+    if (row0 >= a.I) return;
+    const uint32_t rb = a.gate_rb;
+    const size_t mbytes = (size_t)a.I * rb;
+    Buf gw = make_buf((const void *)a.gate[e], (uint32_t)mbytes);
+    Buf uw = make_buf((const void *)a.up[e], (uint32_t)mbytes);
+    const float *gb = a.gbias ? (const float *)a.gbias[e] : nullptr;
+    const float *ub = a.ubias ? (const float *)a.ubias[e] : nullptr;
+    for (int j = 0; j < ne; j++) {
+        const int p = p0 + j;
+        Q8Row xr = q8_row(a.xq, a.p_row[p]);
+        for (int rs = 0; rs < rows_per_wave; rs += G) {
+            const int r = row0 + rs + seg;
+            const bool rv = rs + seg < rows_per_wave && r < a.I;
+            float vg = 0.f, vu = 0.f;
+            if (rv) {
+                for (int t = 0; t < T; t++) {
+                    const int item = sl + t * S;
+                    if (item < nitems) {
+                        typename F::X xs = F::load_x(xr, item);
+                        typename F::W wg = F::load_w(gw, (uint32_t)r * rb, item);
+                        typename F::W wu = F::load_w(uw, (uint32_t)r * rb, item);
+                        vg += F::value(wg, xs, item);
+                        vu += F::value(wu, xs, item);
+                    }
+                }
+            }
+            vg = seg_sum<S>(vg);
+            vu = seg_sum<S>(vu);
+            if (rv && sl == 0) {
+                if (gb) {
+                    vg += gb[r];
+                    vu += ub[r];
+                }
+                a.hidden[(size_t)p * a.I + r] = act_fn(a.act, vg, vu);
+            }
+        }
+    }
+}
+
+/* Phase B: grid (x: wave groups over the D rows, y: expert).  Only experts
+ * whose down format is `fmt` run (one launch per format present). */
+template <class F, int S>
+__global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, int nitems, int T,
+                                               int rows_per_wave) {
+    constexpr int G = 64 / S;
+    const int e = blockIdx.y;
+    if (a.down_fmt[e] != fmt) return;
+    const int p0 = a.p_off[e], ne = a.p_off[e + 1] - p0;
+    if (ne == 0) return;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int row0 = wave * rows_per_wave;
+    if (row0 >= a.D) return;
+    Buf dw = make_buf((const void *)a.down[e], (uint32_t)((size_t)a.D * rb));
+    const float *db = a.dbias ? (const float *)a.dbias[e] : nullptr;
+    for (int j = 0; j < ne; j++) {
+        const int p = p0 + j;
+        Q8Row xr = q8_row(a.hq, p);
+        const float w = a.p_w[p];
+        for (int rs = 0; rs < rows_per_wave; rs += G) {
+            const int r = row0 + rs + seg;
+            const bool rv = rs + seg < rows_per_wave && r < a.D;
+            float v = 0.f;
+            if (rv) {
+                for (int t = 0; t < T; t++) {
+                    const int item = sl + t * S;
+                    if (item < nitems) {
+                        typename F::X xs = F::load_x(xr, item);
+                        typename F::W wd = F::load_w(dw, (uint32_t)r * rb, item);
+                        v += F::value(wd, xs, item);
+                    }
+                }
+            }
+            v = seg_sum<S>(v);
+            if (rv && sl == 0) a.part[(size_t)p * a.D + r] = w * (v + (db ? db[r] : 0.f));
+        }
+    }
+}
+
+/* out[row][c] += part[p][c] for the pairs p of `row`, in expert order. */
+__global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
+    const size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (idx >= (size_t)a.k * a.D) return;
+    const int row = (int)(idx / a.D), c = (int)(idx % a.D);
+    float o = a.out[idx];
+    for (int q = a.r_off[row]; q < a.r_off[row + 1]; q++) o += a.part[(size_t)a.r_pair[q] * a.D + c];
+    a.out[idx] = o;
+}
+
+/* ======================= integer-sum probe ======================= */
+
+template <class F, int S>
+__global__ __launch_bounds__(256) void k_isums(const uint8_t *__restrict__ W, uint32_t rb, int nrows, Q8Rows x,
+                                               int nitems, int T, int nsums_row, int32_t *out) {
+    constexpr int G = 64 / S;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    const int r = wave * G + seg;
+    if (r >= nrows) return;
+    Buf wb = make_buf(W, (uint32_t)((size_t)nrows * rb));
+    Q8Row xr = q8_row(x, 0);
+    for (int t = 0; t < T; t++) {
+        const int item = sl + t * S;
+        if (item >= nitems) continue;
+        typename F::W w = F::load_w(wb, (uint32_t)r * rb, item);
+        typename F::X xs = F::load_x(xr, item);
+        int s[F::NSUMS > 0 ? F::NSUMS : 1];
+        F::isums(w, xs, s);
+        for (int i = 0; i < F::NSUMS; i++) out[(size_t)r * nsums_row + F::isum_index(item, i)] = s[i];
+    }
+}
+
+/* ======================= small helpers ======================= */
+
+/* RMSNorm of each row (one workgroup per row): out = x * (1/sqrt(ss/n + eps)) * w */
+__global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
+                                                  float *__restrict__ out, int n, float eps) {
+    __shared__ float red[4];
+    const float *xr = x + (size_t)blockIdx.x * n;
+    float *orow = out + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xr[i] * xr[i];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += red[i];
+    const float scale = 1.f / sqrtf(tot / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = (xr[i] * scale) * (w ? w[i] : 1.f);
+}
+
+__global__ __launch_bounds__(256) void k_synth_fill(int kind, uint64_t seed, uint8_t *dst, uint64_t nbytes) {
+    const uint64_t nwords = (nbytes + 7) / 8;
+    for (uint64_t wi = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; wi < nwords;
+         wi += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t p0 = wi * 8;
+        if (p0 + 8 <= nbytes) {
+            uint64_t v = 0;
+            for (int b = 0; b < 8; b++) v |= (uint64_t)tg_syn_byte(kind, seed, p0 + b) << (8 * b);
+            reinterpret_cast<uint64_t *>(dst)[wi] = v;
+        } else {
+            for (uint64_t p = p0; p < nbytes; p++) dst[p] = tg_syn_byte(kind, seed, p);
+        }
+    }
+}
+
+/* ======================= launchers ======================= */
+
+static int pick_S(int nitems, int *T) {
+    /* fewest lane slots S*T (S power of two <= 64); ties go to larger S */
+    int bestS = 64, bestT = (nitems + 63) / 64, best = bestS * bestT;
+    for (int S = 32; S >= 8; S >>= 1) {
+        int t = (nitems + S - 1) / S;
+        if (S * t < best) {
+            best = S * t;
+            bestS = S;
+            bestT = t;
+        }
+    }
+    *T = bestT;
+    return bestS;
+}
+
+int items_per_row(int fmt, int ncols) {
+    switch (fmt) {
+        case TG_FMT_Q4K: return ncols / 256 * 4;
+        case TG_FMT_Q6K: return ncols / 256 * 4;
+        case TG_FMT_MXFP4: return ncols / 32;
+        case TG_FMT_Q80: return ncols / 32;
+        case TG_FMT_F16: return ncols / 8;
+        default: return -1;
+    }
+}
+
+uint32_t row_bytes(int fmt, int ncols) {
+    switch (fmt) {
+        case TG_FMT_Q4K: return (uint32_t)(ncols / 256) * 144u;
+        case TG_FMT_Q6K: return (uint32_t)(ncols / 256) * 210u;
+        case TG_FMT_MXFP4: return (uint32_t)(ncols / 32) * 17u;
+        case TG_FMT_Q80: return (uint32_t)(ncols / 32) * 34u;
+        default: return (uint32_t)ncols * 2u;
+    }
+}
+
+#define TG_DISPATCH_S(S_, CALL) \
+    switch (S_) {               \
+        case 8: CALL(8); break; \
+        case 16: CALL(16); break; \
+        case 32: CALL(32); break; \
+        default: CALL(64); break; \
+    }
+
+#define TG_DISPATCH_F(fmt, BODY)                    \
+    switch (fmt) {                                  \
+        case TG_FMT_Q4K: { typedef FQ4K F; BODY; } break;   \
+        case TG_FMT_Q6K: { typedef FQ6K F; BODY; } break;   \
+        case TG_FMT_MXFP4: { typedef FMXFP4 F; BODY; } break; \
+        case TG_FMT_Q80: { typedef FQ80 F; BODY; } break;   \
+        default: { typedef FF16 F; BODY; } break;   \
+    }
+
+void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st) {
+    const int waves = nrows * out.nb;
+    if (waves <= 0) return;
+    hipLaunchKernelGGL(k_quantize_q8, dim3((waves + 3) / 4), dim3(256), 0, st, x, ncols, nrows, xstride, out);
+}
+
+void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *bias, const Q8Rows &x, int k,
+                 float *y, long ystride, hipStream_t st) {
+    int T;
+    const int nitems = items_per_row(fmt, ncols);
+    const int S = pick_S(nitems, &T);
+    const uint32_t rb = row_bytes(fmt, ncols);
+    const int G = 64 / S;
+    const int rpw = G * 2;
+    const int waves = (nrows + rpw - 1) / rpw;
+    dim3 grid((waves + 3) / 4);
+#define CALL(S_) hipLaunchKernelGGL((k_gemv<F, S_>), grid, dim3(256), 0, st, W, rb, nrows, bias, x, k, y, ystride, nitems, T, rpw)
+    TG_DISPATCH_F(fmt, TG_DISPATCH_S(S, CALL))
+#undef CALL
+}
+
+void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows &x, int nsums_row, int32_t *out,
+                  hipStream_t st) {
+    int T;
+    const int nitems = items_per_row(fmt, ncols);
+    const int S = pick_S(nitems, &T);
+    const uint32_t rb = row_bytes(fmt, ncols);
+    const int G = 64 / S;
+    const int waves = (nrows + G - 1) / G;
+    dim3 grid((waves + 3) / 4);
+#define CALL(S_) hipLaunchKernelGGL((k_isums<F, S_>), grid, dim3(256), 0, st, W, rb, nrows, x, nitems, T, nsums_row, out)
+    TG_DISPATCH_F(fmt, TG_DISPATCH_S(S, CALL))
+#undef CALL
+}
+
+void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
+                const std::function<void(int)> *mark) {
+    /* 1. quantize the k input rows */
+    launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
+    if (mark) (*mark)(1);
+    /* 2. phase A */
+    {
+        int T;
+        const int nitems = items_per_row(a.gate_fmt, a.D);
+        const int S = pick_S(nitems, &T);
+        const int rpw = 64 / S;
+        const int waves = (a.I + rpw - 1) / rpw;
+        dim3 grid((waves + 3) / 4, a.n);
+#define CALL(S_) hipLaunchKernelGGL((k_moe_a<F, S_>), grid, dim3(256), 0, st, a, nitems, T, rpw)
+        TG_DISPATCH_F(a.gate_fmt, TG_DISPATCH_S(S, CALL))
+#undef CALL
+    }
+    if (mark) (*mark)(2);
+    /* 3. quantize the hidden rows */
+    launch_quantize(a.hidden, a.I, a.P, a.I, a.hq, st);
+    if (mark) (*mark)(3);
+    /* 4. phase B, once per down format present */
+    for (int i = 0; i < n_down_fmts; i++) {
+        const int fmt = down_fmts_present[i];
+        int T;
+        const int nitems = items_per_row(fmt, a.I);
+        const int S = pick_S(nitems, &T);
+        const int rpw = 64 / S;
+        const int waves = (a.D + rpw - 1) / rpw;
+        const uint32_t rb = row_bytes(fmt, a.I);
+        dim3 grid((waves + 3) / 4, a.n);
+#define CALL(S_) hipLaunchKernelGGL((k_moe_b<F, S_>), grid, dim3(256), 0, st, a, fmt, rb, nitems, T, rpw)
+        TG_DISPATCH_F(fmt, TG_DISPATCH_S(S, CALL))
+#undef CALL
+    }
+    if (mark) (*mark)(4);
+    /* 5. combine */
+    const size_t n = (size_t)a.k * a.D;
+    hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+    if (mark) (*mark)(5);
+}
+
+void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st) {
+    hipLaunchKernelGGL(k_rms_norm, dim3(nrows), dim3(256), 0, st, x, w, out, n, eps);
+}
+
+void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st) {
+    hipLaunchKernelGGL(k_synth_fill, dim3(4096), dim3(256), 0, st, kind, seed, (uint8_t *)dst, nbytes);
+}
+
+}  // namespace tg
