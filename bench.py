@@ -136,10 +136,47 @@ def cpu_baseline(routes, sample_layers, min_seconds=10.0, max_reps=400):
     }
 
 
-def read_traffic():
+def copy_probe(tg, nbytes=1 << 30, iters=20):
+    """Measured HBM reference: a plain copy kernel over 1 GiB (read + write)."""
+    lib = tg.lib()
+    a, b = tg.DeviceArray(nbytes), tg.DeviceArray(nbytes)
+    lib.tg_hip_synth_fill(-1, 1, a.ptr, nbytes, None)
+    lib.tg_hip_copy_time(a.ptr, b.ptr, nbytes, 2)
+    ms = lib.tg_hip_copy_time(a.ptr, b.ptr, nbytes, iters)
+    a.free()
+    b.free()
+    per = ms / iters
+    return {"copy_bytes": nbytes, "avg_ms": round(per, 4),
+            "gbps_read_plus_write": round(2 * nbytes / (per * 1e-3) / 1e9, 1)}
+
+
+def phase_breakdown(tg, step, layers):
+    """Mean microseconds per layer spent between the persistent kernel's
+    checkpoints (one extra step with device timestamps)."""
+    lib = tg.lib()
+    buf = tg.DeviceArray(2 * layers * 16 * 8)
+    lib.tg_hip_decode_set_timing(step, buf.ptr)
+    lib.tg_hip_decode_run(step, None)
+    lib.tg_hip_synchronize()
+    lib.tg_hip_decode_set_timing(step, None)
+    t = buf.download(np.uint64, 2 * layers * 16).reshape(2, layers, 16).astype(np.float64) * 0.01  # 100 MHz -> us
+    buf.free()
+    # checkpoints: 0 layer start, 1 h collected, 2 q8(x) ready, 8 first gate/up dots,
+    # 9 reduced, 3 hidden values in LDS, 4 hidden collected, 5 q8(hidden), 6 combined, 7 h published
+    seq = [(0, 1, "wait_h"), (1, 2, "norm_q8"), (2, 8, "gate_up_dots"), (8, 9, "gate_up_reduce"),
+           (9, 3, "gate_up_rest"), (3, 4, "publish_wait_hidden"), (4, 5, "q8_hidden"), (5, 6, "down_combine"),
+           (6, 7, "publish_h")]
+    out = {}
+    for w, tag in ((0, "wg0"), (1, "wglast")):
+        out[tag] = {n: round(float((t[w, 1:, b] - t[w, 1:, a]).mean()), 3) for a, b, n in seq}
+        out[tag]["layer"] = round(float((t[w, 2:, 0] - t[w, 1:-1, 0]).mean()), 3)
+    return out
+
+
+def read_traffic(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
-    p = ROOT / "profiles" / "pmc_moe_gate_up_qwen_decode.txt"
+    p = ROOT / "profiles" / name
     if not p.exists():
         return None
     for line in p.read_text().splitlines():
@@ -156,7 +193,10 @@ def main():
     ap.add_argument("--layers", type=int, default=L)
     ap.add_argument("--cpu-layers", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--mode", choices=["persistent", "graph", "eager"], default="persistent",
+                    help="persistent: one cooperative kernel per step; graph: per-layer kernels in a HIP graph")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only time a plain 1 GiB device copy (HBM reference / counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the expert path is "
@@ -165,6 +205,9 @@ def main():
 
     import tinygiant_amd as tg
     lib = tg.lib()
+    if args.copy_probe:
+        print(json.dumps(copy_probe(tg)), flush=True)
+        return 0
     name = ctypes.create_string_buffer(256)
     lib.tg_hip_device_name(name, 256)
     log(f"device: {name.value.decode()}")
@@ -178,8 +221,8 @@ def main():
     h = tg.DeviceArray(D * 4)
     h.upload(h0)
     parr = (ctypes.c_void_p * layers)(*plans)
-    step = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, None, ctypes.c_float(1e-6), h.ptr,
-                                    0 if args.no_graph else 1)
+    mode = {"eager": 0, "graph": 1, "persistent": 2}[args.mode]
+    step = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, None, ctypes.c_float(1e-6), h.ptr, mode)
     if not step:
         raise RuntimeError(tg.last_error())
 
@@ -190,22 +233,36 @@ def main():
     ms = lib.tg_hip_decode_time(step, args.steps)
     lib.tg_hip_synchronize()
     wall = time.perf_counter() - t0
+    if lib.tg_hip_decode_status(step) != 0:
+        raise RuntimeError("persistent decode: a grid barrier timed out")
     ms_step = ms / args.steps
     bytes_step = layers * TOPK * EXPERT_B
     tok_s = 1e3 / ms_step
     log(f"timed {args.steps} steps: {ms:.2f} ms events, {wall * 1e3:.2f} ms wall")
 
-    # per-kernel durations of one eager step (HIP events on the library stream)
-    kms = (ctypes.c_float * 6)()
-    kn = (ctypes.c_int * 6)()
-    lib.tg_hip_decode_kernel_times(step, kms, kn)
-    names = ["rms_norm", "quantize_x", "gate_up", "quantize_h", "down", "combine"]
-    per_kernel = {names[i]: {"avg_us": round(kms[i] / max(kn[i], 1) * 1e3, 2), "launches": kn[i]}
-                  for i in range(6)}
-    gu_us = kms[2] / max(kn[2], 1) * 1e3
-    gu_bytes = TOPK * 2 * GATE_B
-    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
-    traffic = read_traffic()
+    phases = None
+    if mode == 2:
+        phases = phase_breakdown(tg, step, layers)
+        log(f"phase breakdown (us per layer, first/last workgroup): {json.dumps(phases)}")
+    if mode == 2:
+        # the whole step is one kernel: its launch duration is the step time
+        per_kernel = {"k_decode_qwen": {"avg_us": round(ms_step * 1e3, 2), "launches": args.steps}}
+        kernel_name = "k_decode_qwen (persistent: 48 layers x (gate/up + down), one launch per token)"
+        k_bytes, k_us = bytes_step, ms_step * 1e3
+        traffic = read_traffic("pmc_decode_qwen_step.txt")
+    else:
+        # per-kernel durations of one eager step (HIP events on the library stream)
+        kms = (ctypes.c_float * 6)()
+        kn = (ctypes.c_int * 6)()
+        lib.tg_hip_decode_kernel_times(step, kms, kn)
+        names = ["rms_norm", "quantize_x", "gate_up", "quantize_h", "down", "combine"]
+        per_kernel = {names[i]: {"avg_us": round(kms[i] / max(kn[i], 1) * 1e3, 2), "launches": kn[i]}
+                      for i in range(6)}
+        kernel_name = "k_moe_a<FQ4K,32> (gate+up+SiLU, 8 experts)"
+        k_us = kms[2] / max(kn[2], 1) * 1e3
+        k_bytes = TOPK * 2 * GATE_B
+        traffic = read_traffic("pmc_moe_gate_up_qwen_decode.txt")
+    achieved = k_bytes / (k_us * 1e-6) / 1e9
     log(f"kernels: {json.dumps(per_kernel)}")
 
     result = {
@@ -226,17 +283,18 @@ def main():
                         "D=2048 I=768, q4_K gate/up + q6_K down, batch 1, h += MoE(RMSNorm(h))",
             "layers": layers, "experts_per_layer": E, "top_k": TOPK, "embed_dim": D, "inter_dim": I,
             "resident_bytes": layers * E * EXPERT_B, "weight_bytes_per_step": bytes_step,
-            "graph": not args.no_graph,
+            "mode": args.mode,
         },
         "weight_gbps": round(bytes_step / (ms_step * 1e-3) / 1e9, 1),
         "hbm_frac": round(bytes_step / (ms_step * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "roofline": {
-            "kernel": "k_moe_a<FQ4K,32> (gate+up+SiLU, 8 experts)",
+            "kernel": kernel_name,
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "bytes_per_launch": gu_bytes, "avg_us": round(gu_us, 2),
+            "bytes_per_launch": k_bytes, "avg_us": round(k_us, 2),
         },
         "kernels": per_kernel,
+        "phases_us": phases,
         "device": name.value.decode(),
     }
     lib.tg_hip_decode_destroy(step)

@@ -179,16 +179,32 @@ void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev,
 /* Device-resident decode step over L planned layers sharing one hidden
  * state h_dev [k][embed_dim]: h <- h + MoE_l(RMSNorm_l(h)) for each layer
  * (tinygiant/engine.py:281-282,335-341).  norm_w_dev may be NULL (weight 1).
- * With use_graph the launch sequence is captured once into a HIP graph. */
+ * mode 0 queues the per-layer kernels, 1 replays them as one HIP graph,
+ * 2 runs the whole step as one persistent cooperative kernel (k = 1,
+ * D = 2048, I = 768, Q4_K gate/up, Q6_K down, SiLU, no biases, exactly 8
+ * active experts per layer, <= 64 layers, 256 co-resident workgroups). */
 typedef struct tg_hip_decode tg_hip_decode;
 tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers,
                                     const float *const *norm_w_dev, float eps, float *h_dev,
-                                    int use_graph);
+                                    int mode);
+int tg_hip_decode_status(tg_hip_decode *step);   /* 1 if a persistent step's barrier timed out */
+/* Stage-wise parity probe of the persistent step: while set, each layer
+ * writes a record of tg_hip_decode_debug_bytes() bytes (h in, RMSNorm x,
+ * q8(x), hidden, q8(hidden)) into debug_dev[layer]. */
+void tg_hip_decode_set_debug(tg_hip_decode *step, void *debug_dev);
+size_t tg_hip_decode_debug_bytes(void);
+/* Phase timestamps of the persistent step (100 MHz device clock): while set,
+ * times_dev [2][L][16] uint64 receives up to 16 checkpoints per layer of the
+ * first and the last workgroup. */
+void tg_hip_decode_set_timing(tg_hip_decode *step, void *times_dev);
 void tg_hip_decode_run(tg_hip_decode *step, void *stream);
 float tg_hip_decode_time(tg_hip_decode *step, int iters);   /* ms for iters steps, HIP events */
 void tg_hip_decode_kernel_times(tg_hip_decode *step, float *ms_out /*[6]*/, int *n_out /*[6]*/);
 void tg_hip_decode_destroy(tg_hip_decode *step);
 void tg_hip_device_name(char *buf, int n);
+/* nbytes (multiple of 16) device-to-device `iters` times with a plain copy
+ * kernel; returns milliseconds (HIP events): measured HBM reference point. */
+float tg_hip_copy_time(const void *src_dev, void *dst_dev, uint64_t nbytes, int iters);
 
 #ifdef __cplusplus
 }

@@ -29,6 +29,7 @@
 #include <mutex>
 #include <vector>
 
+#include "tg_decode.h"
 #include "tg_kernels.h"
 #include "tg_synth.h"
 
@@ -891,13 +892,57 @@ TG_API void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *o
 struct tg_hip_decode {
     std::vector<tg_hip_moe_plan *> plans;
     std::vector<const float *> norm_w;
-    int L = 0, D = 0, k = 0;
+    int L = 0, D = 0, k = 0, mode = 0;
     float eps = 1e-6f;
     float *h = nullptr;
     float *x = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
+    /* persistent mode */
+    DecodeLayer *layers = nullptr;
+    float *hidden = nullptr;
+    unsigned *sync = nullptr;
+    unsigned base = 0;
+    int grid = 0;
+    uint8_t *debug = nullptr;
+    uint64_t *times = nullptr;
 };
+
+/* the persistent kernel covers k = 1 steps of the Qwen expert shape */
+static bool persistent_ok(tg_hip_decode *d, std::vector<DecodeLayer> &out) {
+    const DecodeShape sh = decode_qwen_shape();
+    for (int l = 0; l < d->L; l++) {
+        const HostPlan &h = d->plans[l]->h;
+        if (h.k != 1 || h.D != sh.D || h.I != sh.I || h.gate_fmt != sh.gate_fmt || h.act != TG_ACT_SILU ||
+            h.has_gb || h.has_ub || h.has_db) {
+            set_err("persistent decode: layer %d is not a 1-row SiLU Q4_K gate/up step of %dx%d without biases", l,
+                    sh.D, sh.I);
+            return false;
+        }
+        DecodeLayer ly;
+        memset(&ly, 0, sizeof ly);
+        for (int e = 0; e < h.n; e++) {
+            if (h.p_off[e + 1] == h.p_off[e]) continue;
+            if (ly.n >= sh.maxe || h.down_fmt[e] != sh.down_fmt) {
+                set_err("persistent decode: layer %d needs %d active experts with Q6_K down", l, sh.maxe);
+                return false;
+            }
+            ly.gate[ly.n] = (const uint8_t *)(uintptr_t)h.gate[e];
+            ly.up[ly.n] = (const uint8_t *)(uintptr_t)h.up[e];
+            ly.down[ly.n] = (const uint8_t *)(uintptr_t)h.down[e];
+            ly.w[ly.n] = h.p_w[h.p_off[e]];
+            ly.n++;
+        }
+        if (ly.n != sh.maxe) {
+            set_err("persistent decode: layer %d has %d active experts, the kernel runs exactly %d", l, ly.n,
+                    sh.maxe);
+            return false;
+        }
+        ly.norm_w = d->norm_w.empty() ? nullptr : d->norm_w[l];
+        out.push_back(ly);
+    }
+    return true;
+}
 
 static void decode_enqueue(tg_hip_decode *d, hipStream_t st) {
     for (int l = 0; l < d->L; l++) {
@@ -935,7 +980,41 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
     }
     d->eps = eps;
     d->h = h_dev;
+    d->mode = use_graph;
     HIPCHECK(hipMalloc(&d->x, (size_t)d->k * d->D * 4));
+    if (use_graph == 2) {
+        std::vector<DecodeLayer> ls;
+        if (!persistent_ok(d, ls)) {
+            HIPCHECK(hipFree(d->x));
+            delete d;
+            return nullptr;
+        }
+        int cus = 0;
+        HIPCHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g.dev));
+        const int maxg = decode_qwen_max_grid();
+        if (d->L > 64) {
+            set_err("persistent decode: at most 64 layers per step");
+            HIPCHECK(hipFree(d->x));
+            delete d;
+            return nullptr;
+        }
+        if (maxg < DECODE_GRID) {
+            set_err("persistent decode: needs %d co-resident workgroups (CUs %d, co-resident %d)", DECODE_GRID, cus,
+                    maxg);
+            HIPCHECK(hipFree(d->x));
+            delete d;
+            return nullptr;
+        }
+        d->grid = DECODE_GRID;
+        HIPCHECK(hipMalloc(&d->layers, ls.size() * sizeof(DecodeLayer)));
+        HIPCHECK(hipMemcpy(d->layers, ls.data(), ls.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice));
+        const size_t sb = decode_qwen_slot_bytes(d->grid);
+        HIPCHECK(hipMalloc(&d->hidden, sb));   /* the exchange slots */
+        HIPCHECK(hipMemset(d->hidden, 0, sb));
+        HIPCHECK(hipMalloc(&d->sync, 256));
+        HIPCHECK(hipMemset(d->sync, 0, 256));
+        return d;
+    }
     if (use_graph) {
         hipStream_t cs;
         HIPCHECK(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
@@ -952,11 +1031,44 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!d) return;
     hipStream_t st = stream ? (hipStream_t)stream : g.st;
-    if (d->exec)
+    if (d->mode == 2) {
+        HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
+                                    d->grid, st));
+        d->base += 2u * (unsigned)d->L;
+    } else if (d->exec) {
         HIPCHECK(hipGraphLaunch(d->exec, st));
-    else
+    } else {
         decode_enqueue(d, st);
+    }
     HIPCHECK(hipGetLastError());
+}
+
+/* Persistent steps write one debug record per layer into debug_dev
+ * (tg_hip_decode_debug_bytes() each) while it is set; NULL turns it off. */
+TG_API void tg_hip_decode_set_debug(tg_hip_decode *d, void *debug_dev) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (d) d->debug = (uint8_t *)debug_dev;
+}
+
+TG_API size_t tg_hip_decode_debug_bytes(void) { return (size_t)DecodeDebug::BYTES; }
+
+/* Persistent steps record 16 phase timestamps per layer (100 MHz device
+ * clock) of the first and the last workgroup into times_dev
+ * [2][L][16] (uint64) while it is set; NULL turns it off. */
+TG_API void tg_hip_decode_set_timing(tg_hip_decode *d, void *times_dev) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (d) d->times = (uint64_t *)times_dev;
+}
+
+/* 0 if every persistent step so far completed its grid barriers; 1 if a
+ * barrier wait timed out (the results of that step are invalid). */
+TG_API int tg_hip_decode_status(tg_hip_decode *d) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d || d->mode != 2) return 0;
+    unsigned w;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipMemcpy(&w, d->sync, 4, hipMemcpyDeviceToHost));
+    return w ? 1 : 0;
 }
 
 TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
@@ -966,6 +1078,9 @@ TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
     if (d->exec) HIPCHECK(hipGraphExecDestroy(d->exec));
     if (d->graph) HIPCHECK(hipGraphDestroy(d->graph));
     HIPCHECK(hipFree(d->x));
+    if (d->layers) HIPCHECK(hipFree(d->layers));
+    if (d->hidden) HIPCHECK(hipFree(d->hidden));
+    if (d->sync) HIPCHECK(hipFree(d->sync));
     delete d;
 }
 
@@ -999,6 +1114,7 @@ TG_API void tg_hip_decode_kernel_times(tg_hip_decode *d, float *ms_out, int *n_o
         ms_out[i] = 0.f;
         n_out[i] = 0;
     }
+    if (d->mode == 2) return;   /* one kernel per step: tg_hip_decode_time is its duration */
     std::vector<hipEvent_t> ev;
     std::vector<int> cls;
     auto mark = [&](int c) {
@@ -1038,4 +1154,28 @@ TG_API void tg_hip_device_name(char *buf, int n) {
     hipDeviceProp_t pr;
     HIPCHECK(hipGetDeviceProperties(&pr, g.dev));
     snprintf(buf, (size_t)n, "%s (%s, %d CUs)", pr.name, pr.gcnArchName, pr.multiProcessorCount);
+}
+
+/* Copies nbytes (multiple of 16) device-to-device with a plain vector-load
+ * kernel `iters` times on the library stream; returns ms (HIP events).  The
+ * reference point for measured HBM bandwidth and for counter calibration. */
+TG_API float tg_hip_copy_time(const void *src_dev, void *dst_dev, uint64_t nbytes, int iters) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    if (nbytes % 16 || iters <= 0) {
+        set_err("tg_hip_copy_time: nbytes must be a multiple of 16");
+        return 0.f;
+    }
+    hipEvent_t a, b;
+    HIPCHECK(hipEventCreate(&a));
+    HIPCHECK(hipEventCreate(&b));
+    HIPCHECK(hipEventRecord(a, g.st));
+    for (int i = 0; i < iters; i++) launch_copy(src_dev, dst_dev, nbytes, g.st);
+    HIPCHECK(hipEventRecord(b, g.st));
+    HIPCHECK(hipEventSynchronize(b));
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, a, b));
+    HIPCHECK(hipEventDestroy(a));
+    HIPCHECK(hipEventDestroy(b));
+    return ms;
 }

@@ -1,0 +1,53 @@
+/*
+ * tg_decode.h -- the persistent decode-step kernel's interface (internal).
+ */
+#ifndef TG_DECODE_H
+#define TG_DECODE_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tg {
+
+constexpr int DECODE_MAXE = 8;    /* the persistent step runs exactly 8 experts per layer */
+constexpr int DECODE_GRID = 256;   /* ... on 256 co-resident workgroups (one per MI355X CU) */
+
+/* One layer of the step: its active experts (device pointers), their router
+ * weights and the RMSNorm weight applied to h before the layer (null = 1). */
+struct DecodeLayer {
+    const uint8_t *gate[DECODE_MAXE];
+    const uint8_t *up[DECODE_MAXE];
+    const uint8_t *down[DECODE_MAXE];
+    float w[DECODE_MAXE];
+    const float *norm_w;
+    int n;
+};
+
+/* Per-layer debug record written by workgroup 0 when a debug buffer is set
+ * (stage-wise parity of the persistent step): byte offsets for D = 2048,
+ * I = 768.  h_in f32[D] | x f32[D] | xq i8[D] | xd f32[D/256] | xs32 i32[D/32] |
+ * hidden f32[8][I] | hq i8[8][I] | hd f32[8][I/256] | hs16 i32[8][I/16] */
+struct DecodeDebug {
+    static constexpr int D = 2048, I = 768, E = DECODE_MAXE;
+    static constexpr int HIN = 0, X = HIN + D * 4, XQ = X + D * 4, XD = XQ + D, XS32 = XD + (D / 256) * 4,
+                         HID = XS32 + (D / 32) * 4, HQ = HID + E * I * 4, HD = HQ + E * I,
+                         HS16 = HD + E * (I / 256) * 4, BYTES = HS16 + E * (I / 16) * 4;
+};
+
+/* Shape the persistent kernel is built for; the host checks a step against it. */
+struct DecodeShape {
+    int D, I, gate_fmt, down_fmt, maxe, threads;
+};
+DecodeShape decode_qwen_shape();
+
+/* Queues one step.  slots_dev holds decode_qwen_slot_bytes(grid) zeroed
+ * bytes; `base` advances by 2 * L per launch (slot tags are base-relative);
+ * abort_dev is one word, nonzero after a timed-out wait.  Returns the status
+ * of the cooperative launch. */
+size_t decode_qwen_slot_bytes(int grid);
+hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
+                              unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
+                              int grid, hipStream_t st);
+int decode_qwen_max_grid();
+
+}  // namespace tg
+#endif

@@ -77,6 +77,64 @@ __device__ inline int dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+/* ---- DPP cross-lane reductions ----
+ * GFX9 DPP controls: quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
+ * row_half_mirror = 0x141, row_mirror = 0x140, row_bcast:15 = 0x142,
+ * row_bcast:31 = 0x143.  Each step adds a lane's value to one partner's, so
+ * every lane of a group holds the same (commutatively identical) sum. */
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline int dpp_i(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xF, false);
+}
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ inline float dpp_f(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+/* sum over aligned groups of S lanes (S = 2..64); the result is exact in
+ * the group's last lane (lane % S == S - 1), and in every lane for S <= 16 */
+template <int S>
+__device__ inline float seg_sum_last(float v) {
+    static_assert(S >= 2 && S <= 64 && (S & (S - 1)) == 0, "segment");
+    v += dpp_f<0xB1>(v, v);
+    if (S >= 4) v += dpp_f<0x4E>(v, v);
+    if (S >= 8) v += dpp_f<0x141>(v, v);
+    if (S >= 16) v += dpp_f<0x140>(v, v);
+    if (S >= 32) v += dpp_f<0x142, 0xA>(0.f, v);
+    if (S >= 64) v += dpp_f<0x143, 0xC>(0.f, v);
+    return v;
+}
+template <int S>
+__device__ inline int seg_isum_last(int v) {
+    v += dpp_i<0xB1>(v, v);
+    if (S >= 4) v += dpp_i<0x4E>(v, v);
+    if (S >= 8) v += dpp_i<0x141>(v, v);
+    if (S >= 16) v += dpp_i<0x140>(v, v);
+    if (S >= 32) v += dpp_i<0x142, 0xA>(0, v);
+    if (S >= 64) v += dpp_i<0x143, 0xC>(0, v);
+    return v;
+}
+/* wave-wide sum / max, broadcast to every lane (fixed combination order) */
+__device__ inline float wave_sum(float v) {
+    v = seg_sum_last<16>(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return (a + b) + (c + d);
+}
+__device__ inline float wave_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v, v));
+    v = fmaxf(v, dpp_f<0x4E>(v, v));
+    v = fmaxf(v, dpp_f<0x141>(v, v));
+    v = fmaxf(v, dpp_f<0x140>(v, v));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 15));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 31));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 47));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
 /* ---- segment reductions (segments of S lanes, S power of two <= 64) ---- */
 
 template <int S>
@@ -214,7 +272,7 @@ struct FQ6K {
         r.qlb = ld16(w, p + 64 * h + 32 + l0);
         r.qh = ld16(w, p + 128 + 32 * h + l0);
         r.sc = ld8(w, p + 192 + 8 * h);
-        r.d = ld2(w, p + 208);
+        r.d = ld4(w, p + 206);   /* sc[14], sc[15], d: d is the high half */
         return r;
     }
     __device__ static inline X load_x(const Q8Row &x, int item) {
@@ -267,7 +325,7 @@ struct FQ6K {
         int sc2 = (int)(int8_t)(w.sc.y >> (8 * odd));
         int sc3 = (int)(int8_t)(w.sc.y >> (8 * odd + 16));
         int A = sc0 * s[0] + sc1 * s[1] + sc2 * s[2] + sc3 * s[3];
-        return ref_f16(w.d) * x.d * (float)A;
+        return ref_f16(w.d >> 16) * x.d * (float)A;
     }
     __device__ static inline int isum_index(int item, int i) {
         int u = item & 3;
@@ -286,7 +344,7 @@ struct FMXFP4 {
     __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
         uint32_t p = row_off + (uint32_t)item * 17u;
         W r;
-        r.e = ld1(w, p);
+        r.e = ld4(w, p);   /* e8m0 byte + 3 code bytes: the low byte is e */
         r.c = ld16(w, p + 1);
         return r;
     }
@@ -325,7 +383,7 @@ struct FMXFP4 {
     __device__ static inline float value(const W &w, const X &x, int item) {
         int s;
         isums(w, x, &s);
-        return x.d * e8m0_half(w.e) * (float)s;
+        return x.d * e8m0_half(w.e & 0xFFu) * (float)s;
     }
     __device__ static inline int isum_index(int item, int) { return item; }
 };
@@ -341,7 +399,7 @@ struct FQ80 {
     __device__ static inline W load_w(Buf w, uint32_t row_off, int item) {
         uint32_t p = row_off + (uint32_t)item * 34u;
         W r;
-        r.d = ld2(w, p);
+        r.d = ld4(w, p);   /* d + 2 quant bytes: ref_f16 keeps the low half */
         r.q0 = ld16(w, p + 2);
         r.q1 = ld16(w, p + 18);
         return r;

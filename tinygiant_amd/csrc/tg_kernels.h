@@ -50,6 +50,7 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
                 const std::function<void(int)> *mark = nullptr);
 void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st);
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st);
+void launch_copy(const void *src, void *dst, uint64_t nbytes, hipStream_t st);
 
 }  // namespace tg
 #endif

@@ -280,6 +280,13 @@ __global__ __launch_bounds__(256) void k_synth_fill(int kind, uint64_t seed, uin
     }
 }
 
+/* Plain 16-byte-per-lane copy: the reference kernel for measured HBM
+ * bandwidth and for calibrating the FETCH_SIZE / WRITE_SIZE counters. */
+__global__ __launch_bounds__(256) void k_copy(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, uint64_t n16) {
+    for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
 /* ======================= launchers ======================= */
 
 static int pick_S(int nitems, int *T) {
@@ -418,6 +425,10 @@ void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int 
 
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st) {
     hipLaunchKernelGGL(k_synth_fill, dim3(4096), dim3(256), 0, st, kind, seed, (uint8_t *)dst, nbytes);
+}
+
+void launch_copy(const void *src, void *dst, uint64_t nbytes, hipStream_t st) {
+    hipLaunchKernelGGL(k_copy, dim3(256 * 16), dim3(256), 0, st, (const u32x4 *)src, (u32x4 *)dst, nbytes / 16);
 }
 
 }  // namespace tg
