@@ -5,7 +5,7 @@ Workload: the Qwen3-30B-A3B expert decode step -- 48 layers, each with its own
 HBM), top-8 experts per layer drawn from a Zipf(1.1) popularity over a seeded
 permutation, router weights softmaxed over the selected 8, batch 1, and the
 hidden state carried layer to layer as h <- h + MoE_l(RMSNorm(h)) (eps 1e-6,
-tinygiant/engine.py:281-282,335-341).  One step = one token through all 48
+synthetic norm weight U[0.5, 1.5]; tinygiant/engine.py:281-282,335-341).  One step = one token through all 48
 expert layers.
 
 Prints one JSON line.  `value` is tokens/s of the device-resident step with
@@ -90,6 +90,13 @@ def setup_gpu(tg, layers, routes):
     return bufs, plans
 
 
+def norm_weights(layers):
+    """Synthetic RMSNorm weights applied to h before each layer's experts
+    (the reference's ffn_norm), U[0.5, 1.5]."""
+    rng = np.random.default_rng(SEED + 2)
+    return [rng.uniform(0.5, 1.5, D).astype(np.float32) for _ in range(layers)]
+
+
 def cpu_baseline(routes, sample_layers, min_seconds=10.0, max_reps=400):
     """Oracle (scalar C restatement) over the first `sample_layers` layers of
     the same step: same seeds, same routing, same RMSNorm chain."""
@@ -108,15 +115,15 @@ def cpu_baseline(routes, sample_layers, min_seconds=10.0, max_reps=400):
         u = [S.matrix_host(0, S.tensor_seed(SEED, l, int(e), 1), I, D) for e in idx]
         d = [S.matrix_host(2, S.tensor_seed(SEED, l, int(e), 2), D, I) for e in idx]
         layers.append((g, u, d, w.reshape(-1, 1).astype(np.float32)))
-    ones = np.ones(D, np.float32)
+    nws = norm_weights(sample_layers)
     h = np.random.default_rng(SEED + 1).standard_normal(D).astype(np.float32)
     per_layer = []
     t_total = 0.0
     reps = 0
     while reps < max_reps and (t_total < min_seconds or reps == 0):
-        for (g, u, d, w) in layers:
+        for l, (g, u, d, w) in enumerate(layers):
             t0 = time.perf_counter()
-            x = oracle.rms_norm(h, ones, 1e-6)
+            x = oracle.rms_norm(h, nws[l], 1e-6)
             out = h.reshape(1, D).copy()
             oracle.moe_v2(g, u, d, 0, [2] * len(g), None, None, None, 0, w, x.reshape(1, D), out, I)
             h = out.reshape(D)
@@ -161,11 +168,10 @@ def phase_breakdown(tg, step, layers):
     lib.tg_hip_decode_set_timing(step, None)
     t = buf.download(np.uint64, 2 * layers * 16).reshape(2, layers, 16).astype(np.float64) * 0.01  # 100 MHz -> us
     buf.free()
-    # checkpoints: 0 layer start, 1 h collected, 2 q8(x) ready, 8 first gate/up dots,
-    # 9 reduced, 3 hidden values in LDS, 4 hidden collected, 5 q8(hidden), 6 combined, 7 h published
-    seq = [(0, 1, "wait_h"), (1, 2, "norm_q8"), (2, 8, "gate_up_dots"), (8, 9, "gate_up_reduce"),
-           (9, 3, "gate_up_rest"), (3, 4, "publish_wait_hidden"), (4, 5, "q8_hidden"), (5, 6, "down_combine"),
-           (6, 7, "publish_h")]
+    # checkpoints: 0 layer start, 1 h gathered, 2 q8(x) ready, 3 gate/up done, 4 hidden gathered,
+    # 5 q8(hidden), 6 down done, 7 cross-XCD hop done, 8 combined and published
+    seq = [(0, 1, "gather_h"), (1, 2, "norm_q8"), (2, 3, "gate_up"), (3, 4, "hidden_xchg"),
+           (4, 5, "q8_hidden"), (5, 6, "down"), (6, 7, "xcd_hop"), (7, 8, "combine")]
     out = {}
     for w, tag in ((0, "wg0"), (1, "wglast")):
         out[tag] = {n: round(float((t[w, 1:, b] - t[w, 1:, a]).mean()), 3) for a, b, n in seq}
@@ -220,9 +226,16 @@ def main():
     h0 = np.random.default_rng(SEED + 1).standard_normal(D).astype(np.float32)
     h = tg.DeviceArray(D * 4)
     h.upload(h0)
+    nbufs = []
+    for w in norm_weights(layers):
+        a = tg.DeviceArray(D * 4)
+        a.upload(w)
+        nbufs.append(a)
     parr = (ctypes.c_void_p * layers)(*plans)
+    narr = (ctypes.c_void_p * layers)(*[a.ptr for a in nbufs])
     mode = {"eager": 0, "graph": 1, "persistent": 2}[args.mode]
-    step = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, None, ctypes.c_float(1e-6), h.ptr, mode)
+    step = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, ctypes.addressof(narr), ctypes.c_float(1e-6),
+                                    h.ptr, mode)
     if not step:
         raise RuntimeError(tg.last_error())
 

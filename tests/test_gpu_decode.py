@@ -55,6 +55,13 @@ class Layers:
         lib = tg.lib()
         rng = np.random.default_rng(seed)
         self.host, self.bufs, self.plans, self.rw = [], [], [], []
+        # RMSNorm weights of each layer (the reference's ffn_norm), U[0.5, 1.5]
+        self.norm_host = [rng.uniform(0.5, 1.5, D).astype(np.float32) for _ in range(L)]
+        self.norm = []
+        for w in self.norm_host:
+            a = tg.DeviceArray(D * 4)
+            a.upload(w)
+            self.norm.append(a)
         gb_, db_ = I * (D // 256) * 144, D * (I // 256) * 210
         for l in range(L):
             experts, rw = S.routing_rows(rng, 1, 128, 8)
@@ -83,10 +90,12 @@ class Layers:
             self.rw.append(rw)
         lib.tg_hip_synchronize()
 
-    def decode(self, h_dev, mode):
+    def decode(self, h_dev, mode, norm=False):
         lib = self.tg.lib()
         arr = (ctypes.c_void_p * self.L)(*self.plans)
-        d = lib.tg_hip_decode_create(ctypes.addressof(arr), self.L, None, ctypes.c_float(1e-6), h_dev, mode)
+        nw = (ctypes.c_void_p * self.L)(*[a.ptr for a in self.norm]) if norm else None
+        d = lib.tg_hip_decode_create(ctypes.addressof(arr), self.L, ctypes.addressof(nw) if norm else None,
+                                     ctypes.c_float(1e-6), h_dev, mode)
         assert d, self.tg.last_error()
         return d
 
@@ -94,15 +103,15 @@ class Layers:
         lib = self.tg.lib()
         for p in self.plans:
             lib.tg_hip_moe_plan_destroy(p)
-        for b in self.bufs:
+        for b in self.bufs + self.norm:
             b.free()
 
 
-def _run(tg, layers, mode, h0, steps=1, debug=None):
+def _run(tg, layers, mode, h0, steps=1, debug=None, norm=False):
     lib = tg.lib()
     h = tg.DeviceArray(D * 4)
     h.upload(h0)
-    d = layers.decode(h.ptr, mode)
+    d = layers.decode(h.ptr, mode, norm)
     if debug is not None:
         lib.tg_hip_decode_set_debug(d, debug.ptr)
     for _ in range(steps):
@@ -122,27 +131,29 @@ def qwen3(tg):
     ly.close()
 
 
-def test_decode_graph_equals_eager(tg, qwen3):
-    say("decode graph vs eager")
+@pytest.mark.parametrize("norm", [False, True])
+def test_decode_graph_equals_eager(tg, qwen3, norm):
+    say(f"decode graph vs eager norm={norm}")
     h0 = np.random.default_rng(1).standard_normal(D).astype(np.float32)
-    a, _ = _run(tg, qwen3, 0, h0, steps=2)
-    b, _ = _run(tg, qwen3, 1, h0, steps=2)
+    a, _ = _run(tg, qwen3, 0, h0, steps=2, norm=norm)
+    b, _ = _run(tg, qwen3, 1, h0, steps=2, norm=norm)
     assert a.tobytes() == b.tobytes()
 
 
-def test_decode_persistent_stagewise(tg, orc, qwen3):
-    say("decode persistent stage-wise")
+@pytest.mark.parametrize("norm", [False, True])
+def test_decode_persistent_stagewise(tg, orc, qwen3, norm):
+    say(f"decode persistent stage-wise norm={norm}")
     off = _dbg_offsets()
     assert off["BYTES"] == tg.lib().tg_hip_decode_debug_bytes()
     L = qwen3.L
     dbg = tg.DeviceArray(L * off["BYTES"])
     h0 = np.random.default_rng(2).standard_normal(D).astype(np.float32)
-    h_final, status = _run(tg, qwen3, 2, h0, debug=dbg)
+    h_final, status = _run(tg, qwen3, 2, h0, debug=dbg, norm=norm)
     assert status == 0, "grid barrier timed out"
     raw = dbg.download(np.uint8, L * off["BYTES"]).reshape(L, off["BYTES"])
     dbg.free()
-    ones = np.ones(D, np.float32)
     for l in range(L):
+        nw = qwen3.norm_host[l] if norm else np.ones(D, np.float32)
         rec = raw[l]
         f32 = lambda o, n: rec[o:o + 4 * n].view(np.float32)
         hin = f32(off["HIN"], D)
@@ -150,7 +161,7 @@ def test_decode_persistent_stagewise(tg, orc, qwen3):
         if l == 0:
             assert np.array_equal(hin, h0)
         # N
-        x_ref = orc.rms_norm(hin, ones, 1e-6)
+        x_ref = orc.rms_norm(hin, nw, 1e-6)
         assert np.abs(x - x_ref).max() <= 2e-6 * np.abs(x_ref).max(), l
         # Q1
         q = orc.quantize_q8(x)
@@ -180,14 +191,15 @@ def test_decode_persistent_stagewise(tg, orc, qwen3):
         assert err <= 1e-5, (l, err)
 
 
-def test_decode_persistent_matches_graph(tg, qwen3):
+@pytest.mark.parametrize("norm", [False, True])
+def test_decode_persistent_matches_graph(tg, qwen3, norm):
     """Same step through the persistent kernel and the graph of per-layer
     kernels: both follow the reference arithmetic; they may differ only by
     q8 rounding flips of intermediate values (sanity bound)."""
-    say("decode persistent vs graph")
+    say(f"decode persistent vs graph norm={norm}")
     h0 = np.random.default_rng(3).standard_normal(D).astype(np.float32)
-    a, _ = _run(tg, qwen3, 1, h0)
-    b, st = _run(tg, qwen3, 2, h0)
+    a, _ = _run(tg, qwen3, 1, h0, norm=norm)
+    b, st = _run(tg, qwen3, 2, h0, norm=norm)
     assert st == 0
     rel = np.abs(a - b).max() / np.abs(a).max()
     say(f"  persistent vs graph rel {rel:.2e}")
@@ -199,7 +211,7 @@ def test_decode_persistent_repeatable(tg, qwen3):
     (grid barriers, expert-order combine: no atomics on data)."""
     say("decode persistent repeatable")
     h0 = np.random.default_rng(4).standard_normal(D).astype(np.float32)
-    a, s1 = _run(tg, qwen3, 2, h0, steps=3)
-    b, s2 = _run(tg, qwen3, 2, h0, steps=3)
+    a, s1 = _run(tg, qwen3, 2, h0, steps=3, norm=True)
+    b, s2 = _run(tg, qwen3, 2, h0, steps=3, norm=True)
     assert s1 == 0 and s2 == 0
     assert a.tobytes() == b.tobytes()

@@ -22,8 +22,9 @@ struct DecodeLayer {
     int n;
 };
 
-/* Per-layer debug record written by workgroup 0 when a debug buffer is set
- * (stage-wise parity of the persistent step): byte offsets for D = 2048,
+/* Per-layer debug record written when a debug buffer is set (stage-wise
+ * parity of the persistent step; h and x parts by workgroup 0, expert slot
+ * e's hidden parts by the workgroup that owns expert e): byte offsets for D = 2048,
  * I = 768.  h_in f32[D] | x f32[D] | xq i8[D] | xd f32[D/256] | xs32 i32[D/32] |
  * hidden f32[8][I] | hq i8[8][I] | hd f32[8][I/256] | hs16 i32[8][I/16] */
 struct DecodeDebug {

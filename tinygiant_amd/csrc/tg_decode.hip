@@ -6,25 +6,34 @@
  * (tinygiant/engine.py:281-282,335-341 per layer; the expert math is
  * moe_phase_a / moe_phase_b of csrc/libtinygiant.c:1279-1384 for k = 1).
  *
- * Layout: one workgroup of NW compute waves (+1) per CU, all co-resident.
- * Each layer is two phases:
- *   A  every workgroup rebuilds q8(RMSNorm(h)) in LDS, then its waves compute
- *      gate/up rows (two rows per wave step for Q4_K, D = 2048) and write the
- *      activated hidden values;
- *   B  every workgroup re-quantizes all experts' hidden rows into LDS, then for
- *      each group of four output rows wave e computes expert e's down rows;
- *      the workgroup adds them to h in expert order (the reference's combine
- *      order, csrc/libtinygiant.c:1428-1434) and writes h.
- * Each phase's weights are loaded into registers as soon as the previous
- * phase has published its results, so the weight stream overlaps the
- * exchange that the next phase waits for.
+ * Placement.  One workgroup per CU, 256 workgroups; the dispatcher places
+ * workgroup g on XCD g % 8, so workgroup g = x + 8 j is rank j (of 32) on
+ * XCD x.  XCD x owns the layer's x-th active expert: its 32 workgroups split
+ * that expert's gate/up rows (24 each) and down rows (64 each), so the
+ * hidden vector an expert produces never leaves its XCD.  Per layer:
+ *   1  gather h: the 32 ranks of an XCD all-gather their 64-row slices of h
+ *   2  RMSNorm + q8 of h, in LDS, on every workgroup (8 blocks, one per wave)
+ *   3  gate/up rows of the workgroup's expert -> SwiGLU -> 24 hidden values
+ *   4  the XCD all-gathers its expert's 768 hidden values
+ *   5  q8 of the hidden vector (3 blocks)
+ *   6  down rows [64 j, 64 j + 64) of the expert
+ *   7  cross-XCD hop: rank j of every XCD exchanges its 64 down values, so
+ *      each holds all 8 experts' outputs for rows [64 j, 64 j + 64)
+ *   8  h[r] += w_e * out_e[r] in expert order (the reference's combine order,
+ *      csrc/libtinygiant.c:1428-1434); all 8 XCDs compute the same bits for
+ *      the slice and publish it for step 1 of the next layer.
+ * Only step 7 crosses XCDs.  Each layer's weights are loaded into registers
+ * one layer ahead (gate/up after step 3, down and the RMSNorm weight after
+ * step 6), so the weight stream overlaps the exchanges.
  *
- * Workgroups exchange h and the hidden values through epoch-tagged 16-byte
- * slots written and polled with device-scope coherent vector accesses; a
- * ninth wave per workgroup does the polling, so it never waits behind the
- * compute waves' outstanding weight loads.  Every wait is bounded and a
- * timed-out wait raises an abort flag that releases every other waiter, so
- * the grid always drains.
+ * Exchanges use epoch-tagged 16-byte slots {tag, v0, v1, v2}, written and
+ * polled with device-coherent (sc1) vector accesses so the tag and its values
+ * arrive together.  Two communication waves per workgroup do the polling and
+ * publishing, so a poll never waits behind the compute waves' outstanding
+ * weight loads.  Every wait is bounded; a timed-out wait raises an abort flag
+ * that releases every other waiter, so the grid always drains.  Placement
+ * only affects speed: every exchange is device-coherent wherever the
+ * workgroups run.
  */
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -47,30 +56,38 @@ constexpr int D = 2048, I = 768;      /* Qwen3-30B-A3B expert shape */
 constexpr int NBD = D / 256, NBI = I / 256;
 constexpr int GATE_RB = NBD * 144;    /* Q4_K row of D values */
 constexpr int DOWN_RB = NBI * 210;    /* Q6_K row of I values */
-constexpr int SA = 32;                /* lanes per gate/up row: 8 blocks x 4 items */
-constexpr int SB = 16;                /* lanes per down row: 3 blocks x 4 items = 12 used */
-constexpr int MAX_A = 2;              /* gate/up wave steps per wave per layer */
-constexpr int MAX_RG = 2;             /* down row groups per workgroup per layer */
-constexpr int MAX_B = 3;              /* (row group, expert) down items per wave per layer */
-constexpr int HS = 3;                 /* h slots per workgroup (8 rows, 3 values a slot) */
-constexpr int GS = 8;                 /* hidden slots per workgroup (<= 24 values) */
-constexpr int MAXPOLL = 16;           /* slots one communication lane polls */
-constexpr unsigned SPIN_LIMIT = 1u << 20;
-constexpr int MAX_LAYERS = 64;        /* layer descriptors staged in LDS */
 constexpr int NE = DECODE_MAXE;       /* active experts per layer (top-8 at k = 1) */
 constexpr int NWG = DECODE_GRID;      /* workgroups: one per CU */
-constexpr int PER_WG_A = NE * (I / 2) / NWG;   /* gate/up wave steps per workgroup: 12 */
-static_assert(NE * (I / 2) % NWG == 0, "gate/up steps divide over the grid");
-static_assert(PER_WG_A <= NW * MAX_A, "gate/up steps fit the waves");
-static_assert(2 * PER_WG_A <= 3 * GS, "hidden values fit the slots");
-static_assert(D / 4 <= MAX_RG * NWG && D / 4 > NWG, "row groups: two per workgroup");
-static_assert(MAX_RG * NE <= NW * MAX_B, "down items fit the waves");
+constexpr int NX = 8;                 /* XCDs; workgroup g runs on XCD g % NX */
+constexpr int NR = NWG / NX;          /* ranks (workgroups) per XCD */
+constexpr int RA = I / NR;            /* gate/up rows per workgroup: 24 */
+constexpr int RB = D / NR;            /* down rows (and h rows) per workgroup: 64 */
+constexpr int SA = 32;                /* lanes per gate/up row: 8 blocks x 4 items */
+constexpr int SB = 16;                /* lanes per down row: 3 blocks x 4 items = 12 used */
+constexpr int STEPS_A = RA / 2;       /* two-row wave steps: 12 */
+constexpr int STEPS_B = RB / 4;       /* four-row wave steps: 16 */
+constexpr int MAX_A = (STEPS_A + NW - 1) / NW;   /* 2 */
+constexpr int MAX_B = (STEPS_B + NW - 1) / NW;   /* 3 */
+constexpr int VPS = 3;                /* values per slot */
+constexpr int GS = RA / VPS;          /* hidden slots per workgroup: 8 */
+constexpr int PS = (RB + VPS - 1) / VPS;   /* slots per 64-row slice: 22 */
+constexpr unsigned SPIN_LIMIT = 1u << 20;
+constexpr int MAX_LAYERS = 64;        /* layer descriptors staged in LDS */
 constexpr int NTS = 16;               /* timestamps per layer */
+static_assert(NE == NX, "one expert per XCD");
+static_assert(NR * RA == I && NR * RB == D && RA % VPS == 0, "row split");
+static_assert(MAX_A == 2 && MAX_B == 3, "register budget assumes 2 gate/up and 3 down steps");
+static_assert((NR - 1) * PS <= 6 * CL && (NR - 1) * GS <= 2 * CL && (NX - 1) * PS <= 2 * CL, "poll shares");
+static_assert(NBI <= NA && NBD == NA, "q8 blocks per wave");
 
 /* A slot is 16 bytes {tag, v0, v1, v2} written and read as one vector access
- * with device-scope coherence (sc1), so the tag and its values arrive
- * together; consumers poll the tag of the epoch they need. */
+ * with device-scope coherence (sc1). */
 constexpr int CPOL_SC1 = 16;
+/* slot regions (u32x4 index), each double buffered by layer parity:
+ *   h slices  [2][NWG][PS]   rows [64 j, 64 j + 64) of the layer output
+ *   hidden    [2][NWG][GS]   the workgroup's 24 hidden values
+ *   partials  [2][NWG][PS]   the workgroup's 64 down values (unweighted) */
+constexpr uint32_t HSL = 0, GSL = 2u * NWG * PS, PSL = GSL + 2u * NWG * GS, NSLOTS = PSL + 2u * NWG * PS;
 
 /* ---- LDS images of q8 rows ---- */
 struct __attribute__((aligned(16))) LdsX {   /* q8(RMSNorm(h)) : D values */
@@ -78,10 +95,10 @@ struct __attribute__((aligned(16))) LdsX {   /* q8(RMSNorm(h)) : D values */
     float d[NBD];
     int32_t s32[NBD * 8];
 };
-struct __attribute__((aligned(16))) LdsH {   /* q8(hidden_e) for every expert : I values each */
-    int8_t qs[DECODE_MAXE][I];
-    float d[DECODE_MAXE][NBI];
-    int32_t s16[DECODE_MAXE][NBI * 16];
+struct __attribute__((aligned(16))) LdsH {   /* q8(hidden) of this XCD's expert : I values */
+    int8_t qs[I];
+    float d[NBI];
+    int32_t s16[NBI * 16];
 };
 
 __device__ inline FQ4K::X q4k_x_lds(const LdsX &x, int item) {
@@ -98,20 +115,20 @@ __device__ inline FQ4K::X q4k_x_lds(const LdsX &x, int item) {
     return r;
 }
 
-__device__ inline FQ6K::X q6k_x_lds(const LdsH &h, int e, int item) {
+__device__ inline FQ6K::X q6k_x_lds(const LdsH &h, int item) {
     const int b = item >> 2, u = item & 3, hh = u >> 1, l0 = (u & 1) * 16;
-    const int8_t *base = h.qs[e] + b * 256 + 128 * hh + l0;
+    const int8_t *base = h.qs + b * 256 + 128 * hh + l0;
     FQ6K::X r;
     r.x0 = *reinterpret_cast<const u32x4 *>(base);
     r.x1 = *reinterpret_cast<const u32x4 *>(base + 32);
     r.x2 = *reinterpret_cast<const u32x4 *>(base + 64);
     r.x3 = *reinterpret_cast<const u32x4 *>(base + 96);
     const int sg = b * 16 + 8 * hh + (u & 1);
-    r.s0 = h.s16[e][sg];
-    r.s1 = h.s16[e][sg + 2];
-    r.s2 = h.s16[e][sg + 4];
-    r.s3 = h.s16[e][sg + 6];
-    r.d = h.d[e][b];
+    r.s0 = h.s16[sg];
+    r.s1 = h.s16[sg + 2];
+    r.s2 = h.s16[sg + 4];
+    r.s3 = h.s16[sg + 6];
+    r.d = h.d[b];
     return r;
 }
 
@@ -138,26 +155,37 @@ __device__ inline uint32_t q8_block_wave(float v0, float v1, float v2, float v3,
 
 __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 
-/* Polls `count` slots (this lane's share, slot indices first, first + CL, ...)
- * until each carries `tag`, handing every arrived slot to `take`.  All
- * pending slots are re-read as one batch per round.  Returns false if the
- * wait timed out or another workgroup aborted. */
-template <class Take>
-__device__ inline bool poll_slots(Buf sl, uint32_t slot_base, int first, int count, unsigned tag, unsigned *abort_flag,
-                                  Take take) {
-    uint32_t pending = (1u << count) - 1u;   /* count <= MAXPOLL < 32 */
+__device__ inline void put_slot(Buf sl, uint32_t slot, unsigned tag, float a, float b, float c) {
+    u32x4 v;
+    v.x = tag;
+    v.y = __float_as_uint(a);
+    v.z = __float_as_uint(b);
+    v.w = __float_as_uint(c);
+    __builtin_amdgcn_raw_buffer_store_b128(v, sl.r, (int)(slot * 16u), 0, CPOL_SC1);
+}
+
+/* Polls this communication lane's share of `total` slots (flat indices
+ * cl, cl + CL, ...; slot(f) maps a flat index to a slot) until each carries
+ * `tag`, handing every arrived slot to take(f, v).  All pending slots are
+ * re-read as one batch per round.  Returns false if the wait timed out or
+ * another workgroup aborted. */
+template <int MAXP, class Slot, class Take>
+__device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsigned *abort_flag, Slot slot, Take take) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int i = 0; i < MAXP; i++)
+        if (cl + CL * i < total) pending |= 1u << i;
     unsigned spins = 0;
     while (pending) {
-        u32x4 v[MAXPOLL];
+        u32x4 v[MAXP];
 #pragma unroll
-        for (int i = 0; i < MAXPOLL; i++)
+        for (int i = 0; i < MAXP; i++)
             if (pending & (1u << i))
-                v[i] = __builtin_amdgcn_raw_buffer_load_b128(sl.r, (int)((slot_base + first + CL * i) * 16), 0,
-                                                             CPOL_SC1);
+                v[i] = __builtin_amdgcn_raw_buffer_load_b128(sl.r, (int)(slot(cl + CL * i) * 16u), 0, CPOL_SC1);
 #pragma unroll
-        for (int i = 0; i < MAXPOLL; i++)
+        for (int i = 0; i < MAXP; i++)
             if ((pending & (1u << i)) && v[i].x == tag) {
-                take(first + CL * i, v[i]);
+                take(cl + CL * i, v[i]);
                 pending &= ~(1u << i);
             }
         if (!pending) break;
@@ -174,81 +202,75 @@ __device__ inline bool poll_slots(Buf sl, uint32_t slot_base, int first, int cou
 
 }  // namespace
 
-/* Slot layout (u32x4 each, double buffered by layer parity):
- *   hslots [2][grid][HS]  rows of h written by phase B (8 rows per workgroup)
- *   gslots [2][grid][GS]  hidden values written by phase A (<= 24 per workgroup)
- * tags are base + 2 * layer + phase + 1, so a launch never mistakes a slot
- * of an earlier epoch for its own. */
+/* Tags are base + layer + 1 in every region, so a launch never mistakes a
+ * slot of an earlier layer or launch for its own.  A slot of parity p is
+ * rewritten two layers later only after every reader of it has published
+ * something the writer waited for in between. */
 __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restrict__ layers, int L, float *h,
                                                     u32x4 *slots, unsigned *abort_flag, unsigned base, float eps,
                                                     uint8_t *dbg, uint64_t *times) {
     __shared__ __attribute__((aligned(16))) float hx[D];          /* this layer's input h */
     __shared__ __attribute__((aligned(16))) float nws[D];         /* this layer's RMSNorm weight */
-    __shared__ __attribute__((aligned(16))) float hid[DECODE_MAXE][I];
+    __shared__ __attribute__((aligned(16))) float hid[I];         /* this XCD's expert hidden vector */
     __shared__ LdsX sx;
     __shared__ LdsH sh;
     __shared__ float red[NA];
-    __shared__ float part[MAX_RG][DECODE_MAXE][4];
-    __shared__ float aval[3 * GS];
-    __shared__ float hout[3 * HS];
+    __shared__ float aval[RA];
+    __shared__ float pp[NE][RB];                                  /* down values of every expert, own rows */
     __shared__ int lds_fail;
     __shared__ DecodeLayer lys[MAX_LAYERS];
 
-    constexpr int nwg = NWG;
     int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid when >= 0 */
+    const int ct = (int)threadIdx.x;             /* compute lane, valid when < NW * 64 */
     if (threadIdx.x == 0) lds_fail = 0;
     const int wg = blockIdx.x;
-    const uint32_t hs_base = 0, gs_base = 2u * nwg * HS;
-    Buf sl = make_buf(slots, (uint32_t)(2u * nwg * (HS + GS) * 16u));
+    const int xe = wg % NX, rk = wg / NX;        /* expert slot (= XCD) and rank */
+    Buf sl = make_buf(slots, NSLOTS * 16u);
 
     typename FQ4K::W wg_[MAX_A], wu_[MAX_A];
     typename FQ6K::W wd_[MAX_B];
+    u32x4 nw0, nw1;                              /* next layer's RMSNorm weight (compute lanes) */
 
-    /* phase A steps: (expert, pair of rows); PER_WG_A consecutive steps a workgroup */
-    auto a_step = [&](const DecodeLayer &, int i, int &e, int &r) -> bool {
-        const int local = wave + i * NW;
-        const int s = wg * PER_WG_A + local;
-        if (wave >= NW || local >= PER_WG_A) return false;
-        e = s / (I / 2);
-        r = (s % (I / 2)) * 2 + (lane >> 5);
-        return true;
-    };
     /* loads are unconditional so the registers' live ranges end at their
      * use; an inactive step reads through an empty descriptor (zeros, no
      * memory access) */
     auto load_a = [&](const DecodeLayer &ly) {
+        const bool cw = wave < NW;
+        Buf gb = make_buf_uniform(cw ? ly.gate[xe] : nullptr, cw ? (uint32_t)I * GATE_RB : 0u);
+        Buf ub = make_buf_uniform(cw ? ly.up[xe] : nullptr, cw ? (uint32_t)I * GATE_RB : 0u);
 #pragma unroll
         for (int i = 0; i < MAX_A; i++) {
-            int e = 0, r = 0;
-            const bool act = a_step(ly, i, e, r);
-            const uint32_t nb = act ? (uint32_t)I * GATE_RB : 0u;
-            Buf gb = make_buf(act ? ly.gate[e] : nullptr, nb);
-            Buf ub = make_buf(act ? ly.up[e] : nullptr, nb);
-            wg_[i] = FQ4K::load_w(gb, (uint32_t)r * GATE_RB, lane & 31);
-            wu_[i] = FQ4K::load_w(ub, (uint32_t)r * GATE_RB, lane & 31);
+            const int s = wave + i * NW;
+            /* an out-of-range step reads past the rows (zeros) */
+            const uint32_t r = s < STEPS_A ? (uint32_t)(RA * rk + 2 * s + (lane >> 5)) : (uint32_t)I;
+            wg_[i] = FQ4K::load_w(gb, r * GATE_RB, lane & 31);
+            wu_[i] = FQ4K::load_w(ub, r * GATE_RB, lane & 31);
         }
     };
-    /* phase B: row groups rg = wg + i * grid (4 rows each, i < MAX_RG); the
-     * (row group, expert) items are spread over the compute waves */
-    auto nrg = [&]() { return wg + nwg < D / 4 ? 2 : 1; };
-    auto b_item = [&](const DecodeLayer &, int t, int &i, int &e) -> bool {
-        const int it = wave + t * NW;
-        if (wave >= NW || it >= nrg() * NE) return false;
-        i = it / NE;
-        e = it % NE;
-        return true;
-    };
     auto load_b = [&](const DecodeLayer &ly) {
+        const bool cw = wave < NW;
+        Buf db = make_buf_uniform(cw ? ly.down[xe] : nullptr, cw ? (uint32_t)D * DOWN_RB : 0u);
+        const int item = (lane & 15) < NBI * 4 ? (lane & 15) : 0;
 #pragma unroll
         for (int t = 0; t < MAX_B; t++) {
-            int i = 0, e = 0;
-            const bool act = b_item(ly, t, i, e);
-            const int item = (lane & 15) < NBI * 4 ? (lane & 15) : 0;
-            const int r = (wg + i * nwg) * 4 + (lane >> 4);
-            Buf db = make_buf(act ? ly.down[e] : nullptr, act ? (uint32_t)D * DOWN_RB : 0u);
-            wd_[t] = FQ6K::load_w(db, (uint32_t)r * DOWN_RB, item);
+            const int q = wave + t * NW;
+            const uint32_t r = q < STEPS_B ? (uint32_t)(RB * rk + 4 * q + (lane >> 4)) : (uint32_t)D;
+            wd_[t] = FQ6K::load_w(db, r * DOWN_RB, item);
+        }
+    };
+    /* RMSNorm weight: compute lane t holds float4 t and (t < 128) float4 384 + t */
+    auto load_nw = [&](const DecodeLayer &ly) {
+        const bool on = wave < NW && ly.norm_w != nullptr;
+        Buf nb = make_buf_uniform(on ? ly.norm_w : nullptr, on ? (uint32_t)D * 4u : 0u);
+        nw0 = ld16(nb, (uint32_t)ct * 16u);
+        nw1 = ld16(nb, (uint32_t)(NW * 64 + ct) * 16u);
+    };
+    auto store_nw = [&]() {
+        if (wave < NW) {
+            reinterpret_cast<u32x4 *>(nws)[ct] = nw0;
+            if (ct < D / 4 - NW * 64) reinterpret_cast<u32x4 *>(nws)[NW * 64 + ct] = nw1;
         }
     };
 
@@ -262,55 +284,52 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     }
     for (int t = threadIdx.x; t < D / 4; t += NT) reinterpret_cast<u32x4 *>(hx)[t] = reinterpret_cast<const u32x4 *>(h)[t];
     __syncthreads();
+    load_nw(lys[0]);
     load_a(lys[0]);
+    load_b(lys[0]);
+    store_nw();
 
     for (int l = 0; l < L; l++) {
         const DecodeLayer &ly = lys[l];
         const unsigned par = (unsigned)(l & 1);
-        /* an opaque copy of the communication lane keeps the slot address and
-         * scatter arithmetic inside the loop instead of hoisted (and live)
-         * across every layer */
+        const unsigned tag = base + (unsigned)l + 1u;
+        const bool has_nw = ly.norm_w != nullptr;
+        /* an opaque copy of the lane keeps per-lane address arithmetic inside
+         * the loop instead of hoisted (and live) across every layer */
         int clv = cl;
         asm volatile("" : "+v"(clv));
         asm volatile("" : "+v"(lane));
         /* optional phase timestamps (100 MHz clock) of the first and last workgroup */
-        const bool tw = times && threadIdx.x == 0 && (wg == 0 || wg == nwg - 1);
+        const bool tw = times && threadIdx.x == 0 && (wg == 0 || wg == NWG - 1);
         uint64_t *tr = tw ? times + ((size_t)(wg == 0 ? 0 : 1) * L + l) * NTS : nullptr;
         if (tw) tr[0] = wall_clock64();
-        /* ---- phase A: collect h from the previous layer's phase B ---- */
+        /* ---- 1: gather h from the other ranks of this XCD ---- */
         if (l > 0) {
             if (cl >= 0) {
-                const unsigned tag = base + 2u * (unsigned)(l - 1) + 2u;
-                const int total = nwg * HS;
-                const int cnt = total > clv ? (total - clv + CL - 1) / CL : 0;
-                const bool ok = poll_slots(sl, hs_base + ((par ^ 1u) * nwg * HS), clv, cnt, tag, abort_flag,
-                                           [&](int s, const u32x4 &v) {
-                                               const int p = s / HS, j = s % HS;
-                                               const float vv[3] = {__uint_as_float(v.y), __uint_as_float(v.z),
-                                                                    __uint_as_float(v.w)};
-#pragma unroll
-                                               for (int k = 0; k < 3; k++) {
-                                                   const int q = 3 * j + k;
-                                                   const int rg = p + (q >> 2) * nwg;
-                                                   if (q < 8 && rg < D / 4) hx[rg * 4 + (q & 3)] = vv[k];
-                                               }
-                                           });
+                const bool ok = poll_slots<6>(
+                    sl, clv, (NR - 1) * PS, base + (unsigned)l, abort_flag,
+                    [&](int f) {
+                        const int jj = f / PS, t = f % PS;
+                        const int j = jj + (jj >= rk);
+                        return HSL + ((par ^ 1u) * NWG + (uint32_t)(xe + NX * j)) * PS + (uint32_t)t;
+                    },
+                    [&](int f, const u32x4 &v) {
+                        const int jj = f / PS, t = f % PS;
+                        const int j = jj + (jj >= rk);
+                        float *o = hx + RB * j + VPS * t;
+                        o[0] = __uint_as_float(v.y);
+                        if (VPS * t + 1 < RB) o[1] = __uint_as_float(v.z);
+                        if (VPS * t + 2 < RB) o[2] = __uint_as_float(v.w);
+                    });
                 if (!ok) lds_fail = 1;
+            } else {
+                store_nw();
             }
             __syncthreads();
             if (lds_fail) return;
         }
-        /* the RMSNorm weight reaches LDS through the communication waves (the
-         * compute waves keep only weight loads in flight) */
-        const float *nw = ly.norm_w;
-        if (nw) {
-            if (cl >= 0)
-                for (int t = cl; t < D / 4; t += CL)
-                    reinterpret_cast<u32x4 *>(nws)[t] = reinterpret_cast<const u32x4 *>(nw)[t];
-            __syncthreads();
-        }
         if (tw) tr[1] = wall_clock64();
-        /* RMSNorm (weight 1 or norm_w) then q8, all in LDS; wave w owns block w */
+        /* ---- 2: RMSNorm (weight norm_w or 1) then q8, in LDS; wave w owns block w ---- */
         {
             const u32x4 hv = reinterpret_cast<const u32x4 *>(hx)[threadIdx.x];
             float v0 = __uint_as_float(hv.x), v1 = __uint_as_float(hv.y);
@@ -324,12 +343,17 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
 #pragma unroll
             for (int i = 0; i < NA; i++) tot += red[i];
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
-            const int c = threadIdx.x * 4;
             const u32x4 hv = reinterpret_cast<const u32x4 *>(hx)[threadIdx.x];
-            const float v0 = (__uint_as_float(hv.x) * scale) * (nw ? nws[c] : 1.f);
-            const float v1 = (__uint_as_float(hv.y) * scale) * (nw ? nws[c + 1] : 1.f);
-            const float v2 = (__uint_as_float(hv.z) * scale) * (nw ? nws[c + 2] : 1.f);
-            const float v3 = (__uint_as_float(hv.w) * scale) * (nw ? nws[c + 3] : 1.f);
+            u32x4 wv;
+            if (has_nw) {
+                wv = reinterpret_cast<const u32x4 *>(nws)[threadIdx.x];
+            } else {
+                wv.x = wv.y = wv.z = wv.w = __float_as_uint(1.f);
+            }
+            const float v0 = (__uint_as_float(hv.x) * scale) * __uint_as_float(wv.x);
+            const float v1 = (__uint_as_float(hv.y) * scale) * __uint_as_float(wv.y);
+            const float v2 = (__uint_as_float(hv.z) * scale) * __uint_as_float(wv.z);
+            const float v3 = (__uint_as_float(hv.w) * scale) * __uint_as_float(wv.w);
             const uint32_t q = q8_block_wave(v0, v1, v2, v3, lane, &sx.d[wave], &sx.s32[wave * 8], nullptr);
             reinterpret_cast<uint32_t *>(sx.qs)[threadIdx.x] = q;
             if (dbg && wg == 0) {
@@ -352,123 +376,140 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (threadIdx.x < NBD * 8)
                 reinterpret_cast<int32_t *>(rec + DecodeDebug::XS32)[threadIdx.x] = sx.s32[threadIdx.x];
         }
-        /* gate/up rows of this workgroup */
+        /* ---- 3: gate/up rows [24 rk, 24 rk + 24) of expert xe -> SwiGLU ---- */
+        if (wave < NW) {
 #pragma unroll
-        for (int i = 0; i < MAX_A; i++) {
-            int e, r;
-            const bool act = a_step(ly, i, e, r);
-            float vg = 0.f, vu = 0.f;
-            if (act) {
+            for (int i = 0; i < MAX_A; i++) {
+                const int s = wave + i * NW;
                 const int item = lane & 31;
                 FQ4K::X xs = q4k_x_lds(sx, item);
-                vg = FQ4K::value(wg_[i], xs, item);
-                vu = FQ4K::value(wu_[i], xs, item);
+                float vg = FQ4K::value(wg_[i], xs, item);
+                float vu = FQ4K::value(wu_[i], xs, item);
+                vg = seg_sum_last<SA>(vg);
+                vu = seg_sum_last<SA>(vu);
+                if (s < STEPS_A && (lane & 31) == 31) aval[2 * s + (lane >> 5)] = silu_mul(vg, vu);
             }
-            if (tw && i == 0) tr[8] = wall_clock64();
-            vg = seg_sum_last<SA>(vg);
-            vu = seg_sum_last<SA>(vu);
-            if (tw && i == 0) tr[9] = wall_clock64();
-            if (act && (lane & 31) == 31) aval[2 * (wave + i * NW) + (lane >> 5)] = silu_mul(vg, vu);
+            /* the next layer's gate/up rows load while this layer finishes */
+            if (l + 1 < L) load_a(lys[l + 1]);
         }
         __syncthreads();
         if (tw) tr[3] = wall_clock64();
-        /* publish: GS slots of 3 values (workgroup-local value order) */
-        if (threadIdx.x < GS) {
-            u32x4 v;
-            v.x = base + 2u * (unsigned)l + 1u;   /* slots past 2 * PER_WG_A values carry no data */
-            v.y = __float_as_uint(aval[3 * threadIdx.x]);
-            v.z = __float_as_uint(aval[3 * threadIdx.x + 1]);
-            v.w = __float_as_uint(aval[3 * threadIdx.x + 2]);
-            __builtin_amdgcn_raw_buffer_store_b128(v, sl.r, (int)((gs_base + (par * nwg + wg) * GS + threadIdx.x) * 16),
-                                                   0, CPOL_SC1);
-        }
-        /* ---- phase B: fetch the down rows while the hidden values travel ---- */
-        if (wave < NW) load_b(ly);
+        /* ---- 4: all-gather the expert's hidden vector within the XCD ---- */
         if (cl >= 0) {
-            const unsigned tag = base + 2u * (unsigned)l + 1u;
-            const int total = nwg * GS;
-            const int cnt = total > clv ? (total - clv + CL - 1) / CL : 0;
-            const bool ok = poll_slots(sl, gs_base + par * nwg * GS, clv, cnt, tag, abort_flag,
-                                       [&](int s, const u32x4 &v) {
-                                           const int p = s / GS, j = s % GS;
-                                           const float vv[3] = {__uint_as_float(v.y), __uint_as_float(v.z),
-                                                                __uint_as_float(v.w)};
-#pragma unroll
-                                           for (int k = 0; k < 3; k++) {
-                                               const int q = 3 * j + k;      /* value index in producer p */
-                                               const int loc = q >> 1;
-                                               const int st = p * PER_WG_A + loc;
-                                               if (loc < PER_WG_A)
-                                                   hid[st / (I / 2)][(st % (I / 2)) * 2 + (q & 1)] = vv[k];
-                                           }
-                                       });
+            if (clv < GS)
+                put_slot(sl, GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, aval[VPS * clv],
+                         aval[VPS * clv + 1], aval[VPS * clv + 2]);
+            if (clv < RA) hid[RA * rk + clv] = aval[clv];
+            const bool ok = poll_slots<2>(
+                sl, clv, (NR - 1) * GS, tag, abort_flag,
+                [&](int f) {
+                    const int jj = f / GS, t = f % GS;
+                    const int j = jj + (jj >= rk);
+                    return GSL + (par * NWG + (uint32_t)(xe + NX * j)) * GS + (uint32_t)t;
+                },
+                [&](int f, const u32x4 &v) {
+                    const int jj = f / GS, t = f % GS;
+                    const int j = jj + (jj >= rk);
+                    float *o = hid + RA * j + VPS * t;
+                    o[0] = __uint_as_float(v.y);
+                    o[1] = __uint_as_float(v.z);
+                    o[2] = __uint_as_float(v.w);
+                });
             if (!ok) lds_fail = 1;
         }
         __syncthreads();
         if (lds_fail) return;
         if (tw) tr[4] = wall_clock64();
-        /* q8 of every expert's hidden row: NBI blocks per expert, one wave per block */
-        for (int blk = wave; blk < NE * NBI; blk += NA) {
-            const int e = blk / NBI, b = blk % NBI;
-            const u32x4 hv = reinterpret_cast<const u32x4 *>(&hid[e][b * 256])[lane];
+        /* ---- 5: q8 of the hidden vector, one wave per 256-block ---- */
+        if (wave < NBI) {
+            const int b = wave;
+            const u32x4 hv = reinterpret_cast<const u32x4 *>(hid + b * 256)[lane];
             const uint32_t q = q8_block_wave(__uint_as_float(hv.x), __uint_as_float(hv.y), __uint_as_float(hv.z),
-                                             __uint_as_float(hv.w), lane, &sh.d[e][b], nullptr, &sh.s16[e][b * 16]);
-            reinterpret_cast<uint32_t *>(sh.qs[e] + b * 256)[lane] = q;
-            if (dbg && wg == 0) {
+                                             __uint_as_float(hv.w), lane, &sh.d[b], nullptr, &sh.s16[b * 16]);
+            reinterpret_cast<uint32_t *>(sh.qs + b * 256)[lane] = q;
+            if (dbg && rk == 0) {   /* workgroups 0..7: expert slot xe's record */
                 uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
-                reinterpret_cast<u32x4 *>(rec + DecodeDebug::HID + (e * I + b * 256) * 4)[lane] = hv;
-                reinterpret_cast<uint32_t *>(rec + DecodeDebug::HQ + e * I + b * 256)[lane] = q;
+                reinterpret_cast<u32x4 *>(rec + DecodeDebug::HID + (xe * I + b * 256) * 4)[lane] = hv;
+                reinterpret_cast<uint32_t *>(rec + DecodeDebug::HQ + xe * I + b * 256)[lane] = q;
             }
         }
         __syncthreads();
         if (tw) tr[5] = wall_clock64();
-        if (dbg && wg == 0) {
+        if (dbg && rk == 0) {
             uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
-            if (threadIdx.x < DECODE_MAXE * NBI)
-                reinterpret_cast<float *>(rec + DecodeDebug::HD)[threadIdx.x] = (&sh.d[0][0])[threadIdx.x];
-            for (int t = threadIdx.x; t < DECODE_MAXE * NBI * 16; t += NT)
-                reinterpret_cast<int32_t *>(rec + DecodeDebug::HS16)[t] = (&sh.s16[0][0])[t];
+            if (threadIdx.x < NBI) reinterpret_cast<float *>(rec + DecodeDebug::HD)[xe * NBI + threadIdx.x] = sh.d[threadIdx.x];
+            if (threadIdx.x < NBI * 16)
+                reinterpret_cast<int32_t *>(rec + DecodeDebug::HS16)[xe * NBI * 16 + threadIdx.x] = sh.s16[threadIdx.x];
         }
-        /* down rows of every (row group, expert) item, then the combine in
-         * expert order */
+        /* ---- 6: down rows [64 rk, 64 rk + 64) of expert xe ---- */
+        if (wave < NW) {
 #pragma unroll
-        for (int t = 0; t < MAX_B; t++) {
-            int i, e;
-            const bool act = b_item(ly, t, i, e);
-            const int item = lane & 15;
-            float v = 0.f;
-            if (act && item < NBI * 4) {
-                FQ6K::X xs = q6k_x_lds(sh, e, item);
-                v = FQ6K::value(wd_[t], xs, item);
+            for (int t = 0; t < MAX_B; t++) {
+                const int q = wave + t * NW;
+                const int item = lane & 15;
+                float v = 0.f;
+                if (item < NBI * 4) {
+                    FQ6K::X xs = q6k_x_lds(sh, item);
+                    v = FQ6K::value(wd_[t], xs, item);
+                }
+                v = seg_sum_last<SB>(v);
+                if (q < STEPS_B && (lane & 15) == 15) pp[xe][4 * q + (lane >> 4)] = v;
             }
-            v = seg_sum_last<SB>(v);
-            if (act && (lane & 15) == 15) part[i][e][lane >> 4] = v;
-        }
-        __syncthreads();
-        if ((int)threadIdx.x < 4 * nrg()) {
-            const int i = threadIdx.x >> 2, t4 = threadIdx.x & 3;
-            const int r = (wg + i * nwg) * 4 + t4;
-            float o = hx[r];
-#pragma unroll
-            for (int e = 0; e < NE; e++) o += ly.w[e] * part[i][e][t4];
-            hout[threadIdx.x] = o;
-            if (l == L - 1) h[r] = o;
+            /* the next layer's RMSNorm weight and down rows load while h travels */
+            if (l + 1 < L) {
+                load_nw(lys[l + 1]);
+                load_b(lys[l + 1]);
+            }
         }
         __syncthreads();
         if (tw) tr[6] = wall_clock64();
-        /* publish this workgroup's h rows for the next layer */
-        if (l + 1 < L && threadIdx.x < HS) {
-            u32x4 v;
-            v.x = base + 2u * (unsigned)l + 2u;
-            v.y = __float_as_uint(hout[3 * threadIdx.x]);
-            v.z = __float_as_uint(hout[3 * threadIdx.x + 1]);
-            v.w = __float_as_uint(hout[3 * threadIdx.x + 2]);
-            __builtin_amdgcn_raw_buffer_store_b128(v, sl.r, (int)((hs_base + (par * nwg + wg) * HS + threadIdx.x) * 16),
-                                                   0, CPOL_SC1);
+        /* ---- 7: cross-XCD hop: rank rk of every XCD trades its 64 down values ---- */
+        if (cl >= 0) {
+            if (clv < PS) {
+                const int r0 = VPS * clv;
+                put_slot(sl, PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, pp[xe][r0],
+                         r0 + 1 < RB ? pp[xe][r0 + 1] : 0.f, r0 + 2 < RB ? pp[xe][r0 + 2] : 0.f);
+            }
+            const bool ok = poll_slots<2>(
+                sl, clv, (NX - 1) * PS, tag, abort_flag,
+                [&](int f) {
+                    const int xx = f / PS, t = f % PS;
+                    const int x = xx + (xx >= xe);
+                    return PSL + (par * NWG + (uint32_t)(x + NX * rk)) * PS + (uint32_t)t;
+                },
+                [&](int f, const u32x4 &v) {
+                    const int xx = f / PS, t = f % PS;
+                    const int x = xx + (xx >= xe);
+                    float *o = pp[x] + VPS * t;
+                    o[0] = __uint_as_float(v.y);
+                    if (VPS * t + 1 < RB) o[1] = __uint_as_float(v.z);
+                    if (VPS * t + 2 < RB) o[2] = __uint_as_float(v.w);
+                });
+            if (!ok) lds_fail = 1;
         }
-        /* the next layer's gate/up rows load while h travels */
-        if (l + 1 < L && wave < NW) load_a(lys[l + 1]);
+        __syncthreads();
+        if (lds_fail) return;
         if (tw) tr[7] = wall_clock64();
+        /* ---- 8: combine rows [64 rk, 64 rk + 64) in expert order, publish ---- */
+        if (cl >= 0 && clv < PS) {
+            float o[VPS];
+#pragma unroll
+            for (int k = 0; k < VPS; k++) {
+                const int rl = VPS * clv + k;
+                if (rl < RB) {
+                    float a = hx[RB * rk + rl];
+#pragma unroll
+                    for (int e = 0; e < NE; e++) a += ly.w[e] * pp[e][rl];
+                    o[k] = a;
+                    hx[RB * rk + rl] = a;
+                    if (l == L - 1 && xe == 0) h[RB * rk + rl] = a;
+                } else {
+                    o[k] = 0.f;
+                }
+            }
+            if (l + 1 < L) put_slot(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], o[1], o[2]);
+        }
+        if (tw) tr[8] = wall_clock64();
     }
 }
 
@@ -483,7 +524,7 @@ int decode_qwen_max_grid() {
     return per_cu * pr.multiProcessorCount;
 }
 
-size_t decode_qwen_slot_bytes(int grid) { return (size_t)2 * grid * (HS + GS) * 16; }
+size_t decode_qwen_slot_bytes(int) { return (size_t)NSLOTS * 16; }
 
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
                               unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,

@@ -41,6 +41,16 @@ __device__ inline Buf make_buf(const void *p, uint32_t nbytes) {
     b.r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)nbytes, 0x00020000);
     return b;
 }
+/* Descriptor for a pointer that is wave-uniform although the compiler cannot
+ * prove it (e.g. read from LDS): readfirstlane keeps the descriptor in SGPRs,
+ * where a VGPR descriptor would wrap every access in a waterfall loop. */
+__device__ inline Buf make_buf_uniform(const void *p, uint32_t nbytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32));
+    const uint32_t n = (uint32_t)__builtin_amdgcn_readfirstlane((int)nbytes);
+    return make_buf((const void *)(uintptr_t)(((uint64_t)hi << 32) | lo), n);
+}
 __device__ inline u32x4 ld16(Buf b, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, 0);
 }
