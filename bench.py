@@ -179,6 +179,41 @@ def phase_breakdown(tg, step, layers):
     return out
 
 
+def boundary_probe(tg, routes, calls=50):
+    """The reference's own entry point through ctypes: tg_moe_forward_rows_v2
+    on host input/output arrays for one layer (k = 1), its 24 weight matrices
+    made HBM-resident with tg_mlock as tinygiant/cache.py:153-162 does.  Each
+    call copies the 8 KB input in and the 8 KB output back over PCIe and
+    synchronizes, so this is the per-layer latency an unchanged engine sees."""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    idx, w = routes[0]
+    mats = []
+    for e in idx:
+        for part, kind, nb in ((0, 0, I * (D // 256) * 144), (1, 0, I * (D // 256) * 144),
+                               (2, 2, D * (I // 256) * 210)):
+            m = tg.synth_host(kind, S.tensor_seed(SEED, 0, int(e), part), nb)
+            if lib.tg_mlock(m.ctypes.data, ctypes.c_size_t(m.nbytes)) != 0:
+                raise RuntimeError("tg_mlock failed")
+            mats.append(m)
+    n = len(idx)
+    gates, ups, downs = mats[0::3], mats[1::3], mats[2::3]
+    x = np.random.default_rng(SEED + 3).standard_normal((1, D)).astype(np.float32)
+    rw = w.reshape(-1, 1).astype(np.float32)
+    out = np.zeros((1, D), np.float32)
+    for _ in range(5):
+        tg.moe_forward_rows_v2(gates, ups, downs, 0, [2] * n, None, None, None, 0, rw, x, out, I)
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        tg.moe_forward_rows_v2(gates, ups, downs, 0, [2] * n, None, None, None, 0, rw, x, out, I)
+    dt = (time.perf_counter() - t0) / calls
+    for m in mats:
+        lib.tg_hip_unregister(m.ctypes.data)
+    return {"entry": "tg_moe_forward_rows_v2 via ctypes, host buffers, tg_mlock-resident weights, k=1",
+            "us_per_layer_call": round(dt * 1e6, 1), "weight_gbps": round(n * EXPERT_B / dt / 1e9, 1),
+            "tok_s_if_48_calls": round(1.0 / (dt * L), 1)}
+
+
 def read_traffic(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
@@ -199,8 +234,10 @@ def main():
     ap.add_argument("--layers", type=int, default=L)
     ap.add_argument("--cpu-layers", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--mode", choices=["persistent", "graph", "eager"], default="persistent",
-                    help="persistent: one cooperative kernel per step; graph: per-layer kernels in a HIP graph")
+    ap.add_argument("--no-boundary", action="store_true", help="skip the ctypes-entry latency probe")
+    ap.add_argument("--mode", choices=["persistent", "persistent-plain", "graph", "eager"], default="persistent",
+                    help="persistent: one cooperative kernel per step (persistent-plain: the same kernel through "
+                         "a plain launch, for profilers); graph: per-layer kernels in a HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only time a plain 1 GiB device copy (HBM reference / counter calibration)")
     args = ap.parse_args()
@@ -233,7 +270,7 @@ def main():
         nbufs.append(a)
     parr = (ctypes.c_void_p * layers)(*plans)
     narr = (ctypes.c_void_p * layers)(*[a.ptr for a in nbufs])
-    mode = {"eager": 0, "graph": 1, "persistent": 2}[args.mode]
+    mode = {"eager": 0, "graph": 1, "persistent": 2, "persistent-plain": 3}[args.mode]
     step = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, ctypes.addressof(narr), ctypes.c_float(1e-6),
                                     h.ptr, mode)
     if not step:
@@ -254,10 +291,10 @@ def main():
     log(f"timed {args.steps} steps: {ms:.2f} ms events, {wall * 1e3:.2f} ms wall")
 
     phases = None
-    if mode == 2:
+    if mode >= 2:
         phases = phase_breakdown(tg, step, layers)
         log(f"phase breakdown (us per layer, first/last workgroup): {json.dumps(phases)}")
-    if mode == 2:
+    if mode >= 2:
         # the whole step is one kernel: its launch duration is the step time
         per_kernel = {"k_decode_qwen": {"avg_us": round(ms_step * 1e3, 2), "launches": args.steps}}
         kernel_name = "k_decode_qwen (persistent: 48 layers x (gate/up + down), one launch per token)"
@@ -313,8 +350,11 @@ def main():
     lib.tg_hip_decode_destroy(step)
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
-    for b in bufs:
+    for b in bufs + nbufs:
         b.free()
+    if not args.no_boundary:
+        log("boundary probe ...")
+        result["boundary"] = boundary_probe(tg, routes)
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(routes, min(args.cpu_layers, layers))

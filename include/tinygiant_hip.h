@@ -182,7 +182,10 @@ void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev,
  * mode 0 queues the per-layer kernels, 1 replays them as one HIP graph,
  * 2 runs the whole step as one persistent cooperative kernel (k = 1,
  * D = 2048, I = 768, Q4_K gate/up, Q6_K down, SiLU, no biases, exactly 8
- * active experts per layer, <= 64 layers, 256 co-resident workgroups). */
+ * active experts per layer, <= 64 layers, 256 co-resident workgroups);
+ * 3 launches the same kernel with a plain launch (for tools that do not
+ * follow cooperative launches; needs an otherwise idle device, and a step
+ * whose workgroups are not all resident ends with status 1). */
 typedef struct tg_hip_decode tg_hip_decode;
 tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers,
                                     const float *const *norm_w_dev, float eps, float *h_dev,

@@ -215,3 +215,15 @@ def test_decode_persistent_repeatable(tg, qwen3):
     b, s2 = _run(tg, qwen3, 2, h0, steps=3, norm=True)
     assert s1 == 0 and s2 == 0
     assert a.tobytes() == b.tobytes()
+
+
+def test_decode_plain_launch_equals_cooperative(tg, qwen3):
+    """Mode 3 runs the same persistent kernel through a plain launch: on an
+    idle device every workgroup is resident, and the result is bit-identical
+    to the cooperative launch's."""
+    say("decode persistent plain launch vs cooperative")
+    h0 = np.random.default_rng(5).standard_normal(D).astype(np.float32)
+    a, s1 = _run(tg, qwen3, 2, h0, steps=2, norm=True)
+    b, s2 = _run(tg, qwen3, 3, h0, steps=2, norm=True)
+    assert s1 == 0 and s2 == 0
+    assert a.tobytes() == b.tobytes()

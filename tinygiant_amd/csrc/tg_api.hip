@@ -980,9 +980,15 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
     }
     d->eps = eps;
     d->h = h_dev;
+    if (use_graph < 0 || use_graph > 3) {
+        set_err("tg_hip_decode_create: mode %d (0 kernels, 1 graph, 2 persistent, 3 persistent plain launch)",
+                use_graph);
+        delete d;
+        return nullptr;
+    }
     d->mode = use_graph;
     HIPCHECK(hipMalloc(&d->x, (size_t)d->k * d->D * 4));
-    if (use_graph == 2) {
+    if (use_graph >= 2) {
         std::vector<DecodeLayer> ls;
         if (!persistent_ok(d, ls)) {
             HIPCHECK(hipFree(d->x));
@@ -1031,9 +1037,9 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!d) return;
     hipStream_t st = stream ? (hipStream_t)stream : g.st;
-    if (d->mode == 2) {
+    if (d->mode >= 2) {
         HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
-                                    d->grid, st));
+                                    d->grid, d->mode == 2, st));
         d->base += 2u * (unsigned)d->L;
     } else if (d->exec) {
         HIPCHECK(hipGraphLaunch(d->exec, st));
@@ -1064,7 +1070,7 @@ TG_API void tg_hip_decode_set_timing(tg_hip_decode *d, void *times_dev) {
  * barrier wait timed out (the results of that step are invalid). */
 TG_API int tg_hip_decode_status(tg_hip_decode *d) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!d || d->mode != 2) return 0;
+    if (!d || d->mode < 2) return 0;
     unsigned w;
     HIPCHECK(hipStreamSynchronize(g.st));
     HIPCHECK(hipMemcpy(&w, d->sync, 4, hipMemcpyDeviceToHost));
@@ -1114,7 +1120,7 @@ TG_API void tg_hip_decode_kernel_times(tg_hip_decode *d, float *ms_out, int *n_o
         ms_out[i] = 0.f;
         n_out[i] = 0;
     }
-    if (d->mode == 2) return;   /* one kernel per step: tg_hip_decode_time is its duration */
+    if (d->mode >= 2) return;   /* one kernel per step: tg_hip_decode_time is its duration */
     std::vector<hipEvent_t> ev;
     std::vector<int> cls;
     auto mark = [&](int c) {

@@ -42,12 +42,15 @@ DecodeShape decode_qwen_shape();
 
 /* Queues one step.  slots_dev holds decode_qwen_slot_bytes(grid) zeroed
  * bytes; `base` advances by 2 * L per launch (slot tags are base-relative);
- * abort_dev is one word, nonzero after a timed-out wait.  Returns the status
- * of the cooperative launch. */
+ * abort_dev is one word, nonzero after a timed-out wait.  A cooperative
+ * launch fails unless every workgroup can be resident at once; a plain launch
+ * relies on the device being otherwise idle (the occupancy check at set-up
+ * shows one workgroup fits per CU), and a workgroup that never starts only
+ * makes the others' bounded waits time out.  Returns the launch status. */
 size_t decode_qwen_slot_bytes(int grid);
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
                               unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
-                              int grid, hipStream_t st);
+                              int grid, bool cooperative, hipStream_t st);
 int decode_qwen_max_grid();
 
 }  // namespace tg

@@ -528,10 +528,11 @@ size_t decode_qwen_slot_bytes(int) { return (size_t)NSLOTS * 16; }
 
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
                               unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
-                              int grid, hipStream_t st) {
+                              int grid, bool cooperative, hipStream_t st) {
     void *args[] = {(void *)&layers_dev, (void *)&L, (void *)&h_dev, (void *)&slots_dev, (void *)&abort_dev,
                     (void *)&base, (void *)&eps, (void *)&debug_dev, (void *)&times_dev};
-    return hipLaunchCooperativeKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
+    if (cooperative) return hipLaunchCooperativeKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
+    return hipLaunchKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
 }
 
 }  // namespace tg
