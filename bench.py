@@ -161,13 +161,17 @@ def phase_breakdown(tg, step, layers):
     """Mean microseconds per layer spent between the persistent kernel's
     checkpoints (one extra step with device timestamps)."""
     lib = tg.lib()
-    buf = tg.DeviceArray(2 * layers * 16 * 8)
+    nwg, nts = 256, 24
+    buf = tg.DeviceArray(nwg * layers * nts * 8)
     lib.tg_hip_decode_set_timing(step, buf.ptr)
     lib.tg_hip_decode_run(step, None)
     lib.tg_hip_synchronize()
     lib.tg_hip_decode_set_timing(step, None)
-    t = buf.download(np.uint64, 2 * layers * 16).reshape(2, layers, 16).astype(np.float64) * 0.01  # 100 MHz -> us
+    t = buf.download(np.uint64, nwg * layers * nts).reshape(nwg, layers, nts).astype(np.float64) * 0.01  # -> us
     buf.free()
+    if os.environ.get("TG_TIMES_DUMP"):
+        np.save(os.environ["TG_TIMES_DUMP"], t)
+    t = t[[0, nwg - 1]]
     # checkpoints: 0 layer start, 1 h gathered, 2 q8(x) ready, 3 gate/up done, 4 hidden gathered,
     # 5 q8(hidden), 6 down done, 7 cross-XCD hop done, 8 combined and published
     seq = [(0, 1, "gather_h"), (1, 2, "norm_q8"), (2, 3, "gate_up"), (3, 4, "hidden_xchg"),

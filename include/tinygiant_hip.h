@@ -196,9 +196,9 @@ int tg_hip_decode_status(tg_hip_decode *step);   /* 1 if a persistent step's bar
  * q8(x), hidden, q8(hidden)) into debug_dev[layer]. */
 void tg_hip_decode_set_debug(tg_hip_decode *step, void *debug_dev);
 size_t tg_hip_decode_debug_bytes(void);
-/* Phase timestamps of the persistent step (100 MHz device clock): while set,
- * times_dev [2][L][16] uint64 receives up to 16 checkpoints per layer of the
- * first and the last workgroup. */
+/* Phase timing of the persistent step: while set, times_dev [256][L][24]
+ * uint64 receives up to 24 words per layer of every workgroup (timestamps of
+ * the 100 MHz device clock and exchange poll round counts). */
 void tg_hip_decode_set_timing(tg_hip_decode *step, void *times_dev);
 void tg_hip_decode_run(tg_hip_decode *step, void *stream);
 float tg_hip_decode_time(tg_hip_decode *step, int iters);   /* ms for iters steps, HIP events */

@@ -1058,9 +1058,9 @@ TG_API void tg_hip_decode_set_debug(tg_hip_decode *d, void *debug_dev) {
 
 TG_API size_t tg_hip_decode_debug_bytes(void) { return (size_t)DecodeDebug::BYTES; }
 
-/* Persistent steps record 16 phase timestamps per layer (100 MHz device
- * clock) of the first and the last workgroup into times_dev
- * [2][L][16] (uint64) while it is set; NULL turns it off. */
+/* Persistent steps record up to 24 timing words per layer (timestamps of
+ * the 100 MHz device clock, poll round counts) of every workgroup into
+ * times_dev [256][L][24] (uint64) while it is set; NULL turns it off. */
 TG_API void tg_hip_decode_set_timing(tg_hip_decode *d, void *times_dev) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (d) d->times = (uint64_t *)times_dev;

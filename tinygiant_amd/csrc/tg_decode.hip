@@ -23,8 +23,12 @@
  *      csrc/libtinygiant.c:1428-1434); all 8 XCDs compute the same bits for
  *      the slice and publish it for step 1 of the next layer.
  * Only step 7 crosses XCDs.  Each layer's weights are loaded into registers
- * one layer ahead (gate/up after step 3, down and the RMSNorm weight after
- * step 6), so the weight stream overlaps the exchanges.
+ * one layer ahead: a compute lane holds one Q4_K block (gate or up) and one
+ * Q6_K half-block (down).  The next layer's gate/up blocks are issued during
+ * step 4 and its down half-blocks and RMSNorm weight during step 7, while the
+ * compute waves would otherwise wait; the six compute waves issue one after
+ * another so few weight requests sit in the CU's memory queue ahead of the
+ * exchange polls.
  *
  * Exchanges use epoch-tagged 16-byte slots {tag, v0, v1, v2}, written and
  * polled with device-coherent (sc1) vector accesses so the tag and its values
@@ -62,74 +66,163 @@ constexpr int NX = 8;                 /* XCDs; workgroup g runs on XCD g % NX */
 constexpr int NR = NWG / NX;          /* ranks (workgroups) per XCD */
 constexpr int RA = I / NR;            /* gate/up rows per workgroup: 24 */
 constexpr int RB = D / NR;            /* down rows (and h rows) per workgroup: 64 */
-constexpr int SA = 32;                /* lanes per gate/up row: 8 blocks x 4 items */
-constexpr int SB = 16;                /* lanes per down row: 3 blocks x 4 items = 12 used */
-constexpr int STEPS_A = RA / 2;       /* two-row wave steps: 12 */
-constexpr int STEPS_B = RB / 4;       /* four-row wave steps: 16 */
-constexpr int MAX_A = (STEPS_A + NW - 1) / NW;   /* 2 */
-constexpr int MAX_B = (STEPS_B + NW - 1) / NW;   /* 3 */
+constexpr int HB = 2 * NBI;           /* Q6_K half-blocks per down row: 6 */
+constexpr int XST = 272;              /* LDS stride of a q8(x) 256-block (bank-conflict padding) */
+constexpr int HST = 144;              /* LDS stride of a q8(hidden) 128-value half-block */
 constexpr int VPS = 3;                /* values per slot */
 constexpr int GS = RA / VPS;          /* hidden slots per workgroup: 8 */
 constexpr int PS = (RB + VPS - 1) / VPS;   /* slots per 64-row slice: 22 */
 constexpr unsigned SPIN_LIMIT = 1u << 20;
 constexpr int MAX_LAYERS = 64;        /* layer descriptors staged in LDS */
-constexpr int NTS = 16;               /* timestamps per layer */
+constexpr int NTS = 24;               /* timing words per layer */
 static_assert(NE == NX, "one expert per XCD");
 static_assert(NR * RA == I && NR * RB == D && RA % VPS == 0, "row split");
-static_assert(MAX_A == 2 && MAX_B == 3, "register budget assumes 2 gate/up and 3 down steps");
+static_assert(2 * RA * NBD == NW * 64, "gate/up: one Q4_K block per compute lane");
+static_assert(RB * HB == NW * 64, "down: one Q6_K half-block per compute lane");
 static_assert((NR - 1) * PS <= 6 * CL && (NR - 1) * GS <= 2 * CL && (NX - 1) * PS <= 2 * CL, "poll shares");
 static_assert(NBI <= NA && NBD == NA, "q8 blocks per wave");
 
-/* A slot is 16 bytes {tag, v0, v1, v2} written and read as one vector access
- * with device-scope coherence (sc1). */
-constexpr int CPOL_SC1 = 16;
+/* A slot is 16 bytes {tag, v0, v1, v2} written and read as one vector access,
+ * so its tag and values arrive together.  Cross-XCD slots are stored and
+ * loaded with device-scope coherence (sc1: the store writes through to
+ * memory, the load does not allocate in the reader's L2, so it never sees a
+ * stale line).  Slots read only inside the writer's XCD are stored plainly
+ * (the line stays in that XCD's L2) and loaded with sc1, which bypasses the
+ * CU's L1 and reads the L2 line: measured coherent, and ~0.4 us faster per
+ * exchange than writing through to memory. */
+constexpr int CPOL_PLAIN = 0, CPOL_SC1 = 16;
+constexpr int PREFETCH_STAGGER = 8;   /* s_sleep units (64 cycles) between compute waves' prefetch issue */
 /* slot regions (u32x4 index), each double buffered by layer parity:
  *   h slices  [2][NWG][PS]   rows [64 j, 64 j + 64) of the layer output
  *   hidden    [2][NWG][GS]   the workgroup's 24 hidden values
  *   partials  [2][NWG][PS]   the workgroup's 64 down values (unweighted) */
 constexpr uint32_t HSL = 0, GSL = 2u * NWG * PS, PSL = GSL + 2u * NWG * GS, NSLOTS = PSL + 2u * NWG * PS;
 
-/* ---- LDS images of q8 rows ---- */
-struct __attribute__((aligned(16))) LdsX {   /* q8(RMSNorm(h)) : D values */
-    int8_t qs[D];
+/* ---- LDS images of q8 rows (blocks padded so the lanes of a wave reading
+ * different blocks hit different banks) ---- */
+struct __attribute__((aligned(16))) LdsX {   /* q8(RMSNorm(h)) : D values, block b at b * XST */
+    int8_t qs[NBD * XST];
     float d[NBD];
     int32_t s32[NBD * 8];
 };
-struct __attribute__((aligned(16))) LdsH {   /* q8(hidden) of this XCD's expert : I values */
-    int8_t qs[I];
+struct __attribute__((aligned(16))) LdsH {   /* q8(hidden) of this XCD's expert : I values, */
+    int8_t qs[HB * HST];                     /* half-block hb = 2 b + h at hb * HST */
     float d[NBI];
     int32_t s16[NBI * 16];
 };
 
-__device__ inline FQ4K::X q4k_x_lds(const LdsX &x, int item) {
-    const int b = item >> 2, g = item & 3;
-    const u32x4 *p = reinterpret_cast<const u32x4 *>(x.qs + b * 256 + 64 * g);
-    FQ4K::X r;
-    r.a0 = p[0];
-    r.a1 = p[1];
-    r.b0 = p[2];
-    r.b1 = p[3];
-    r.s_lo = x.s32[b * 8 + 2 * g];
-    r.s_hi = x.s32[b * 8 + 2 * g + 1];
-    r.d = x.d[b];
+/* One lane's Q4_K block (144 bytes: d, dmin, scales[12], qs[128]). */
+struct Q4Blk {
+    u32x4 w[9];
+};
+__device__ inline Q4Blk load_q4blk(Buf b, uint32_t off) {
+    Q4Blk r;
+#pragma unroll
+    for (int i = 0; i < 9; i++) r.w[i] = ld16(b, off + 16u * i);
     return r;
 }
+/* dot_q4k_q8 of one block (csrc/libtinygiant.c:223-272): integer sums per
+ * 32-value sub-block are exact; per group g the float combine is
+ * d*(sc_lo*lo + sc_hi*hi) - dmin*(m_lo*bs_lo + m_hi*bs_hi) (both brackets
+ * below 2^24), scaled by the q8 block scale.  Scales and mins are the
+ * get_scale_min_k4 unpack (:146-155) done four bytes at a time. */
+__device__ inline float dot_q4blk(const Q4Blk &q, const int8_t *xq, const int32_t *s32, float xd) {
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    const float d = ref_f16(q.w[0].x & 0xFFFFu), dmin = ref_f16(q.w[0].x >> 16);
+    const uint32_t s0 = q.w[0].y, s1 = q.w[0].z, s2 = q.w[0].w;
+    const uint32_t scl = s0 & 0x3F3F3F3Fu, mnl = s1 & 0x3F3F3F3Fu;
+    const uint32_t sch = (s2 & m4) | ((s0 >> 2) & 0x30303030u);
+    const uint32_t mnh = ((s2 >> 4) & m4) | ((s1 >> 2) & 0x30303030u);
+    const u32x4 bs0 = *reinterpret_cast<const u32x4 *>(s32), bs1 = *reinterpret_cast<const u32x4 *>(s32 + 4);
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const u32x4 *xp = reinterpret_cast<const u32x4 *>(xq + 64 * g);
+        const u32x4 xa0 = xp[0], xa1 = xp[1], xb0 = xp[2], xb1 = xp[3];
+        const u32x4 qa = q.w[1 + 2 * g], qb = q.w[2 + 2 * g];
+        int lo = 0, hi = 0;
+        lo = dot4(qa.x & m4, xa0.x, lo); lo = dot4(qa.y & m4, xa0.y, lo);
+        lo = dot4(qa.z & m4, xa0.z, lo); lo = dot4(qa.w & m4, xa0.w, lo);
+        lo = dot4(qb.x & m4, xa1.x, lo); lo = dot4(qb.y & m4, xa1.y, lo);
+        lo = dot4(qb.z & m4, xa1.z, lo); lo = dot4(qb.w & m4, xa1.w, lo);
+        hi = dot4((qa.x >> 4) & m4, xb0.x, hi); hi = dot4((qa.y >> 4) & m4, xb0.y, hi);
+        hi = dot4((qa.z >> 4) & m4, xb0.z, hi); hi = dot4((qa.w >> 4) & m4, xb0.w, hi);
+        hi = dot4((qb.x >> 4) & m4, xb1.x, hi); hi = dot4((qb.y >> 4) & m4, xb1.y, hi);
+        hi = dot4((qb.z >> 4) & m4, xb1.z, hi); hi = dot4((qb.w >> 4) & m4, xb1.w, hi);
+        const uint32_t scw = g < 2 ? scl : sch, mnw = g < 2 ? mnl : mnh;
+        const int sh0 = 16 * (g & 1);
+        const int sc_lo = (int)((scw >> sh0) & 0xFFu), sc_hi = (int)((scw >> (sh0 + 8)) & 0xFFu);
+        const int m_lo = (int)((mnw >> sh0) & 0xFFu), m_hi = (int)((mnw >> (sh0 + 8)) & 0xFFu);
+        const int bs_lo = (int)(g < 2 ? (g == 0 ? bs0.x : bs0.z) : (g == 2 ? bs1.x : bs1.z));
+        const int bs_hi = (int)(g < 2 ? (g == 0 ? bs0.y : bs0.w) : (g == 2 ? bs1.y : bs1.w));
+        acc += d * (float)(sc_lo * lo + sc_hi * hi) - dmin * (float)(m_lo * bs_lo + m_hi * bs_hi);
+    }
+    return xd * acc;
+}
 
-__device__ inline FQ6K::X q6k_x_lds(const LdsH &h, int item) {
-    const int b = item >> 2, u = item & 3, hh = u >> 1, l0 = (u & 1) * 16;
-    const int8_t *base = h.qs + b * 256 + 128 * hh + l0;
-    FQ6K::X r;
-    r.x0 = *reinterpret_cast<const u32x4 *>(base);
-    r.x1 = *reinterpret_cast<const u32x4 *>(base + 32);
-    r.x2 = *reinterpret_cast<const u32x4 *>(base + 64);
-    r.x3 = *reinterpret_cast<const u32x4 *>(base + 96);
-    const int sg = b * 16 + 8 * hh + (u & 1);
-    r.s0 = h.s16[sg];
-    r.s1 = h.s16[sg + 2];
-    r.s2 = h.s16[sg + 4];
-    r.s3 = h.s16[sg + 6];
-    r.d = h.d[b];
+/* One lane's half of a Q6_K block: 64 bytes of ql, 32 of qh, 8 int8
+ * sub-scales and the f16 d. */
+struct Q6Half {
+    u32x4 la0, la1, lb0, lb1, h0, h1;
+    u32x2 sc;
+    uint32_t d;   /* d is the high 16 bits */
+};
+__device__ inline Q6Half load_q6half(Buf b, uint32_t blk, int h) {
+    Q6Half r;
+    const uint32_t ql = blk + 64u * h, qh = blk + 128u + 32u * h;
+    r.la0 = ld16(b, ql);
+    r.la1 = ld16(b, ql + 16);
+    r.lb0 = ld16(b, ql + 32);
+    r.lb1 = ld16(b, ql + 48);
+    r.h0 = ld16(b, qh);
+    r.h1 = ld16(b, qh + 16);
+    r.sc = ld8(b, blk + 192u + 8u * h);
+    r.d = ld4(b, blk + 206u);
     return r;
+}
+/* dot_q6k_q8 over one 128-value half (csrc/libtinygiant.c:384-443):
+ * q = (ql nibble | 2 qh bits << 4) - 32; the 16-value integer sums are
+ * exact (the -32 offset is folded in with the 16-value x sums) and weighted
+ * by their int8 sub-scales in integer, then scaled by d and the q8 scale. */
+__device__ inline float dot_q6half(const Q6Half &q, const int8_t *xq, const int32_t *s16, float xd) {
+    const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
+    const u32x4 *xp = reinterpret_cast<const u32x4 *>(xq);
+    int S[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) S[i] = 0;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const u32x4 &A = j < 4 ? q.la0 : q.la1;
+        const u32x4 &B = j < 4 ? q.lb0 : q.lb1;
+        const u32x4 &H = j < 4 ? q.h0 : q.h1;
+        const int c = j & 3;
+        const uint32_t la = c == 0 ? A.x : c == 1 ? A.y : c == 2 ? A.z : A.w;
+        const uint32_t lb = c == 0 ? B.x : c == 1 ? B.y : c == 2 ? B.z : B.w;
+        const uint32_t hh = c == 0 ? H.x : c == 1 ? H.y : c == 2 ? H.z : H.w;
+        const uint32_t q1 = (la & m4) | ((hh << 4) & m2);
+        const uint32_t q2 = (lb & m4) | ((hh << 2) & m2);
+        const uint32_t q3 = ((la >> 4) & m4) | (hh & m2);
+        const uint32_t q4 = ((lb >> 4) & m4) | ((hh >> 2) & m2);
+        const int hf = j >> 2;   /* 16-value group within each 32-value run */
+        const u32x4 x1 = xp[(j >> 2)], x2 = xp[2 + (j >> 2)], x3 = xp[4 + (j >> 2)], x4 = xp[6 + (j >> 2)];
+        const uint32_t a1 = c == 0 ? x1.x : c == 1 ? x1.y : c == 2 ? x1.z : x1.w;
+        const uint32_t a2 = c == 0 ? x2.x : c == 1 ? x2.y : c == 2 ? x2.z : x2.w;
+        const uint32_t a3 = c == 0 ? x3.x : c == 1 ? x3.y : c == 2 ? x3.z : x3.w;
+        const uint32_t a4 = c == 0 ? x4.x : c == 1 ? x4.y : c == 2 ? x4.z : x4.w;
+        S[0 + hf] = dot4(q1, a1, S[0 + hf]);
+        S[2 + hf] = dot4(q2, a2, S[2 + hf]);
+        S[4 + hf] = dot4(q3, a3, S[4 + hf]);
+        S[6 + hf] = dot4(q4, a4, S[6 + hf]);
+    }
+    const u32x4 t0 = *reinterpret_cast<const u32x4 *>(s16), t1 = *reinterpret_cast<const u32x4 *>(s16 + 4);
+    const int xs[8] = {(int)t0.x, (int)t0.y, (int)t0.z, (int)t0.w, (int)t1.x, (int)t1.y, (int)t1.z, (int)t1.w};
+    int A = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int sc = (int)(int8_t)((i < 4 ? q.sc.x : q.sc.y) >> (8 * (i & 3)));
+        A += sc * (S[i] - 32 * xs[i]);
+    }
+    return ref_f16(q.d >> 16) * xd * (float)A;
 }
 
 /* q8 of 4 consecutive values per lane of one wave = one 256-block
@@ -155,13 +248,14 @@ __device__ inline uint32_t q8_block_wave(float v0, float v1, float v2, float v3,
 
 __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 
+template <int POL>
 __device__ inline void put_slot(Buf sl, uint32_t slot, unsigned tag, float a, float b, float c) {
     u32x4 v;
     v.x = tag;
     v.y = __float_as_uint(a);
     v.z = __float_as_uint(b);
     v.w = __float_as_uint(c);
-    __builtin_amdgcn_raw_buffer_store_b128(v, sl.r, (int)(slot * 16u), 0, CPOL_SC1);
+    __builtin_amdgcn_raw_buffer_store_b128(v, sl.r, (int)(slot * 16u), 0, POL);
 }
 
 /* Polls this communication lane's share of `total` slots (flat indices
@@ -170,7 +264,8 @@ __device__ inline void put_slot(Buf sl, uint32_t slot, unsigned tag, float a, fl
  * re-read as one batch per round.  Returns false if the wait timed out or
  * another workgroup aborted. */
 template <int MAXP, class Slot, class Take>
-__device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsigned *abort_flag, Slot slot, Take take) {
+__device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsigned *abort_flag, Slot slot, Take take,
+                                  unsigned *rounds = nullptr) {
     uint32_t pending = 0;
 #pragma unroll
     for (int i = 0; i < MAXP; i++)
@@ -191,6 +286,7 @@ __device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsig
         if (!pending) break;
         if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
             return false;
+        if (rounds) *rounds = spins;
         if (spins > SPIN_LIMIT) {
             __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             return false;
@@ -215,7 +311,8 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     __shared__ LdsX sx;
     __shared__ LdsH sh;
     __shared__ float red[NA];
-    __shared__ float aval[RA];
+    __shared__ float gu[2 * RA];                                  /* gate and up row sums */
+    __shared__ float part6[RB * HB];                              /* down half-block partial dots */
     __shared__ float pp[NE][RB];                                  /* down values of every expert, own rows */
     __shared__ int lds_fail;
     __shared__ DecodeLayer lys[MAX_LAYERS];
@@ -229,36 +326,31 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     const int xe = wg % NX, rk = wg / NX;        /* expert slot (= XCD) and rank */
     Buf sl = make_buf(slots, NSLOTS * 16u);
 
-    typename FQ4K::W wg_[MAX_A], wu_[MAX_A];
-    typename FQ6K::W wd_[MAX_B];
+    Q4Blk wa;                                    /* this lane's gate or up block */
+    Q6Half wb;                                   /* this lane's down half-block */
     u32x4 nw0, nw1;                              /* next layer's RMSNorm weight (compute lanes) */
+    /* gate/up: compute lane t owns block t % 8 of row-task t / 8 (tasks 0-23
+     * gate rows, 24-47 up rows); down: compute lane t owns half-block t % 6
+     * of down row t / 6 */
+    const int ta = ct >> 3, ba = ct & 7;
+    const int tb = ct / HB, hbb = ct % HB;
 
     /* loads are unconditional so the registers' live ranges end at their
      * use; an inactive step reads through an empty descriptor (zeros, no
      * memory access) */
     auto load_a = [&](const DecodeLayer &ly) {
+        /* waves 0-2 hold gate rows, waves 3-5 up rows (uniform per wave) */
         const bool cw = wave < NW;
-        Buf gb = make_buf_uniform(cw ? ly.gate[xe] : nullptr, cw ? (uint32_t)I * GATE_RB : 0u);
-        Buf ub = make_buf_uniform(cw ? ly.up[xe] : nullptr, cw ? (uint32_t)I * GATE_RB : 0u);
-#pragma unroll
-        for (int i = 0; i < MAX_A; i++) {
-            const int s = wave + i * NW;
-            /* an out-of-range step reads past the rows (zeros) */
-            const uint32_t r = s < STEPS_A ? (uint32_t)(RA * rk + 2 * s + (lane >> 5)) : (uint32_t)I;
-            wg_[i] = FQ4K::load_w(gb, r * GATE_RB, lane & 31);
-            wu_[i] = FQ4K::load_w(ub, r * GATE_RB, lane & 31);
-        }
+        const uint8_t *m = wave < NW / 2 ? ly.gate[xe] : ly.up[xe];
+        Buf gb = make_buf_uniform(cw ? m : nullptr, cw ? (uint32_t)I * GATE_RB : 0u);
+        const uint32_t r = (uint32_t)(RA * rk + (ta % RA));
+        wa = load_q4blk(gb, r * GATE_RB + (uint32_t)ba * 144u);
     };
     auto load_b = [&](const DecodeLayer &ly) {
         const bool cw = wave < NW;
         Buf db = make_buf_uniform(cw ? ly.down[xe] : nullptr, cw ? (uint32_t)D * DOWN_RB : 0u);
-        const int item = (lane & 15) < NBI * 4 ? (lane & 15) : 0;
-#pragma unroll
-        for (int t = 0; t < MAX_B; t++) {
-            const int q = wave + t * NW;
-            const uint32_t r = q < STEPS_B ? (uint32_t)(RB * rk + 4 * q + (lane >> 4)) : (uint32_t)D;
-            wd_[t] = FQ6K::load_w(db, r * DOWN_RB, item);
-        }
+        const uint32_t r = (uint32_t)(RB * rk + tb);
+        wb = load_q6half(db, r * DOWN_RB + (uint32_t)(hbb >> 1) * 210u, hbb & 1);
     };
     /* RMSNorm weight: compute lane t holds float4 t and (t < 128) float4 384 + t */
     auto load_nw = [&](const DecodeLayer &ly) {
@@ -299,13 +391,17 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         int clv = cl;
         asm volatile("" : "+v"(clv));
         asm volatile("" : "+v"(lane));
-        /* optional phase timestamps (100 MHz clock) of the first and last workgroup */
-        const bool tw = times && threadIdx.x == 0 && (wg == 0 || wg == NWG - 1);
-        uint64_t *tr = tw ? times + ((size_t)(wg == 0 ? 0 : 1) * L + l) * NTS : nullptr;
+        /* optional phase timestamps (100 MHz clock): thread 0 after each phase,
+         * communication lane 0 when it publishes (checkpoints 9-11) */
+        const bool tw = times && threadIdx.x == 0;
+        const bool tc = times && clv == 0;
+        uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
         if (tw) tr[0] = wall_clock64();
         /* ---- 1: gather h from the other ranks of this XCD ---- */
         if (l > 0) {
             if (cl >= 0) {
+                unsigned rounds = 0;
+                if (tc) tr[15] = wall_clock64();
                 const bool ok = poll_slots<6>(
                     sl, clv, (NR - 1) * PS, base + (unsigned)l, abort_flag,
                     [&](int f) {
@@ -320,7 +416,12 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                         o[0] = __uint_as_float(v.y);
                         if (VPS * t + 1 < RB) o[1] = __uint_as_float(v.z);
                         if (VPS * t + 2 < RB) o[2] = __uint_as_float(v.w);
-                    });
+                    },
+                    tc ? &rounds : nullptr);
+                if (tc) {
+                    tr[16] = wall_clock64();
+                    tr[17] = rounds;
+                }
                 if (!ok) lds_fail = 1;
             } else {
                 store_nw();
@@ -355,7 +456,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             const float v2 = (__uint_as_float(hv.z) * scale) * __uint_as_float(wv.z);
             const float v3 = (__uint_as_float(hv.w) * scale) * __uint_as_float(wv.w);
             const uint32_t q = q8_block_wave(v0, v1, v2, v3, lane, &sx.d[wave], &sx.s32[wave * 8], nullptr);
-            reinterpret_cast<uint32_t *>(sx.qs)[threadIdx.x] = q;
+            reinterpret_cast<uint32_t *>(sx.qs + wave * XST)[lane] = q;
             if (dbg && wg == 0) {
                 uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
                 reinterpret_cast<u32x4 *>(rec + DecodeDebug::HIN)[threadIdx.x] = hv;
@@ -376,30 +477,32 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (threadIdx.x < NBD * 8)
                 reinterpret_cast<int32_t *>(rec + DecodeDebug::XS32)[threadIdx.x] = sx.s32[threadIdx.x];
         }
-        /* ---- 3: gate/up rows [24 rk, 24 rk + 24) of expert xe -> SwiGLU ---- */
+        /* ---- 3: gate/up rows [24 rk, 24 rk + 24) of expert xe, one block per lane ---- */
         if (wave < NW) {
-#pragma unroll
-            for (int i = 0; i < MAX_A; i++) {
-                const int s = wave + i * NW;
-                const int item = lane & 31;
-                FQ4K::X xs = q4k_x_lds(sx, item);
-                float vg = FQ4K::value(wg_[i], xs, item);
-                float vu = FQ4K::value(wu_[i], xs, item);
-                vg = seg_sum_last<SA>(vg);
-                vu = seg_sum_last<SA>(vu);
-                if (s < STEPS_A && (lane & 31) == 31) aval[2 * s + (lane >> 5)] = silu_mul(vg, vu);
-            }
-            /* the next layer's gate/up rows load while this layer finishes */
-            if (l + 1 < L) load_a(lys[l + 1]);
+            float v = dot_q4blk(wa, sx.qs + ba * XST, sx.s32 + ba * 8, sx.d[ba]);
+            v = seg_sum_last<NBD>(v);
+            if (ba == NBD - 1) gu[ta] = v;
         }
         __syncthreads();
         if (tw) tr[3] = wall_clock64();
         /* ---- 4: all-gather the expert's hidden vector within the XCD ---- */
+        /* meanwhile the compute waves issue the next layer's gate/up blocks,
+         * one wave after another, so the weight requests queued ahead of the
+         * polls stay short */
+        if (cl < 0 && l + 1 < L) {
+            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
+            load_a(lys[l + 1]);
+        }
         if (cl >= 0) {
-            if (clv < GS)
-                put_slot(sl, GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, aval[VPS * clv],
-                         aval[VPS * clv + 1], aval[VPS * clv + 2]);
-            if (clv < RA) hid[RA * rk + clv] = aval[clv];
+            if (clv < GS) {
+                const int i = VPS * clv;
+                put_slot<CPOL_PLAIN>(sl, GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, silu_mul(gu[i], gu[RA + i]),
+                         silu_mul(gu[i + 1], gu[RA + i + 1]), silu_mul(gu[i + 2], gu[RA + i + 2]));
+            }
+            if (tc) tr[9] = wall_clock64();
+            if (clv < RA) hid[RA * rk + clv] = silu_mul(gu[clv], gu[RA + clv]);
+            unsigned rounds = 0;
+            if (tc) tr[12] = wall_clock64();
             const bool ok = poll_slots<2>(
                 sl, clv, (NR - 1) * GS, tag, abort_flag,
                 [&](int f) {
@@ -414,7 +517,12 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                     o[0] = __uint_as_float(v.y);
                     o[1] = __uint_as_float(v.z);
                     o[2] = __uint_as_float(v.w);
-                });
+                },
+                tc ? &rounds : nullptr);
+            if (tc) {
+                tr[13] = wall_clock64();
+                tr[14] = rounds;
+            }
             if (!ok) lds_fail = 1;
         }
         __syncthreads();
@@ -426,7 +534,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             const u32x4 hv = reinterpret_cast<const u32x4 *>(hid + b * 256)[lane];
             const uint32_t q = q8_block_wave(__uint_as_float(hv.x), __uint_as_float(hv.y), __uint_as_float(hv.z),
                                              __uint_as_float(hv.w), lane, &sh.d[b], nullptr, &sh.s16[b * 16]);
-            reinterpret_cast<uint32_t *>(sh.qs + b * 256)[lane] = q;
+            reinterpret_cast<uint32_t *>(sh.qs + (2 * b + (lane >> 5)) * HST)[lane & 31] = q;
             if (dbg && rk == 0) {   /* workgroups 0..7: expert slot xe's record */
                 uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
                 reinterpret_cast<u32x4 *>(rec + DecodeDebug::HID + (xe * I + b * 256) * 4)[lane] = hv;
@@ -441,35 +549,39 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (threadIdx.x < NBI * 16)
                 reinterpret_cast<int32_t *>(rec + DecodeDebug::HS16)[xe * NBI * 16 + threadIdx.x] = sh.s16[threadIdx.x];
         }
-        /* ---- 6: down rows [64 rk, 64 rk + 64) of expert xe ---- */
+        /* ---- 6: down rows [64 rk, 64 rk + 64) of expert xe, one half-block per lane ---- */
         if (wave < NW) {
-#pragma unroll
-            for (int t = 0; t < MAX_B; t++) {
-                const int q = wave + t * NW;
-                const int item = lane & 15;
-                float v = 0.f;
-                if (item < NBI * 4) {
-                    FQ6K::X xs = q6k_x_lds(sh, item);
-                    v = FQ6K::value(wd_[t], xs, item);
-                }
-                v = seg_sum_last<SB>(v);
-                if (q < STEPS_B && (lane & 15) == 15) pp[xe][4 * q + (lane >> 4)] = v;
-            }
-            /* the next layer's RMSNorm weight and down rows load while h travels */
-            if (l + 1 < L) {
-                load_nw(lys[l + 1]);
-                load_b(lys[l + 1]);
-            }
+            const int b = hbb >> 1;
+            part6[ct] = dot_q6half(wb, sh.qs + hbb * HST, sh.s16 + b * 16 + 8 * (hbb & 1), sh.d[b]);
         }
         __syncthreads();
         if (tw) tr[6] = wall_clock64();
         /* ---- 7: cross-XCD hop: rank rk of every XCD trades its 64 down values ---- */
+        /* meanwhile the next layer's RMSNorm weight and down rows are issued */
+        if (cl < 0 && l + 1 < L) {
+            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
+            load_nw(lys[l + 1]);
+            load_b(lys[l + 1]);
+        }
         if (cl >= 0) {
             if (clv < PS) {
-                const int r0 = VPS * clv;
-                put_slot(sl, PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, pp[xe][r0],
-                         r0 + 1 < RB ? pp[xe][r0 + 1] : 0.f, r0 + 2 < RB ? pp[xe][r0 + 2] : 0.f);
+                /* row sums of the six half-block dots, in half-block order */
+                float o[VPS];
+#pragma unroll
+                for (int k = 0; k < VPS; k++) {
+                    const int rl = VPS * clv + k;
+                    float a = 0.f;
+                    if (rl < RB) {
+#pragma unroll
+                        for (int i = 0; i < HB; i++) a += part6[HB * rl + i];
+                        pp[xe][rl] = a;
+                    }
+                    o[k] = a;
+                }
+                put_slot<CPOL_SC1>(sl, PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], o[1], o[2]);
             }
+            if (tc) tr[10] = wall_clock64();
+            unsigned rounds = 0;
             const bool ok = poll_slots<2>(
                 sl, clv, (NX - 1) * PS, tag, abort_flag,
                 [&](int f) {
@@ -484,7 +596,12 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                     o[0] = __uint_as_float(v.y);
                     if (VPS * t + 1 < RB) o[1] = __uint_as_float(v.z);
                     if (VPS * t + 2 < RB) o[2] = __uint_as_float(v.w);
-                });
+                },
+                tc ? &rounds : nullptr);
+            if (tc) {
+                tr[18] = wall_clock64();
+                tr[19] = rounds;
+            }
             if (!ok) lds_fail = 1;
         }
         __syncthreads();
@@ -507,7 +624,8 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                     o[k] = 0.f;
                 }
             }
-            if (l + 1 < L) put_slot(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], o[1], o[2]);
+            if (l + 1 < L) put_slot<CPOL_PLAIN>(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], o[1], o[2]);
+            if (tc) tr[11] = wall_clock64();
         }
         if (tw) tr[8] = wall_clock64();
     }
