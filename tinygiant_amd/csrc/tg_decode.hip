@@ -91,7 +91,7 @@ static_assert(NBI <= NA && NBD == NA, "q8 blocks per wave");
  * CU's L1 and reads the L2 line: measured coherent, and ~0.4 us faster per
  * exchange than writing through to memory. */
 constexpr int CPOL_PLAIN = 0, CPOL_SC1 = 16;
-constexpr int PREFETCH_STAGGER = 8;   /* s_sleep units (64 cycles) between compute waves' prefetch issue */
+constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units (64 cycles) between compute waves' prefetch issue */
 /* slot regions (u32x4 index), each double buffered by layer parity:
  *   h slices  [2][NWG][PS]   rows [64 j, 64 j + 64) of the layer output
  *   hidden    [2][NWG][GS]   the workgroup's 24 hidden values
@@ -494,13 +494,15 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             load_a(lys[l + 1]);
         }
         if (cl >= 0) {
+            /* SwiGLU, one value per lane of the first communication wave; the
+             * same wave then publishes them (its LDS accesses run in order) */
+            if (clv < RA) hid[RA * rk + clv] = silu_mul(gu[clv], gu[RA + clv]);
+            __builtin_amdgcn_wave_barrier();
             if (clv < GS) {
-                const int i = VPS * clv;
-                put_slot<CPOL_PLAIN>(sl, GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, silu_mul(gu[i], gu[RA + i]),
-                         silu_mul(gu[i + 1], gu[RA + i + 1]), silu_mul(gu[i + 2], gu[RA + i + 2]));
+                const float *a = hid + RA * rk + VPS * clv;
+                put_slot<CPOL_PLAIN>(sl, GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, a[0], a[1], a[2]);
             }
             if (tc) tr[9] = wall_clock64();
-            if (clv < RA) hid[RA * rk + clv] = silu_mul(gu[clv], gu[RA + clv]);
             unsigned rounds = 0;
             if (tc) tr[12] = wall_clock64();
             const bool ok = poll_slots<2>(
@@ -564,21 +566,19 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             load_b(lys[l + 1]);
         }
         if (cl >= 0) {
+            /* row sums of the six half-block dots, in half-block order, one row
+             * per lane of the first communication wave, which then publishes */
+            if (clv < RB) {
+                float a = 0.f;
+#pragma unroll
+                for (int i = 0; i < HB; i++) a += part6[HB * clv + i];
+                pp[xe][clv] = a;
+            }
+            __builtin_amdgcn_wave_barrier();
             if (clv < PS) {
-                /* row sums of the six half-block dots, in half-block order */
-                float o[VPS];
-#pragma unroll
-                for (int k = 0; k < VPS; k++) {
-                    const int rl = VPS * clv + k;
-                    float a = 0.f;
-                    if (rl < RB) {
-#pragma unroll
-                        for (int i = 0; i < HB; i++) a += part6[HB * rl + i];
-                        pp[xe][rl] = a;
-                    }
-                    o[k] = a;
-                }
-                put_slot<CPOL_SC1>(sl, PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], o[1], o[2]);
+                const int r0 = VPS * clv;
+                put_slot<CPOL_SC1>(sl, PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, pp[xe][r0],
+                                   r0 + 1 < RB ? pp[xe][r0 + 1] : 0.f, r0 + 2 < RB ? pp[xe][r0 + 2] : 0.f);
             }
             if (tc) tr[10] = wall_clock64();
             unsigned rounds = 0;
@@ -608,23 +608,22 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         if (lds_fail) return;
         if (tw) tr[7] = wall_clock64();
         /* ---- 8: combine rows [64 rk, 64 rk + 64) in expert order, publish ---- */
-        if (cl >= 0 && clv < PS) {
-            float o[VPS];
+        /* one row per lane of the first communication wave, which then
+         * publishes the slice */
+        if (cl >= 0 && clv < RB) {
+            const int r = RB * rk + clv;
+            float a = hx[r];
 #pragma unroll
-            for (int k = 0; k < VPS; k++) {
-                const int rl = VPS * clv + k;
-                if (rl < RB) {
-                    float a = hx[RB * rk + rl];
-#pragma unroll
-                    for (int e = 0; e < NE; e++) a += ly.w[e] * pp[e][rl];
-                    o[k] = a;
-                    hx[RB * rk + rl] = a;
-                    if (l == L - 1 && xe == 0) h[RB * rk + rl] = a;
-                } else {
-                    o[k] = 0.f;
-                }
+            for (int e = 0; e < NE; e++) a += ly.w[e] * pp[e][clv];
+            hx[r] = a;
+            if (l == L - 1 && xe == 0) h[r] = a;
+            __builtin_amdgcn_wave_barrier();
+            if (l + 1 < L && clv < PS) {
+                const float *o = hx + RB * rk + VPS * clv;
+                const int r0 = VPS * clv;
+                put_slot<CPOL_PLAIN>(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0],
+                                     r0 + 1 < RB ? o[1] : 0.f, r0 + 2 < RB ? o[2] : 0.f);
             }
-            if (l + 1 < L) put_slot<CPOL_PLAIN>(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], o[1], o[2]);
             if (tc) tr[11] = wall_clock64();
         }
         if (tw) tr[8] = wall_clock64();
