@@ -81,6 +81,8 @@ static_assert(2 * RA * NBD == NW * 64, "gate/up: one Q4_K block per compute lane
 static_assert(RB * HB == NW * 64, "down: one Q6_K half-block per compute lane");
 static_assert((NR - 1) * PS <= 6 * CL && (NR - 1) * GS <= 2 * CL && (NX - 1) * PS <= 2 * CL, "poll shares");
 static_assert(NBI <= NA && NBD == NA, "q8 blocks per wave");
+static_assert(RB == VPS * (PS - 1) + 1, "the last slice slot holds one row and the slice's sum of h^2");
+static_assert(NR % NA == 0, "layer-0 slice sums: whole slices per wave");
 
 /* A slot is 16 bytes {tag, v0, v1, v2} written and read as one vector access,
  * so its tag and values arrive together.  Cross-XCD slots are stored and
@@ -155,7 +157,9 @@ __device__ inline float dot_q4blk(const Q4Blk &q, const int8_t *xq, const int32_
         const int m_lo = (int)((mnw >> sh0) & 0xFFu), m_hi = (int)((mnw >> (sh0 + 8)) & 0xFFu);
         const int bs_lo = (int)(g < 2 ? (g == 0 ? bs0.x : bs0.z) : (g == 2 ? bs1.x : bs1.z));
         const int bs_hi = (int)(g < 2 ? (g == 0 ? bs0.y : bs0.w) : (g == 2 ? bs1.y : bs1.w));
-        acc += d * (float)(sc_lo * lo + sc_hi * hi) - dmin * (float)(m_lo * bs_lo + m_hi * bs_hi);
+        /* |sums| < 2^23 and scales < 2^6: 24-bit multiplies are exact */
+        acc += d * (float)(__mul24(sc_lo, lo) + __mul24(sc_hi, hi)) -
+               dmin * (float)(__mul24(m_lo, bs_lo) + __mul24(m_hi, bs_hi));
     }
     return xd * acc;
 }
@@ -220,7 +224,7 @@ __device__ inline float dot_q6half(const Q6Half &q, const int8_t *xq, const int3
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int sc = (int)(int8_t)((i < 4 ? q.sc.x : q.sc.y) >> (8 * (i & 3)));
-        A += sc * (S[i] - 32 * xs[i]);
+        A += __mul24(sc, S[i] - 32 * xs[i]);   /* |S - 32 xs| < 2^18: exact */
     }
     return ref_f16(q.d >> 16) * xd * (float)A;
 }
@@ -310,7 +314,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     __shared__ __attribute__((aligned(16))) float hid[I];         /* this XCD's expert hidden vector */
     __shared__ LdsX sx;
     __shared__ LdsH sh;
-    __shared__ float red[NA];
+    __shared__ float ssq[NR];                                     /* sum of h^2 of each 64-row slice */
     __shared__ float gu[2 * RA];                                  /* gate and up row sums */
     __shared__ float part6[RB * HB];                              /* down half-block partial dots */
     __shared__ float pp[NE][RB];                                  /* down values of every expert, own rows */
@@ -376,6 +380,14 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     }
     for (int t = threadIdx.x; t < D / 4; t += NT) reinterpret_cast<u32x4 *>(hx)[t] = reinterpret_cast<const u32x4 *>(h)[t];
     __syncthreads();
+    /* slice sums of h^2 for layer 0 (later layers receive them with h) */
+#pragma unroll
+    for (int i = 0; i < NR / NA; i++) {
+        const int sl = wave * (NR / NA) + i;
+        const float v = hx[RB * sl + lane];
+        const float ss = wave_sum(v * v);
+        if (lane == 0) ssq[sl] = ss;
+    }
     load_nw(lys[0]);
     load_a(lys[0]);
     load_b(lys[0]);
@@ -414,8 +426,12 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                         const int j = jj + (jj >= rk);
                         float *o = hx + RB * j + VPS * t;
                         o[0] = __uint_as_float(v.y);
-                        if (VPS * t + 1 < RB) o[1] = __uint_as_float(v.z);
-                        if (VPS * t + 2 < RB) o[2] = __uint_as_float(v.w);
+                        if (t == PS - 1) {
+                            ssq[j] = __uint_as_float(v.z);   /* the last slot carries the slice's sum of h^2 */
+                        } else {
+                            o[1] = __uint_as_float(v.z);
+                            o[2] = __uint_as_float(v.w);
+                        }
                     },
                     tc ? &rounds : nullptr);
                 if (tc) {
@@ -430,19 +446,13 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (lds_fail) return;
         }
         if (tw) tr[1] = wall_clock64();
-        /* ---- 2: RMSNorm (weight norm_w or 1) then q8, in LDS; wave w owns block w ---- */
-        {
-            const u32x4 hv = reinterpret_cast<const u32x4 *>(hx)[threadIdx.x];
-            float v0 = __uint_as_float(hv.x), v1 = __uint_as_float(hv.y);
-            float v2 = __uint_as_float(hv.z), v3 = __uint_as_float(hv.w);
-            const float ss = wave_sum(v0 * v0 + v1 * v1 + v2 * v2 + v3 * v3);
-            if (lane == 0) red[wave] = ss;
-        }
-        __syncthreads();
+        /* ---- 2: RMSNorm (weight norm_w or 1) then q8, in LDS; wave w owns block w.
+         * sum h^2 = the 32 slice sums in rank order (each a fixed DPP tree) ---- */
+        if (l == 0) __syncthreads();
         {
             float tot = 0.f;
 #pragma unroll
-            for (int i = 0; i < NA; i++) tot += red[i];
+            for (int i = 0; i < NR; i++) tot += ssq[i];
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
             const u32x4 hv = reinterpret_cast<const u32x4 *>(hx)[threadIdx.x];
             u32x4 wv;
@@ -617,12 +627,14 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             for (int e = 0; e < NE; e++) a += ly.w[e] * pp[e][clv];
             hx[r] = a;
             if (l == L - 1 && xe == 0) h[r] = a;
+            const float ss = wave_sum(a * a);   /* this slice's sum of h^2, for the next RMSNorm */
+            if (clv == 0) ssq[rk] = ss;
             __builtin_amdgcn_wave_barrier();
             if (l + 1 < L && clv < PS) {
                 const float *o = hx + RB * rk + VPS * clv;
-                const int r0 = VPS * clv;
+                const bool last = clv == PS - 1;   /* row 63 alone, plus the slice sum */
                 put_slot<CPOL_PLAIN>(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0],
-                                     r0 + 1 < RB ? o[1] : 0.f, r0 + 2 < RB ? o[2] : 0.f);
+                                     last ? ss : o[1], last ? 0.f : o[2]);
             }
             if (tc) tr[11] = wall_clock64();
         }
