@@ -218,6 +218,41 @@ def boundary_probe(tg, routes, calls=50):
             "tok_s_if_48_calls": round(1.0 / (dt * L), 1)}
 
 
+def head_probe(tg, ks=(1, 5, 9), iters=20):
+    """The q6_K output head of Qwen3-30B-A3B (151936 x 2048, 255,252,480 B) over
+    k verify rows with the argmax fused in (tg_hip_head_argmax_dev, RMSNorm
+    weight applied): time per call from HIP events, weight bytes read once."""
+    lib = tg.lib()
+    nrows, ncols = 151936, 2048
+    nbytes = nrows * (ncols // 256) * 210
+    head = tg.DeviceArray(nbytes)
+    lib.tg_hip_synth_fill(2, SEED + 17, head.ptr, nbytes, None)
+    rng = np.random.default_rng(SEED + 18)
+    norm = tg.DeviceArray(ncols * 4)
+    norm.upload(rng.uniform(0.5, 1.5, ncols).astype(np.float32))
+    out = {"rows": nrows, "cols": ncols, "fmt": "q6_K", "weight_bytes": nbytes, "k": {}}
+    for k in ks:
+        x = tg.DeviceArray(k * ncols * 4)
+        x.upload(rng.standard_normal((k, ncols)).astype(np.float32))
+        am = tg.DeviceArray(k * 4)
+        sc = tg.DeviceArray(lib.tg_hip_head_scratch_bytes(k, nrows, ncols))
+        args = (2, head.ptr, x.ptr, norm.ptr, ctypes.c_float(1e-6), k, nrows, ncols, None, am.ptr, None, sc.ptr, None)
+        for _ in range(3):
+            lib.tg_hip_head_argmax_dev(*args)
+        lib.tg_hip_mark(0)
+        for _ in range(iters):
+            lib.tg_hip_head_argmax_dev(*args)
+        lib.tg_hip_mark(1)
+        us = lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
+        out["k"][k] = {"us": round(us, 2), "weight_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                       "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        for a in (x, am, sc):
+            a.free()
+    head.free()
+    norm.free()
+    return out
+
+
 def read_traffic(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
@@ -239,6 +274,7 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-boundary", action="store_true", help="skip the ctypes-entry latency probe")
+    ap.add_argument("--no-head", action="store_true", help="skip the q6_K output head + argmax probe")
     ap.add_argument("--mode", choices=["persistent", "persistent-plain", "graph", "eager"], default="persistent",
                     help="persistent: one cooperative kernel per step (persistent-plain: the same kernel through "
                          "a plain launch, for profilers); graph: per-layer kernels in a HIP graph")
@@ -359,6 +395,9 @@ def main():
     if not args.no_boundary:
         log("boundary probe ...")
         result["boundary"] = boundary_probe(tg, routes)
+    if not args.no_head:
+        log("output head probe ...")
+        result["head_argmax"] = head_probe(tg)
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(routes, min(args.cpu_layers, layers))

@@ -176,6 +176,21 @@ size_t tg_hip_matmul_scratch_bytes(int k, int ncols);
 void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n,
                          float eps, void *stream);
 
+/* Output head over k (1..16) device-resident rows with the argmax fused in:
+ * x_j = RMSNorm(inputs_j) * norm_w (skipped when norm_w_dev is NULL),
+ * logits[j][r] = dot(mat row r, q8(x_j)) and argmax_dev[j] = the first r
+ * with the largest logit, maxval_dev[j] its logit (may be NULL).  Replaces
+ * the reference's per-row tg_rms_norm + tg_matmul over the head
+ * (tinygiant/engine.py:347-354) and numpy.argmax over each row
+ * (tinygiant/specdec.py:77,90); Q6_K heads of 2048 columns read the head
+ * once for all rows.  logits_dev (k x nrows) may be NULL; scratch_dev holds
+ * tg_hip_head_scratch_bytes(k, nrows, ncols) bytes. */
+void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *inputs_dev,
+                            const float *norm_w_dev, float eps, int k, int nrows, int ncols,
+                            float *logits_dev, int32_t *argmax_dev, float *maxval_dev,
+                            void *scratch_dev, void *stream);
+size_t tg_hip_head_scratch_bytes(int k, int nrows, int ncols);
+
 /* Device-resident decode step over L planned layers sharing one hidden
  * state h_dev [k][embed_dim]: h <- h + MoE_l(RMSNorm_l(h)) for each layer
  * (tinygiant/engine.py:281-282,335-341).  norm_w_dev may be NULL (weight 1).
@@ -205,6 +220,10 @@ float tg_hip_decode_time(tg_hip_decode *step, int iters);   /* ms for iters step
 void tg_hip_decode_kernel_times(tg_hip_decode *step, float *ms_out /*[6]*/, int *n_out /*[6]*/);
 void tg_hip_decode_destroy(tg_hip_decode *step);
 void tg_hip_device_name(char *buf, int n);
+/* Event marks (slots 0..7) on the library stream; tg_hip_marks_ms waits for
+ * mark b and returns the milliseconds between marks a and b. */
+void tg_hip_mark(int slot);
+float tg_hip_marks_ms(int a, int b);
 /* nbytes (multiple of 16) device-to-device `iters` times with a plain copy
  * kernel; returns milliseconds (HIP events): measured HBM reference point. */
 float tg_hip_copy_time(const void *src_dev, void *dst_dev, uint64_t nbytes, int iters);

@@ -30,6 +30,7 @@
 #include <vector>
 
 #include "tg_decode.h"
+#include "tg_head.h"
 #include "tg_kernels.h"
 #include "tg_synth.h"
 
@@ -875,6 +876,50 @@ TG_API void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_de
 
 TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k, ncols); }
 
+/* ---- output head with fused argmax ----
+ * Scratch: q8 rows | 16 argmax keys | RMSNorm'd rows | logits (only when the
+ * format has no fused kernel and the caller passes no logits buffer). */
+static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+TG_API size_t tg_hip_head_scratch_bytes(int k, int nrows, int ncols) {
+    if (k <= 0 || nrows <= 0 || ncols <= 0) return 0;
+    return align256(q8_bytes(k, ncols)) + align256(16 * 8) + align256((size_t)k * ncols * 4) +
+           align256((size_t)k * nrows * 4);
+}
+
+TG_API void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *inputs_dev, const float *norm_w_dev,
+                                   float eps, int k, int nrows, int ncols, float *logits_dev, int32_t *argmax_dev,
+                                   float *maxval_dev, void *scratch_dev, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!fmt_ok(fmt) || ncols <= 0 || ncols % 32 || nrows <= 0 || k <= 0 || k > 16 || !argmax_dev || !scratch_dev) {
+        set_err("tg_hip_head_argmax_dev: bad format, shape or arguments (1 <= k <= 16)");
+        return;
+    }
+    ensure_init();
+    hipStream_t st = stream ? (hipStream_t)stream : g.st;
+    uint8_t *sp = (uint8_t *)scratch_dev;
+    uint8_t *q8p = sp;
+    unsigned long long *keys = (unsigned long long *)(sp + align256(q8_bytes(k, ncols)));
+    float *normed = (float *)((uint8_t *)keys + align256(16 * 8));
+    float *lg_scratch = (float *)((uint8_t *)normed + align256((size_t)k * ncols * 4));
+    const float *xin = inputs_dev;
+    if (norm_w_dev) {
+        launch_rms_norm(inputs_dev, norm_w_dev, normed, k, ncols, eps, st);
+        xin = normed;
+    }
+    Q8Rows q = q8_view(q8p, k, ncols, xin);
+    if (fmt != TG_FMT_F16) launch_quantize(xin, ncols, k, ncols, q, st);
+    if (head_fast_ok(fmt, ncols, k)) {
+        launch_head_q6k((const uint8_t *)mat_dev, nrows, q, k, logits_dev, keys, st);
+    } else {
+        float *lg = logits_dev ? logits_dev : lg_scratch;
+        launch_gemv(fmt, (const uint8_t *)mat_dev, nrows, ncols, nullptr, q, k, lg, nrows, st);
+        launch_argmax_rows(lg, nrows, k, keys, st);
+    }
+    launch_argmax_finish(keys, k, argmax_dev, maxval_dev, st);
+    HIPCHECK(hipGetLastError());
+}
+
 TG_API void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n, float eps,
                                 void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
@@ -1165,6 +1210,36 @@ TG_API void tg_hip_device_name(char *buf, int n) {
 /* Copies nbytes (multiple of 16) device-to-device with a plain vector-load
  * kernel `iters` times on the library stream; returns ms (HIP events).  The
  * reference point for measured HBM bandwidth and for counter calibration. */
+/* Event marks on the library stream, for timing queued device work. */
+static hipEvent_t g_marks[8];
+static bool g_marks_ready = false;
+
+TG_API void tg_hip_mark(int slot) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+    if (slot < 0 || slot >= 8) {
+        set_err("tg_hip_mark: slot must be 0..7");
+        return;
+    }
+    if (!g_marks_ready) {
+        for (auto &e : g_marks) HIPCHECK(hipEventCreate(&e));
+        g_marks_ready = true;
+    }
+    HIPCHECK(hipEventRecord(g_marks[slot], g.st));
+}
+
+TG_API float tg_hip_marks_ms(int a, int b) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g_marks_ready || a < 0 || a >= 8 || b < 0 || b >= 8) {
+        set_err("tg_hip_marks_ms: record both marks first");
+        return 0.f;
+    }
+    HIPCHECK(hipEventSynchronize(g_marks[b]));
+    float ms = 0.f;
+    HIPCHECK(hipEventElapsedTime(&ms, g_marks[a], g_marks[b]));
+    return ms;
+}
+
 TG_API float tg_hip_copy_time(const void *src_dev, void *dst_dev, uint64_t nbytes, int iters) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     ensure_init();
