@@ -221,6 +221,50 @@ def boundary_probe(tg, routes, calls=50):
             "tok_s_if_48_calls": round(1.0 / (dt * L), 1)}
 
 
+def verify_probe(tg, base, ks=(5, 9), iters=20):
+    """One layer of a self-speculative verify batch: k rows (the draft tokens
+    plus t0), each picking its own top-8 of the 128 resident experts of layer 0
+    (Zipf), through the planned multi-row MoE path (tg_hip_moe_plan_run: q8,
+    gate/up + SwiGLU, q8 of hidden, down, expert-order combine).  Weight
+    bytes = every expert of the union, read once."""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    rng = np.random.default_rng(SEED + 19)
+    perm = rng.permutation(E)
+    out = {}
+    for k in ks:
+        experts, rw = S.routing_rows(rng, k, E, TOPK, 1.1, perm)
+        n = len(experts)
+        gp = (ctypes.c_void_p * n)(*[base + int(e) * GATE_B for e in experts])
+        up = (ctypes.c_void_p * n)(*[base + E * GATE_B + int(e) * GATE_B for e in experts])
+        dp = (ctypes.c_void_p * n)(*[base + 2 * E * GATE_B + int(e) * DOWN_B for e in experts])
+        fm = np.full(n, tg.FMT_Q6K, np.int32)
+        rwc = np.ascontiguousarray(rw, np.float32)
+        plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
+                                          tg.FMT_Q4K, fm.ctypes.data, None, None, None, tg.ACT_SILU, n,
+                                          rwc.ctypes.data, k, D, I)
+        if not plan:
+            raise RuntimeError(tg.last_error())
+        x = tg.DeviceArray(k * D * 4)
+        x.upload(rng.standard_normal((k, D)).astype(np.float32))
+        y = tg.DeviceArray(k * D * 4)
+        for _ in range(3):
+            lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None)
+        lib.tg_hip_mark(0)
+        for _ in range(iters):
+            lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None)
+        lib.tg_hip_mark(1)
+        us = lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
+        nbytes = n * EXPERT_B
+        out[k] = {"experts": n, "rows_per_expert_max": int((rw != 0).sum(axis=1).max()), "us": round(us, 2),
+                  "weight_bytes": nbytes, "weight_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                  "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        lib.tg_hip_moe_plan_destroy(plan)
+        x.free()
+        y.free()
+    return out
+
+
 def head_probe(tg, ks=(1, 5, 9), iters=20):
     """The q6_K output head of Qwen3-30B-A3B (151936 x 2048, 255,252,480 B) over
     k verify rows with the argmax fused in (tg_hip_head_argmax_dev, RMSNorm
@@ -278,6 +322,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-boundary", action="store_true", help="skip the ctypes-entry latency probe")
     ap.add_argument("--no-head", action="store_true", help="skip the q6_K output head + argmax probe")
+    ap.add_argument("--no-verify", action="store_true", help="skip the k-row verify-batch layer probe")
     ap.add_argument("--mode", choices=["persistent", "persistent-plain", "graph", "eager"], default="persistent",
                     help="persistent: one cooperative kernel per step (persistent-plain: the same kernel through "
                          "a plain launch, for profilers); graph: per-layer kernels in a HIP graph")
@@ -396,6 +441,9 @@ def main():
         "device": name.value.decode(),
     }
     lib.tg_hip_decode_destroy(step)
+    if not args.no_verify:
+        log("verify batch probe ...")
+        result["verify_layer"] = verify_probe(tg, bufs[0].ptr)
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
     for b in bufs + nbufs:
