@@ -176,6 +176,18 @@ size_t tg_hip_matmul_scratch_bytes(int k, int ncols);
 void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n,
                          float eps, void *stream);
 
+/* MoE router over k device-resident rows x_j (normalized hidden states):
+ * logits = router (n_experts x dim f32) . x_j (+ bias), the top_k experts by
+ * descending logit into idx_dev [k][top_k], and their weights, a softmax over
+ * the selected logits only, into w_dev [k][top_k] (replaces Router.logits,
+ * _topk and _weights, tinygiant/router.py:29-42, for selection without cache
+ * bias; n_experts <= 256, top_k <= 64).  scratch_dev holds
+ * tg_hip_route_scratch_bytes(k, n_experts) bytes (the logits). */
+void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const float *x_dev, int k,
+                      int n_experts, int dim, int top_k, int32_t *idx_dev, float *w_dev,
+                      void *scratch_dev, void *stream);
+size_t tg_hip_route_scratch_bytes(int k, int n_experts);
+
 /* Output head over k (1..16) device-resident rows with the argmax fused in:
  * x_j = RMSNorm(inputs_j) * norm_w (skipped when norm_w_dev is NULL),
  * logits[j][r] = dot(mat row r, q8(x_j)) and argmax_dev[j] = the first r

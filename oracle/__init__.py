@@ -222,3 +222,23 @@ def expert_forward(q4_data, x, output, weight, D, I):
     lib().or_expert_forward(_p(q4_data), np.ascontiguousarray(x, np.float32).ctypes.data,
                             output.ctypes.data, weight, D, I)
     return output
+
+
+def route(router, bias, x, top_k):
+    """Restates Router.logits, _topk and _weights (tinygiant/router.py:29-42)
+    for one normalized row x: float32 logits = router @ x (+ bias), the top_k
+    experts by descending logit, and float32 softmax weights over the selected
+    logits only.  Returns (logits, idx, weights).
+
+    Pinned by: a full sort of the logits on small inputs (selection and
+    order), and closed forms of the softmax (weights sum to 1, are decreasing
+    with the logits, and equal for equal logits) in tests/test_oracle_pins.py."""
+    router = np.asarray(router, np.float32)
+    logits = router @ np.asarray(x, np.float32)
+    if bias is not None:
+        logits = logits + np.asarray(bias, np.float32)
+    idx = np.argpartition(logits, -top_k)[-top_k:]
+    idx = idx[np.argsort(logits[idx])[::-1]]
+    sel = logits[idx]
+    e = np.exp(sel - sel.max())
+    return logits, idx, (e / e.sum()).astype(np.float32)

@@ -349,3 +349,24 @@ def test_moe_v2_skips_exact_zero_and_accumulates(orc):
     only = orc.moe_v2(gates[:1], ups[:1], downs[:1], O.FMT_Q4K, [O.FMT_Q6K], None, None, None, O.ACT_SILU,
                       rw[:1, :1], x[:1], np.zeros((1, D), np.float32), I)
     assert np.array_equal(out[0], base[0] + only[0])
+
+
+def test_route_oracle_selection_and_softmax(orc):
+    """The router restatement against a full sort and softmax closed forms."""
+    rng = np.random.default_rng(5)
+    for n_exp, dim, top_k in ((16, 32, 4), (128, 64, 8), (32, 16, 1)):
+        router = rng.standard_normal((n_exp, dim)).astype(np.float32)
+        x = rng.standard_normal(dim).astype(np.float32)
+        bias = rng.standard_normal(n_exp).astype(np.float32)
+        logits, idx, w = orc.route(router, bias, x, top_k)
+        full = np.argsort(-logits.astype(np.float64), kind="stable")
+        assert list(idx) == list(full[:top_k])
+        assert np.allclose(logits, router.astype(np.float64) @ x.astype(np.float64) + bias, rtol=1e-5, atol=1e-5)
+        assert abs(float(w.sum()) - 1.0) < 1e-6
+        assert np.all(np.diff(w) <= 0)
+        ref = np.exp(logits[idx].astype(np.float64) - logits[idx].max())
+        assert np.allclose(w, ref / ref.sum(), rtol=1e-6, atol=1e-7)
+    # equal logits get equal weights
+    router = np.ones((8, 4), np.float32)
+    _, idx, w = orc.route(router, None, np.ones(4, np.float32), 4)
+    assert np.allclose(w, 0.25)

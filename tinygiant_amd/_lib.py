@@ -93,6 +93,8 @@ def register_extensions(lib):
     _reg(lib.tg_hip_matmul_scratch_bytes, [CI, CI], SZ)
     _reg(lib.tg_hip_head_argmax_dev, [CI, VP, VP, VP, CF, CI, CI, CI, VP, VP, VP, VP, VP])
     _reg(lib.tg_hip_head_scratch_bytes, [CI, CI, CI], SZ)
+    _reg(lib.tg_hip_route_dev, [VP, VP, VP, CI, CI, CI, CI, VP, VP, VP, VP])
+    _reg(lib.tg_hip_route_scratch_bytes, [CI, CI], SZ)
     _reg(lib.tg_hip_mark, [CI])
     _reg(lib.tg_hip_marks_ms, [CI, CI], CF)
     _reg(lib.tg_hip_rms_norm_dev, [VP, VP, VP, CI, CI, CF, VP])

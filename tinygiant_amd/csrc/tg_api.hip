@@ -31,6 +31,7 @@
 
 #include "tg_decode.h"
 #include "tg_head.h"
+#include "tg_route.h"
 #include "tg_kernels.h"
 #include "tg_synth.h"
 
@@ -875,6 +876,23 @@ TG_API void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_de
 }
 
 TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k, ncols); }
+
+/* ---- router ---- */
+TG_API size_t tg_hip_route_scratch_bytes(int k, int n_experts) { return (size_t)k * n_experts * 4; }
+
+TG_API void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const float *x_dev, int k, int n_experts,
+                             int dim, int top_k, int32_t *idx_dev, float *w_dev, void *scratch_dev, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!router_dev || !x_dev || !idx_dev || !w_dev || !scratch_dev || k <= 0 || dim <= 0 || n_experts <= 0 ||
+        n_experts > 256 || top_k <= 0 || top_k > 64 || top_k > n_experts) {
+        set_err("tg_hip_route_dev: bad arguments (n_experts <= 256, 1 <= top_k <= 64)");
+        return;
+    }
+    ensure_init();
+    launch_route(router_dev, bias_dev, x_dev, k, n_experts, dim, top_k, (float *)scratch_dev, idx_dev, w_dev,
+                 stream ? (hipStream_t)stream : g.st);
+    HIPCHECK(hipGetLastError());
+}
 
 /* ---- output head with fused argmax ----
  * Scratch: q8 rows | 16 argmax keys | RMSNorm'd rows | logits (only when the

@@ -1,0 +1,17 @@
+/*
+ * tg_route.h -- the device router (internal launch interface).
+ */
+#ifndef TG_ROUTE_H
+#define TG_ROUTE_H
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tg {
+
+/* logits [k][n_experts] (scratch), idx/w [k][k_top]; k_top <= 64,
+ * n_experts <= 256 */
+void launch_route(const float *router, const float *bias, const float *x, int k, int n_experts, int dim, int k_top,
+                  float *logits, int32_t *idx, float *w, hipStream_t st);
+
+}  // namespace tg
+#endif

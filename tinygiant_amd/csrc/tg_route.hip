@@ -1,0 +1,119 @@
+/*
+ * tg_route.hip -- the MoE router on the device: per input row, logits over
+ * the experts, the top-k experts by descending logit and their weights as a
+ * softmax over the selected logits only (Router.logits/_topk/_weights,
+ * tinygiant/router.py:29-42; selection without cache bias, router.py:62-63).
+ *
+ *   k_route_logits   one wave per expert row: f32 router row . x_j (+ bias)
+ *                    for every input row j, lanes accumulating in fixed
+ *                    order and a fixed DPP tree
+ *   k_route_topk     one wave per input row: top-k by repeated wave argmax
+ *                    (larger logit first, lower expert index on equal
+ *                    logits), then exp(l - max) / sum with the sum grouped
+ *                    as numpy's float32 pairwise sum groups 8 values
+ */
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "tg_device.hpp"
+#include "tg_route.h"
+
+namespace tg {
+
+/* logits[j][e] = router[e] . x_j (+ bias[e]); one wave per expert row */
+__global__ __launch_bounds__(256) void k_route_logits(const float *__restrict__ router, const float *__restrict__ bias,
+                                                      const float *__restrict__ x, int k, int n_experts, int dim,
+                                                      float *logits) {
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (e >= n_experts) return;   /* uniform per wave */
+    const float *w = router + (size_t)e * dim;
+    for (int j = 0; j < k; j++) {
+        const float *xr = x + (size_t)j * dim;
+        float acc = 0.f;
+        for (int i = lane; i < dim; i += 64) acc = fmaf(w[i], xr[i], acc);
+        acc = wave_sum(acc);
+        if (lane == 0) logits[(size_t)j * n_experts + e] = bias ? acc + bias[e] : acc;
+    }
+}
+
+/* top-k + softmax over the selected, one wave per input row (k_top <= 64,
+ * n_experts <= 256) */
+__global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ logits, int n_experts, int k_top,
+                                                   int32_t *idx_out, float *w_out) {
+    const int lane = threadIdx.x;
+    const int j = blockIdx.x;
+    const float *lg = logits + (size_t)j * n_experts;
+    float v[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int e = lane + 64 * t;
+        v[t] = e < n_experts ? lg[e] : -INFINITY;
+    }
+    float sel_l = 0.f;   /* lane s keeps the s-th selected logit */
+    int sel_e = 0;
+    for (int s = 0; s < k_top; s++) {
+        /* lane-local best: larger logit, then lower index */
+        float bv = v[0];
+        int be = lane;
+#pragma unroll
+        for (int t = 1; t < 4; t++)
+            if (v[t] > bv) {
+                bv = v[t];
+                be = lane + 64 * t;
+            }
+        /* wave best by the same rule */
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oe = __shfl_xor(be, o, 64);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        if (lane == s) {
+            sel_l = bv;
+            sel_e = be;
+        }
+        if ((be & 63) == lane) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                if (t == (be >> 6)) v[t] = -INFINITY;
+        }
+    }
+    /* softmax over the selected (descending order, so the max is the first) */
+    const float mx = __shfl(sel_l, 0, 64);
+    const float ex = lane < k_top ? expf(sel_l - mx) : 0.f;
+    float sum;
+    if (k_top >= 8) {
+        /* numpy's pairwise float32 sum for 8 <= n <= 128: eight running sums
+         * over whole groups of 8, ((r0+r1)+(r2+r3))+((r4+r5)+(r6+r7)), then
+         * the n % 8 leftovers one by one */
+        float r[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) r[q] = __shfl(ex, q, 64);
+        int i = 8;
+        for (; i + 8 <= k_top; i += 8)
+#pragma unroll
+            for (int q = 0; q < 8; q++) r[q] += __shfl(ex, i + q, 64);
+        sum = ((r[0] + r[1]) + (r[2] + r[3])) + ((r[4] + r[5]) + (r[6] + r[7]));
+        for (; i < k_top; i++) sum += __shfl(ex, i, 64);
+    } else {
+        sum = 0.f;
+        for (int q = 0; q < k_top; q++) sum += __shfl(ex, q, 64);
+    }
+    if (lane < k_top) {
+        idx_out[(size_t)j * k_top + lane] = sel_e;
+        w_out[(size_t)j * k_top + lane] = ex / sum;
+    }
+}
+
+void launch_route(const float *router, const float *bias, const float *x, int k, int n_experts, int dim, int k_top,
+                  float *logits, int32_t *idx, float *w, hipStream_t st) {
+    hipLaunchKernelGGL(k_route_logits, dim3((n_experts + 3) / 4), dim3(256), 0, st, router, bias, x, k, n_experts, dim,
+                       logits);
+    hipLaunchKernelGGL(k_route_topk, dim3(k), dim3(64), 0, st, logits, n_experts, k_top, idx, w);
+}
+
+}  // namespace tg
