@@ -265,6 +265,131 @@ def verify_probe(tg, base, ks=(5, 9), iters=20):
     return out
 
 
+def _time_calls(lib, fn, iters):
+    for _ in range(3):
+        fn()
+    lib.tg_hip_mark(0)
+    for _ in range(iters):
+        fn()
+    lib.tg_hip_mark(1)
+    return lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
+
+
+def configs_probe(tg, iters=20):
+    """The other workloads of this path on their device-resident entry points:
+      q4k_matvec        one 768x2048 q4_K GEMV, one row (tg_hip_matmul_dev)
+      qwen_layer_plan   one Qwen3 layer, 8 experts, 1 token, per-layer kernels
+                        (tg_hip_moe_plan_run)
+      gptoss_decode     gpt-oss-120b-shaped step: 36 layers x top-4 of 128
+                        resident MXFP4 experts (D = I = 2880, biases, clamped
+                        SwiGLU), h <- h + MoE(RMSNorm(h)), HIP-graph mode
+      gptoss_prefill    64 tokens through one gpt-oss layer (top-4 each), the
+                        grouped multi-row path"""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    out = {}
+    rng = np.random.default_rng(SEED + 23)
+    # q4_K matvec
+    mat = tg.DeviceArray(GATE_B)
+    lib.tg_hip_synth_fill(0, SEED + 24, mat.ptr, GATE_B, None)
+    x = tg.DeviceArray(D * 4)
+    x.upload(rng.standard_normal(D).astype(np.float32))
+    y = tg.DeviceArray(I * 4)
+    sc = tg.DeviceArray(lib.tg_hip_matmul_scratch_bytes(1, D))
+    us = _time_calls(lib, lambda: lib.tg_hip_matmul_dev(0, mat.ptr, None, x.ptr, y.ptr, I, D, 1, sc.ptr, None), iters)
+    out["q4k_matvec"] = {"rows": I, "cols": D, "us": round(us, 2), "weight_bytes": GATE_B,
+                         "weight_gbps": round(GATE_B / (us * 1e-6) / 1e9, 1)}
+    for a in (mat, x, y, sc):
+        a.free()
+
+    # gpt-oss: 36 layers of 128 MXFP4 experts
+    GD, GL, GE, GK = 2880, 36, 128, 4
+    mrb = (GD // 32) * 17
+    mat_b = GD * mrb
+    exp_b = 3 * mat_b
+    perm = rng.permutation(GE)
+    bufs, plans, bias_bufs, norms = [], [], [], []
+    for l in range(GL):
+        buf = tg.DeviceArray(GE * exp_b)
+        for e in range(GE):
+            for part in range(3):
+                lib.tg_hip_synth_fill(3, S.tensor_seed(SEED + 25, l, e, part), buf.ptr + (e * 3 + part) * mat_b,
+                                      mat_b, None)
+        bufs.append(buf)
+        idx = np.sort(S.zipf_topk(rng, GE, GK, 1.1, perm))
+        w = S.router_weights(rng, GK)
+        ptrs = [(ctypes.c_void_p * GK)(*[buf.ptr + (int(e) * 3 + p) * mat_b for e in idx]) for p in range(3)]
+        bl = []
+        for p in range(3):
+            bb = tg.DeviceArray(GK * GD * 4)
+            bb.upload((rng.standard_normal((GK, GD)) * 0.05).astype(np.float32))
+            bl.append(bb)
+            bias_bufs.append(bb)
+        bptr = [(ctypes.c_void_p * GK)(*[bl[p].ptr + i * GD * 4 for i in range(GK)]) for p in range(3)]
+        fm = np.full(GK, tg.FMT_MXFP4, np.int32)
+        rwc = np.ascontiguousarray(w.reshape(GK, 1), np.float32)
+        plan = lib.tg_hip_moe_plan_create(*[ctypes.addressof(q) for q in ptrs], tg.FMT_MXFP4, fm.ctypes.data,
+                                          *[ctypes.addressof(q) for q in bptr], tg.ACT_GPTOSS, GK, rwc.ctypes.data,
+                                          1, GD, GD)
+        if not plan:
+            raise RuntimeError(tg.last_error())
+        plans.append(plan)
+        nw = tg.DeviceArray(GD * 4)
+        nw.upload(rng.uniform(0.5, 1.5, GD).astype(np.float32))
+        norms.append(nw)
+    h = tg.DeviceArray(GD * 4)
+    h.upload(rng.standard_normal(GD).astype(np.float32))
+    parr = (ctypes.c_void_p * GL)(*plans)
+    narr = (ctypes.c_void_p * GL)(*[a.ptr for a in norms])
+    step = lib.tg_hip_decode_create(ctypes.addressof(parr), GL, ctypes.addressof(narr), ctypes.c_float(1e-5), h.ptr, 1)
+    if not step:
+        raise RuntimeError(tg.last_error())
+    for _ in range(3):
+        lib.tg_hip_decode_run(step, None)
+    ms = lib.tg_hip_decode_time(step, iters) / iters
+    step_b = GL * GK * exp_b
+    out["gptoss_decode"] = {"layers": GL, "experts_per_layer": GE, "top_k": GK, "dim": GD,
+                            "resident_bytes": GL * GE * exp_b, "weight_bytes_per_step": step_b,
+                            "mode": "graph", "ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+                            "weight_gbps": round(step_b / (ms * 1e-3) / 1e9, 1),
+                            "hbm_frac": round(step_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    lib.tg_hip_decode_destroy(step)
+    for p in plans:
+        lib.tg_hip_moe_plan_destroy(p)
+    # 64-token prefill through layer 0
+    kp = 64
+    experts, rw = S.routing_rows(rng, kp, GE, GK, 1.1, perm)
+    n = len(experts)
+    ptrs = [(ctypes.c_void_p * n)(*[bufs[0].ptr + (int(e) * 3 + p) * mat_b for e in experts]) for p in range(3)]
+    bl = []
+    for p in range(3):
+        bb = tg.DeviceArray(n * GD * 4)
+        bb.upload((rng.standard_normal((n, GD)) * 0.05).astype(np.float32))
+        bl.append(bb)
+    bptr = [(ctypes.c_void_p * n)(*[bl[p].ptr + i * GD * 4 for i in range(n)]) for p in range(3)]
+    fm = np.full(n, tg.FMT_MXFP4, np.int32)
+    rwc = np.ascontiguousarray(rw, np.float32)
+    plan = lib.tg_hip_moe_plan_create(*[ctypes.addressof(q) for q in ptrs], tg.FMT_MXFP4, fm.ctypes.data,
+                                      *[ctypes.addressof(q) for q in bptr], tg.ACT_GPTOSS, n, rwc.ctypes.data,
+                                      kp, GD, GD)
+    if not plan:
+        raise RuntimeError(tg.last_error())
+    xp = tg.DeviceArray(kp * GD * 4)
+    xp.upload(rng.standard_normal((kp, GD)).astype(np.float32))
+    yp = tg.DeviceArray(kp * GD * 4)
+    us = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, xp.ptr, yp.ptr, None), iters)
+    ops = 2 * kp * GK * 3 * GD * GD
+    out["gptoss_prefill"] = {"tokens": kp, "experts": n, "rows_per_expert_max": int((rw != 0).sum(axis=1).max()),
+                             "us": round(us, 2), "weight_bytes": n * exp_b,
+                             "weight_gbps": round(n * exp_b / (us * 1e-6) / 1e9, 1),
+                             "int8_tops": round(ops / (us * 1e-6) / 1e12, 2),
+                             "frac_of_int8_peak": round(ops / (us * 1e-6) / 5.0e15, 5)}
+    lib.tg_hip_moe_plan_destroy(plan)
+    for a in bufs + bias_bufs + norms + bl + [h, xp, yp]:
+        a.free()
+    return out
+
+
 def head_probe(tg, ks=(1, 5, 9), iters=20):
     """The q6_K output head of Qwen3-30B-A3B (151936 x 2048, 255,252,480 B) over
     k verify rows with the argmax fused in (tg_hip_head_argmax_dev, RMSNorm
@@ -323,6 +448,8 @@ def main():
     ap.add_argument("--no-boundary", action="store_true", help="skip the ctypes-entry latency probe")
     ap.add_argument("--no-head", action="store_true", help="skip the q6_K output head + argmax probe")
     ap.add_argument("--no-verify", action="store_true", help="skip the k-row verify-batch layer probe")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other workloads (q4_K matvec, gpt-oss decode and prefill)")
     ap.add_argument("--mode", choices=["persistent", "persistent-plain", "graph", "eager"], default="persistent",
                     help="persistent: one cooperative kernel per step (persistent-plain: the same kernel through "
                          "a plain launch, for profilers); graph: per-layer kernels in a HIP graph")
@@ -454,6 +581,9 @@ def main():
     if not args.no_head:
         log("output head probe ...")
         result["head_argmax"] = head_probe(tg)
+    if not args.no_configs:
+        log("other workloads ...")
+        result["other_workloads"] = configs_probe(tg)
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(routes, min(args.cpu_layers, layers))
