@@ -283,8 +283,9 @@ def configs_probe(tg, iters=20):
       gptoss_decode     gpt-oss-120b-shaped step: 36 layers x top-4 of 128
                         resident MXFP4 experts (D = I = 2880, biases, clamped
                         SwiGLU), h <- h + MoE(RMSNorm(h)), HIP-graph mode
-      gptoss_prefill    64 tokens through one gpt-oss layer (top-4 each), the
-                        grouped multi-row path"""
+      gptoss_prefill    64 tokens through one gpt-oss layer (top-4 each): the
+                        int8 MFMA expert phases, and for comparison the
+                        per-pair kernels"""
     import tinygiant_amd.synth as S
     lib = tg.lib()
     out = {}
@@ -378,9 +379,15 @@ def configs_probe(tg, iters=20):
     xp.upload(rng.standard_normal((kp, GD)).astype(np.float32))
     yp = tg.DeviceArray(kp * GD * 4)
     us = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, xp.ptr, yp.ptr, None), iters)
+    # the same call with every expert on the per-pair kernels
+    prev = lib.tg_hip_set_moe_grouped_min_rows(0)
+    us_pp = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, xp.ptr, yp.ptr, None), iters)
+    lib.tg_hip_set_moe_grouped_min_rows(prev)
     ops = 2 * kp * GK * 3 * GD * GD
     out["gptoss_prefill"] = {"tokens": kp, "experts": n, "rows_per_expert_max": int((rw != 0).sum(axis=1).max()),
-                             "us": round(us, 2), "weight_bytes": n * exp_b,
+                             "path": "int8 MFMA phases" if int((rw != 0).sum(axis=1).max()) >= prev else "per-pair",
+                             "us": round(us, 2), "us_per_pair_kernels": round(us_pp, 2),
+                             "weight_bytes": n * exp_b,
                              "weight_gbps": round(n * exp_b / (us * 1e-6) / 1e9, 1),
                              "int8_tops": round(ops / (us * 1e-6) / 1e12, 2),
                              "frac_of_int8_peak": round(ops / (us * 1e-6) / 5.0e15, 5)}

@@ -232,6 +232,13 @@ float tg_hip_decode_time(tg_hip_decode *step, int iters);   /* ms for iters step
 void tg_hip_decode_kernel_times(tg_hip_decode *step, float *ms_out /*[6]*/, int *n_out /*[6]*/);
 void tg_hip_decode_destroy(tg_hip_decode *step);
 void tg_hip_device_name(char *buf, int n);
+/* MXFP4 expert layers whose busiest expert holds at least `rows` pairs run
+ * their gate/up and down phases on int8 MFMA (each weight block read once per
+ * 64 pairs; same per-block integer sums and f32 order as dot_mxfp4_q8,
+ * csrc/libtinygiant.c:533-547); 0 keeps every layer on the per-pair kernels.
+ * Default 4.  Returns the previous setting.  No counterpart in the
+ * reference, which has one CPU kernel for every row count. */
+int tg_hip_set_moe_grouped_min_rows(int rows);
 /* Event marks (slots 0..7) on the library stream; tg_hip_marks_ms waits for
  * mark b and returns the milliseconds between marks a and b. */
 void tg_hip_mark(int slot);

@@ -280,7 +280,7 @@ void build_pairs(HostPlan &h, const float *row_weights) {
 /* Lays out tables + scratch in `base` (device) and the table image in `img`
  * (host); returns MoeArgs pointing into base. */
 struct Layout {
-    size_t tables, tables_len, xin, xq, hidden, hq, part, out, total;
+    size_t tables, tables_len, xin, xq, hidden, hq, part, out, xp, hp, total;
 };
 
 Layout plan_layout(const HostPlan &h) {
@@ -292,6 +292,7 @@ Layout plan_layout(const HostPlan &h) {
     t += 6 * (size_t)n * 8;                 /* gate, up, down, gbias, ubias, dbias */
     t += (size_t)n * 4;                     /* down_fmt */
     t += (size_t)(n + 1) * 4 + (size_t)P * 4 + (size_t)P * 4 + (size_t)(k + 1) * 4 + (size_t)P * 4;
+    t += (size_t)4 * (n + 1) * 4 + 16;      /* active expert lists and their cost prefixes */
     L.tables_len = t + 64;
     b.take(L.tables_len);
     L.xin = b.take((size_t)k * h.D * 4);
@@ -299,6 +300,10 @@ Layout plan_layout(const HostPlan &h) {
     L.hidden = b.take((size_t)P * h.I * 4);
     L.hq = b.take(q8_bytes(P, h.I));
     L.part = b.take((size_t)P * h.D * 4);
+    /* fp8 halves of the q8 rows for the MXFP4 MFMA phases (2 bytes a value) */
+    const bool mx_down = std::find(h.down_fmt.begin(), h.down_fmt.end(), (int)TG_FMT_MXFP4) != h.down_fmt.end();
+    L.xp = h.gate_fmt == TG_FMT_MXFP4 ? b.take((size_t)std::max(k, 1) * h.D * 2) : 0;
+    L.hp = mx_down ? b.take((size_t)P * h.I * 2) : 0;
     L.out = b.take((size_t)k * h.D * 4);
     L.total = b.off;
     return L;
@@ -338,6 +343,8 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     a.hidden = (float *)(dev + L.hidden);
     a.hq = q8_view(dev + L.hq, std::max(h.P, 1), h.I, a.hidden);
     a.part = (float *)(dev + L.part);
+    a.xp = L.xp ? dev + L.xp : nullptr;
+    a.hp = L.hp ? dev + L.hp : nullptr;
     a.out = (float *)(dev + L.out);
     a.n = n;
     a.k = k;
@@ -347,6 +354,38 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     a.act = h.act;
     a.gate_fmt = h.gate_fmt;
     a.gate_rb = row_bytes(h.gate_fmt, h.D);
+    a.max_rows = 0;
+    a.mx_aligned = 1;
+    std::vector<int> act_a, act_b;
+    for (int e = 0; e < n; e++) {
+        if (h.p_off[e + 1] == h.p_off[e]) continue;
+        a.max_rows = std::max(a.max_rows, h.p_off[e + 1] - h.p_off[e]);
+        if (h.gate_fmt == TG_FMT_MXFP4 && ((h.gate[e] | h.up[e]) & 15)) a.mx_aligned = 0;
+        if (h.down_fmt[e] == TG_FMT_MXFP4 && (h.down[e] & 15)) a.mx_aligned = 0;
+        act_a.push_back(e);
+        if (h.down_fmt[e] == TG_FMT_MXFP4) act_b.push_back(e);
+    }
+    a.n_act_a = (int)act_a.size();
+    a.n_act_b = (int)act_b.size();
+    /* cost of one item (16 rows of an expert) in the MFMA phases, in
+     * quarter microseconds measured for D = I = 2880: one slab with its
+     * first pass of 16 pairs (gate/up 10, down 5), and 19 / 18 per further
+     * pass, which waits for its q8 operands */
+    std::vector<int> cum;
+    auto prefix = [&](const std::vector<int> &lst, int rows, int base, int per_pass) {
+        int c = 0;
+        cum.push_back(0);
+        for (int e : lst) {
+            const int passes = (h.p_off[e + 1] - h.p_off[e] + 15) / 16;
+            c += ((rows + 15) / 16) * (base + per_pass * (passes - 1));
+            cum.push_back(c);
+        }
+    };
+    prefix(act_a, h.I, 10, 19);
+    prefix(act_b, h.D, 5, 18);
+    act_a.insert(act_a.end(), act_b.begin(), act_b.end());
+    a.mx_act = (const int *)put(act_a.data(), act_a.size() * 4);
+    a.mx_cum = (const int *)put(cum.data(), cum.size() * 4);
     return a;
 }
 
@@ -818,6 +857,10 @@ TG_API tg_hip_moe_plan *tg_hip_moe_plan_create(const void *const *gate_dev, cons
     h.has_gb = gate_bias_dev != nullptr;
     h.has_ub = up_bias_dev != nullptr;
     h.has_db = down_bias_dev != nullptr;
+    if (h.has_gb != h.has_ub) {
+        set_err("moe plan: gate and up biases must both be given or both be NULL");
+        return nullptr;
+    }
     for (int e = 0; e < n_experts; e++) {
         h.gate.push_back((uint64_t)(uintptr_t)gate_dev[e]);
         h.up.push_back((uint64_t)(uintptr_t)up_dev[e]);
@@ -1225,9 +1268,15 @@ TG_API void tg_hip_device_name(char *buf, int n) {
     snprintf(buf, (size_t)n, "%s (%s, %d CUs)", pr.name, pr.gcnArchName, pr.multiProcessorCount);
 }
 
-/* Copies nbytes (multiple of 16) device-to-device with a plain vector-load
- * kernel `iters` times on the library stream; returns ms (HIP events).  The
- * reference point for measured HBM bandwidth and for counter calibration. */
+/* Pairs per expert from which MXFP4 expert layers take the int8 MFMA phases
+ * (0: never); returns the previous setting. */
+TG_API int tg_hip_set_moe_grouped_min_rows(int rows) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = grouped_min_rows();
+    set_grouped_min_rows(rows);
+    return prev;
+}
+
 /* Event marks on the library stream, for timing queued device work. */
 static hipEvent_t g_marks[8];
 static bool g_marks_ready = false;
@@ -1258,6 +1307,9 @@ TG_API float tg_hip_marks_ms(int a, int b) {
     return ms;
 }
 
+/* Copies nbytes (multiple of 16) device-to-device with a plain vector-load
+ * kernel `iters` times on the library stream; returns ms (HIP events).  The
+ * reference point for measured HBM bandwidth and for counter calibration. */
 TG_API float tg_hip_copy_time(const void *src_dev, void *dst_dev, uint64_t nbytes, int iters) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     ensure_init();

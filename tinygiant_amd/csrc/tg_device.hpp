@@ -478,5 +478,18 @@ struct FF16 {
     __device__ static inline int isum_index(int, int) { return 0; }
 };
 
+/* expert activation (csrc/libtinygiant.c:1250-1257; the
+ * comparisons keep a NaN as the reference's if-chains do): SiLU(g) * u, or the
+ * clamped gpt-oss form g * sigmoid(1.702 g) * (u + 1) */
+__device__ inline float act_fn(int act, float g, float u) {
+    if (act == TG_ACT_GPTOSS) {
+        g = g > 7.f ? 7.f : g;
+        u = u > 7.f ? 7.f : (u < -7.f ? -7.f : u);
+        return g / (1.f + expf(-1.702f * g)) * (u + 1.f);
+    }
+    return g / (1.f + expf(-g)) * u;
+}
+
+
 }  // namespace tg
 #endif

@@ -34,6 +34,12 @@ struct MoeArgs {
     float *out;                             /* [k][D] accumulated output */
     int n, k, P, D, I, act, gate_fmt;
     uint32_t gate_rb;
+    int max_rows;                           /* most pairs of any one expert */
+    int mx_aligned;                         /* every MXFP4 matrix of an active expert starts 16-byte aligned */
+    const int *mx_act;                      /* active experts, then active experts with an MXFP4 down matrix */
+    const int *mx_cum;                      /* cost prefix of each list (n_act + 1 entries each) */
+    uint8_t *xp, *hp;                       /* fp8 halves of xq / hq rows in MFMA order, or null */
+    int n_act_a, n_act_b;
 };
 
 int items_per_row(int fmt, int ncols);
@@ -48,6 +54,17 @@ void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows 
  * 1 quantize(x), 2 gate/up, 3 quantize(hidden), 4 down, 5 combine */
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
                 const std::function<void(int)> *mark = nullptr);
+/* MXFP4 phases on block-scaled MFMA with LDS-resident weight slabs
+ * (tg_grouped.hip): every weight byte is read once whatever the pairs per
+ * expert.  launch_mx_split prepares the fp8 halves of q8 rows. */
+bool grouped_lds_ok(int D, int I);
+void launch_mx_split(const Q8Rows &q, int nrows, int ncols, uint8_t *dst, hipStream_t st);
+void launch_moe_a_mx(const MoeArgs &a, hipStream_t st);
+void launch_moe_b_mx(const MoeArgs &a, hipStream_t st);
+/* pairs per expert from which launch_moe takes the MFMA phases for MXFP4
+ * experts; 0 switches them off */
+void set_grouped_min_rows(int rows);
+int grouped_min_rows();
 void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st);
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st);
 void launch_copy(const void *src, void *dst, uint64_t nbytes, hipStream_t st);

@@ -110,15 +110,6 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uin
 
 /* ======================= MoE phases ======================= */
 
-__device__ inline float act_fn(int act, float g, float u) {
-    if (act == TG_ACT_GPTOSS) {
-        g = fminf(g, 7.f);
-        u = fminf(fmaxf(u, -7.f), 7.f);
-        return g / (1.f + expf(-1.702f * g)) * (u + 1.f);
-    }
-    return g / (1.f + expf(-g)) * u;
-}
-
 /* Phase A: grid (x: wave groups over the I rows, y: expert).  hidden[p][r] for
  * every pair p of the expert. */
 template <class F, int S>
@@ -160,10 +151,8 @@ __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int
             vg = seg_sum<S>(vg);
             vu = seg_sum<S>(vu);
             if (rv && sl == 0) {
-                if (gb) {
-                    vg += gb[r];
-                    vu += ub[r];
-                }
+                if (gb) vg += gb[r];
+                if (ub) vu += ub[r];
                 a.hidden[(size_t)p * a.I + r] = act_fn(a.act, vg, vu);
             }
         }
@@ -377,13 +366,34 @@ void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows 
 #undef CALL
 }
 
+static int g_grouped_min_rows = 4;
+
+void set_grouped_min_rows(int rows) { g_grouped_min_rows = rows < 0 ? 0 : rows; }
+int grouped_min_rows() { return g_grouped_min_rows; }
+
+/* the MFMA phases address each weight matrix and q8 table with one 31-bit
+ * buffer range, copy 16-byte aligned slabs, and hold two slabs of a gate/up
+ * row group in 64 KiB of LDS */
+static bool grouped_fits(const MoeArgs &a) {
+    const uint64_t lim = 1ull << 31;
+    const uint64_t gu = (uint64_t)a.I * row_bytes(TG_FMT_MXFP4, a.D);
+    const uint64_t dn = (uint64_t)a.D * row_bytes(TG_FMT_MXFP4, a.I);
+    const uint64_t xq = (uint64_t)a.k * a.xq.nb * 256, hq = (uint64_t)a.P * a.hq.nb * 256;
+    return a.mx_aligned && gu < lim && dn < lim && xq < lim && hq < lim && grouped_lds_ok(a.D, a.I);
+}
+
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
                 const std::function<void(int)> *mark) {
     /* 1. quantize the k input rows */
     launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
     if (mark) (*mark)(1);
-    /* 2. phase A */
-    {
+    /* 2. phase A: MXFP4 experts with many pairs take the MFMA kernel, which
+     * reads each weight block once for up to 64 pairs */
+    const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
+    if (mx_grouped && a.gate_fmt == TG_FMT_MXFP4 && a.xp) {
+        launch_mx_split(a.xq, a.k, a.D, a.xp, st);
+        launch_moe_a_mx(a, st);
+    } else {
         int T;
         const int nitems = items_per_row(a.gate_fmt, a.D);
         const int S = pick_S(nitems, &T);
@@ -401,6 +411,11 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
     /* 4. phase B, once per down format present */
     for (int i = 0; i < n_down_fmts; i++) {
         const int fmt = down_fmts_present[i];
+        if (mx_grouped && fmt == TG_FMT_MXFP4 && a.hp) {
+            launch_mx_split(a.hq, a.P, a.I, a.hp, st);
+            launch_moe_b_mx(a, st);
+            continue;
+        }
         int T;
         const int nitems = items_per_row(fmt, a.I);
         const int S = pick_S(nitems, &T);
