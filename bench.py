@@ -389,8 +389,8 @@ def configs_probe(tg, iters=20):
                              "us": round(us, 2), "us_per_pair_kernels": round(us_pp, 2),
                              "weight_bytes": n * exp_b,
                              "weight_gbps": round(n * exp_b / (us * 1e-6) / 1e9, 1),
-                             "int8_tops": round(ops / (us * 1e-6) / 1e12, 2),
-                             "frac_of_int8_peak": round(ops / (us * 1e-6) / 5.0e15, 5)}
+                             "mfma_tops": round(ops / (us * 1e-6) / 1e12, 2),
+                             "frac_of_fp8_mfma_peak": round(ops / (us * 1e-6) / 5.0e15, 5)}
     lib.tg_hip_moe_plan_destroy(plan)
     for a in bufs + bias_bufs + norms + bl + [h, xp, yp]:
         a.free()

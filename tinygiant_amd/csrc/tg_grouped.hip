@@ -264,7 +264,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     /* the expert of the item being issued, and its matrices */
     int iss_ai = -1;
     Buf iss_w[NM];
-    u32x4 v[NM][CH];
+    u32x4 vA[NM][CH], vB[NM][CH];   /* slabs of two items ahead, alternating */
     auto set_issuer = [&](int ai) {
         iss_ai = ai;
         const int e = ldc(act, ai);
@@ -274,8 +274,9 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
             iss_w[m] = make_buf_uniform((const void *)(uintptr_t)base, mbytes);
         }
     };
-    auto issue = [&](int it) {
-        const uint32_t off = (uint32_t)(it % nslab) * 16u * rb;
+    auto issue = [&](u32x4 (&v)[NM][CH], int item) {
+        if (item / nslab != iss_ai) set_issuer(item / nslab);
+        const uint32_t off = (uint32_t)(item % nslab) * 16u * rb;
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
@@ -351,80 +352,76 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
         }
     };
 
-    /* first item: its slabs, q8 operands, biases and pair weights */
+    /* first item: its slabs, q8 operands, biases and pair weights, then the
+     * second item's slabs */
     Expert cur = expert(it / nslab), nxt = cur;
     fetch_pairs(cur, xrows, wts);
     xrow[0] = xrows[0];
-    set_issuer(cur.ai);
-    issue(it);
+    issue(vA, it);
     load_batch(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
     int er = ep_row(it);
     float bias0 = __uint_as_float(ld4(cur.bias[0], (uint32_t)er * 4u));
     float bias1 = __uint_as_float(ld4(cur.bias[1], (uint32_t)er * 4u));
     float wt = wts[0];
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < it_end) issue(vB, it + 1);
 
-    /* Per item, loads are issued in one fixed order -- the next expert's
-     * input rows, the next item's slabs, then (after the compute) the next
-     * item's q8 operands, biases and pair weights -- and loads complete in
-     * order, so no wait for this item's operands waits for a younger slab. */
-    while (it < it_end) {
+    /* Per item, loads are issued in one fixed order: the next expert's pair
+     * rows (when it changes), then after the compute the next item's q8
+     * operands, biases and pair weights, then the slabs two items ahead.
+     * Loads complete in order, so no wait for an item's operands ever waits
+     * for a younger slab, and every slab has a whole item of lead. */
+    float acc[NM][MT][4];
+    /* one pass: the partial sums of every wave to LDS, then 256 threads add
+     * them in wave order and write one result each */
+    auto finish = [&](int t0) {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int vv = 0; vv < 4; vv++) red[((w * NM + m) * 4 + vv) * 64 + lane] = acc[m][0][vv];
+        __syncthreads();
+        const int j = t0 + (el & 15);
+        if (tid < 256 && j < cur.ne && er < rows) {
+            float r2[NM];
+#pragma unroll
+            for (int m = 0; m < NM; m++) {
+                float sum = red[(m * 4 + ev) * 64 + el];
+#pragma unroll
+                for (int ww = 1; ww < NWAVE; ww++) sum += red[((ww * NM + m) * 4 + ev) * 64 + el];
+                r2[m] = sum;
+            }
+            const int p = cur.p0 + j;
+            if (DOWN) {
+                a.part[(size_t)p * a.D + er] = wt * (r2[0] + (cur.has0 ? bias0 : 0.f));
+            } else {
+                float gv = r2[0], uv = r2[NM - 1];
+                if (cur.has0) gv += bias0;
+                if (cur.has1) uv += bias1;
+                a.hidden[(size_t)p * a.I + er] = act_fn(a.act, gv, uv);
+            }
+        }
+    };
+    auto zero = [&]() {
+#pragma unroll
+        for (int m = 0; m < NM; m++)
+#pragma unroll
+            for (int vv = 0; vv < 4; vv++) acc[m][0][vv] = 0.f;
+    };
+    auto step = [&](u32x4 (&v)[NM][CH]) {
         const int nx = it + 1;
         const bool has_nx = nx < it_end;
         const bool new_ex = has_nx && nx / nslab != cur.ai;
         if (new_ex) {
             nxt = expert(nx / nslab);
             fetch_pairs(nxt, nxrows, nwts);
-            if (nxt.ai != iss_ai) set_issuer(nxt.ai);
         }
-        /* a multi-pass item issues the next slabs after its last pass's
-         * operands, so that no pass waits for them */
-        const bool multi = cur.ne > 16 * MT;
         __syncthreads();   /* the previous item is done with LDS */
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
             for (int c = 0; c < CH; c++)
                 *(u32x4 *)((uint8_t *)lds + m * sstride + (uint32_t)(tid + NT * c) * 16u) = v[m][c];
-        __builtin_amdgcn_sched_barrier(0);
-        if (has_nx && !multi) issue(nx);
         __syncthreads();
-
-        /* one pass: the partial sums of every wave to LDS, then 256 threads
-         * add them in wave order and write one result each */
-        float acc[NM][MT][4];
-        auto finish = [&](int t0) {
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int vv = 0; vv < 4; vv++) red[((w * NM + m) * 4 + vv) * 64 + lane] = acc[m][0][vv];
-            __syncthreads();
-            const int j = t0 + (el & 15);
-            if (tid < 256 && j < cur.ne && er < rows) {
-                float r2[NM];
-#pragma unroll
-                for (int m = 0; m < NM; m++) {
-                    float sum = red[(m * 4 + ev) * 64 + el];
-#pragma unroll
-                    for (int ww = 1; ww < NWAVE; ww++) sum += red[((ww * NM + m) * 4 + ev) * 64 + el];
-                    r2[m] = sum;
-                }
-                const int p = cur.p0 + j;
-                if (DOWN) {
-                    a.part[(size_t)p * a.D + er] = wt * (r2[0] + (cur.has0 ? bias0 : 0.f));
-                } else {
-                    float gv = r2[0], uv = r2[NM - 1];
-                    if (cur.has0) gv += bias0;
-                    if (cur.has1) uv += bias1;
-                    a.hidden[(size_t)p * a.I + er] = act_fn(a.act, gv, uv);
-                }
-            }
-        };
-        auto zero = [&]() {
-#pragma unroll
-            for (int m = 0; m < NM; m++)
-#pragma unroll
-                for (int vv = 0; vv < 4; vv++) acc[m][0][vv] = 0.f;
-        };
         /* first pass: its first batch of q8 operands is in registers */
         zero();
         mma_batch<NM, MT>(lds, sstride, rb, xb, b0w, min(b1w, b0w + XB), 1, lane, acc);
@@ -448,18 +445,10 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
             xrow[0] = k < NPRE ? r : pair_row(cur, t0 + c16);
             if (DOWN) wt = k < NPRE ? wk : pair_w(cur, t0 + (el & 15));
             zero();
-            /* at least one batch, so that every wave issues its share of the
-             * next slabs (a wave's block range may be empty) */
-            int bb = b0w;
-            do {
+            for (int bb = b0w; bb < b1w; bb += XB) {
                 load_batch(xb, xs, bb, min(b1w, bb + XB), 1, xrow, g);
-                if (bb + XB >= b1w && t0 + 16 * MT >= cur.ne && has_nx) {
-                    __builtin_amdgcn_sched_barrier(0);
-                    issue(nx);
-                }
                 mma_batch<NM, MT>(lds, sstride, rb, xb, bb, min(b1w, bb + XB), 1, lane, acc);
-                bb += XB;
-            } while (bb < b1w);
+            }
             finish(t0);
         }
         /* the next item's q8 operands (unless this item's first-pass ones
@@ -481,7 +470,15 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
             bias1 = __uint_as_float(ld4(cur.bias[1], (uint32_t)er * 4u));
             wt = wts[0];
         }
+        /* then the slabs two items ahead, into the registers just stored */
+        __builtin_amdgcn_sched_barrier(0);
+        if (it + 2 < it_end) issue(v, it + 2);
         it = nx;
+    };
+    while (it < it_end) {
+        step(vA);
+        if (it >= it_end) break;
+        step(vB);
     }
 }
 
