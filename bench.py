@@ -432,6 +432,62 @@ def head_probe(tg, ks=(1, 5, 9), iters=20):
     return out
 
 
+def attention_probe(tg, kv_lens=(512, 4096), iters=20):
+    """Decode attention of one Qwen3-30B-A3B layer on the device
+    (tg_hip_attention_dev): D 2048, 32 query heads, 4 KV heads of 128, q4_K
+    q/k/o, q6_K v, QK norm, f32 KV cache.  Algorithmic bytes: the four
+    projection matrices plus one read of the attended K and V rows."""
+    lib = tg.lib()
+    D, nh, nkv, hd = 2048, 32, 4, 128
+    qd, kd = nh * hd, nkv * hd
+    kv_max = max(kv_lens) + 1
+    fmts = (0, 0, 2, 0)
+    shapes = ((qd, D), (kd, D), (kd, D), (D, qd))
+    rng = np.random.default_rng(SEED + 31)
+    mats, wbytes = [], 0
+    for i, ((r, c), f) in enumerate(zip(shapes, fmts)):
+        nb = r * lib.tg_row_bytes(f, c)
+        m = tg.DeviceArray(nb)
+        lib.tg_hip_synth_fill(f, SEED + 32 + i, m.ptr, nb, None)
+        mats.append(m)
+        wbytes += nb
+    norms = []
+    for _ in range(2):
+        a = tg.DeviceArray(hd * 4)
+        a.upload(rng.uniform(0.5, 1.5, hd).astype(np.float32))
+        norms.append(a)
+    half = hd // 2
+    ang = np.arange(kv_max)[:, None] / (10000.0 ** (np.arange(half)[None, :] * 2.0 / hd))
+    rc, rs = tg.DeviceArray(kv_max * half * 4), tg.DeviceArray(kv_max * half * 4)
+    rc.upload(np.cos(ang).astype(np.float32))
+    rs.upload(np.sin(ang).astype(np.float32))
+    cache = [tg.DeviceArray(nkv * kv_max * hd * 4) for _ in range(2)]
+    for a in cache:
+        a.upload((rng.standard_normal(nkv * kv_max * hd)).astype(np.float32))
+    x, y = tg.DeviceArray(D * 4), tg.DeviceArray(D * 4)
+    x.upload(rng.standard_normal(D).astype(np.float32))
+    sc = tg.DeviceArray(lib.tg_hip_attention_scratch_bytes(D, nh, nkv, hd, kv_max))
+    out = {"embed_dim": D, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "formats": "q4_K q/k/o, q6_K v",
+           "weight_bytes": wbytes, "kv_len": {}}
+    for L in kv_lens:
+        args = (*fmts, *[m.ptr for m in mats], None, None, None, None, norms[0].ptr, norms[1].ptr, None,
+                cache[0].ptr, cache[1].ptr, L, kv_max, 0, rc.ptr, rs.ptr, x.ptr, y.ptr, D, nh, nkv, hd, L,
+                ctypes.c_float(1e-6), None, sc.ptr, None)
+        for _ in range(3):
+            lib.tg_hip_attention_dev(*args)
+        lib.tg_hip_mark(0)
+        for _ in range(iters):
+            lib.tg_hip_attention_dev(*args)
+        lib.tg_hip_mark(1)
+        us = lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
+        nbytes = wbytes + 2 * nkv * (L + 1) * hd * 4
+        out["kv_len"][L] = {"us": round(us, 2), "bytes": nbytes, "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                            "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    for a in mats + norms + cache + [rc, rs, x, y, sc]:
+        a.free()
+    return out
+
+
 def read_traffic(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
@@ -588,6 +644,7 @@ def main():
     if not args.no_head:
         log("output head probe ...")
         result["head_argmax"] = head_probe(tg)
+        result["attention_layer"] = attention_probe(tg)
     if not args.no_configs:
         log("other workloads ...")
         result["other_workloads"] = configs_probe(tg)

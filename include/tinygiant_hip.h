@@ -188,6 +188,27 @@ void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const floa
                       void *scratch_dev, void *stream);
 size_t tg_hip_route_scratch_bytes(int k, int n_experts);
 
+/* Decode attention for one row with every pointer on the device (replaces
+ * tg_attention_v2, csrc/libtinygiant.c:939-983, with the same arguments and
+ * meaning): q8 of input, Q/K/V projections (+ biases), the optional per-head
+ * QK RMS norm, RoPE at pos, K/V rows stored at kv_len of kv_k / kv_v
+ * [n_kv_heads][kv_max][head_dim], GQA softmax attention over the last
+ * `window` positions (0: all) with optional per-head sink logits, and the
+ * output projection into output (overwritten).  att_out, when not NULL,
+ * receives the per-head attention output [n_heads * head_dim] before the
+ * output projection.  scratch holds tg_hip_attention_scratch_bytes(...)
+ * bytes.  Shapes: embed_dim % 32 == 0, head_dim % 4 == 0 and <= 128,
+ * n_heads / n_kv_heads integral and <= 8, kv_len < kv_max <= 65536;
+ * kv_k and kv_v 16-byte aligned. */
+void tg_hip_attention_dev(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk,
+                          const void *wv, const void *wo, const float *bq, const float *bk, const float *bv,
+                          const float *bo, const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                          float *kv_k, float *kv_v, int kv_len, int kv_max, int window, const float *rope_cos,
+                          const float *rope_sin, const float *input, float *output, int embed_dim, int n_heads,
+                          int n_kv_heads, int head_dim, int pos, float eps, float *att_out, void *scratch,
+                          void *stream);
+size_t tg_hip_attention_scratch_bytes(int embed_dim, int n_heads, int n_kv_heads, int head_dim, int kv_max);
+
 /* Output head over k (1..16) device-resident rows with the argmax fused in:
  * x_j = RMSNorm(inputs_j) * norm_w (skipped when norm_w_dev is NULL),
  * logits[j][r] = dot(mat row r, q8(x_j)) and argmax_dev[j] = the first r

@@ -64,6 +64,8 @@ def lib():
         L.or_moe_forward_rows_v2.argtypes = [VP, VP, VP, CI, VP, VP, VP, VP, CI, CI, VP, VP, VP, CI, CI, CI]
         L.or_moe_forward_rows_v2_ex.argtypes = [VP, VP, VP, CI, VP, VP, VP, VP, CI, CI, VP, VP, VP, CI, CI, CI,
                                                 VP, VP]
+        L.or_attention_v2.argtypes = [CI, CI, CI, CI, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, CI, CI,
+                                      CI, VP, VP, VP, VP, CI, CI, CI, CI, CI, CF, VP]
         L.or_expert_forward.argtypes = [VP, VP, VP, CF, CI, CI]
         L.or_expert_forward_mixed.argtypes = [VP, VP, VP, CI, VP, VP, CF, CI, CI]
         _lib = L
@@ -164,6 +166,27 @@ def matmul_q4k_scalar(mat, x, nrows, ncols):
     mat = np.ascontiguousarray(mat, dtype=np.uint8)
     lib().or_matmul_q4k_scalar(mat.ctypes.data, x.ctypes.data, out.ctypes.data, nrows, ncols)
     return out
+
+
+def attention_v2(fmts, w, b, q_norm_w, k_norm_w, sinks, kv_k, kv_v, kv_len, kv_max, window, rope_cos, rope_sin,
+                 x, embed_dim, n_heads, n_kv_heads, head_dim, pos, eps):
+    """tg_attention_v2 for one row (csrc/libtinygiant.c:939-983).  fmts and w
+    hold (q, k, v, o); b the four biases or None; kv_k / kv_v are updated in
+    place.  Returns (output [embed_dim], attention output [n_heads*head_dim])."""
+    ws = [np.ascontiguousarray(m) for m in w]
+    bs = [None if v is None else np.ascontiguousarray(v, np.float32) for v in (b or (None,) * 4)]
+    opt = [None if v is None else np.ascontiguousarray(v, np.float32) for v in (q_norm_w, k_norm_w, sinks)]
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(embed_dim, np.float32)
+    att = np.zeros(n_heads * head_dim, np.float32)
+    rc = np.ascontiguousarray(rope_cos, np.float32)
+    rs = np.ascontiguousarray(rope_sin, np.float32)
+    assert kv_k.flags.c_contiguous and kv_v.flags.c_contiguous and kv_k.dtype == np.float32
+    lib().or_attention_v2(*fmts, *[m.ctypes.data for m in ws], *[_p(v) for v in bs], *[_p(v) for v in opt],
+                          kv_k.ctypes.data, kv_v.ctypes.data, kv_len, kv_max, window, rc.ctypes.data, rs.ctypes.data,
+                          x.ctypes.data, out.ctypes.data, embed_dim, n_heads, n_kv_heads, head_dim, pos, eps,
+                          att.ctypes.data)
+    return out, att
 
 
 def rms_norm(x, w, eps):

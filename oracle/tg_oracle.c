@@ -467,6 +467,118 @@ void or_rms_norm(const float *x, const float *weight, float *out, int dim, float
     for (i = 0; i < dim; i++) out[i] = (x[i] * scale) * weight[i];
 }
 
+/* Restates apply_rope_inplace (csrc/libtinygiant.c:702-719): NeoX halves,
+ * x1' = x1*c - x2*s (vmlsq: multiply, then subtract), x2' = x2*c + x1*s
+ * (vfmaq: fused).  Pinned by: pos 0 with cos 1 / sin 0 is the identity, the
+ * rotation of each (x1, x2) pair against complex multiplication in float64,
+ * and the norm of each pair kept (tests/test_oracle_pins.py). */
+static void rope_inplace(float *x, int n_heads, int head_dim, const float *cos_t, const float *sin_t, int pos) {
+    int half = head_dim / 2;
+    const float *c = cos_t + (size_t)pos * half, *s = sin_t + (size_t)pos * half;
+    for (int h = 0; h < n_heads; h++) {
+        float *xh = x + (size_t)h * head_dim;
+        for (int i = 0; i < half; i++) {
+            float x1 = xh[i], x2 = xh[half + i];
+            float p = x2 * s[i];
+            xh[i] = x1 * c[i] - p;
+            xh[half + i] = fmaf(x1, s[i], x2 * c[i]);
+        }
+    }
+}
+
+/* Restates head_task (csrc/libtinygiant.c:862-904) for one query head:
+ * scores over [start, seq_len) with the dot as four fused lane sums added
+ * pairwise (vaddvq) plus a scalar tail, max seeded with the sink logit (or
+ * -1e30), sum of exps seeded with exp(sink - max) (or 0), then
+ * out += (e_t / sum) * v_t (fused in 4-wide steps, plain in the tail).
+ * Pinned by: one position gives v exactly, identical keys give the mean of
+ * V, a window of 1 attends only the newest position, a huge sink drives the
+ * output to zero, and a float64 softmax attention on random inputs. */
+static void head_attend(const float *q_h, const float *k_cache, const float *v_cache, float *out_h, int start,
+                        int seq_len, int head_dim, float inv_sqrt, const float *sink) {
+    int n = seq_len - start;
+    float *sc = (float *)malloc(sizeof(float) * (size_t)(n > 0 ? n : 1));
+    float mx = sink ? *sink : -1e30f;
+    for (int t = start; t < seq_len; t++) {
+        const float *kt = k_cache + (size_t)t * head_dim;
+        float acc[4] = {0, 0, 0, 0};
+        int d = 0;
+        for (; d + 3 < head_dim; d += 4)
+            for (int l = 0; l < 4; l++) acc[l] = fmaf(q_h[d + l], kt[d + l], acc[l]);
+        float dot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+        for (; d < head_dim; d++) dot += q_h[d] * kt[d];
+        sc[t - start] = dot * inv_sqrt;
+        if (sc[t - start] > mx) mx = sc[t - start];
+    }
+    float sum = sink ? expf(*sink - mx) : 0.f;
+    for (int t = start; t < seq_len; t++) {
+        sc[t - start] = expf(sc[t - start] - mx);
+        sum += sc[t - start];
+    }
+    float inv = 1.f / sum;
+    memset(out_h, 0, (size_t)head_dim * sizeof(float));
+    for (int t = start; t < seq_len; t++) {
+        float w = sc[t - start] * inv;
+        const float *vt = v_cache + (size_t)t * head_dim;
+        int d = 0;
+        for (; d + 3 < head_dim; d += 4)
+            for (int l = 0; l < 4; l++) out_h[d + l] = fmaf(w, vt[d + l], out_h[d + l]);
+        for (; d < head_dim; d++) out_h[d] += w * vt[d];
+    }
+    free(sc);
+}
+
+/* Restates tg_attention_v2 (csrc/libtinygiant.c:939-983): q8 of the input,
+ * Q/K/V projections (dot + bias, F16 from the f32 input), the optional QK
+ * RMS norm per head (only when q_norm_w is given, k with k_norm_w), RoPE at
+ * pos, the K/V rows stored at kv_len of each KV head, GQA attention of every
+ * query head over [start, kv_len] with the optional sink and sliding window,
+ * and the output projection through tg_matmul (q8 of the attention output).
+ * The projections are or_matmul (pinned above); the rest is pinned as noted
+ * on rope_inplace and head_attend. */
+void or_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk, const void *wv,
+                     const void *wo, const float *bq, const float *bk, const float *bv, const float *bo,
+                     const float *q_norm_w, const float *k_norm_w, const float *sinks, float *kv_k, float *kv_v,
+                     int kv_len, int kv_max, int window, const float *rope_cos, const float *rope_sin,
+                     const float *input, float *output, int embed_dim, int n_heads, int n_kv_heads, int head_dim,
+                     int pos, float eps, float *att_out) {
+    int q_dim = n_heads * head_dim, kv_dim = n_kv_heads * head_dim, ratio = n_heads / n_kv_heads;
+    float *q = (float *)malloc(sizeof(float) * (size_t)q_dim);
+    float *k = (float *)malloc(sizeof(float) * (size_t)kv_dim);
+    float *v = (float *)malloc(sizeof(float) * (size_t)kv_dim);
+    float *att = (float *)malloc(sizeof(float) * (size_t)q_dim);
+    or_matmul(fmt_q, wq, bq, input, q, q_dim, embed_dim);
+    or_matmul(fmt_k, wk, bk, input, k, kv_dim, embed_dim);
+    or_matmul(fmt_v, wv, bv, input, v, kv_dim, embed_dim);
+    if (q_norm_w) {
+        for (int h = 0; h < n_heads; h++)
+            or_rms_norm(q + (size_t)h * head_dim, q_norm_w, q + (size_t)h * head_dim, head_dim, eps);
+        for (int h = 0; h < n_kv_heads; h++)
+            or_rms_norm(k + (size_t)h * head_dim, k_norm_w, k + (size_t)h * head_dim, head_dim, eps);
+    }
+    rope_inplace(q, n_heads, head_dim, rope_cos, rope_sin, pos);
+    rope_inplace(k, n_kv_heads, head_dim, rope_cos, rope_sin, pos);
+    for (int h = 0; h < n_kv_heads; h++) {
+        memcpy(kv_k + ((size_t)h * kv_max + kv_len) * head_dim, k + (size_t)h * head_dim, sizeof(float) * head_dim);
+        memcpy(kv_v + ((size_t)h * kv_max + kv_len) * head_dim, v + (size_t)h * head_dim, sizeof(float) * head_dim);
+    }
+    int seq_len = kv_len + 1;
+    int start = (window > 0 && seq_len > window) ? seq_len - window : 0;
+    float inv_sqrt = 1.f / sqrtf((float)head_dim);
+    for (int h = 0; h < n_heads; h++) {
+        int kh = h / ratio;
+        head_attend(q + (size_t)h * head_dim, kv_k + (size_t)kh * kv_max * head_dim,
+                    kv_v + (size_t)kh * kv_max * head_dim, att + (size_t)h * head_dim, start, seq_len, head_dim,
+                    inv_sqrt, sinks ? &sinks[h] : NULL);
+    }
+    if (att_out) memcpy(att_out, att, sizeof(float) * (size_t)q_dim);
+    or_matmul(fmt_o, wo, bo, att, output, embed_dim, q_dim);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+}
+
 /* act_fn (csrc/libtinygiant.c:1250-1257) */
 static float act_fn(int act, float g, float u) {
     if (act == OR_ACT_GPTOSS) {

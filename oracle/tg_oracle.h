@@ -77,6 +77,18 @@ void     or_moe_forward_rows_v2_ex(const uint8_t *const *gate_ptrs, const uint8_
                                    const float *row_weights, const float *inputs, float *output,
                                    int k, int embed_dim, int inter_dim,
                                    const float *hidden_in, float *hidden_out);
+/* Decode attention for one row (tg_attention_v2).  att_out, when not NULL,
+ * receives the per-head attention output [n_heads * head_dim] before the
+ * output projection. */
+void     or_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o,
+                         const void *wq, const void *wk, const void *wv, const void *wo,
+                         const float *bq, const float *bk, const float *bv, const float *bo,
+                         const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                         float *kv_k, float *kv_v, int kv_len, int kv_max, int window,
+                         const float *rope_cos, const float *rope_sin,
+                         const float *input, float *output,
+                         int embed_dim, int n_heads, int n_kv_heads, int head_dim, int pos, float eps,
+                         float *att_out);
 void     or_expert_forward(const uint8_t *q4_data, const float *input, float *output,
                            float weight, int embed_dim, int inter_dim);
 void     or_expert_forward_mixed(const uint8_t *gate, const uint8_t *up, const void *down,

@@ -370,3 +370,136 @@ def test_route_oracle_selection_and_softmax(orc):
     router = np.ones((8, 4), np.float32)
     _, idx, w = orc.route(router, None, np.ones(4, np.float32), 4)
     assert np.allclose(w, 0.25)
+
+
+# ---- decode attention (tg_attention_v2, csrc/libtinygiant.c:939-983) ----
+
+def _attn_case(seed, D=256, nh=8, nkv=2, hd=32, kv_max=40, kv_len=17, zero_q=False, bias=True, norms=True):
+    """F16 projections (exact f32 dots), random cache rows below kv_len, RoPE
+    tables of a 10000-base NeoX rotation."""
+    rng = np.random.default_rng(seed)
+    qd, kd = nh * hd, nkv * hd
+
+    def f16(rows, cols, scale=0.1):
+        return (rng.standard_normal((rows, cols)) * scale).astype(np.float16).view(np.uint8).reshape(-1)
+
+    w = [np.zeros(qd * D * 2, np.uint8) if zero_q else f16(qd, D), f16(kd, D), f16(kd, D), f16(D, qd)]
+    b = [rng.standard_normal(n).astype(np.float32) * 0.1 for n in (qd, kd, kd, D)] if bias else None
+    if zero_q and b is not None:
+        b[0] = np.zeros(qd, np.float32)
+    qn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norms else None
+    kn = rng.uniform(0.5, 1.5, hd).astype(np.float32) if norms else None
+    half = hd // 2
+    ang = np.arange(kv_max)[:, None] / (10000.0 ** (np.arange(half)[None, :] * 2.0 / hd))
+    rc, rs = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    kv_k = np.zeros((nkv, kv_max, hd), np.float32)
+    kv_v = np.zeros((nkv, kv_max, hd), np.float32)
+    kv_k[:, :kv_len] = rng.standard_normal((nkv, kv_len, hd))
+    kv_v[:, :kv_len] = rng.standard_normal((nkv, kv_len, hd))
+    x = rng.standard_normal(D).astype(np.float32)
+    return dict(w=w, b=b, qn=qn, kn=kn, rc=rc, rs=rs, kv_k=kv_k, kv_v=kv_v, x=x, D=D, nh=nh, nkv=nkv, hd=hd,
+                kv_max=kv_max, kv_len=kv_len)
+
+
+def _attn_run(orc, c, window=0, sinks=None, rc=None, rs=None):
+    F16 = O.FMT_F16
+    return orc.attention_v2((F16,) * 4, c["w"], c["b"], c["qn"], c["kn"], sinks, c["kv_k"], c["kv_v"], c["kv_len"],
+                            c["kv_max"], window, c["rc"] if rc is None else rc, c["rs"] if rs is None else rs, c["x"],
+                            c["D"], c["nh"], c["nkv"], c["hd"], c["kv_len"], 1e-6)
+
+
+def _proj64(c, i, rows):
+    m = c["w"][i].view(np.float16).astype(np.float64).reshape(rows, -1)
+    inp = c["x"].astype(np.float64)
+    y = m @ inp
+    return y + (c["b"][i] if c["b"] is not None else 0.0)
+
+
+def test_attention_one_position_returns_v(orc):
+    """kv_len 0: the softmax over one position is 1, so each head's output is
+    its KV head's new V row, exactly."""
+    c = _attn_case(1, kv_len=0)
+    _, att = _attn_run(orc, c)
+    ratio = c["nh"] // c["nkv"]
+    for h in range(c["nh"]):
+        assert np.array_equal(att[h * c["hd"]:(h + 1) * c["hd"]], c["kv_v"][h // ratio, 0])
+
+
+def test_attention_zero_query_is_mean_of_v(orc):
+    """Zero Q weights and bias: every score is 0, the softmax is uniform and
+    each head's output is the mean of its KV head's V rows in the window."""
+    for window in (0, 6):
+        c = _attn_case(2, zero_q=True)
+        _, att = _attn_run(orc, c, window=window)
+        seq = c["kv_len"] + 1
+        start = seq - window if window and seq > window else 0
+        ratio = c["nh"] // c["nkv"]
+        for h in range(c["nh"]):
+            want = c["kv_v"][h // ratio, start:seq].astype(np.float64).mean(axis=0)
+            assert np.abs(att[h * c["hd"]:(h + 1) * c["hd"]] - want).max() < 1e-5
+
+
+def test_attention_window_one_and_huge_sink(orc):
+    """A window of 1 attends only the new row (output = new V exactly); a sink
+    logit far above every score takes all the weight (output 0)."""
+    c = _attn_case(3)
+    _, att = _attn_run(orc, c, window=1)
+    ratio = c["nh"] // c["nkv"]
+    for h in range(c["nh"]):
+        assert np.array_equal(att[h * c["hd"]:(h + 1) * c["hd"]], c["kv_v"][h // ratio, c["kv_len"]])
+    c = _attn_case(3)
+    _, att = _attn_run(orc, c, sinks=np.full(c["nh"], 1e4, np.float32))
+    assert np.abs(att).max() == 0.0
+
+
+def test_attention_unit_rope_stores_normed_k(orc):
+    """cos 1 / sin 0 tables make RoPE the identity: the stored K row is the
+    QK-normed projection (float64 within 1e-5)."""
+    c = _attn_case(4)
+    ones = np.ones_like(c["rc"])
+    zeros = np.zeros_like(c["rs"])
+    _attn_run(orc, c, rc=ones, rs=zeros)
+    k = _proj64(c, 1, c["nkv"] * c["hd"]).reshape(c["nkv"], c["hd"])
+    k = k / np.sqrt((k * k).mean(axis=1, keepdims=True) + 1e-6) * c["kn"].astype(np.float64)
+    assert np.abs(c["kv_k"][:, c["kv_len"]] - k).max() < 1e-5 * np.abs(k).max()
+    v = _proj64(c, 2, c["nkv"] * c["hd"]).reshape(c["nkv"], c["hd"])
+    assert np.abs(c["kv_v"][:, c["kv_len"]] - v).max() < 1e-5 * np.abs(v).max()
+
+
+@pytest.mark.parametrize("window,sink", [(0, False), (9, True)])
+def test_attention_vs_float64(orc, window, sink):
+    """The whole step against a float64 restatement: projections, QK norm,
+    RoPE as complex rotation, GQA head mapping, window, sinks, output
+    projection of the attention output."""
+    c = _attn_case(5 + window)
+    nh, nkv, hd, L = c["nh"], c["nkv"], c["hd"], c["kv_len"]
+    sinks = np.random.default_rng(7).standard_normal(nh).astype(np.float32) if sink else None
+    cache_k, cache_v = c["kv_k"].astype(np.float64), c["kv_v"].astype(np.float64)
+    out, att = _attn_run(orc, c, window=window, sinks=sinks)
+    q = _proj64(c, 0, nh * hd).reshape(nh, hd)
+    k = _proj64(c, 1, nkv * hd).reshape(nkv, hd)
+    v = _proj64(c, 2, nkv * hd).reshape(nkv, hd)
+    q = q / np.sqrt((q * q).mean(axis=1, keepdims=True) + 1e-6) * c["qn"]
+    k = k / np.sqrt((k * k).mean(axis=1, keepdims=True) + 1e-6) * c["kn"]
+    half = hd // 2
+    rot = c["rc"][L].astype(np.float64) + 1j * c["rs"][L].astype(np.float64)
+
+    def rope(a):
+        z = (a[:, :half] + 1j * a[:, half:]) * rot
+        return np.concatenate([z.real, z.imag], axis=1)
+
+    q, k = rope(q), rope(k)
+    cache_k[:, L], cache_v[:, L] = k, v
+    seq = L + 1
+    start = seq - window if window and seq > window else 0
+    att64 = np.zeros((nh, hd))
+    for h in range(nh):
+        s = cache_k[h // (nh // nkv), start:seq] @ q[h] / np.sqrt(hd)
+        logits = np.concatenate([s, [sinks[h]]]) if sink else s
+        p = np.exp(logits - logits.max())
+        p = p / p.sum()
+        att64[h] = p[:len(s)] @ cache_v[h // (nh // nkv), start:seq]
+    assert np.abs(att - att64.reshape(-1)).max() < 1e-5 * np.abs(att64).max()
+    assert np.abs(c["kv_k"][:, L] - k).max() < 1e-5 * np.abs(k).max()
+    o = c["w"][3].view(np.float16).astype(np.float64).reshape(c["D"], -1) @ att.astype(np.float64) + c["b"][3]
+    assert np.abs(out - o).max() < 1e-5 * np.abs(o).max()

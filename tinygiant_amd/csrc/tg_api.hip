@@ -31,6 +31,7 @@
 
 #include "tg_decode.h"
 #include "tg_head.h"
+#include "tg_attn.h"
 #include "tg_route.h"
 #include "tg_kernels.h"
 #include "tg_synth.h"
@@ -919,6 +920,177 @@ TG_API void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_de
 }
 
 TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k, ncols); }
+
+/* ---- decode attention (tg_attention_v2, csrc/libtinygiant.c:939-983) ----
+ * Scratch: q8 of the input | Q, K, V projections | roped Q | chunk partials |
+ * attention output | its q8. */
+struct AttnLayout {
+    size_t xq, qkv, q, part, att, aq, total;
+};
+
+static AttnLayout attn_layout(int embed_dim, int n_heads, int n_kv, int head_dim, int kv_max) {
+    AttnLayout L;
+    Bump b;
+    const size_t q_dim = (size_t)n_heads * head_dim, kv_dim = (size_t)n_kv * head_dim;
+    const size_t nch = ((size_t)kv_max + ATTN_CHUNK - 1) / ATTN_CHUNK;
+    L.xq = b.take(q8_bytes(1, embed_dim));
+    L.qkv = b.take((q_dim + 2 * kv_dim) * 4);
+    L.q = b.take(q_dim * 4);
+    L.part = b.take((size_t)n_heads * nch * (head_dim + 2) * 4);
+    L.att = b.take(q_dim * 4);
+    L.aq = b.take(q8_bytes(1, (int)q_dim));
+    L.total = b.off;
+    return L;
+}
+
+static bool attn_validate(const char *who, int fmt_q, int fmt_k, int fmt_v, int fmt_o, const float *q_norm_w,
+                          const float *k_norm_w, int kv_len, int kv_max, int window, int embed_dim, int n_heads,
+                          int n_kv, int head_dim, int pos) {
+    if (!fmt_ok(fmt_q) || !fmt_ok(fmt_k) || !fmt_ok(fmt_v) || !fmt_ok(fmt_o)) {
+        set_err("%s: unsupported weight format", who);
+        return false;
+    }
+    if (embed_dim <= 0 || embed_dim % 32 || n_heads <= 0 || n_kv <= 0 || n_heads % n_kv ||
+        n_heads / n_kv > ATTN_MAX_GQA || head_dim <= 0 || head_dim % 4 || head_dim > ATTN_MAX_HEAD_DIM ||
+        (n_heads * head_dim) % 32) {
+        set_err("%s: unsupported shape (embed_dim %% 32 == 0, head_dim %% 4 == 0 and <= %d, n_heads / n_kv_heads "
+                "integral and <= %d)", who, ATTN_MAX_HEAD_DIM, ATTN_MAX_GQA);
+        return false;
+    }
+    if (kv_len < 0 || kv_len >= kv_max || kv_max > ATTN_CHUNK * ATTN_MAX_CHUNKS || window < 0 || pos < 0) {
+        set_err("%s: need 0 <= kv_len < kv_max <= %d, window >= 0, pos >= 0", who, ATTN_CHUNK * ATTN_MAX_CHUNKS);
+        return false;
+    }
+    if (q_norm_w && !k_norm_w) {
+        set_err("%s: q_norm_w without k_norm_w (the reference dereferences it)", who);
+        return false;
+    }
+    return true;
+}
+
+/* every pointer on the device; rope rows are the tables at pos */
+static void attn_run(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk, const void *wv,
+                     const void *wo, const float *bq, const float *bk, const float *bv, const float *bo,
+                     const float *q_norm_w, const float *k_norm_w, const float *sinks, float *kv_k, float *kv_v,
+                     int kv_len, int kv_max, int window, const float *rope_cos_row, const float *rope_sin_row,
+                     const float *input, float *output, int embed_dim, int n_heads, int n_kv, int head_dim, float eps,
+                     float *att_out, uint8_t *scratch, hipStream_t st) {
+    const AttnLayout L = attn_layout(embed_dim, n_heads, n_kv, head_dim, kv_max);
+    const int q_dim = n_heads * head_dim, kv_dim = n_kv * head_dim;
+    float *qkv = (float *)(scratch + L.qkv);
+    Q8Rows xq = q8_view(scratch + L.xq, 1, embed_dim, input);
+    if (fmt_q != TG_FMT_F16 || fmt_k != TG_FMT_F16 || fmt_v != TG_FMT_F16)
+        launch_quantize(input, embed_dim, 1, embed_dim, xq, st);
+    launch_gemv(fmt_q, (const uint8_t *)wq, q_dim, embed_dim, bq, xq, 1, qkv, q_dim, st);
+    launch_gemv(fmt_k, (const uint8_t *)wk, kv_dim, embed_dim, bk, xq, 1, qkv + q_dim, kv_dim, st);
+    launch_gemv(fmt_v, (const uint8_t *)wv, kv_dim, embed_dim, bv, xq, 1, qkv + q_dim + kv_dim, kv_dim, st);
+    float *att = (float *)(scratch + L.att);
+    launch_attention_core(qkv, q_norm_w, k_norm_w, sinks, kv_k, kv_v, kv_len, kv_max, window, rope_cos_row,
+                          rope_sin_row, n_heads, n_kv, head_dim, eps, (float *)(scratch + L.q),
+                          (float *)(scratch + L.part), att, st);
+    Q8Rows aq = q8_view(scratch + L.aq, 1, q_dim, att);
+    if (fmt_o != TG_FMT_F16) launch_quantize(att, q_dim, 1, q_dim, aq, st);
+    launch_gemv(fmt_o, (const uint8_t *)wo, embed_dim, q_dim, bo, aq, 1, output, embed_dim, st);
+    if (att_out) HIPCHECK(hipMemcpyAsync(att_out, att, (size_t)q_dim * 4, hipMemcpyDeviceToDevice, st));
+}
+
+TG_API size_t tg_hip_attention_scratch_bytes(int embed_dim, int n_heads, int n_kv_heads, int head_dim, int kv_max) {
+    if (embed_dim <= 0 || n_heads <= 0 || n_kv_heads <= 0 || head_dim <= 0 || kv_max <= 0) return 0;
+    return attn_layout(embed_dim, n_heads, n_kv_heads, head_dim, kv_max).total;
+}
+
+TG_API void tg_hip_attention_dev(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk,
+                                 const void *wv, const void *wo, const float *bq, const float *bk, const float *bv,
+                                 const float *bo, const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                                 float *kv_k, float *kv_v, int kv_len, int kv_max, int window, const float *rope_cos,
+                                 const float *rope_sin, const float *input, float *output, int embed_dim, int n_heads,
+                                 int n_kv_heads, int head_dim, int pos, float eps, float *att_out, void *scratch,
+                                 void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!attn_validate("tg_hip_attention_dev", fmt_q, fmt_k, fmt_v, fmt_o, q_norm_w, k_norm_w, kv_len, kv_max, window,
+                       embed_dim, n_heads, n_kv_heads, head_dim, pos))
+        return;
+    if (!wq || !wk || !wv || !wo || !kv_k || !kv_v || !rope_cos || !rope_sin || !input || !output || !scratch) {
+        set_err("tg_hip_attention_dev: null weight, cache, table, input, output or scratch pointer");
+        return;
+    }
+    if (((uintptr_t)kv_k | (uintptr_t)kv_v) & 15) {
+        set_err("tg_hip_attention_dev: kv_k and kv_v must be 16-byte aligned");
+        return;
+    }
+    ensure_init();
+    const size_t half = (size_t)head_dim / 2;
+    attn_run(fmt_q, fmt_k, fmt_v, fmt_o, wq, wk, wv, wo, bq, bk, bv, bo, q_norm_w, k_norm_w, sinks, kv_k, kv_v, kv_len,
+             kv_max, window, rope_cos + (size_t)pos * half, rope_sin + (size_t)pos * half, input, output, embed_dim,
+             n_heads, n_kv_heads, head_dim, eps, att_out, (uint8_t *)scratch, stream ? (hipStream_t)stream : g.st);
+    HIPCHECK(hipGetLastError());
+}
+
+/* tg_attention_v2 with the reference's host pointers (csrc/libtinygiant.c:939-983).
+ * Registered ranges (tg_mlock) are used in place: weights, and the KV arrays,
+ * whose device copy the kernels update; everything else is staged for the
+ * call.  The new K and V rows are also written into the host arrays at kv_len
+ * and output is overwritten, as the reference does. */
+TG_API void tg_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk,
+                            const void *wv, const void *wo, const float *bq, const float *bk, const float *bv,
+                            const float *bo, const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                            float *kv_k, float *kv_v, int kv_len, int kv_max, int window, const float *rope_cos,
+                            const float *rope_sin, const float *input, float *output, int embed_dim, int n_heads,
+                            int n_kv_heads, int head_dim, int pos, float eps) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!attn_validate("tg_attention_v2", fmt_q, fmt_k, fmt_v, fmt_o, q_norm_w, k_norm_w, kv_len, kv_max, window,
+                       embed_dim, n_heads, n_kv_heads, head_dim, pos))
+        return;
+    ensure_init();
+    const int q_dim = n_heads * head_dim, kv_dim = n_kv_heads * head_dim;
+    const size_t half = (size_t)head_dim / 2;
+    const AttnLayout AL = attn_layout(embed_dim, n_heads, n_kv_heads, head_dim, kv_max);
+    Bump bump;
+    bump.off = AL.total;
+    const size_t io_in = bump.take((size_t)embed_dim * 4), io_out = bump.take((size_t)embed_dim * 4);
+    Stager sg;
+    sg.bump = &bump;
+    struct Ptr {
+        uintptr_t v;
+        bool staged;
+    };
+    auto res = [&](const void *p, size_t n) -> Ptr {
+        Ptr r{0, false};
+        if (p) r.v = sg.resolve(p, n, &r.staged);
+        return r;
+    };
+    const size_t cache_bytes = (size_t)n_kv_heads * kv_max * head_dim * 4;
+    Ptr pq = res(wq, (size_t)q_dim * row_bytes(fmt_q, embed_dim)), pk = res(wk, (size_t)kv_dim * row_bytes(fmt_k, embed_dim));
+    Ptr pv = res(wv, (size_t)kv_dim * row_bytes(fmt_v, embed_dim)), po = res(wo, (size_t)embed_dim * row_bytes(fmt_o, q_dim));
+    Ptr pbq = res(bq, (size_t)q_dim * 4), pbk = res(bk, (size_t)kv_dim * 4), pbv = res(bv, (size_t)kv_dim * 4);
+    Ptr pbo = res(bo, (size_t)embed_dim * 4);
+    Ptr pqn = res(q_norm_w, (size_t)head_dim * 4), pkn = res(k_norm_w, (size_t)head_dim * 4);
+    Ptr psk = res(sinks, (size_t)n_heads * 4);
+    Ptr pkk = res(kv_k, cache_bytes), pkv = res(kv_v, cache_bytes);
+    Ptr prc = res(rope_cos + (size_t)pos * half, half * 4), prs = res(rope_sin + (size_t)pos * half, half * 4);
+    uint8_t *dev = arena(bump.off);
+    auto dp = [&](const Ptr &p) -> void * {
+        if (!p.v && !p.staged) return nullptr;
+        return p.staged ? (void *)(dev + p.v) : (void *)p.v;
+    };
+    for (auto &it : sg.items) HIPCHECK(hipMemcpyAsync(dev + it.off, it.host, it.n, hipMemcpyHostToDevice, g.st));
+    HIPCHECK(hipMemcpyAsync(dev + io_in, input, (size_t)embed_dim * 4, hipMemcpyHostToDevice, g.st));
+    float *dkk = (float *)dp(pkk), *dkv = (float *)dp(pkv);
+    attn_run(fmt_q, fmt_k, fmt_v, fmt_o, dp(pq), dp(pk), dp(pv), dp(po), (const float *)dp(pbq), (const float *)dp(pbk),
+             (const float *)dp(pbv), (const float *)dp(pbo), (const float *)dp(pqn), (const float *)dp(pkn),
+             (const float *)dp(psk), dkk, dkv, kv_len, kv_max, window, (const float *)dp(prc), (const float *)dp(prs),
+             (const float *)(dev + io_in), (float *)(dev + io_out), embed_dim, n_heads, n_kv_heads, head_dim, eps,
+             nullptr, dev, g.st);
+    HIPCHECK(hipGetLastError());
+    /* the new rows back into the host arrays, the output */
+    for (int h = 0; h < n_kv_heads; h++) {
+        const size_t off = ((size_t)h * kv_max + kv_len) * head_dim;
+        HIPCHECK(hipMemcpyAsync(kv_k + off, dkk + off, (size_t)head_dim * 4, hipMemcpyDeviceToHost, g.st));
+        HIPCHECK(hipMemcpyAsync(kv_v + off, dkv + off, (size_t)head_dim * 4, hipMemcpyDeviceToHost, g.st));
+    }
+    HIPCHECK(hipMemcpyAsync(output, dev + io_out, (size_t)embed_dim * 4, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+}
 
 /* ---- router ---- */
 TG_API size_t tg_hip_route_scratch_bytes(int k, int n_experts) { return (size_t)k * n_experts * 4; }

@@ -1,0 +1,24 @@
+/*
+ * tg_attn.h -- device decode attention (internal launch interface).
+ */
+#ifndef TG_ATTN_H
+#define TG_ATTN_H
+#include <hip/hip_runtime.h>
+
+#define ATTN_CHUNK 32          /* sequence positions per workgroup */
+#define ATTN_MAX_HEAD_DIM 128  /* head_dim: even, multiple of 4, at most this */
+#define ATTN_MAX_GQA 8         /* query heads per KV head, at most this */
+#define ATTN_MAX_CHUNKS 2048   /* kv_max <= ATTN_CHUNK * ATTN_MAX_CHUNKS */
+
+namespace tg {
+
+/* qkv: [q_dim | kv_dim | kv_dim] projection outputs; rope rows are the
+ * cos/sin tables at pos; q_scratch [q_dim]; part
+ * [n_heads][ceil(span / ATTN_CHUNK)][head_dim + 2]; att [q_dim] */
+void launch_attention_core(const float *qkv, const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                           float *kv_k, float *kv_v, int kv_len, int kv_max, int window, const float *rope_cos_row,
+                           const float *rope_sin_row, int n_heads, int n_kv, int head_dim, float eps, float *q_scratch,
+                           float *part, float *att, hipStream_t st);
+
+}  // namespace tg
+#endif

@@ -5,10 +5,10 @@
  *
  * They exist so that tinygiant/_lib.py (which binds every symbol at load
  * time) and tinygiant/engine.py run unchanged against libtinygiant_hip.
- * Quantized projections inside attention go through tg_matmul, i.e. the
- * GPU GEMV; the remaining small f32 arithmetic (norms, RoPE, softmax over the
- * KV cache) runs here on the host, single-threaded.  Semantics follow
- * csrc/libtinygiant.c line for line where cited.
+ * tg_attention_v2 runs on the GPU (tg_api.hip, tg_attn.hip); the f32-weight
+ * attention entry point here keeps its small arithmetic on the host,
+ * single-threaded, and tg_attention_decode_q4 forwards to tg_attention_v2.
+ * Semantics follow csrc/libtinygiant.c line for line where cited.
  */
 #include <math.h>
 #include <stddef.h>
@@ -22,6 +22,13 @@
 
 extern "C" void tg_matmul(int fmt, const void *mat, const float *bias, const float *input, float *output,
                           int nrows, int ncols);
+/* on the GPU (tg_api.hip) */
+extern "C" void tg_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk,
+                                const void *wv, const void *wo, const float *bq, const float *bk, const float *bv,
+                                const float *bo, const float *q_norm_w, const float *k_norm_w, const float *sinks,
+                                float *kv_k, float *kv_v, int kv_len, int kv_max, int window, const float *rope_cos,
+                                const float *rope_sin, const float *input, float *output, int embed_dim, int n_heads,
+                                int n_kv_heads, int head_dim, int pos, float eps);
 extern "C" void tg_expert_forward_mixed(const uint8_t *gate_q4, const uint8_t *up_q4, const void *down_data,
                                         int down_format, const float *input, float *output, float weight,
                                         int embed_dim, int inter_dim);
@@ -146,40 +153,6 @@ TG_API void tg_attention_decode(const float *wq, const float *wk, const float *w
                &att[(size_t)h * head_dim], 0, kv_len + 1, head_dim, inv_sqrt, nullptr);
     }
     tg_f32_matvec(wo, att.data(), output, embed_dim, q_dim);
-}
-
-/* tg_attention_v2 (csrc/libtinygiant.c:939-983): any weight format, biases,
- * optional QK norm, sinks and sliding window; projections on the GPU. */
-TG_API void tg_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq, const void *wk,
-                            const void *wv, const void *wo, const float *bq, const float *bk, const float *bv,
-                            const float *bo, const float *q_norm_w, const float *k_norm_w, const float *sinks,
-                            float *kv_k, float *kv_v, int kv_len, int kv_max, int window, const float *rope_cos,
-                            const float *rope_sin, const float *input, float *output, int embed_dim, int n_heads,
-                            int n_kv_heads, int head_dim, int pos, float eps) {
-    int q_dim = n_heads * head_dim, kv_dim = n_kv_heads * head_dim, ratio = n_heads / n_kv_heads;
-    std::vector<float> q(q_dim), k(kv_dim), v(kv_dim), att(q_dim);
-    tg_matmul(fmt_q, wq, bq, input, q.data(), q_dim, embed_dim);
-    tg_matmul(fmt_k, wk, bk, input, k.data(), kv_dim, embed_dim);
-    tg_matmul(fmt_v, wv, bv, input, v.data(), kv_dim, embed_dim);
-    if (q_norm_w) {
-        for (int h = 0; h < n_heads; h++) tg_rms_norm(&q[(size_t)h * head_dim], q_norm_w, &q[(size_t)h * head_dim], head_dim, eps);
-        for (int h = 0; h < n_kv_heads; h++) tg_rms_norm(&k[(size_t)h * head_dim], k_norm_w, &k[(size_t)h * head_dim], head_dim, eps);
-    }
-    rope(q.data(), n_heads, head_dim, rope_cos, rope_sin, pos);
-    rope(k.data(), n_kv_heads, head_dim, rope_cos, rope_sin, pos);
-    for (int h = 0; h < n_kv_heads; h++) {
-        memcpy(kv_k + ((size_t)h * kv_max + kv_len) * head_dim, &k[(size_t)h * head_dim], head_dim * 4);
-        memcpy(kv_v + ((size_t)h * kv_max + kv_len) * head_dim, &v[(size_t)h * head_dim], head_dim * 4);
-    }
-    int seq_len = kv_len + 1;
-    int start = (window > 0 && seq_len > window) ? seq_len - window : 0;
-    float inv_sqrt = 1.f / sqrtf((float)head_dim);
-    for (int h = 0; h < n_heads; h++) {
-        int kh = h / ratio;
-        attend(&q[(size_t)h * head_dim], kv_k + (size_t)kh * kv_max * head_dim, kv_v + (size_t)kh * kv_max * head_dim,
-               &att[(size_t)h * head_dim], start, seq_len, head_dim, inv_sqrt, sinks ? &sinks[h] : nullptr);
-    }
-    tg_matmul(fmt_o, wo, bo, att.data(), output, embed_dim, q_dim);
 }
 
 /* tg_attention_decode_q4 (csrc/libtinygiant.c:985-1036): Q4_K q/k/o, f16 v */
