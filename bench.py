@@ -488,6 +488,50 @@ def attention_probe(tg, kv_lens=(512, 4096), iters=20):
     return out
 
 
+def loader_probe(tg, n_layers=2):
+    """The on-disk expert cache into HBM (tinygiant_amd/loader.py): writes
+    n_layers Qwen3-30B-A3B layer files in the reference's cache format (128
+    experts of q4_K gate/up and q6_K down, 391.6 MB per layer) to a temporary
+    directory and times HBMExpertCache over them.  The files were just
+    written, so the read comes from the page cache: the figure is the
+    host-to-HBM side of a load (pread into pinned buffers overlapped with the
+    copies), not the speed of a cold disk."""
+    import shutil
+    import tempfile
+    from tinygiant_amd.loader import HBMExpertCache
+    gb, db = GATE_B, DOWN_B
+    per = EXPERT_B
+    d = tempfile.mkdtemp(prefix="tg_cache_")
+    try:
+        rng = np.random.default_rng(SEED + 77)
+        index = {"n_layers": n_layers, "n_experts": E, "embed_dim": D, "layers": {}}
+        for layer in range(n_layers):
+            name = f"layer_{layer:03d}.q4.bin"
+            with open(os.path.join(d, name), "wb") as f:
+                for _ in range(E):
+                    f.write(rng.bytes(per))
+            index["layers"][str(layer)] = {
+                "file": name, "total_bytes": E * per,
+                "tensor_formats": {"gate": "q4_k", "up": "q4_k", "down": "q6_k"},
+                "expert_offsets": {str(e): {"offset": e * per, "sizes": {"gate": gb, "up": gb, "down": db}}
+                                   for e in range(E)}}
+        with open(os.path.join(d, "index.json"), "w") as f:
+            json.dump(index, f)
+        out = {}
+        HBMExpertCache(d, layers=[0], chunk_mb=256).close()     # pinned buffers allocated once
+        for chunk_mb in (32, 64, 128, 256):
+            t0 = time.perf_counter()
+            c = HBMExpertCache(d, chunk_mb=chunk_mb)
+            s = time.perf_counter() - t0
+            out[f"chunk_{chunk_mb}mb"] = {"bytes": c.bytes_loaded, "seconds": round(s, 4),
+                                          "gbps": round(c.bytes_loaded / s / 1e9, 2)}
+            c.close()
+        out["source"] = "page cache (files just written)"
+        return out
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def read_traffic(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
     PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
@@ -511,6 +555,7 @@ def main():
     ap.add_argument("--no-boundary", action="store_true", help="skip the ctypes-entry latency probe")
     ap.add_argument("--no-head", action="store_true", help="skip the q6_K output head + argmax probe")
     ap.add_argument("--no-verify", action="store_true", help="skip the k-row verify-batch layer probe")
+    ap.add_argument("--no-loader", action="store_true", help="skip the expert-cache -> HBM load probe")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the other workloads (q4_K matvec, gpt-oss decode and prefill)")
     ap.add_argument("--mode", choices=["persistent", "persistent-plain", "graph", "eager"], default="persistent",
@@ -645,6 +690,9 @@ def main():
         log("output head probe ...")
         result["head_argmax"] = head_probe(tg)
         result["attention_layer"] = attention_probe(tg)
+    if not args.no_loader:
+        log("expert cache load probe ...")
+        result["cache_load"] = loader_probe(tg)
     if not args.no_configs:
         log("other workloads ...")
         result["other_workloads"] = configs_probe(tg)

@@ -188,6 +188,17 @@ void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const floa
                       void *scratch_dev, void *stream);
 size_t tg_hip_route_scratch_bytes(int k, int n_experts);
 
+/* Copies nbytes of the file at path, from file_offset on, into device
+ * memory at dev_dst: pread into two pinned staging buffers of chunk_bytes
+ * (at least 1 MiB) while the previous chunk's host-to-device copy runs.
+ * Returns the bytes copied, or -1 with tg_hip_last_error() set (missing
+ * file, short file, no pinned memory).  The native part of the expert-cache
+ * loader (tinygiant_amd/loader.py), which uploads the reference's on-disk
+ * expert cache (index.json + layer_NNN.q4.bin, tinygiant/relayout.py:147-162,
+ * 287-300, read by tinygiant/cache.py:29-54) whole into HBM. */
+int64_t tg_hip_upload_file(const char *path, uint64_t file_offset, uint64_t nbytes, void *dev_dst,
+                           uint64_t chunk_bytes);
+
 /* Decode attention for one row with every pointer on the device (replaces
  * tg_attention_v2, csrc/libtinygiant.c:939-983, with the same arguments and
  * meaning): q8 of input, Q/K/V projections (+ biases), the optional per-head

@@ -98,6 +98,8 @@ def register_extensions(lib):
     _reg(lib.tg_hip_attention_dev, [CI, CI, CI, CI, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, CI, CI, CI,
                                     VP, VP, VP, VP, CI, CI, CI, CI, CI, CF, VP, VP, VP])
     _reg(lib.tg_hip_attention_scratch_bytes, [CI, CI, CI, CI, CI], SZ)
+    _reg(lib.tg_hip_upload_file, [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_uint64, VP, ctypes.c_uint64],
+         ctypes.c_int64)
     _reg(lib.tg_hip_mark, [CI])
     _reg(lib.tg_hip_set_moe_grouped_min_rows, [CI], CI)
     _reg(lib.tg_hip_marks_ms, [CI, CI], CF)

@@ -23,10 +23,13 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
+#include <fcntl.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <map>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "tg_decode.h"
@@ -1090,6 +1093,102 @@ TG_API void tg_attention_v2(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const vo
     }
     HIPCHECK(hipMemcpyAsync(output, dev + io_out, (size_t)embed_dim * 4, hipMemcpyDeviceToHost, g.st));
     HIPCHECK(hipStreamSynchronize(g.st));
+}
+
+/* ---- file -> HBM upload (the expert-cache loader's native part) ----
+ * Two pinned staging buffers: while one is being copied to the device, the
+ * next chunk of the file is read into the other, by UP_THREADS threads each
+ * reading a contiguous share (one thread copying out of the page cache runs
+ * at about 9 GB/s, well under the host-to-device link). */
+static uint8_t *g_up_buf[2] = {nullptr, nullptr};
+static size_t g_up_cap = 0;
+static hipEvent_t g_up_ev[2];
+static const int UP_THREADS = 8;
+
+/* Reads n bytes at file offset off into dst; returns how many bytes were read
+ * before the first share that ended early (n when none did). */
+static uint64_t read_span(int fd, uint8_t *dst, uint64_t n, uint64_t off) {
+    const uint64_t min_share = 1u << 20;
+    int t = (int)std::min<uint64_t>(UP_THREADS, std::max<uint64_t>(1, n / min_share));
+    const uint64_t share = (n + t - 1) / t;
+    std::vector<uint64_t> got(t, 0);
+    auto work = [&](int i) {
+        const uint64_t b = (uint64_t)i * share, e = std::min(n, b + share);
+        uint64_t p = b;
+        while (p < e) {
+            const ssize_t r = pread(fd, dst + p, e - p, (off_t)(off + p));
+            if (r <= 0) break;
+            p += (uint64_t)r;
+        }
+        got[i] = p - b;
+    };
+    std::vector<std::thread> th;
+    for (int i = 1; i < t; i++) th.emplace_back(work, i);
+    work(0);
+    for (auto &x : th) x.join();
+    uint64_t done = 0;
+    for (int i = 0; i < t; i++) {
+        done += got[i];
+        if (got[i] < std::min(n, (uint64_t)(i + 1) * share) - (uint64_t)i * share) break;
+    }
+    return done;
+}
+
+TG_API int64_t tg_hip_upload_file(const char *path, uint64_t file_offset, uint64_t nbytes, void *dev_dst,
+                                  uint64_t chunk_bytes) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!path || !dev_dst) {
+        set_err("tg_hip_upload_file: null path or destination");
+        return -1;
+    }
+    ensure_init();
+    if (chunk_bytes < (1u << 20)) chunk_bytes = 1u << 20;
+    if (chunk_bytes > g_up_cap) {
+        for (int i = 0; i < 2; i++) {
+            if (g_up_buf[i]) {
+                HIPCHECK(hipEventSynchronize(g_up_ev[i]));
+                HIPCHECK(hipHostFree(g_up_buf[i]));
+            } else {
+                HIPCHECK(hipEventCreateWithFlags(&g_up_ev[i], hipEventDisableTiming));
+                HIPCHECK(hipEventRecord(g_up_ev[i], g.st));
+            }
+            if (hipHostMalloc((void **)&g_up_buf[i], chunk_bytes, hipHostMallocDefault) != hipSuccess) {
+                (void)hipGetLastError();
+                g_up_buf[i] = nullptr;
+                g_up_cap = 0;
+                set_err("tg_hip_upload_file: cannot allocate %llu bytes of pinned memory",
+                        (unsigned long long)chunk_bytes);
+                return -1;
+            }
+        }
+        g_up_cap = chunk_bytes;
+    }
+    const int fd = open(path, O_RDONLY);
+    if (fd < 0) {
+        set_err("tg_hip_upload_file: cannot open %s", path);
+        return -1;
+    }
+    uint64_t done = 0;
+    int slot = 0;
+    while (done < nbytes) {
+        const uint64_t n = std::min<uint64_t>(g_up_cap, nbytes - done);
+        HIPCHECK(hipEventSynchronize(g_up_ev[slot]));   /* the copy that last used this buffer */
+        const uint64_t got = read_span(fd, g_up_buf[slot], n, file_offset + done);
+        if (got < n) {
+            close(fd);
+            HIPCHECK(hipStreamSynchronize(g.st));
+            set_err("tg_hip_upload_file: %s ends at %llu, %llu bytes short", path,
+                    (unsigned long long)(file_offset + done + got), (unsigned long long)(nbytes - done - got));
+            return -1;
+        }
+        HIPCHECK(hipMemcpyAsync((uint8_t *)dev_dst + done, g_up_buf[slot], n, hipMemcpyHostToDevice, g.st));
+        HIPCHECK(hipEventRecord(g_up_ev[slot], g.st));
+        done += n;
+        slot ^= 1;
+    }
+    close(fd);
+    HIPCHECK(hipStreamSynchronize(g.st));
+    return (int64_t)done;
 }
 
 /* ---- router ---- */
