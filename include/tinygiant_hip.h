@@ -239,9 +239,14 @@ size_t tg_hip_head_scratch_bytes(int k, int nrows, int ncols);
  * state h_dev [k][embed_dim]: h <- h + MoE_l(RMSNorm_l(h)) for each layer
  * (tinygiant/engine.py:281-282,335-341).  norm_w_dev may be NULL (weight 1).
  * mode 0 queues the per-layer kernels, 1 replays them as one HIP graph,
- * 2 runs the whole step as one persistent cooperative kernel (k = 1,
- * D = 2048, I = 768, Q4_K gate/up, Q6_K down, SiLU, no biases, exactly 8
- * active experts per layer, <= 64 layers, 256 co-resident workgroups);
+ * 2 runs the whole step as one persistent cooperative kernel on 256
+ * co-resident workgroups, <= 64 layers of k = 1, for two expert shapes:
+ *   Qwen3-30B-A3B: D = 2048, I = 768, Q4_K gate/up, Q6_K down, SiLU, no
+ *     biases, exactly 8 active experts per layer;
+ *   gpt-oss-120b: D = I = 2880, MXFP4 gate/up/down, the clamped SwiGLU,
+ *     optional biases, exactly 4 active experts per layer (MXFP4 dots on
+ *     block-scaled MFMA: the reference's per-block integer sums, f32
+ *     additions grouped differently);
  * 3 launches the same kernel with a plain launch (for tools that do not
  * follow cooperative launches; needs an otherwise idle device, and a step
  * whose workgroups are not all resident ends with status 1). */
@@ -251,10 +256,13 @@ tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers,
                                     int mode);
 int tg_hip_decode_status(tg_hip_decode *step);   /* 1 if a persistent step's barrier timed out */
 /* Stage-wise parity probe of the persistent step: while set, each layer
- * writes a record of tg_hip_decode_debug_bytes() bytes (h in, RMSNorm x,
- * q8(x), hidden, q8(hidden)) into debug_dev[layer]. */
+ * writes a record of tg_hip_decode_record_bytes(step) bytes into
+ * debug_dev[layer]: for the Qwen3 kernel (tg_hip_decode_debug_bytes()) h in,
+ * RMSNorm x, q8(x), hidden, q8(hidden); for the gpt-oss kernel h in, x and
+ * each expert slot's hidden vector (f32). */
 void tg_hip_decode_set_debug(tg_hip_decode *step, void *debug_dev);
 size_t tg_hip_decode_debug_bytes(void);
+size_t tg_hip_decode_record_bytes(tg_hip_decode *step);
 /* Phase timing of the persistent step: while set, times_dev [256][L][24]
  * uint64 receives up to 24 words per layer of every workgroup (timestamps of
  * the 100 MHz device clock and exchange poll round counts). */
@@ -265,9 +273,10 @@ void tg_hip_decode_kernel_times(tg_hip_decode *step, float *ms_out /*[6]*/, int 
 void tg_hip_decode_destroy(tg_hip_decode *step);
 void tg_hip_device_name(char *buf, int n);
 /* MXFP4 expert layers whose busiest expert holds at least `rows` pairs run
- * their gate/up and down phases on int8 MFMA (each weight block read once per
- * 64 pairs; same per-block integer sums and f32 order as dot_mxfp4_q8,
- * csrc/libtinygiant.c:533-547); 0 keeps every layer on the per-pair kernels.
+ * their gate/up and down phases on block-scaled MFMA (each weight block read
+ * once per 64 pairs; the per-block integer sums of dot_mxfp4_q8,
+ * csrc/libtinygiant.c:533-547, with the f32 additions grouped differently);
+ * 0 keeps every layer on the per-pair kernels.
  * Default 4.  Returns the previous setting.  No counterpart in the
  * reference, which has one CPU kernel for every row count. */
 int tg_hip_set_moe_grouped_min_rows(int rows);

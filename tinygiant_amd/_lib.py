@@ -114,6 +114,7 @@ def register_extensions(lib):
     _reg(lib.tg_hip_decode_status, [VP], CI)
     _reg(lib.tg_hip_decode_set_debug, [VP, VP])
     _reg(lib.tg_hip_decode_debug_bytes, [], SZ)
+    _reg(lib.tg_hip_decode_record_bytes, [VP], SZ)
     _reg(lib.tg_hip_decode_set_timing, [VP, VP])
     _reg(lib.tg_hip_device_name, [ctypes.c_char_p, CI])
     _reg(lib.tg_hip_copy_time, [VP, VP, U64, CI], CF)

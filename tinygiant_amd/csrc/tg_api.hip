@@ -1223,8 +1223,9 @@ TG_API void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *in
                                    float eps, int k, int nrows, int ncols, float *logits_dev, int32_t *argmax_dev,
                                    float *maxval_dev, void *scratch_dev, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!fmt_ok(fmt) || ncols <= 0 || ncols % 32 || nrows <= 0 || k <= 0 || k > 16 || !argmax_dev || !scratch_dev) {
-        set_err("tg_hip_head_argmax_dev: bad format, shape or arguments (1 <= k <= 16)");
+    if (!fmt_ok(fmt) || ncols <= 0 || ncols % 32 || nrows <= 0 || k <= 0 || k > 16 || !argmax_dev || !scratch_dev ||
+        (norm_w_dev && !rms_norm_fits(ncols))) {
+        set_err("tg_hip_head_argmax_dev: bad format, shape or arguments (1 <= k <= 16, ncols <= 16384 with a norm)");
         return;
     }
     ensure_init();
@@ -1234,13 +1235,18 @@ TG_API void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *in
     unsigned long long *keys = (unsigned long long *)(sp + align256(q8_bytes(k, ncols)));
     float *normed = (float *)((uint8_t *)keys + align256(16 * 8));
     float *lg_scratch = (float *)((uint8_t *)normed + align256((size_t)k * ncols * 4));
-    const float *xin = inputs_dev;
-    if (norm_w_dev) {
-        launch_rms_norm(inputs_dev, norm_w_dev, normed, k, ncols, eps, st);
-        xin = normed;
-    }
+    const float *xin = norm_w_dev ? normed : inputs_dev;
     Q8Rows q = q8_view(q8p, k, ncols, xin);
-    if (fmt != TG_FMT_F16) launch_quantize(xin, ncols, k, ncols, q, st);
+    if (norm_w_dev) {
+        /* RMSNorm fused with q8 of the normed rows */
+        if (fmt != TG_FMT_F16) {
+            launch_rms_norm_q8(inputs_dev, norm_w_dev, normed, k, ncols, eps, q, st);
+        } else {
+            launch_rms_norm(inputs_dev, norm_w_dev, normed, k, ncols, eps, st);
+        }
+    } else if (fmt != TG_FMT_F16) {
+        launch_quantize(xin, ncols, k, ncols, q, st);
+    }
     if (head_fast_ok(fmt, ncols, k)) {
         launch_head_q6k((const uint8_t *)mat_dev, nrows, q, k, logits_dev, keys, st);
     } else {
@@ -1255,6 +1261,10 @@ TG_API void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *in
 TG_API void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n, float eps,
                                 void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!x_dev || !out_dev || nrows <= 0 || !rms_norm_fits(n)) {
+        set_err("tg_hip_rms_norm_dev: bad arguments (1 <= n <= 16384)");
+        return;
+    }
     ensure_init();
     launch_rms_norm(x_dev, w_dev, out_dev, nrows, n, eps, stream ? (hipStream_t)stream : g.st);
     HIPCHECK(hipGetLastError());
@@ -1275,8 +1285,11 @@ struct tg_hip_decode {
     float *x = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
-    /* persistent mode */
+    /* persistent mode: kind 0 the Qwen3 kernel (layers), 1 the gpt-oss
+     * kernel (layers_mx) */
+    int kind = 0;
     DecodeLayer *layers = nullptr;
+    DecodeLayerMx *layers_mx = nullptr;
     float *hidden = nullptr;
     unsigned *sync = nullptr;
     unsigned base = 0;
@@ -1285,7 +1298,46 @@ struct tg_hip_decode {
     uint64_t *times = nullptr;
 };
 
-/* the persistent kernel covers k = 1 steps of the Qwen expert shape */
+/* the gpt-oss kernel covers k = 1 steps of 4 MXFP4 experts of 2880 x 2880
+ * with the clamped SwiGLU (biases optional) */
+static bool persistent_mx_ok(tg_hip_decode *d, std::vector<DecodeLayerMx> &out) {
+    for (int l = 0; l < d->L; l++) {
+        const HostPlan &h = d->plans[l]->h;
+        if (h.k != 1 || h.D != DECODE_MX_D || h.I != DECODE_MX_D || h.gate_fmt != TG_FMT_MXFP4 ||
+            h.act != TG_ACT_GPTOSS) {
+            set_err("persistent decode: layer %d is not a 1-row gpt-oss MXFP4 step of %dx%d", l, DECODE_MX_D,
+                    DECODE_MX_D);
+            return false;
+        }
+        DecodeLayerMx ly;
+        memset(&ly, 0, sizeof ly);
+        for (int e = 0; e < h.n; e++) {
+            if (h.p_off[e + 1] == h.p_off[e]) continue;
+            if (ly.n >= DECODE_MX_E || h.down_fmt[e] != TG_FMT_MXFP4) {
+                set_err("persistent decode: layer %d needs %d active experts with MXFP4 down", l, DECODE_MX_E);
+                return false;
+            }
+            ly.gate[ly.n] = (const uint8_t *)(uintptr_t)h.gate[e];
+            ly.up[ly.n] = (const uint8_t *)(uintptr_t)h.up[e];
+            ly.down[ly.n] = (const uint8_t *)(uintptr_t)h.down[e];
+            ly.gb[ly.n] = h.has_gb ? (const float *)(uintptr_t)h.gbias[e] : nullptr;
+            ly.ub[ly.n] = h.has_ub ? (const float *)(uintptr_t)h.ubias[e] : nullptr;
+            ly.db[ly.n] = h.has_db ? (const float *)(uintptr_t)h.dbias[e] : nullptr;
+            ly.w[ly.n] = h.p_w[h.p_off[e]];
+            ly.n++;
+        }
+        if (ly.n != DECODE_MX_E) {
+            set_err("persistent decode: layer %d has %d active experts, the kernel runs exactly %d", l, ly.n,
+                    DECODE_MX_E);
+            return false;
+        }
+        ly.norm_w = d->norm_w.empty() ? nullptr : d->norm_w[l];
+        out.push_back(ly);
+    }
+    return true;
+}
+
+/* the Qwen3 kernel covers k = 1 steps of the Qwen expert shape */
 static bool persistent_ok(tg_hip_decode *d, std::vector<DecodeLayer> &out) {
     const DecodeShape sh = decode_qwen_shape();
     for (int l = 0; l < d->L; l++) {
@@ -1321,16 +1373,19 @@ static bool persistent_ok(tg_hip_decode *d, std::vector<DecodeLayer> &out) {
     return true;
 }
 
+/* Per layer: RMSNorm of h fused with q8 of the result (into the plan's q8
+ * rows), then the MoE kernels, which add into h.  A layer without pairs
+ * leaves h as it is. */
 static void decode_enqueue(tg_hip_decode *d, hipStream_t st) {
     for (int l = 0; l < d->L; l++) {
-        launch_rms_norm(d->h, d->norm_w.empty() ? nullptr : d->norm_w[l], d->x, d->k, d->D, d->eps, st);
         tg_hip_moe_plan *p = d->plans[l];
         if (p->h.P == 0) continue;
         MoeArgs a = p->a;
         a.xin = d->x;
         a.xq.f = d->x;
         a.out = d->h;
-        launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), st);
+        launch_rms_norm_q8(d->h, d->norm_w.empty() ? nullptr : d->norm_w[l], d->x, d->k, d->D, d->eps, a.xq, st);
+        launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), st, nullptr, false);
     }
 }
 
@@ -1346,6 +1401,11 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
     d->L = n_layers;
     d->D = plans[0]->h.D;
     d->k = plans[0]->h.k;
+    if (!rms_norm_fits(d->D)) {
+        set_err("tg_hip_decode_create: D = %d is above the RMSNorm kernel's 16384", d->D);
+        delete d;
+        return nullptr;
+    }
     for (int l = 0; l < n_layers; l++) {
         if (!plans[l] || plans[l]->h.D != d->D || plans[l]->h.k != d->k) {
             set_err("tg_hip_decode_create: layer %d has a different shape", l);
@@ -1367,14 +1427,17 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
     HIPCHECK(hipMalloc(&d->x, (size_t)d->k * d->D * 4));
     if (use_graph >= 2) {
         std::vector<DecodeLayer> ls;
-        if (!persistent_ok(d, ls)) {
+        std::vector<DecodeLayerMx> lm;
+        const HostPlan &h0 = d->plans[0]->h;
+        d->kind = h0.gate_fmt == TG_FMT_MXFP4 && h0.D == DECODE_MX_D ? 1 : 0;
+        if (d->kind == 1 ? !persistent_mx_ok(d, lm) : !persistent_ok(d, ls)) {
             HIPCHECK(hipFree(d->x));
             delete d;
             return nullptr;
         }
         int cus = 0;
         HIPCHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, g.dev));
-        const int maxg = decode_qwen_max_grid();
+        const int maxg = d->kind == 1 ? decode_mx_max_grid() : decode_qwen_max_grid();
         if (d->L > 64) {
             set_err("persistent decode: at most 64 layers per step");
             HIPCHECK(hipFree(d->x));
@@ -1389,9 +1452,14 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
             return nullptr;
         }
         d->grid = DECODE_GRID;
-        HIPCHECK(hipMalloc(&d->layers, ls.size() * sizeof(DecodeLayer)));
-        HIPCHECK(hipMemcpy(d->layers, ls.data(), ls.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice));
-        const size_t sb = decode_qwen_slot_bytes(d->grid);
+        if (d->kind == 1) {
+            HIPCHECK(hipMalloc(&d->layers_mx, lm.size() * sizeof(DecodeLayerMx)));
+            HIPCHECK(hipMemcpy(d->layers_mx, lm.data(), lm.size() * sizeof(DecodeLayerMx), hipMemcpyHostToDevice));
+        } else {
+            HIPCHECK(hipMalloc(&d->layers, ls.size() * sizeof(DecodeLayer)));
+            HIPCHECK(hipMemcpy(d->layers, ls.data(), ls.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice));
+        }
+        const size_t sb = d->kind == 1 ? decode_mx_slot_bytes() : decode_qwen_slot_bytes(d->grid);
         HIPCHECK(hipMalloc(&d->hidden, sb));   /* the exchange slots */
         HIPCHECK(hipMemset(d->hidden, 0, sb));
         HIPCHECK(hipMalloc(&d->sync, 256));
@@ -1414,7 +1482,11 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!d) return;
     hipStream_t st = stream ? (hipStream_t)stream : g.st;
-    if (d->mode >= 2) {
+    if (d->mode >= 2 && d->kind == 1) {
+        HIPCHECK(launch_decode_mx(d->layers_mx, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
+                                  d->mode == 2, st));
+        d->base += 2u * (unsigned)d->L;
+    } else if (d->mode >= 2) {
         HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
                                     d->grid, d->mode == 2, st));
         d->base += 2u * (unsigned)d->L;
@@ -1434,6 +1506,14 @@ TG_API void tg_hip_decode_set_debug(tg_hip_decode *d, void *debug_dev) {
 }
 
 TG_API size_t tg_hip_decode_debug_bytes(void) { return (size_t)DecodeDebug::BYTES; }
+
+/* Per-layer debug record bytes of this step's persistent kernel (the Qwen3
+ * record above, or the gpt-oss record: h_in | x | hidden of each expert slot,
+ * f32 of width 2880); 0 for a step that is not persistent. */
+TG_API size_t tg_hip_decode_record_bytes(tg_hip_decode *d) {
+    if (!d || d->mode < 2) return 0;
+    return d->kind == 1 ? (size_t)DecodeDebugMx::BYTES : (size_t)DecodeDebug::BYTES;
+}
 
 /* Persistent steps record up to 24 timing words per layer (timestamps of
  * the 100 MHz device clock, poll round counts) of every workgroup into
@@ -1462,6 +1542,7 @@ TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
     if (d->graph) HIPCHECK(hipGraphDestroy(d->graph));
     HIPCHECK(hipFree(d->x));
     if (d->layers) HIPCHECK(hipFree(d->layers));
+    if (d->layers_mx) HIPCHECK(hipFree(d->layers_mx));
     if (d->hidden) HIPCHECK(hipFree(d->hidden));
     if (d->sync) HIPCHECK(hipFree(d->sync));
     delete d;
@@ -1508,17 +1589,17 @@ TG_API void tg_hip_decode_kernel_times(tg_hip_decode *d, float *ms_out, int *n_o
         cls.push_back(c);
     };
     for (int l = 0; l < d->L; l++) {
-        mark(-1);
-        launch_rms_norm(d->h, d->norm_w.empty() ? nullptr : d->norm_w[l], d->x, d->k, d->D, d->eps, g.st);
-        mark(0);
         tg_hip_moe_plan *p = d->plans[l];
         if (p->h.P == 0) continue;
         MoeArgs a = p->a;
         a.xin = d->x;
         a.xq.f = d->x;
         a.out = d->h;
+        mark(-1);
+        launch_rms_norm_q8(d->h, d->norm_w.empty() ? nullptr : d->norm_w[l], d->x, d->k, d->D, d->eps, a.xq, g.st);
+        mark(0);
         std::function<void(int)> mk = [&](int c) { mark(c); };
-        launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), g.st, &mk);
+        launch_moe(a, p->h.fmts_present.data(), (int)p->h.fmts_present.size(), g.st, &mk, false);
     }
     HIPCHECK(hipStreamSynchronize(g.st));
     for (size_t i = 1; i < ev.size(); i++) {

@@ -34,6 +34,34 @@ struct DecodeDebug {
                          HS16 = HD + E * (I / 256) * 4, BYTES = HS16 + E * (I / 16) * 4;
 };
 
+/* The gpt-oss-120b step (tg_decode_mx.hip): D = I = 2880, exactly 4 MXFP4
+ * experts per layer with optional gate/up/down biases (f32 device vectors)
+ * and the clamped SwiGLU. */
+constexpr int DECODE_MX_E = 4;
+constexpr int DECODE_MX_D = 2880;
+struct DecodeLayerMx {
+    const uint8_t *gate[DECODE_MX_E];
+    const uint8_t *up[DECODE_MX_E];
+    const uint8_t *down[DECODE_MX_E];
+    const float *gb[DECODE_MX_E];
+    const float *ub[DECODE_MX_E];
+    const float *db[DECODE_MX_E];
+    float w[DECODE_MX_E];
+    const float *norm_w;
+    int n, pad;
+};
+/* Its per-layer debug record: h_in f32[D] | x f32[D] (workgroup 0) |
+ * hidden f32[4][D] (expert slot e's by workgroup 2e) */
+struct DecodeDebugMx {
+    static constexpr int D = DECODE_MX_D, E = DECODE_MX_E;
+    static constexpr int HIN = 0, X = HIN + D * 4, HID = X + D * 4, BYTES = HID + E * D * 4;
+};
+int decode_mx_max_grid();
+size_t decode_mx_slot_bytes();
+hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
+                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, bool cooperative,
+                            hipStream_t st);
+
 /* Shape the persistent kernel is built for; the host checks a step against it. */
 struct DecodeShape {
     int D, I, gate_fmt, down_fmt, maxe, threads;

@@ -46,6 +46,7 @@
 #include "tg_common.h"
 #include "tg_decode.h"
 #include "tg_device.hpp"
+#include "tg_xchg.hpp"
 
 namespace tg {
 
@@ -72,7 +73,6 @@ constexpr int HST = 144;              /* LDS stride of a q8(hidden) 128-value ha
 constexpr int VPS = 3;                /* values per slot */
 constexpr int GS = RA / VPS;          /* hidden slots per workgroup: 8 */
 constexpr int PS = (RB + VPS - 1) / VPS;   /* slots per 64-row slice: 22 */
-constexpr unsigned SPIN_LIMIT = 1u << 20;
 constexpr int MAX_LAYERS = 64;        /* layer descriptors staged in LDS */
 constexpr int NTS = 24;               /* timing words per layer */
 static_assert(NE == NX, "one expert per XCD");
@@ -92,7 +92,6 @@ static_assert(NR % NA == 0, "layer-0 slice sums: whole slices per wave");
  * (the line stays in that XCD's L2) and loaded with sc1, which bypasses the
  * CU's L1 and reads the L2 line: measured coherent, and ~0.4 us faster per
  * exchange than writing through to memory. */
-constexpr int CPOL_PLAIN = 0, CPOL_SC1 = 16;
 constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units (64 cycles) between compute waves' prefetch issue */
 /* slot regions (u32x4 index), each double buffered by layer parity:
  *   h slices  [2][NWG][PS]   rows [64 j, 64 j + 64) of the layer output
@@ -252,54 +251,6 @@ __device__ inline uint32_t q8_block_wave(float v0, float v1, float v2, float v3,
 
 __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 
-template <int POL>
-__device__ inline void put_slot(Buf sl, uint32_t slot, unsigned tag, float a, float b, float c) {
-    u32x4 v;
-    v.x = tag;
-    v.y = __float_as_uint(a);
-    v.z = __float_as_uint(b);
-    v.w = __float_as_uint(c);
-    __builtin_amdgcn_raw_buffer_store_b128(v, sl.r, (int)(slot * 16u), 0, POL);
-}
-
-/* Polls this communication lane's share of `total` slots (flat indices
- * cl, cl + CL, ...; slot(f) maps a flat index to a slot) until each carries
- * `tag`, handing every arrived slot to take(f, v).  All pending slots are
- * re-read as one batch per round.  Returns false if the wait timed out or
- * another workgroup aborted. */
-template <int MAXP, class Slot, class Take>
-__device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsigned *abort_flag, Slot slot, Take take,
-                                  unsigned *rounds = nullptr) {
-    uint32_t pending = 0;
-#pragma unroll
-    for (int i = 0; i < MAXP; i++)
-        if (cl + CL * i < total) pending |= 1u << i;
-    unsigned spins = 0;
-    while (pending) {
-        u32x4 v[MAXP];
-#pragma unroll
-        for (int i = 0; i < MAXP; i++)
-            if (pending & (1u << i))
-                v[i] = __builtin_amdgcn_raw_buffer_load_b128(sl.r, (int)(slot(cl + CL * i) * 16u), 0, CPOL_SC1);
-#pragma unroll
-        for (int i = 0; i < MAXP; i++)
-            if ((pending & (1u << i)) && v[i].x == tag) {
-                take(cl + CL * i, v[i]);
-                pending &= ~(1u << i);
-            }
-        if (!pending) break;
-        if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            return false;
-        if (rounds) *rounds = spins;
-        if (spins > SPIN_LIMIT) {
-            __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return false;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return true;
-}
-
 }  // namespace
 
 /* Tags are base + layer + 1 in every region, so a launch never mistakes a
@@ -414,7 +365,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (cl >= 0) {
                 unsigned rounds = 0;
                 if (tc) tr[15] = wall_clock64();
-                const bool ok = poll_slots<6>(
+                const bool ok = poll_slots<CL, 6>(
                     sl, clv, (NR - 1) * PS, base + (unsigned)l, abort_flag,
                     [&](int f) {
                         const int jj = f / PS, t = f % PS;
@@ -515,7 +466,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (tc) tr[9] = wall_clock64();
             unsigned rounds = 0;
             if (tc) tr[12] = wall_clock64();
-            const bool ok = poll_slots<2>(
+            const bool ok = poll_slots<CL, 2>(
                 sl, clv, (NR - 1) * GS, tag, abort_flag,
                 [&](int f) {
                     const int jj = f / GS, t = f % GS;
@@ -592,7 +543,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             }
             if (tc) tr[10] = wall_clock64();
             unsigned rounds = 0;
-            const bool ok = poll_slots<2>(
+            const bool ok = poll_slots<CL, 2>(
                 sl, clv, (NX - 1) * PS, tag, abort_flag,
                 [&](int f) {
                     const int xx = f / PS, t = f % PS;

@@ -1,0 +1,617 @@
+/*
+ * tg_decode_mx.hip -- persistent single-launch expert decode step for the
+ * gpt-oss-120b expert shape: one token, D = I = 2880, top-4 MXFP4 experts
+ * with gate/up/down biases and the clamped SwiGLU, every layer
+ *     h <- h + sum_e w_e * (down_e(q8(act(gate_e . q8(x) + bg, up_e . q8(x) + bu))) + bd)
+ * with x = RMSNorm(h) (tinygiant/engine.py:281-282,335-341 per layer; the
+ * expert math is moe_phase_a / moe_phase_b of csrc/libtinygiant.c:1279-1384
+ * for k = 1, the MXFP4 dot of :533-547, the activation of :1250-1257).
+ *
+ * Placement.  256 workgroups, one per CU; workgroup g runs on XCD x = g % 8
+ * as rank j = g / 8 of 32.  The layer's expert e is computed by XCDs 2e and
+ * 2e + 1: its 64 ranks R = 32 (x & 1) + j each own the 45-row slice
+ * [45 R, 45 R + 45) of the expert's gate, up and down rows.  Per layer:
+ *   1  gather h: each XCD's 32 ranks all-gather the 64 slices of h (rank j
+ *      of every XCD holds slices j and 32 + j, see 8)
+ *   2  RMSNorm + q8 of h, then the fp8 halves of q8(x) for the MFMA, in LDS
+ *   3  gate/up rows of the slice on block-scaled MFMA, the K range split
+ *      over the six compute waves (the partial sums are added in wave order)
+ *   4  bias + activation -> 45 hidden values; the expert's 64 ranks (two
+ *      XCDs) all-gather its 2880 hidden values
+ *   5  q8 of the hidden vector and its fp8 halves
+ *   6  down rows of the slice on MFMA -> w_e * (down + bias)
+ *   7  cross-XCD hop: rank j of every XCD trades its 45 weighted down values,
+ *      so each holds all four experts' values for slices j and 32 + j
+ *   8  h[r] += the four experts' values in expert order (the reference's
+ *      combine order, csrc/libtinygiant.c:1428-1434), published for step 1.
+ * The MXFP4 blocks go straight from memory into the MFMA's A operand: a
+ * lane's 17 bytes are one block's e8m0 scale and its 16 code bytes, which the
+ * MFMA takes as 32 e2m1 values under that scale.  q8(x) enters as two fp8
+ * operands, x = 16 (x >> 4) + (x & 15) (both halves exact in e4m3), so the
+ * products are exact and each block's integer sum is the reference's; the
+ * f32 additions are grouped differently (four blocks inside an MFMA, then
+ * per 128 values and per wave), which the f32 bar covers.
+ *
+ * Weights load into registers ahead of use: this layer's down blocks during
+ * the hidden exchange (4), the next layer's gate/up blocks and RMSNorm weight
+ * during the hop (7), while the compute waves would otherwise wait.  Two
+ * communication waves per workgroup do the polling and publishing.
+ */
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "tg_common.h"
+#include "tg_decode.h"
+#include "tg_device.hpp"
+#include "tg_xchg.hpp"
+
+namespace tg {
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int NW = 6;                 /* compute waves per workgroup */
+constexpr int NC = 2;                 /* communication waves per workgroup */
+constexpr int NA = NW + NC;
+constexpr int NT = NA * 64;
+constexpr int CL = NC * 64;           /* communication lanes */
+constexpr int D = 2880;               /* gpt-oss-120b: D = I = 2880 */
+constexpr int NBLK = D / 32;          /* MXFP4 blocks per row: 90 */
+constexpr int RB = NBLK * 17;         /* bytes per MXFP4 row: 1530 */
+constexpr int NQ = (D + 255) / 256;   /* q8 blocks per row: 12, the last holds 64 values */
+constexpr int NCH = (NBLK + 3) / 4;   /* 128-value MFMA chunks per row: 23 */
+constexpr int NSB = 4 * NCH;          /* block slots of the fp8 images (two past the row stay zero) */
+constexpr int NE = DECODE_MX_E;       /* active experts per layer */
+constexpr int NWG = DECODE_GRID;
+constexpr int NX = 8;                 /* XCDs; workgroup g runs on XCD g % NX */
+constexpr int NR = NWG / NX;          /* ranks per XCD: 32 */
+constexpr int NRK = 2 * NR;           /* ranks per expert (two XCDs): 64 */
+constexpr int RS = D / NRK;           /* rows per rank slice: 45 */
+constexpr int NG = 3;                 /* 16-row MFMA groups per slice */
+constexpr int CPW = 4;                /* chunks per compute wave */
+constexpr int VPS = 3;                /* values per slot */
+constexpr int SS = RS / VPS;          /* slots per slice: 15 */
+constexpr int HS = 2 * SS + 2;        /* h slots per rank: two slices and their sums of h^2 */
+constexpr int MAX_LAYERS = 64;
+constexpr int NTS = 24;               /* timing words per layer */
+constexpr int FMT_FP8 = 0, FMT_FP4 = 4, SCALE_1 = 127, SCALE_16 = 131;
+constexpr uint32_t OOB = 0x80000000u;  /* past every buffer: reads zeros, touches no memory */
+constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units between the compute waves' prefetch issue */
+static_assert(NE * 2 == NX, "two XCDs per expert");
+static_assert(NRK * RS == D && RS % VPS == 0 && NG * 16 >= RS && RS <= 64, "slices");
+static_assert(NW * CPW >= NCH && (NW - 1) * CPW < NCH, "chunks per wave");
+static_assert((NR - 1) * HS <= 8 * CL && (NRK - 1) * SS <= 8 * CL && (NX - 1) * SS <= CL, "poll shares");
+static_assert(NQ <= 2 * NA && NQ > NA, "q8 blocks: one or two per wave");
+static_assert(D / 4 <= 2 * NW * 64, "RMSNorm weight: two float4 per compute lane");
+
+/* slot regions (u32x4 index), each double buffered by layer parity:
+ *   h slices  [2][NWG][HS]   slices j and 32 + j of the layer output, sums of h^2
+ *   hidden    [2][NWG][SS]   the rank's 45 hidden values
+ *   parts     [2][NWG][SS]   the rank's 45 weighted down values */
+constexpr uint32_t HSL = 0, GSL = 2u * NWG * HS, PSL = GSL + 2u * NWG * SS, NSLOTS = PSL + 2u * NWG * SS;
+
+/* Per byte of n (each 0..15), entry n of a 16-byte table t0..t3 (entries
+ * 4i..4i+3 in ti, low byte first), by byte permutes. */
+__device__ inline uint32_t lut16(uint32_t n, uint32_t t0, uint32_t t1, uint32_t t2, uint32_t t3) {
+    const uint32_t idx = n & 0x07070707u;
+    const uint32_t a = __builtin_amdgcn_perm(t1, t0, idx), b = __builtin_amdgcn_perm(t3, t2, idx);
+    const uint32_t sel = ((n >> 3) & 0x01010101u) * 0xFFu;
+    return (a & ~sel) | (b & sel);
+}
+/* fp8 e4m3 codes of the halves of four packed q8 values q (-127..127):
+ * hi = q >> 4 (-8..7) and lo = q & 15 (0..15), both exact.  With u = q + 128
+ * per byte, hi is entry u >> 4 of {-8..7} and lo entry u & 15 of {0..15}. */
+__device__ inline void e4m3_halves(uint32_t q4, uint32_t &hi, uint32_t &lo) {
+    const uint32_t u = q4 ^ 0x80808080u;
+    hi = lut16((u >> 4) & 0x0F0F0F0Fu, 0xCACCCED0u, 0xB8C0C4C8u, 0x44403800u, 0x4E4C4A48u);
+    lo = lut16(u & 0x0F0F0F0Fu, 0x44403800u, 0x4E4C4A48u, 0x53525150u, 0x57565554u);
+}
+
+/* One MXFP4 block as an MFMA A operand: e8m0 byte (low byte of e) and the
+ * 16 code bytes. */
+struct MxBlk {
+    uint32_t e;
+    u32x4 c;
+};
+__device__ inline MxBlk load_blk(Buf w, uint32_t off) {
+    MxBlk b;
+    b.e = ld4(w, off);
+    b.c = ld16(w, off == OOB ? OOB : off + 1u);
+    return b;
+}
+
+/* LDS image of one q8 row for the MFMA: per 32-value block, the fp8 codes of
+ * hi = x >> 4 and lo = x & 15 in MFMA K order (byte 2t holds value t, byte
+ * 2t + 1 value 16 + t), plus the q8 scale of each 256-value block. */
+struct __attribute__((aligned(16))) LdsQ {
+    uint8_t sp[NSB][2][32];
+    float d[NQ];
+};
+
+/* q8 of one 256-value block held by a wave (lane l: values 4l..4l+3, zeros
+ * past the row), quantize_q8 (csrc/libtinygiant.c:169-208) in the arithmetic
+ * of k_quantize_q8, written as fp8 halves into block slots 8b .. 8b + 7 of q.
+ * Lanes l and l + 4 hold values t and 16 + t of the same 32-block, which the
+ * MFMA K order interleaves; lane l (l % 8 < 4) writes both. */
+__device__ inline void q8_split_block(float v0, float v1, float v2, float v3, int lane, int b, LdsQ &q) {
+    const float amax = wave_max(fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3))));
+    const float inv = amax > 0.f ? 127.f / amax : 0.f;
+    const int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
+    const int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
+    uint32_t hi, lo;
+    e4m3_halves((uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                    ((uint32_t)(q3 & 0xFF) << 24),
+                hi, lo);
+    const uint32_t hi2 = (uint32_t)__shfl_down((int)hi, 4, 64), lo2 = (uint32_t)__shfl_down((int)lo, 4, 64);
+    const int blk = 8 * b + (lane >> 3), pos = 8 * (lane & 7);
+    if ((lane & 7) < 4 && blk < NSB) {   /* the last q8 block ends inside block slot 91 */
+        /* values t = 4 (l % 8) + i at bytes 2t, values 16 + t at bytes 2t + 1 */
+        auto inter = [](uint32_t a, uint32_t c, int half) {
+            const uint32_t s = 16u * (uint32_t)half;
+            const uint32_t a0 = (a >> s) & 0xFFu, a1 = (a >> (s + 8u)) & 0xFFu;
+            const uint32_t c0 = (c >> s) & 0xFFu, c1 = (c >> (s + 8u)) & 0xFFu;
+            return a0 | (c0 << 8) | (a1 << 16) | (c1 << 24);
+        };
+        uint32_t *ph = reinterpret_cast<uint32_t *>(&q.sp[blk][0][pos]);
+        uint32_t *pl = reinterpret_cast<uint32_t *>(&q.sp[blk][1][pos]);
+        ph[0] = inter(hi, hi2, 0);
+        ph[1] = inter(hi, hi2, 1);
+        pl[0] = inter(lo, lo2, 0);
+        pl[1] = inter(lo, lo2, 1);
+    }
+    if (lane == 0) q.d[b] = amax / 127.f;
+}
+
+/* The B operands (fp8 hi and lo halves of q8(x)) of chunk c for lane group
+ * g = lane / 16: bytes 0..15 are values 16 g .. 16 g + 15 of the chunk and
+ * bytes 16..31 values 64 + 16 g .. in MFMA K order. */
+__device__ inline void load_b(const LdsQ &q, int c, int g, v8i &bh, v8i &bl) {
+    const int b0 = 4 * c + (g >> 1), b1 = b0 + 2, o = 16 * (g & 1);
+    const u32x4 h0 = *reinterpret_cast<const u32x4 *>(&q.sp[b0][0][o]);
+    const u32x4 h1 = *reinterpret_cast<const u32x4 *>(&q.sp[b1][0][o]);
+    const u32x4 l0 = *reinterpret_cast<const u32x4 *>(&q.sp[b0][1][o]);
+    const u32x4 l1 = *reinterpret_cast<const u32x4 *>(&q.sp[b1][1][o]);
+    bh = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+    bl = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+}
+
+/* acc += d * (block-scaled A . B) for one chunk: two chained MFMAs, hi half
+ * under scale 16, lo half under scale 1. */
+__device__ inline void mma_chunk(const MxBlk &a, const v8i &bh, const v8i &bl, float d, v4f &acc) {
+    const v8i av = v8i{(int)a.c.x, (int)a.c.y, (int)a.c.z, (int)a.c.w, 0, 0, 0, 0};
+    const int e = (int)(a.e & 0xFFu);
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+    v4f r = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bh, z, FMT_FP4, FMT_FP8, 0, e, 0, SCALE_16);
+    r = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bl, r, FMT_FP4, FMT_FP8, 0, e, 0, SCALE_1);
+    acc[0] += d * r[0];
+    acc[1] += d * r[1];
+    acc[2] += d * r[2];
+    acc[3] += d * r[3];
+}
+
+}  // namespace
+
+/* Tags are base + layer + 1 in every region, so a launch never mistakes a
+ * slot of an earlier layer or launch for its own.  A slot of parity p is
+ * rewritten two layers later only after every reader of it has published
+ * something the writer waited for in between. */
+__global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restrict__ layers, int L, float *h,
+                                                  u32x4 *slots, unsigned *abort_flag, unsigned base, float eps,
+                                                  uint8_t *dbg, uint64_t *times) {
+    __shared__ __attribute__((aligned(16))) float hx[D];      /* this layer's h */
+    __shared__ __attribute__((aligned(16))) float nws[D];     /* this layer's RMSNorm weight */
+    __shared__ __attribute__((aligned(16))) float hid[D];     /* the expert's hidden vector */
+    __shared__ LdsQ sx, sh;                                   /* fp8 images of q8(x) and q8(hidden) */
+    __shared__ float ssq[NRK];                                /* sum of h^2 of each 45-row slice */
+    __shared__ float red[NW][2 * NG][16];                     /* per-wave partial row sums */
+    __shared__ float pp[NX][RS];                              /* weighted down values of the 8 XCDs */
+    __shared__ int lds_fail;
+    __shared__ DecodeLayerMx lys[MAX_LAYERS];
+
+    int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid when >= 0 */
+    const int ct = (int)threadIdx.x;             /* compute lane, valid when < NW * 64 */
+    if (threadIdx.x == 0) lds_fail = 0;
+    const int wg = blockIdx.x;
+    const int xc = wg % NX, rk = wg / NX;        /* XCD and rank in it */
+    const int xe = xc >> 1, R = NR * (xc & 1) + rk;   /* expert slot and rank in the expert */
+    Buf sl = make_buf(slots, NSLOTS * 16u);
+
+    MxBlk wa[CPW][2 * NG];   /* gate (units 0..2) and up (3..5) blocks of the wave's chunks */
+    MxBlk wb[CPW][NG];       /* down blocks */
+    u32x4 nw0, nw1;          /* next layer's RMSNorm weight (compute lanes) */
+
+    /* block offset of unit row group gr, chunk i of this wave, or OOB */
+    auto blk_off = [&](int gr, int i) -> uint32_t {
+        const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
+        if (c >= NCH || b >= NBLK || sr >= RS) return OOB;
+        return (uint32_t)(RS * R + sr) * (uint32_t)RB + (uint32_t)b * 17u;
+    };
+    /* loads are unconditional so the registers' live ranges end at their
+     * use; an inactive step reads through an empty descriptor */
+    auto load_a = [&](const DecodeLayerMx &ly, bool on) {
+        const bool cw = on && wave < NW;
+        Buf gb = make_buf_uniform(cw ? ly.gate[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
+        Buf ub = make_buf_uniform(cw ? ly.up[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
+#pragma unroll
+        for (int i = 0; i < CPW; i++)
+#pragma unroll
+            for (int gr = 0; gr < NG; gr++) {
+                const uint32_t o = blk_off(gr, i);
+                wa[i][gr] = load_blk(gb, o);
+                wa[i][NG + gr] = load_blk(ub, o);
+            }
+    };
+    auto load_d = [&](const DecodeLayerMx &ly) {
+        const bool cw = wave < NW;
+        Buf db = make_buf_uniform(cw ? ly.down[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
+#pragma unroll
+        for (int i = 0; i < CPW; i++)
+#pragma unroll
+            for (int gr = 0; gr < NG; gr++) wb[i][gr] = load_blk(db, blk_off(gr, i));
+    };
+    auto zero_a = [&]() {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        nw0 = nw1 = z;
+#pragma unroll
+        for (int i = 0; i < CPW; i++)
+#pragma unroll
+            for (int u = 0; u < 2 * NG; u++) wa[i][u] = MxBlk{0u, z};
+    };
+    auto zero_d = [&]() {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int i = 0; i < CPW; i++)
+#pragma unroll
+            for (int gr = 0; gr < NG; gr++) wb[i][gr] = MxBlk{0u, z};
+    };
+    auto load_nw = [&](const DecodeLayerMx &ly, bool use) {
+        const bool on = use && wave < NW && ly.norm_w != nullptr;
+        Buf nb = make_buf_uniform(on ? ly.norm_w : nullptr, on ? (uint32_t)D * 4u : 0u);
+        nw0 = ld16(nb, (uint32_t)ct * 16u);
+        nw1 = ld16(nb, (uint32_t)(NW * 64 + ct) * 16u);
+    };
+    auto store_nw = [&]() {
+        if (wave < NW) {
+            if (ct < D / 4) reinterpret_cast<u32x4 *>(nws)[ct] = nw0;
+            if (ct < D / 4 - NW * 64) reinterpret_cast<u32x4 *>(nws)[NW * 64 + ct] = nw1;
+        }
+    };
+    /* q8 + fp8 halves of a D-value LDS vector (scaled by `scale` and the
+     * RMSNorm weight when norm): wave w quantizes blocks w and w + 8 */
+    auto quantize = [&](const float *src, bool norm, float scale, bool has_nw, LdsQ &q, float *dbg_x) {
+#pragma unroll
+        for (int k = 0; k < 2; k++) {
+            const int b = wave + NA * k;
+            if (b >= NQ) break;   /* uniform */
+            const int i0 = 256 * b + 4 * lane;
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int i = i0 + c;
+                float t = i < D ? src[i] : 0.f;
+                if (norm) t = (t * scale) * (has_nw && i < D ? nws[i] : 1.f);
+                v[c] = t;
+                if (dbg_x && i < D) dbg_x[i] = t;
+            }
+            q8_split_block(v[0], v[1], v[2], v[3], lane, b, q);
+        }
+    };
+
+    /* layer descriptors -> LDS; layer input: the caller's h */
+    {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(layers);
+        uint32_t *dst = reinterpret_cast<uint32_t *>(lys);
+        const int words = L * (int)(sizeof(DecodeLayerMx) / 4);
+        for (int t = threadIdx.x; t < words; t += NT) dst[t] = src[t];
+    }
+    for (int t = threadIdx.x; t < D / 4; t += NT) reinterpret_cast<u32x4 *>(hx)[t] = reinterpret_cast<const u32x4 *>(h)[t];
+    /* the fp8 block slots past the row stay zero (chunk 22 reads them) */
+    for (int t = threadIdx.x; t < (NSB - NBLK) * 64 / 4; t += NT) {
+        reinterpret_cast<uint32_t *>(&sx.sp[NBLK][0][0])[t] = 0u;
+        reinterpret_cast<uint32_t *>(&sh.sp[NBLK][0][0])[t] = 0u;
+    }
+    __syncthreads();
+    /* slice sums of h^2 for layer 0 (later layers receive them with h) */
+    for (int s = wave; s < NRK; s += NA) {
+        const float v = lane < RS ? hx[RS * s + lane] : 0.f;
+        const float t = wave_sum(v * v);
+        if (lane == 0) ssq[s] = t;
+    }
+    load_nw(lys[0], true);
+    load_a(lys[0], true);
+    store_nw();
+    __syncthreads();   /* layer 0's RMSNorm weight is in LDS before step 2 reads it */
+
+    for (int l = 0; l < L; l++) {
+        const DecodeLayerMx &ly = lys[l];
+        const unsigned par = (unsigned)(l & 1);
+        const unsigned tag = base + (unsigned)l + 1u;
+        const bool has_nw = ly.norm_w != nullptr;
+        int clv = cl;
+        asm volatile("" : "+v"(clv));
+        asm volatile("" : "+v"(lane));
+        const bool tw = times && threadIdx.x == 0;
+        const bool tc = times && clv == 0;
+        uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
+        uint8_t *rec = dbg ? dbg + (size_t)l * DecodeDebugMx::BYTES : nullptr;
+        if (tw) tr[0] = wall_clock64();
+        /* ---- 1: gather h: slices j' and 32 + j' from the other ranks of this XCD ---- */
+        if (l > 0) {
+            if (cl >= 0) {
+                unsigned rounds = 0;
+                if (tc) tr[15] = wall_clock64();
+                const bool ok = poll_slots<CL, 8>(
+                    sl, clv, (NR - 1) * HS, base + (unsigned)l, abort_flag,
+                    [&](int f) {
+                        const int jj = f / HS, t = f % HS;
+                        const int j = jj + (jj >= rk);
+                        return HSL + ((par ^ 1u) * NWG + (uint32_t)(xc + NX * j)) * HS + (uint32_t)t;
+                    },
+                    [&](int f, const u32x4 &v) {
+                        const int jj = f / HS, t = f % HS;
+                        const int j = jj + (jj >= rk);
+                        const int half = t / (SS + 1), u = t % (SS + 1);
+                        const int s = NR * half + j;
+                        if (u == SS) {
+                            ssq[s] = __uint_as_float(v.y);
+                        } else {
+                            float *o = hx + RS * s + VPS * u;
+                            o[0] = __uint_as_float(v.y);
+                            o[1] = __uint_as_float(v.z);
+                            o[2] = __uint_as_float(v.w);
+                        }
+                    },
+                    tc ? &rounds : nullptr);
+                if (tc) {
+                    tr[16] = wall_clock64();
+                    tr[17] = rounds;
+                }
+                if (!ok) lds_fail = 1;
+            } else {
+                store_nw();
+            }
+            __syncthreads();
+            if (lds_fail) return;
+        }
+        if (tw) tr[1] = wall_clock64();
+        /* the slice's gate, up and down biases (communication lanes, one row
+         * each): issued after the h polls so none waits behind them */
+        float gbv = 0.f, ubv = 0.f, dbv = 0.f;
+        if (cl >= 0) {
+            const bool on = clv < RS;
+            const uint32_t o = on ? (uint32_t)(RS * R + clv) * 4u : OOB;
+            gbv = __uint_as_float(ld4(make_buf_uniform(ly.gb[xe], ly.gb[xe] ? (uint32_t)D * 4u : 0u), o));
+            ubv = __uint_as_float(ld4(make_buf_uniform(ly.ub[xe], ly.ub[xe] ? (uint32_t)D * 4u : 0u), o));
+            dbv = __uint_as_float(ld4(make_buf_uniform(ly.db[xe], ly.db[xe] ? (uint32_t)D * 4u : 0u), o));
+        }
+        /* ---- 2: RMSNorm (weight or 1) + q8 + fp8 halves of x ---- */
+        {
+            float tot = 0.f;
+#pragma unroll 8
+            for (int i = 0; i < NRK; i++) tot += ssq[i];
+            const float scale = 1.f / sqrtf(tot / (float)D + eps);
+            if (rec && wg == 0)
+                for (int t = threadIdx.x; t < D; t += NT) reinterpret_cast<float *>(rec + DecodeDebugMx::HIN)[t] = hx[t];
+            quantize(hx, true, scale, has_nw, sx,
+                     rec && wg == 0 ? reinterpret_cast<float *>(rec + DecodeDebugMx::X) : nullptr);
+        }
+        __syncthreads();
+        if (tw) tr[2] = wall_clock64();
+        /* ---- 3: gate/up rows of the slice, chunks [4 w, 4 w + 4) of wave w ---- */
+        if (wave < NW) {
+            v4f acc[2 * NG];
+#pragma unroll
+            for (int u = 0; u < 2 * NG; u++) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int c = CPW * wave + i;
+                if (c >= NCH) break;   /* uniform */
+                v8i bh, bl;
+                load_b(sx, c, lane >> 4, bh, bl);
+                const float d = sx.d[c >> 1];
+#pragma unroll
+                for (int u = 0; u < 2 * NG; u++) mma_chunk(wa[i][u], bh, bl, d, acc[u]);
+            }
+            /* column 0 of the MFMA result: lane 16 g holds rows 4 g .. 4 g + 3 */
+            if ((lane & 15) == 0)
+#pragma unroll
+                for (int u = 0; u < 2 * NG; u++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) red[wave][u][4 * (lane >> 4) + v] = acc[u][v];
+        }
+        __syncthreads();
+        if (tw) tr[3] = wall_clock64();
+        /* ---- 4: bias + activation, all-gather the expert's hidden vector ---- */
+        /* meanwhile the compute waves issue this layer's down blocks, one
+         * wave after another */
+        if (cl < 0) {
+            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
+            load_d(ly);
+        } else {
+            zero_d();   /* no loads ahead of the polls in these waves' queue */
+        }
+        if (cl >= 0) {
+            /* row i of the slice: the six waves' partial sums in wave order */
+            if (clv < RS) {
+                const int gi = clv >> 4, ri = clv & 15, row = RS * R + clv;
+                float g = 0.f, u = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; w++) {
+                    g += red[w][gi][ri];
+                    u += red[w][NG + gi][ri];
+                }
+                hid[row] = act_fn(TG_ACT_GPTOSS, g + gbv, u + ubv);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (clv < SS) {
+                const float *a = hid + RS * R + VPS * clv;
+                put_slot<CPOL_SC1>(sl, GSL + (par * NWG + (uint32_t)wg) * SS + (uint32_t)clv, tag, a[0], a[1], a[2]);
+            }
+            if (tc) tr[9] = wall_clock64();
+            unsigned rounds = 0;
+            if (tc) tr[12] = wall_clock64();
+            const bool ok = poll_slots<CL, 8>(
+                sl, clv, (NRK - 1) * SS, tag, abort_flag,
+                [&](int f) {
+                    const int rr = f / SS, t = f % SS;
+                    const int r2 = rr + (rr >= R);
+                    const int w2 = (2 * xe + (r2 >= NR ? 1 : 0)) + NX * (r2 % NR);
+                    return GSL + (par * NWG + (uint32_t)w2) * SS + (uint32_t)t;
+                },
+                [&](int f, const u32x4 &v) {
+                    const int rr = f / SS, t = f % SS;
+                    const int r2 = rr + (rr >= R);
+                    float *o = hid + RS * r2 + VPS * t;
+                    o[0] = __uint_as_float(v.y);
+                    o[1] = __uint_as_float(v.z);
+                    o[2] = __uint_as_float(v.w);
+                },
+                tc ? &rounds : nullptr);
+            if (tc) {
+                tr[13] = wall_clock64();
+                tr[14] = rounds;
+            }
+            if (!ok) lds_fail = 1;
+        }
+        __syncthreads();
+        if (lds_fail) return;
+        if (tw) tr[4] = wall_clock64();
+        /* ---- 5: q8 + fp8 halves of the hidden vector ---- */
+        if (rec && (xc & 1) == 0 && rk == 0)   /* workgroup 2e: expert slot e's record */
+            for (int t = threadIdx.x; t < D; t += NT)
+                reinterpret_cast<float *>(rec + DecodeDebugMx::HID)[xe * D + t] = hid[t];
+        quantize(hid, false, 1.f, false, sh, nullptr);
+        __syncthreads();
+        if (tw) tr[5] = wall_clock64();
+        /* ---- 6: down rows of the slice ---- */
+        if (wave < NW) {
+            v4f acc[NG];
+#pragma unroll
+            for (int u = 0; u < NG; u++) acc[u] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < CPW; i++) {
+                const int c = CPW * wave + i;
+                if (c >= NCH) break;   /* uniform */
+                v8i bh, bl;
+                load_b(sh, c, lane >> 4, bh, bl);
+                const float d = sh.d[c >> 1];
+#pragma unroll
+                for (int u = 0; u < NG; u++) mma_chunk(wb[i][u], bh, bl, d, acc[u]);
+            }
+            if ((lane & 15) == 0)
+#pragma unroll
+                for (int u = 0; u < NG; u++)
+#pragma unroll
+                    for (int v = 0; v < 4; v++) red[wave][u][4 * (lane >> 4) + v] = acc[u][v];
+        }
+        __syncthreads();
+        if (tw) tr[6] = wall_clock64();
+        /* ---- 7: cross-XCD hop: rank rk of every XCD trades its 45 weighted down values ---- */
+        /* meanwhile the next layer's RMSNorm weight and gate/up blocks are issued */
+        /* both paths assign the registers (empty loads past the last layer),
+         * so this layer's blocks are free once they are used */
+        if (cl < 0) {
+            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
+            load_nw(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
+            load_a(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
+        } else {
+            zero_a();
+        }
+        if (cl >= 0) {
+            if (clv < RS) {
+                const int gi = clv >> 4, ri = clv & 15;
+                float v = 0.f;
+#pragma unroll
+                for (int w = 0; w < NW; w++) v += red[w][gi][ri];
+                pp[xc][clv] = ly.w[xe] * (v + dbv);
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (clv < SS) {
+                const float *a = pp[xc] + VPS * clv;
+                put_slot<CPOL_SC1>(sl, PSL + (par * NWG + (uint32_t)wg) * SS + (uint32_t)clv, tag, a[0], a[1], a[2]);
+            }
+            if (tc) tr[10] = wall_clock64();
+            unsigned rounds = 0;
+            const bool ok = poll_slots<CL, 1>(
+                sl, clv, (NX - 1) * SS, tag, abort_flag,
+                [&](int f) {
+                    const int xx = f / SS, t = f % SS;
+                    const int x = xx + (xx >= xc);
+                    return PSL + (par * NWG + (uint32_t)(x + NX * rk)) * SS + (uint32_t)t;
+                },
+                [&](int f, const u32x4 &v) {
+                    const int xx = f / SS, t = f % SS;
+                    const int x = xx + (xx >= xc);
+                    float *o = pp[x] + VPS * t;
+                    o[0] = __uint_as_float(v.y);
+                    o[1] = __uint_as_float(v.z);
+                    o[2] = __uint_as_float(v.w);
+                },
+                tc ? &rounds : nullptr);
+            if (tc) {
+                tr[18] = wall_clock64();
+                tr[19] = rounds;
+            }
+            if (!ok) lds_fail = 1;
+        }
+        __syncthreads();
+        if (lds_fail) return;
+        if (tw) tr[7] = wall_clock64();
+        /* ---- 8: combine slices rk (first communication wave) and 32 + rk
+         * (second) in expert order, publish ---- */
+        if (cl >= 0) {
+            const int half = clv >> 6, ri = clv & 63, s = NR * half + rk;
+            float a = 0.f;
+            if (ri < RS) {
+                const int r = RS * s + ri;
+                a = hx[r];
+#pragma unroll
+                for (int e = 0; e < NE; e++) a += pp[2 * e + half][ri];
+                hx[r] = a;
+                if (l == L - 1 && xc == 0) h[r] = a;
+            }
+            const float sq = wave_sum(a * a);   /* the slice's sum of h^2, for the next RMSNorm */
+            if (ri == 0) ssq[s] = sq;
+            __builtin_amdgcn_wave_barrier();
+            if (l + 1 < L && ri <= SS) {
+                const uint32_t slot = HSL + (par * NWG + (uint32_t)wg) * HS + (uint32_t)((SS + 1) * half + ri);
+                if (ri < SS) {
+                    const float *o = hx + RS * s + VPS * ri;
+                    put_slot<CPOL_PLAIN>(sl, slot, tag, o[0], o[1], o[2]);
+                } else {
+                    put_slot<CPOL_PLAIN>(sl, slot, tag, sq, 0.f, 0.f);
+                }
+            }
+            if (tc) tr[11] = wall_clock64();
+        }
+        if (tw) tr[8] = wall_clock64();
+    }
+}
+
+int decode_mx_max_grid() {
+    int dev = 0, per_cu = 0;
+    hipDeviceProp_t pr;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode_mx, NT, 0) != hipSuccess)
+        return 0;
+    return per_cu * pr.multiProcessorCount;
+}
+
+size_t decode_mx_slot_bytes() { return (size_t)NSLOTS * 16; }
+
+hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
+                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, bool cooperative,
+                            hipStream_t st) {
+    void *args[] = {(void *)&layers_dev, (void *)&L, (void *)&h_dev, (void *)&slots_dev, (void *)&abort_dev,
+                    (void *)&base, (void *)&eps, (void *)&debug_dev, (void *)&times_dev};
+    if (cooperative)
+        return hipLaunchCooperativeKernel((const void *)k_decode_mx, dim3(DECODE_GRID), dim3(NT), args, 0, st);
+    return hipLaunchKernel((const void *)k_decode_mx, dim3(DECODE_GRID), dim3(NT), args, 0, st);
+}
+
+}  // namespace tg

@@ -51,9 +51,10 @@ void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *b
 void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows &x, int nsums_row, int32_t *out,
                   hipStream_t st);
 /* `mark`, when given, is called after each kernel with its class:
- * 1 quantize(x), 2 gate/up, 3 quantize(hidden), 4 down, 5 combine */
+ * 1 quantize(x), 2 gate/up, 3 quantize(hidden), 4 down, 5 combine.
+ * quantize_x false: a.xq already holds q8 of the input rows. */
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
-                const std::function<void(int)> *mark = nullptr);
+                const std::function<void(int)> *mark = nullptr, bool quantize_x = true);
 /* MXFP4 phases on block-scaled MFMA with LDS-resident weight slabs
  * (tg_grouped.hip): every weight byte is read once whatever the pairs per
  * expert.  launch_mx_split prepares the fp8 halves of q8 rows. */
@@ -65,7 +66,12 @@ void launch_moe_b_mx(const MoeArgs &a, hipStream_t st);
  * experts; 0 switches them off */
 void set_grouped_min_rows(int rows);
 int grouped_min_rows();
+/* RMSNorm rows of n <= 16384 values (rms_norm_fits); the _q8 form also
+ * writes q8 of the result to q, bit-identical to launch_quantize over it */
+bool rms_norm_fits(int n);
 void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st);
+void launch_rms_norm_q8(const float *x, const float *w, float *out, int nrows, int n, float eps, const Q8Rows &q,
+                        hipStream_t st);
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st);
 void launch_copy(const void *src, void *dst, uint64_t nbytes, hipStream_t st);
 

@@ -8,7 +8,7 @@
  *   k_moe_b         part = w * (down.q8(hidden) + bd)                      (moe_phase_b, :1329-1384)
  *   k_moe_combine   out[row] += part, experts in index order               (:1428-1434)
  *   k_isums         per-sub-block integer dot sums (bit-exactness probe)
- *   k_rms_norm      x * 1/sqrt(mean(x^2)+eps) * w                          (tg_rms_norm, :680-698)
+ *   k_rms_norm_q8   x * 1/sqrt(mean(x^2)+eps) * w, optionally q8 of it     (tg_rms_norm, :680-698)
  *   k_synth_fill    seeded synthetic weights (tg_synth.h)
  *
  * Every weight and activation read goes through a raw buffer resource sized
@@ -19,6 +19,7 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <algorithm>
 #include <functional>
 
 #include "tg_device.hpp"
@@ -29,19 +30,12 @@ namespace tg {
 
 /* ======================= q8 quantization ======================= */
 
-/* One wave per 256-value block: lane l owns values 4l..4l+3. */
-__global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x, int ncols, int nrows,
-                                                     long xstride, Q8Rows out) {
-    const int lane = threadIdx.x & 63;
-    const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
-    const int nb = out.nb;
-    if (wave >= nrows * nb) return;   /* uniform per wave */
-    const int r = wave / nb, b = wave % nb;
-    const int n = min(256, ncols - b * 256);
-    Buf xb = make_buf(x + (size_t)r * xstride + (size_t)b * 256, (uint32_t)n * 4u);
-    u32x4 raw = ld16(xb, (uint32_t)lane * 16u);   /* zeros past n */
-    float v0 = __uint_as_float(raw.x), v1 = __uint_as_float(raw.y);
-    float v2 = __uint_as_float(raw.z), v3 = __uint_as_float(raw.w);
+/* q8 of one 256-value block held by a wave, lane l owning values 4l..4l+3
+ * (quantize_q8, csrc/libtinygiant.c:169-208): scale amax/127, quants
+ * rint(v * 127/amax), 16- and 32-element sums and the block total, written to
+ * block b of row r. */
+__device__ inline void q8_block_store(float v0, float v1, float v2, float v3, int lane, const Q8Rows &out, int r,
+                                      int b) {
     float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
@@ -51,6 +45,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x
     int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
     uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
                       ((uint32_t)(q3 & 0xFF) << 24);
+    const int nb = out.nb;
     int8_t *qrow = out.qs + ((size_t)r * nb + b) * 256;
     reinterpret_cast<uint32_t *>(qrow)[lane] = packed;
     int s = q0 + q1 + q2 + q3;
@@ -70,12 +65,110 @@ __global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x
     }
 }
 
+/* One wave per 256-value block: lane l owns values 4l..4l+3. */
+__global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x, int ncols, int nrows,
+                                                     long xstride, Q8Rows out) {
+    const int lane = threadIdx.x & 63;
+    const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
+    const int nb = out.nb;
+    if (wave >= nrows * nb) return;   /* uniform per wave */
+    const int r = wave / nb, b = wave % nb;
+    const int n = min(256, ncols - b * 256);
+    Buf xb = make_buf(x + (size_t)r * xstride + (size_t)b * 256, (uint32_t)n * 4u);
+    u32x4 raw = ld16(xb, (uint32_t)lane * 16u);   /* zeros past n */
+    q8_block_store(__uint_as_float(raw.x), __uint_as_float(raw.y), __uint_as_float(raw.z), __uint_as_float(raw.w),
+                   lane, out, r, b);
+}
+
+/* RMSNorm of one row per workgroup, wave w owning the 256-value blocks
+ * w, w + NWR, ... (at most RMS_BPW of them), lane l values 4l..4l+3 of each:
+ * y = (x * (1/sqrt(ss/n + eps))) * w (tg_rms_norm, csrc/libtinygiant.c:680-698;
+ * ss summed per lane, then over the wave, then over the waves in order).
+ * Every load of the row is issued before any is used.  With q8 rows given,
+ * y is quantized in place of a separate k_quantize_q8 over it (same bits). */
+constexpr int RMS_WAVES = 16, RMS_BPW = 4;
+__global__ __launch_bounds__(RMS_WAVES * 64) void k_rms_norm_q8(const float *__restrict__ x, const float *__restrict__ w,
+                                                                float *__restrict__ y, int n, float eps, Q8Rows q) {
+    __shared__ float red[RMS_WAVES];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int r = blockIdx.x;
+    Buf xb = make_buf(x + (size_t)r * n, (uint32_t)n * 4u);
+    Buf wb = make_buf(w, w ? (uint32_t)n * 4u : 0u);
+    float v[RMS_BPW][4], g[RMS_BPW][4];
+#pragma unroll
+    for (int i = 0; i < RMS_BPW; i++) {
+        const uint32_t o = (uint32_t)((wave + nw * i) * 256 + 4 * lane) * 4u;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            v[i][c] = __uint_as_float(ld4(xb, o + 4u * c));   /* zeros past n */
+            g[i][c] = w ? __uint_as_float(ld4(wb, o + 4u * c)) : 1.f;
+        }
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < RMS_BPW; i++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) ss += v[i][c] * v[i][c];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.f;
+    for (int i = 0; i < nw; i++) tot += red[i];
+    const float scale = 1.f / sqrtf(tot / (float)n + eps);
+    float *yr = y + (size_t)r * n;
+#pragma unroll
+    for (int i = 0; i < RMS_BPW; i++) {
+        const int b = wave + nw * i;
+        if (b * 256 >= n) break;   /* uniform per wave */
+        float o4[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            o4[c] = (v[i][c] * scale) * g[i][c];
+            if (b * 256 + 4 * lane + c < n) yr[b * 256 + 4 * lane + c] = o4[c];
+        }
+        if (q.qs) q8_block_store(o4[0], o4[1], o4[2], o4[3], lane, q, r, b);
+    }
+}
+
 /* ======================= generic GEMV ======================= */
+
+constexpr uint32_t ROW_OOB = 0x80000000u;   /* past every weight buffer: reads zeros, touches no memory */
+
+/* acc[m] += the lane's share of dot(row of matrix m, x): items sl, sl + S,
+ * ... below nitems, added in item order.  Loads go out in batches of TB
+ * items before any is used, so a row costs ceil(T / TB) memory round trips
+ * instead of T.  An invalid row (rv false) or an item past the row is read
+ * at an out-of-range offset and adds nothing. */
+template <class F, int S, int TB, int NM>
+__device__ inline void row_dots(const Buf (&w)[NM], uint32_t roff, bool rv, const Q8Row &xr, int sl, int nitems,
+                                int T, float (&acc)[NM]) {
+    for (int t0 = 0; t0 < T; t0 += TB) {
+        typename F::X xs[TB];
+        typename F::W ws[NM][TB];
+#pragma unroll
+        for (int u = 0; u < TB; u++) {
+            const int item = sl + (t0 + u) * S;
+            const bool iv = rv && t0 + u < T && item < nitems;
+            xs[u] = F::load_x(xr, iv ? item : 0);
+#pragma unroll
+            for (int m = 0; m < NM; m++) ws[m][u] = F::load_w(w[m], iv ? roff : ROW_OOB, iv ? item : 0);
+        }
+#pragma unroll
+        for (int u = 0; u < TB; u++) {
+            const int item = sl + (t0 + u) * S;
+            if (rv && t0 + u < T && item < nitems) {
+#pragma unroll
+                for (int m = 0; m < NM; m++) acc[m] += F::value(ws[m][u], xs[u], item);
+            }
+        }
+    }
+}
 
 /* W: nrows rows of rb bytes.  For each activation row j < k:
  *   y[j*ystride + r] = dot(W[r], x_j) + bias[r]
  * Each wave takes `rows_per_wave` consecutive rows in steps of 64/S. */
-template <class F, int S>
+template <class F, int S, int TB>
 __global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uint32_t rb, int nrows,
                                               const float *__restrict__ bias, Q8Rows x, int k, float *y,
                                               long ystride, int nitems, int T, int rows_per_wave) {
@@ -91,18 +184,10 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uin
         for (int rs = 0; rs < rows_per_wave; rs += G) {
             const int rl = rs + seg, r = row0 + rl;
             const bool rv = rl < rows_per_wave && r < nrows;
-            float v = 0.f;
-            if (rv) {
-                for (int t = 0; t < T; t++) {
-                    const int item = sl + t * S;
-                    if (item < nitems) {
-                        typename F::W w = F::load_w(wb, (uint32_t)rl * rb, item);
-                        typename F::X xs = F::load_x(xr, item);
-                        v += F::value(w, xs, item);
-                    }
-                }
-            }
-            v = seg_sum<S>(v);
+            float acc[1] = {0.f};
+            const Buf ws[1] = {wb};
+            row_dots<F, S, TB, 1>(ws, (uint32_t)rl * rb, rv, xr, sl, nitems, T, acc);
+            const float v = seg_sum<S>(acc[0]);
             if (rv && sl == 0) y[(size_t)j * ystride + r] = v + (bias ? bias[r] : 0.f);
         }
     }
@@ -112,7 +197,7 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uin
 
 /* Phase A: grid (x: wave groups over the I rows, y: expert).  hidden[p][r] for
  * every pair p of the expert. */
-template <class F, int S>
+template <class F, int S, int TB>
 __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int rows_per_wave) {
     constexpr int G = 64 / S;
     const int e = blockIdx.y;
@@ -135,21 +220,11 @@ __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int
         for (int rs = 0; rs < rows_per_wave; rs += G) {
             const int r = row0 + rs + seg;
             const bool rv = rs + seg < rows_per_wave && r < a.I;
-            float vg = 0.f, vu = 0.f;
-            if (rv) {
-                for (int t = 0; t < T; t++) {
-                    const int item = sl + t * S;
-                    if (item < nitems) {
-                        typename F::X xs = F::load_x(xr, item);
-                        typename F::W wg = F::load_w(gw, (uint32_t)r * rb, item);
-                        typename F::W wu = F::load_w(uw, (uint32_t)r * rb, item);
-                        vg += F::value(wg, xs, item);
-                        vu += F::value(wu, xs, item);
-                    }
-                }
-            }
-            vg = seg_sum<S>(vg);
-            vu = seg_sum<S>(vu);
+            float acc[2] = {0.f, 0.f};
+            const Buf ws[2] = {gw, uw};
+            row_dots<F, S, TB, 2>(ws, (uint32_t)r * rb, rv, xr, sl, nitems, T, acc);
+            float vg = seg_sum<S>(acc[0]);
+            float vu = seg_sum<S>(acc[1]);
             if (rv && sl == 0) {
                 if (gb) vg += gb[r];
                 if (ub) vu += ub[r];
@@ -161,7 +236,7 @@ __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int
 
 /* Phase B: grid (x: wave groups over the D rows, y: expert).  Only experts
  * whose down format is `fmt` run (one launch per format present). */
-template <class F, int S>
+template <class F, int S, int TB>
 __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, int nitems, int T,
                                                int rows_per_wave) {
     constexpr int G = 64 / S;
@@ -183,18 +258,10 @@ __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, 
         for (int rs = 0; rs < rows_per_wave; rs += G) {
             const int r = row0 + rs + seg;
             const bool rv = rs + seg < rows_per_wave && r < a.D;
-            float v = 0.f;
-            if (rv) {
-                for (int t = 0; t < T; t++) {
-                    const int item = sl + t * S;
-                    if (item < nitems) {
-                        typename F::X xs = F::load_x(xr, item);
-                        typename F::W wd = F::load_w(dw, (uint32_t)r * rb, item);
-                        v += F::value(wd, xs, item);
-                    }
-                }
-            }
-            v = seg_sum<S>(v);
+            float acc[1] = {0.f};
+            const Buf ws[1] = {dw};
+            row_dots<F, S, TB, 1>(ws, (uint32_t)r * rb, rv, xr, sl, nitems, T, acc);
+            const float v = seg_sum<S>(acc[0]);
             if (rv && sl == 0) a.part[(size_t)p * a.D + r] = w * (v + (db ? db[r] : 0.f));
         }
     }
@@ -235,24 +302,6 @@ __global__ __launch_bounds__(256) void k_isums(const uint8_t *__restrict__ W, ui
 }
 
 /* ======================= small helpers ======================= */
-
-/* RMSNorm of each row (one workgroup per row): out = x * (1/sqrt(ss/n + eps)) * w */
-__global__ __launch_bounds__(256) void k_rms_norm(const float *__restrict__ x, const float *__restrict__ w,
-                                                  float *__restrict__ out, int n, float eps) {
-    __shared__ float red[4];
-    const float *xr = x + (size_t)blockIdx.x * n;
-    float *orow = out + (size_t)blockIdx.x * n;
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += xr[i] * xr[i];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += red[i];
-    const float scale = 1.f / sqrtf(tot / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) orow[i] = (xr[i] * scale) * (w ? w[i] : 1.f);
-}
 
 __global__ __launch_bounds__(256) void k_synth_fill(int kind, uint64_t seed, uint8_t *dst, uint64_t nbytes) {
     const uint64_t nwords = (nbytes + 7) / 8;
@@ -321,6 +370,21 @@ uint32_t row_bytes(int fmt, int ncols) {
         case 32: CALL(32); break; \
         default: CALL(64); break; \
     }
+/* S and the load batch TB (1, 2 or 4 items per lane in flight) */
+#define TG_DISPATCH_TB(TB_, S_, CALL)   \
+    switch (TB_) {                      \
+        case 1: CALL(S_, 1); break;     \
+        case 2: CALL(S_, 2); break;     \
+        default: CALL(S_, 4); break;    \
+    }
+#define TG_DISPATCH_ST(S_, TB_, CALL)                  \
+    switch (S_) {                                      \
+        case 8: TG_DISPATCH_TB(TB_, 8, CALL) break;    \
+        case 16: TG_DISPATCH_TB(TB_, 16, CALL) break;  \
+        case 32: TG_DISPATCH_TB(TB_, 32, CALL) break;  \
+        default: TG_DISPATCH_TB(TB_, 64, CALL) break;  \
+    }
+static int pick_TB(int T) { return T >= 3 ? 4 : T; }
 
 #define TG_DISPATCH_F(fmt, BODY)                    \
     switch (fmt) {                                  \
@@ -347,8 +411,10 @@ void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *b
     const int rpw = G * 2;
     const int waves = (nrows + rpw - 1) / rpw;
     dim3 grid((waves + 3) / 4);
-#define CALL(S_) hipLaunchKernelGGL((k_gemv<F, S_>), grid, dim3(256), 0, st, W, rb, nrows, bias, x, k, y, ystride, nitems, T, rpw)
-    TG_DISPATCH_F(fmt, TG_DISPATCH_S(S, CALL))
+    const int TB = pick_TB(T);
+#define CALL(S_, TB_) \
+    hipLaunchKernelGGL((k_gemv<F, S_, TB_>), grid, dim3(256), 0, st, W, rb, nrows, bias, x, k, y, ystride, nitems, T, rpw)
+    TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
 #undef CALL
 }
 
@@ -383,10 +449,12 @@ static bool grouped_fits(const MoeArgs &a) {
 }
 
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
-                const std::function<void(int)> *mark) {
+                const std::function<void(int)> *mark, bool quantize_x) {
     /* 1. quantize the k input rows */
-    launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
-    if (mark) (*mark)(1);
+    if (quantize_x) {
+        launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
+        if (mark) (*mark)(1);
+    }
     /* 2. phase A: MXFP4 experts with many pairs take the MFMA kernel, which
      * reads each weight block once for up to 64 pairs */
     const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
@@ -400,8 +468,9 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         const int rpw = 64 / S;
         const int waves = (a.I + rpw - 1) / rpw;
         dim3 grid((waves + 3) / 4, a.n);
-#define CALL(S_) hipLaunchKernelGGL((k_moe_a<F, S_>), grid, dim3(256), 0, st, a, nitems, T, rpw)
-        TG_DISPATCH_F(a.gate_fmt, TG_DISPATCH_S(S, CALL))
+        const int TB = pick_TB(T);
+#define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_a<F, S_, TB_>), grid, dim3(256), 0, st, a, nitems, T, rpw)
+        TG_DISPATCH_F(a.gate_fmt, TG_DISPATCH_ST(S, TB, CALL))
 #undef CALL
     }
     if (mark) (*mark)(2);
@@ -423,8 +492,9 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         const int waves = (a.D + rpw - 1) / rpw;
         const uint32_t rb = row_bytes(fmt, a.I);
         dim3 grid((waves + 3) / 4, a.n);
-#define CALL(S_) hipLaunchKernelGGL((k_moe_b<F, S_>), grid, dim3(256), 0, st, a, fmt, rb, nitems, T, rpw)
-        TG_DISPATCH_F(fmt, TG_DISPATCH_S(S, CALL))
+        const int TB = pick_TB(T);
+#define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_b<F, S_, TB_>), grid, dim3(256), 0, st, a, fmt, rb, nitems, T, rpw)
+        TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
 #undef CALL
     }
     if (mark) (*mark)(4);
@@ -434,8 +504,18 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
     if (mark) (*mark)(5);
 }
 
+static int rms_waves(int n) { return std::min(RMS_WAVES, (n + 255) / 256); }
+
+bool rms_norm_fits(int n) { return n > 0 && n <= RMS_WAVES * RMS_BPW * 256; }
+
 void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st) {
-    hipLaunchKernelGGL(k_rms_norm, dim3(nrows), dim3(256), 0, st, x, w, out, n, eps);
+    Q8Rows none = {};
+    hipLaunchKernelGGL(k_rms_norm_q8, dim3(nrows), dim3(64 * rms_waves(n)), 0, st, x, w, out, n, eps, none);
+}
+
+void launch_rms_norm_q8(const float *x, const float *w, float *out, int nrows, int n, float eps, const Q8Rows &q,
+                        hipStream_t st) {
+    hipLaunchKernelGGL(k_rms_norm_q8, dim3(nrows), dim3(64 * rms_waves(n)), 0, st, x, w, out, n, eps, q);
 }
 
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st) {
