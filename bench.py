@@ -282,7 +282,9 @@ def configs_probe(tg, iters=20):
                         (tg_hip_moe_plan_run)
       gptoss_decode     gpt-oss-120b-shaped step: 36 layers x top-4 of 128
                         resident MXFP4 experts (D = I = 2880, biases, clamped
-                        SwiGLU), h <- h + MoE(RMSNorm(h)), HIP-graph mode
+                        SwiGLU), h <- h + MoE(RMSNorm(h)), as one persistent
+                        launch (and, for comparison, the graph of per-layer
+                        kernels)
       gptoss_prefill    64 tokens through one gpt-oss layer (top-4 each): the
                         int8 MFMA expert phases, and for comparison the
                         per-pair kernels"""
@@ -342,19 +344,28 @@ def configs_probe(tg, iters=20):
     h.upload(rng.standard_normal(GD).astype(np.float32))
     parr = (ctypes.c_void_p * GL)(*plans)
     narr = (ctypes.c_void_p * GL)(*[a.ptr for a in norms])
-    step = lib.tg_hip_decode_create(ctypes.addressof(parr), GL, ctypes.addressof(narr), ctypes.c_float(1e-5), h.ptr, 1)
-    if not step:
-        raise RuntimeError(tg.last_error())
-    for _ in range(3):
-        lib.tg_hip_decode_run(step, None)
-    ms = lib.tg_hip_decode_time(step, iters) / iters
     step_b = GL * GK * exp_b
+    times = {}
+    for mode, name in ((2, "persistent"), (1, "graph")):
+        step = lib.tg_hip_decode_create(ctypes.addressof(parr), GL, ctypes.addressof(narr), ctypes.c_float(1e-5),
+                                        h.ptr, mode)
+        if not step:
+            raise RuntimeError(tg.last_error())
+        for _ in range(3):
+            lib.tg_hip_decode_run(step, None)
+        times[name] = lib.tg_hip_decode_time(step, iters) / iters
+        if mode == 2 and lib.tg_hip_decode_status(step) != 0:
+            raise RuntimeError("gpt-oss persistent step: an exchange wait timed out")
+        lib.tg_hip_decode_destroy(step)
+    ms = times["persistent"]
     out["gptoss_decode"] = {"layers": GL, "experts_per_layer": GE, "top_k": GK, "dim": GD,
                             "resident_bytes": GL * GE * exp_b, "weight_bytes_per_step": step_b,
-                            "mode": "graph", "ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
+                            "mode": "persistent (k_decode_mx, one launch per token)",
+                            "ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
                             "weight_gbps": round(step_b / (ms * 1e-3) / 1e9, 1),
-                            "hbm_frac": round(step_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-    lib.tg_hip_decode_destroy(step)
+                            "hbm_frac": round(step_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                            "graph_ms_per_step": round(times["graph"], 4),
+                            "graph_tok_s": round(1e3 / times["graph"], 1)}
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
     # 64-token prefill through layer 0
