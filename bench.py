@@ -275,7 +275,7 @@ def _time_calls(lib, fn, iters):
     return lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
 
 
-def configs_probe(tg, iters=20):
+def configs_probe(tg, iters=20, plain=False):
     """The other workloads of this path on their device-resident entry points:
       q4k_matvec        one 768x2048 q4_K GEMV, one row (tg_hip_matmul_dev)
       qwen_layer_plan   one Qwen3 layer, 8 experts, 1 token, per-layer kernels
@@ -284,7 +284,9 @@ def configs_probe(tg, iters=20):
                         resident MXFP4 experts (D = I = 2880, biases, clamped
                         SwiGLU), h <- h + MoE(RMSNorm(h)), as one persistent
                         launch (and, for comparison, the graph of per-layer
-                        kernels)
+                        kernels); plain: the same kernel through a plain
+                        launch and no graph, for profilers (rocprofv3 fails
+                        on cooperative launches and on graph replays)
       gptoss_prefill    64 tokens through one gpt-oss layer (top-4 each): the
                         int8 MFMA expert phases, and for comparison the
                         per-pair kernels"""
@@ -346,7 +348,7 @@ def configs_probe(tg, iters=20):
     narr = (ctypes.c_void_p * GL)(*[a.ptr for a in norms])
     step_b = GL * GK * exp_b
     times = {}
-    for mode, name in ((2, "persistent"), (1, "graph")):
+    for mode, name in ((3, "persistent"),) if plain else ((2, "persistent"), (1, "graph")):
         step = lib.tg_hip_decode_create(ctypes.addressof(parr), GL, ctypes.addressof(narr), ctypes.c_float(1e-5),
                                         h.ptr, mode)
         if not step:
@@ -354,7 +356,7 @@ def configs_probe(tg, iters=20):
         for _ in range(3):
             lib.tg_hip_decode_run(step, None)
         times[name] = lib.tg_hip_decode_time(step, iters) / iters
-        if mode == 2 and lib.tg_hip_decode_status(step) != 0:
+        if mode >= 2 and lib.tg_hip_decode_status(step) != 0:
             raise RuntimeError("gpt-oss persistent step: an exchange wait timed out")
         lib.tg_hip_decode_destroy(step)
     ms = times["persistent"]
@@ -364,8 +366,8 @@ def configs_probe(tg, iters=20):
                             "ms_per_step": round(ms, 4), "tok_s": round(1e3 / ms, 1),
                             "weight_gbps": round(step_b / (ms * 1e-3) / 1e9, 1),
                             "hbm_frac": round(step_b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                            "graph_ms_per_step": round(times["graph"], 4),
-                            "graph_tok_s": round(1e3 / times["graph"], 1)}
+                            "graph_ms_per_step": round(times["graph"], 4) if "graph" in times else None,
+                            "graph_tok_s": round(1e3 / times["graph"], 1) if "graph" in times else None}
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
     # 64-token prefill through layer 0
@@ -706,7 +708,7 @@ def main():
         result["cache_load"] = loader_probe(tg)
     if not args.no_configs:
         log("other workloads ...")
-        result["other_workloads"] = configs_probe(tg)
+        result["other_workloads"] = configs_probe(tg, plain=args.mode == "persistent-plain")
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(routes, min(args.cpu_layers, layers))
