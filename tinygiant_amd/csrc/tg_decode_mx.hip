@@ -27,10 +27,11 @@
  * The MXFP4 blocks go straight from memory into the MFMA's A operand: a
  * lane's 17 bytes are one block's e8m0 scale and its 16 code bytes, which the
  * MFMA takes as 32 e2m1 values under that scale.  q8(x) enters as two fp8
- * operands, x = 16 (x >> 4) + (x & 15) (both halves exact in e4m3), so the
- * products are exact and each block's integer sum is the reference's; the
- * f32 additions are grouped differently (four blocks inside an MFMA, then
- * per 128 values and per wave), which the f32 bar covers.
+ * columns of the B operand, x = 16 (x >> 4) + (x & 15) (both halves exact in
+ * e4m3, column scales 16 and 1), so the products are exact and each block's
+ * integer sum is the reference's; the f32 additions are grouped differently
+ * (four blocks inside an MFMA, then per 128 values, per half and per wave),
+ * which the f32 bar covers.
  *
  * Weights load into registers ahead of use: this layer's down blocks during
  * the hidden exchange (4), the next layer's gate/up blocks and RMSNorm weight
@@ -165,27 +166,28 @@ __device__ inline void q8_split_block(float v0, float v1, float v2, float v3, in
     if (lane == 0) q.d[b] = amax / 127.f;
 }
 
-/* The B operands (fp8 hi and lo halves of q8(x)) of chunk c for lane group
- * g = lane / 16: bytes 0..15 are values 16 g .. 16 g + 15 of the chunk and
- * bytes 16..31 values 64 + 16 g .. in MFMA K order. */
-__device__ inline void load_b(const LdsQ &q, int c, int g, v8i &bh, v8i &bl) {
+/* The B operand of chunk c for this lane: column 0 holds the fp8 hi halves of
+ * q8(x), column 1 the lo halves, columns 2..15 zeros.  Lane l supplies
+ * column l % 16 for K group g = l / 16: bytes 0..15 are values 16 g .. 16 g
+ * + 15 of the chunk and bytes 16..31 values 64 + 16 g .. in MFMA K order. */
+__device__ inline v8i load_b(const LdsQ &q, int c, int lane) {
+    const int g = lane >> 4, col = lane & 15, part = col == 1 ? 1 : 0;
     const int b0 = 4 * c + (g >> 1), b1 = b0 + 2, o = 16 * (g & 1);
-    const u32x4 h0 = *reinterpret_cast<const u32x4 *>(&q.sp[b0][0][o]);
-    const u32x4 h1 = *reinterpret_cast<const u32x4 *>(&q.sp[b1][0][o]);
-    const u32x4 l0 = *reinterpret_cast<const u32x4 *>(&q.sp[b0][1][o]);
-    const u32x4 l1 = *reinterpret_cast<const u32x4 *>(&q.sp[b1][1][o]);
-    bh = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-    bl = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+    const u32x4 x0 = *reinterpret_cast<const u32x4 *>(&q.sp[b0][part][o]);
+    const u32x4 x1 = *reinterpret_cast<const u32x4 *>(&q.sp[b1][part][o]);
+    const int on = col < 2 ? -1 : 0;
+    return v8i{(int)x0.x & on, (int)x0.y & on, (int)x0.z & on, (int)x0.w & on,
+               (int)x1.x & on, (int)x1.y & on, (int)x1.z & on, (int)x1.w & on};
 }
 
-/* acc += d * (block-scaled A . B) for one chunk: two chained MFMAs, hi half
- * under scale 16, lo half under scale 1. */
-__device__ inline void mma_chunk(const MxBlk &a, const v8i &bh, const v8i &bl, float d, v4f &acc) {
+/* acc += d * (block-scaled A . B) for one chunk, one MFMA: column 0 is the
+ * hi half under scale 16, column 1 the lo half under scale 1 (sb is the
+ * lane's B scale); the two columns are added in the row reduction. */
+__device__ inline void mma_chunk(const MxBlk &a, const v8i &bx, int sb, float d, v4f &acc) {
     const v8i av = v8i{(int)a.c.x, (int)a.c.y, (int)a.c.z, (int)a.c.w, 0, 0, 0, 0};
     const int e = (int)(a.e & 0xFFu);
     const v4f z = {0.f, 0.f, 0.f, 0.f};
-    v4f r = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bh, z, FMT_FP4, FMT_FP8, 0, e, 0, SCALE_16);
-    r = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bl, r, FMT_FP4, FMT_FP8, 0, e, 0, SCALE_1);
+    const v4f r = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bx, z, FMT_FP4, FMT_FP8, 0, e, 0, sb);
     acc[0] += d * r[0];
     acc[1] += d * r[1];
     acc[2] += d * r[2];
@@ -206,7 +208,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     __shared__ __attribute__((aligned(16))) float hid[D];     /* the expert's hidden vector */
     __shared__ LdsQ sx, sh;                                   /* fp8 images of q8(x) and q8(hidden) */
     __shared__ float ssq[NRK];                                /* sum of h^2 of each 45-row slice */
-    __shared__ float red[NW][2 * NG][16];                     /* per-wave partial row sums */
+    __shared__ float red[NW][2 * NG][2][16];                  /* per-wave partial row sums: hi and lo columns */
     __shared__ float pp[NX][RS];                              /* weighted down values of the 8 XCDs */
     __shared__ int lds_fail;
     __shared__ DecodeLayerMx lys[MAX_LAYERS];
@@ -220,6 +222,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     const int xc = wg % NX, rk = wg / NX;        /* XCD and rank in it */
     const int xe = xc >> 1, R = NR * (xc & 1) + rk;   /* expert slot and rank in the expert */
     Buf sl = make_buf(slots, NSLOTS * 16u);
+    const int sb = (lane & 15) == 0 ? SCALE_16 : SCALE_1;   /* B scale of this lane's column */
 
     MxBlk wa[CPW][2 * NG];   /* gate (units 0..2) and up (3..5) blocks of the wave's chunks */
     MxBlk wb[CPW][NG];       /* down blocks */
@@ -391,9 +394,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         }
         /* ---- 2: RMSNorm (weight or 1) + q8 + fp8 halves of x ---- */
         {
-            float tot = 0.f;
-#pragma unroll 8
-            for (int i = 0; i < NRK; i++) tot += ssq[i];
+            const float tot = wave_sum(ssq[lane]);   /* the 64 slice sums, one per lane */
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
             if (rec && wg == 0)
                 for (int t = threadIdx.x; t < D; t += NT) reinterpret_cast<float *>(rec + DecodeDebugMx::HIN)[t] = hx[t];
@@ -411,18 +412,17 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             for (int i = 0; i < CPW; i++) {
                 const int c = CPW * wave + i;
                 if (c >= NCH) break;   /* uniform */
-                v8i bh, bl;
-                load_b(sx, c, lane >> 4, bh, bl);
+                const v8i bx = load_b(sx, c, lane);
                 const float d = sx.d[c >> 1];
 #pragma unroll
-                for (int u = 0; u < 2 * NG; u++) mma_chunk(wa[i][u], bh, bl, d, acc[u]);
+                for (int u = 0; u < 2 * NG; u++) mma_chunk(wa[i][u], bx, sb, d, acc[u]);
             }
-            /* column 0 of the MFMA result: lane 16 g holds rows 4 g .. 4 g + 3 */
-            if ((lane & 15) == 0)
+            /* columns 0 and 1 of the MFMA results: lane 16 g + col holds rows 4 g .. 4 g + 3 */
+            if ((lane & 15) < 2)
 #pragma unroll
                 for (int u = 0; u < 2 * NG; u++)
 #pragma unroll
-                    for (int v = 0; v < 4; v++) red[wave][u][4 * (lane >> 4) + v] = acc[u][v];
+                    for (int v = 0; v < 4; v++) red[wave][u][lane & 15][4 * (lane >> 4) + v] = acc[u][v];
         }
         __syncthreads();
         if (tw) tr[3] = wall_clock64();
@@ -442,8 +442,8 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 float g = 0.f, u = 0.f;
 #pragma unroll
                 for (int w = 0; w < NW; w++) {
-                    g += red[w][gi][ri];
-                    u += red[w][NG + gi][ri];
+                    g += red[w][gi][0][ri] + red[w][gi][1][ri];
+                    u += red[w][NG + gi][0][ri] + red[w][NG + gi][1][ri];
                 }
                 hid[row] = act_fn(TG_ACT_GPTOSS, g + gbv, u + ubv);
             }
@@ -497,17 +497,16 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             for (int i = 0; i < CPW; i++) {
                 const int c = CPW * wave + i;
                 if (c >= NCH) break;   /* uniform */
-                v8i bh, bl;
-                load_b(sh, c, lane >> 4, bh, bl);
+                const v8i bx = load_b(sh, c, lane);
                 const float d = sh.d[c >> 1];
 #pragma unroll
-                for (int u = 0; u < NG; u++) mma_chunk(wb[i][u], bh, bl, d, acc[u]);
+                for (int u = 0; u < NG; u++) mma_chunk(wb[i][u], bx, sb, d, acc[u]);
             }
-            if ((lane & 15) == 0)
+            if ((lane & 15) < 2)
 #pragma unroll
                 for (int u = 0; u < NG; u++)
 #pragma unroll
-                    for (int v = 0; v < 4; v++) red[wave][u][4 * (lane >> 4) + v] = acc[u][v];
+                    for (int v = 0; v < 4; v++) red[wave][u][lane & 15][4 * (lane >> 4) + v] = acc[u][v];
         }
         __syncthreads();
         if (tw) tr[6] = wall_clock64();
@@ -527,7 +526,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 const int gi = clv >> 4, ri = clv & 15;
                 float v = 0.f;
 #pragma unroll
-                for (int w = 0; w < NW; w++) v += red[w][gi][ri];
+                for (int w = 0; w < NW; w++) v += red[w][gi][0][ri] + red[w][gi][1][ri];
                 pp[xc][clv] = ly.w[xe] * (v + dbv);
             }
             __builtin_amdgcn_wave_barrier();
