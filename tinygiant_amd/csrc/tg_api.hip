@@ -214,7 +214,7 @@ Q8Rows q8_view(uint8_t *base, int nrows, int ncols, const float *f) {
 struct HostPlan {
     int n = 0, k = 0, P = 0, D = 0, I = 0, act = 0, gate_fmt = 0;
     std::vector<uint64_t> gate, up, down, gbias, ubias, dbias;
-    std::vector<int> down_fmt, p_off, p_row, r_off, r_pair;
+    std::vector<int> down_fmt, p_off, p_row, p_exp, r_off, r_pair;
     std::vector<float> p_w;
     bool has_gb = false, has_ub = false, has_db = false;
     std::vector<int> fmts_present;
@@ -253,6 +253,7 @@ bool validate_moe(int gate_fmt, const int *down_fmts, int n, int k, int D, int I
 void build_pairs(HostPlan &h, const float *row_weights) {
     h.p_off.assign(h.n + 1, 0);
     h.p_row.clear();
+    h.p_exp.clear();
     h.p_w.clear();
     std::vector<std::vector<int>> per_row(h.k);
     for (int e = 0; e < h.n; e++) {
@@ -262,6 +263,7 @@ void build_pairs(HostPlan &h, const float *row_weights) {
             if (w == 0.f) continue;
             per_row[r].push_back((int)h.p_row.size());
             h.p_row.push_back(r);
+            h.p_exp.push_back(e);
             h.p_w.push_back(w);
         }
     }
@@ -295,7 +297,7 @@ Layout plan_layout(const HostPlan &h) {
     size_t t = 0;
     t += 6 * (size_t)n * 8;                 /* gate, up, down, gbias, ubias, dbias */
     t += (size_t)n * 4;                     /* down_fmt */
-    t += (size_t)(n + 1) * 4 + (size_t)P * 4 + (size_t)P * 4 + (size_t)(k + 1) * 4 + (size_t)P * 4;
+    t += (size_t)(n + 1) * 4 + (size_t)P * 4 * 4 + (size_t)(k + 1) * 4 + 8;   /* p_off, p_row, p_exp, p_w, r_off, r_pair */
     t += (size_t)4 * (n + 1) * 4 + 16;      /* active expert lists and their cost prefixes */
     L.tables_len = t + 64;
     b.take(L.tables_len);
@@ -338,6 +340,7 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     a.down_fmt = (const int *)put(h.down_fmt.data(), (size_t)n * 4);
     a.p_off = (const int *)put(h.p_off.data(), (size_t)(n + 1) * 4);
     a.p_row = (const int *)put(h.p_row.data(), (size_t)h.P * 4);
+    a.p_exp = (const int *)put(h.p_exp.data(), (size_t)h.P * 4);
     a.p_w = (const float *)put(h.p_w.data(), (size_t)h.P * 4);
     a.r_off = (const int *)put(h.r_off.data(), (size_t)(k + 1) * 4);
     a.r_pair = (const int *)put(h.r_pair.data(), (size_t)h.P * 4);

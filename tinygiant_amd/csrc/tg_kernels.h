@@ -23,6 +23,7 @@ struct MoeArgs {
     const uint64_t *gbias, *ubias, *dbias;  /* [n] or null; entries may be 0 */
     const int *p_off;                       /* [n+1] first pair of each expert */
     const int *p_row;                       /* [P] input row of the pair */
+    const int *p_exp;                       /* [P] expert of the pair */
     const float *p_w;                       /* [P] router weight of the pair */
     const int *r_off;                       /* [k+1] first entry of each output row */
     const int *r_pair;                      /* [P] pairs of each output row, expert order */

@@ -195,14 +195,14 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uin
 
 /* ======================= MoE phases ======================= */
 
-/* Phase A: grid (x: wave groups over the I rows, y: expert).  hidden[p][r] for
- * every pair p of the expert. */
+/* Phase A: grid (x: wave groups over the I rows, y: pair).  hidden[p][r] of
+ * the pair's expert; the pairs of one expert run side by side (their weight
+ * rows come from the L2 after the first). */
 template <class F, int S, int TB>
 __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int rows_per_wave) {
     constexpr int G = 64 / S;
-    const int e = blockIdx.y;
-    const int p0 = a.p_off[e], ne = a.p_off[e + 1] - p0;
-    if (ne == 0) return;
+    const int p = blockIdx.y;
+    const int e = a.p_exp[p];
     const int lane = threadIdx.x & 63;
     const int seg = lane / S, sl = lane % S;
     const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -214,8 +214,7 @@ __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int
     Buf uw = make_buf((const void *)a.up[e], (uint32_t)mbytes);
     const float *gb = a.gbias ? (const float *)a.gbias[e] : nullptr;
     const float *ub = a.ubias ? (const float *)a.ubias[e] : nullptr;
-    for (int j = 0; j < ne; j++) {
-        const int p = p0 + j;
+    {
         Q8Row xr = q8_row(a.xq, a.p_row[p]);
         for (int rs = 0; rs < rows_per_wave; rs += G) {
             const int r = row0 + rs + seg;
@@ -234,16 +233,15 @@ __global__ __launch_bounds__(256) void k_moe_a(MoeArgs a, int nitems, int T, int
     }
 }
 
-/* Phase B: grid (x: wave groups over the D rows, y: expert).  Only experts
- * whose down format is `fmt` run (one launch per format present). */
+/* Phase B: grid (x: wave groups over the D rows, y: pair).  Only pairs whose
+ * expert's down format is `fmt` run (one launch per format present). */
 template <class F, int S, int TB>
 __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, int nitems, int T,
                                                int rows_per_wave) {
     constexpr int G = 64 / S;
-    const int e = blockIdx.y;
+    const int p = blockIdx.y;
+    const int e = a.p_exp[p];
     if (a.down_fmt[e] != fmt) return;
-    const int p0 = a.p_off[e], ne = a.p_off[e + 1] - p0;
-    if (ne == 0) return;
     const int lane = threadIdx.x & 63;
     const int seg = lane / S, sl = lane % S;
     const int wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -251,8 +249,7 @@ __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, 
     if (row0 >= a.D) return;
     Buf dw = make_buf((const void *)a.down[e], (uint32_t)((size_t)a.D * rb));
     const float *db = a.dbias ? (const float *)a.dbias[e] : nullptr;
-    for (int j = 0; j < ne; j++) {
-        const int p = p0 + j;
+    {
         Q8Row xr = q8_row(a.hq, p);
         const float w = a.p_w[p];
         for (int rs = 0; rs < rows_per_wave; rs += G) {
@@ -467,7 +464,7 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         const int S = pick_S(nitems, &T);
         const int rpw = 64 / S;
         const int waves = (a.I + rpw - 1) / rpw;
-        dim3 grid((waves + 3) / 4, a.n);
+        dim3 grid((waves + 3) / 4, a.P);
         const int TB = pick_TB(T);
 #define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_a<F, S_, TB_>), grid, dim3(256), 0, st, a, nitems, T, rpw)
         TG_DISPATCH_F(a.gate_fmt, TG_DISPATCH_ST(S, TB, CALL))
@@ -491,7 +488,7 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         const int rpw = 64 / S;
         const int waves = (a.D + rpw - 1) / rpw;
         const uint32_t rb = row_bytes(fmt, a.I);
-        dim3 grid((waves + 3) / 4, a.n);
+        dim3 grid((waves + 3) / 4, a.P);
         const int TB = pick_TB(T);
 #define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_b<F, S_, TB_>), grid, dim3(256), 0, st, a, fmt, rb, nitems, T, rpw)
         TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
