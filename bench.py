@@ -641,7 +641,7 @@ def main():
         kms = (ctypes.c_float * 6)()
         kn = (ctypes.c_int * 6)()
         lib.tg_hip_decode_kernel_times(step, kms, kn)
-        names = ["rms_norm", "quantize_x", "gate_up", "quantize_h", "down", "combine"]
+        names = ["rms_norm_q8", "quantize_x", "gate_up", "quantize_h", "down", "combine"]
         per_kernel = {names[i]: {"avg_us": round(kms[i] / max(kn[i], 1) * 1e3, 2), "launches": kn[i]}
                       for i in range(6)}
         kernel_name = "k_moe_a<FQ4K,32> (gate+up+SiLU, 8 experts)"
