@@ -931,7 +931,7 @@ TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k,
  * Scratch: q8 of the input | Q, K, V projections | roped Q | chunk partials |
  * attention output | its q8. */
 struct AttnLayout {
-    size_t xq, qkv, q, part, att, aq, total;
+    size_t xq, qkv, part, att, aq, total;
 };
 
 static AttnLayout attn_layout(int embed_dim, int n_heads, int n_kv, int head_dim, int kv_max) {
@@ -941,7 +941,6 @@ static AttnLayout attn_layout(int embed_dim, int n_heads, int n_kv, int head_dim
     const size_t nch = ((size_t)kv_max + ATTN_CHUNK - 1) / ATTN_CHUNK;
     L.xq = b.take(q8_bytes(1, embed_dim));
     L.qkv = b.take((q_dim + 2 * kv_dim) * 4);
-    L.q = b.take(q_dim * 4);
     L.part = b.take((size_t)n_heads * nch * (head_dim + 2) * 4);
     L.att = b.take(q_dim * 4);
     L.aq = b.take(q8_bytes(1, (int)q_dim));
@@ -987,15 +986,30 @@ static void attn_run(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq,
     Q8Rows xq = q8_view(scratch + L.xq, 1, embed_dim, input);
     if (fmt_q != TG_FMT_F16 || fmt_k != TG_FMT_F16 || fmt_v != TG_FMT_F16)
         launch_quantize(input, embed_dim, 1, embed_dim, xq, st);
-    launch_gemv(fmt_q, (const uint8_t *)wq, q_dim, embed_dim, bq, xq, 1, qkv, q_dim, st);
-    launch_gemv(fmt_k, (const uint8_t *)wk, kv_dim, embed_dim, bk, xq, 1, qkv + q_dim, kv_dim, st);
-    launch_gemv(fmt_v, (const uint8_t *)wv, kv_dim, embed_dim, bv, xq, 1, qkv + q_dim + kv_dim, kv_dim, st);
+    /* Q, K and V projections: one launch per distinct format */
+    const int fmts[3] = {fmt_q, fmt_k, fmt_v};
+    const GemvJob all[3] = {{(const uint8_t *)wq, bq, qkv, q_dim, q_dim},
+                            {(const uint8_t *)wk, bk, qkv + q_dim, kv_dim, kv_dim},
+                            {(const uint8_t *)wv, bv, qkv + q_dim + kv_dim, kv_dim, kv_dim}};
+    for (int i = 0; i < 3; i++) {
+        bool first = true;
+        for (int j = 0; j < i; j++) first &= fmts[j] != fmts[i];
+        if (!first) continue;
+        GemvJobs jobs;
+        int nj = 0;
+        for (int j = i; j < 3; j++)
+            if (fmts[j] == fmts[i]) jobs.j[nj++] = all[j];
+        launch_gemv_multi(fmts[i], jobs, nj, embed_dim, xq, 1, st);
+    }
     float *att = (float *)(scratch + L.att);
-    launch_attention_core(qkv, q_norm_w, k_norm_w, sinks, kv_k, kv_v, kv_len, kv_max, window, rope_cos_row,
-                          rope_sin_row, n_heads, n_kv, head_dim, eps, (float *)(scratch + L.q),
-                          (float *)(scratch + L.part), att, st);
     Q8Rows aq = q8_view(scratch + L.aq, 1, q_dim, att);
-    if (fmt_o != TG_FMT_F16) launch_quantize(att, q_dim, 1, q_dim, aq, st);
+    /* attention; q8 of its output fused into the combine where the block
+     * layout allows */
+    const bool fuse_q8 = fmt_o != TG_FMT_F16 && attention_combine_q8_ok(n_heads, head_dim);
+    launch_attention_core(qkv, q_norm_w, k_norm_w, sinks, kv_k, kv_v, kv_len, kv_max, window, rope_cos_row,
+                          rope_sin_row, n_heads, n_kv, head_dim, eps, (float *)(scratch + L.part), att,
+                          fuse_q8 ? &aq : nullptr, st);
+    if (fmt_o != TG_FMT_F16 && !fuse_q8) launch_quantize(att, q_dim, 1, q_dim, aq, st);
     launch_gemv(fmt_o, (const uint8_t *)wo, embed_dim, q_dim, bo, aq, 1, output, embed_dim, st);
     if (att_out) HIPCHECK(hipMemcpyAsync(att_out, att, (size_t)q_dim * 4, hipMemcpyDeviceToDevice, st));
 }

@@ -177,6 +177,41 @@ struct Q8Row {
     Buf qs, d, s32, s16, f;
 };
 
+/* q8 of one 256-value block held by a wave, lane l owning values 4l..4l+3
+ * (quantize_q8, csrc/libtinygiant.c:169-208): scale amax/127, quants
+ * rint(v * 127/amax), 16- and 32-element sums and the block total, written to
+ * block b of row r. */
+__device__ inline void q8_block_store(float v0, float v1, float v2, float v3, int lane, const Q8Rows &out, int r,
+                                      int b) {
+    float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float sc = amax / 127.f;                  /* correctly rounded */
+    const float inv = amax > 0.f ? 127.f / amax : 0.f;
+    int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
+    int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
+    uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                      ((uint32_t)(q3 & 0xFF) << 24);
+    const int nb = out.nb;
+    int8_t *qrow = out.qs + ((size_t)r * nb + b) * 256;
+    reinterpret_cast<uint32_t *>(qrow)[lane] = packed;
+    int s = q0 + q1 + q2 + q3;
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);            /* 16-element sum */
+    int s32 = s + __shfl_xor(s, 4, 64);   /* 32-element sum */
+    int tot = s32;
+    tot += __shfl_xor(tot, 8, 64);
+    tot += __shfl_xor(tot, 16, 64);
+    tot += __shfl_xor(tot, 32, 64);
+    const size_t rb = (size_t)r * nb + b;
+    if ((lane & 3) == 0) out.s16[rb * 16 + (lane >> 2)] = s;
+    if ((lane & 7) == 0) out.s32[rb * 8 + (lane >> 3)] = s32;
+    if (lane == 0) {
+        out.d[rb] = sc;
+        out.sum[rb] = tot;
+    }
+}
+
 __device__ inline Q8Row q8_row(const Q8Rows &a, int r) {
     Q8Row x;
     x.qs = make_buf(a.qs + (size_t)r * a.nb * 256, (uint32_t)a.nb * 256);

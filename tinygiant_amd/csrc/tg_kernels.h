@@ -49,6 +49,19 @@ uint32_t row_bytes(int fmt, int ncols);
 void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st);
 void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *bias, const Q8Rows &x, int k,
                  float *y, long ystride, hipStream_t st);
+/* up to three matrices of one format and width (ncols) against the same q8
+ * rows, one launch: y_j[r] = dot(W_j row r, x) + bias_j[r] */
+struct GemvJob {
+    const uint8_t *W;
+    const float *bias;
+    float *y;
+    long ystride;
+    int nrows;
+};
+struct GemvJobs {
+    GemvJob j[3];
+};
+void launch_gemv_multi(int fmt, const GemvJobs &jobs, int njobs, int ncols, const Q8Rows &x, int k, hipStream_t st);
 void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows &x, int nsums_row, int32_t *out,
                   hipStream_t st);
 /* `mark`, when given, is called after each kernel with its class:

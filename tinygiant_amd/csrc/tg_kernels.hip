@@ -30,41 +30,6 @@ namespace tg {
 
 /* ======================= q8 quantization ======================= */
 
-/* q8 of one 256-value block held by a wave, lane l owning values 4l..4l+3
- * (quantize_q8, csrc/libtinygiant.c:169-208): scale amax/127, quants
- * rint(v * 127/amax), 16- and 32-element sums and the block total, written to
- * block b of row r. */
-__device__ inline void q8_block_store(float v0, float v1, float v2, float v3, int lane, const Q8Rows &out, int r,
-                                      int b) {
-    float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const float sc = amax / 127.f;                  /* correctly rounded */
-    const float inv = amax > 0.f ? 127.f / amax : 0.f;
-    int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
-    int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
-    uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-                      ((uint32_t)(q3 & 0xFF) << 24);
-    const int nb = out.nb;
-    int8_t *qrow = out.qs + ((size_t)r * nb + b) * 256;
-    reinterpret_cast<uint32_t *>(qrow)[lane] = packed;
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);            /* 16-element sum */
-    int s32 = s + __shfl_xor(s, 4, 64);   /* 32-element sum */
-    int tot = s32;
-    tot += __shfl_xor(tot, 8, 64);
-    tot += __shfl_xor(tot, 16, 64);
-    tot += __shfl_xor(tot, 32, 64);
-    const size_t rb = (size_t)r * nb + b;
-    if ((lane & 3) == 0) out.s16[rb * 16 + (lane >> 2)] = s;
-    if ((lane & 7) == 0) out.s32[rb * 8 + (lane >> 3)] = s32;
-    if (lane == 0) {
-        out.d[rb] = sc;
-        out.sum[rb] = tot;
-    }
-}
-
 /* One wave per 256-value block: lane l owns values 4l..4l+3. */
 __global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x, int ncols, int nrows,
                                                      long xstride, Q8Rows out) {
@@ -169,9 +134,9 @@ __device__ inline void row_dots(const Buf (&w)[NM], uint32_t roff, bool rv, cons
  *   y[j*ystride + r] = dot(W[r], x_j) + bias[r]
  * Each wave takes `rows_per_wave` consecutive rows in steps of 64/S. */
 template <class F, int S, int TB>
-__global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uint32_t rb, int nrows,
-                                              const float *__restrict__ bias, Q8Rows x, int k, float *y,
-                                              long ystride, int nitems, int T, int rows_per_wave) {
+__device__ inline void gemv_rows(const uint8_t *__restrict__ W, uint32_t rb, int nrows,
+                                 const float *__restrict__ bias, const Q8Rows &x, int k, float *y, long ystride,
+                                 int nitems, int T, int rows_per_wave) {
     constexpr int G = 64 / S;
     const int lane = threadIdx.x & 63;
     const int seg = lane / S, sl = lane % S;
@@ -191,6 +156,22 @@ __global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uin
             if (rv && sl == 0) y[(size_t)j * ystride + r] = v + (bias ? bias[r] : 0.f);
         }
     }
+}
+
+template <class F, int S, int TB>
+__global__ __launch_bounds__(256) void k_gemv(const uint8_t *__restrict__ W, uint32_t rb, int nrows,
+                                              const float *__restrict__ bias, Q8Rows x, int k, float *y,
+                                              long ystride, int nitems, int T, int rows_per_wave) {
+    gemv_rows<F, S, TB>(W, rb, nrows, bias, x, k, y, ystride, nitems, T, rows_per_wave);
+}
+
+/* Several matrices of one format and width against the same rows in one
+ * launch: blockIdx.y picks the matrix. */
+template <class F, int S, int TB>
+__global__ __launch_bounds__(256) void k_gemv_multi(GemvJobs jobs, uint32_t rb, Q8Rows x, int k, int nitems, int T,
+                                                    int rows_per_wave) {
+    const GemvJob &jb = jobs.j[blockIdx.y];
+    gemv_rows<F, S, TB>(jb.W, rb, jb.nrows, jb.bias, x, k, jb.y, jb.ystride, nitems, T, rows_per_wave);
 }
 
 /* ======================= MoE phases ======================= */
@@ -411,6 +392,23 @@ void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *b
     const int TB = pick_TB(T);
 #define CALL(S_, TB_) \
     hipLaunchKernelGGL((k_gemv<F, S_, TB_>), grid, dim3(256), 0, st, W, rb, nrows, bias, x, k, y, ystride, nitems, T, rpw)
+    TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
+#undef CALL
+}
+
+void launch_gemv_multi(int fmt, const GemvJobs &jobs, int njobs, int ncols, const Q8Rows &x, int k, hipStream_t st) {
+    int T;
+    const int nitems = items_per_row(fmt, ncols);
+    const int S = pick_S(nitems, &T);
+    const uint32_t rb = row_bytes(fmt, ncols);
+    const int rpw = (64 / S) * 2;
+    int most = 0;
+    for (int i = 0; i < njobs; i++) most = std::max(most, jobs.j[i].nrows);
+    const int waves = (most + rpw - 1) / rpw;
+    dim3 grid((waves + 3) / 4, njobs);
+    const int TB = pick_TB(T);
+#define CALL(S_, TB_) \
+    hipLaunchKernelGGL((k_gemv_multi<F, S_, TB_>), grid, dim3(256), 0, st, jobs, rb, x, k, nitems, T, rpw)
     TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
 #undef CALL
 }
