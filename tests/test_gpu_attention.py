@@ -149,12 +149,14 @@ def _check(orc, c, window, got, ref):
 Q4K, Q6K, Q80, F16 = O.FMT_Q4K, O.FMT_Q6K, O.FMT_Q80, O.FMT_F16
 
 
-@pytest.mark.parametrize("kv_len", [0, 31, 300])
+@pytest.mark.parametrize("kv_len", [0, 31, 300, 1500])
 def test_attention_qwen3_shape(tg, orc, kv_len):
     """Qwen3-30B-A3B attention: D 2048, 32 query heads, 4 KV heads of 128,
-    q4_K q/k/o, q6_K v, QK norm, no biases, full attention."""
+    q4_K q/k/o, q6_K v, QK norm, no biases, full attention.  Spans up to 32
+    chunks of 32 positions combine inside the partial kernel; 1501 positions
+    (47 chunks) take the separate combine kernel."""
     say("attention qwen3", kv_len)
-    c = _case(10 + kv_len, 2048, 32, 4, 128, (Q4K, Q4K, Q6K, Q4K), 512, kv_len, norms=True)
+    c = _case(10 + kv_len, 2048, 32, 4, 128, (Q4K, Q4K, Q6K, Q4K), max(512, kv_len + 1), kv_len, norms=True)
     got = _gpu(tg, c, 0)
     _check(orc, c, 0, got, _oracle(orc, c, 0))
     if kv_len == 0:
@@ -162,6 +164,18 @@ def test_attention_qwen3_shape(tg, orc, kv_len):
         _, att, _, vv = got
         for h in range(32):
             assert np.array_equal(att[h * 128:(h + 1) * 128], vv[h // 8, 0])
+
+
+@pytest.mark.parametrize("kv_len", [300, 1500])
+def test_attention_repeat_is_bit_identical(tg, kv_len):
+    """The same call three times gives the same bits: the ticket counters of
+    the folded combine are cleared by every call's projection launch, and no
+    f32 result depends on which workgroup finishes last."""
+    c = _case(80 + kv_len, 2048, 32, 4, 128, (Q4K, Q4K, Q6K, Q4K), kv_len + 1, kv_len, norms=True)
+    runs = [_gpu(tg, c, 0) for _ in range(3)]
+    for got in runs[1:]:
+        for a, b in zip(got, runs[0]):
+            assert a.tobytes() == b.tobytes()
 
 
 @pytest.mark.parametrize("window,kv_len", [(128, 300), (0, 95), (1, 40)])

@@ -928,10 +928,10 @@ TG_API void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_de
 TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k, ncols); }
 
 /* ---- decode attention (tg_attention_v2, csrc/libtinygiant.c:939-983) ----
- * Scratch: q8 of the input | Q, K, V projections | roped Q | chunk partials |
- * attention output | its q8. */
+ * Scratch: q8 of the input | Q, K, V projections | chunk partials |
+ * attention output | its q8 | one ticket counter per KV head. */
 struct AttnLayout {
-    size_t xq, qkv, part, att, aq, total;
+    size_t xq, qkv, part, att, aq, ctr, total;
 };
 
 static AttnLayout attn_layout(int embed_dim, int n_heads, int n_kv, int head_dim, int kv_max) {
@@ -944,6 +944,7 @@ static AttnLayout attn_layout(int embed_dim, int n_heads, int n_kv, int head_dim
     L.part = b.take((size_t)n_heads * nch * (head_dim + 2) * 4);
     L.att = b.take(q_dim * 4);
     L.aq = b.take(q8_bytes(1, (int)q_dim));
+    L.ctr = b.take((size_t)n_kv * 4);
     L.total = b.off;
     return L;
 }
@@ -983,32 +984,43 @@ static void attn_run(int fmt_q, int fmt_k, int fmt_v, int fmt_o, const void *wq,
     const AttnLayout L = attn_layout(embed_dim, n_heads, n_kv, head_dim, kv_max);
     const int q_dim = n_heads * head_dim, kv_dim = n_kv * head_dim;
     float *qkv = (float *)(scratch + L.qkv);
-    Q8Rows xq = q8_view(scratch + L.xq, 1, embed_dim, input);
-    if (fmt_q != TG_FMT_F16 || fmt_k != TG_FMT_F16 || fmt_v != TG_FMT_F16)
-        launch_quantize(input, embed_dim, 1, embed_dim, xq, st);
-    /* Q, K and V projections: one launch per distinct format */
+    unsigned *ctr = (unsigned *)(scratch + L.ctr);
+    /* Q, K and V projections */
     const int fmts[3] = {fmt_q, fmt_k, fmt_v};
     const GemvJob all[3] = {{(const uint8_t *)wq, bq, qkv, q_dim, q_dim},
                             {(const uint8_t *)wk, bk, qkv + q_dim, kv_dim, kv_dim},
                             {(const uint8_t *)wv, bv, qkv + q_dim + kv_dim, kv_dim, kv_dim}};
-    for (int i = 0; i < 3; i++) {
-        bool first = true;
-        for (int j = 0; j < i; j++) first &= fmts[j] != fmts[i];
-        if (!first) continue;
-        GemvJobs jobs;
-        int nj = 0;
-        for (int j = i; j < 3; j++)
-            if (fmts[j] == fmts[i]) jobs.j[nj++] = all[j];
-        launch_gemv_multi(fmts[i], jobs, nj, embed_dim, xq, 1, st);
+    const bool fused_x = gemv_q8x_ok(fmts, 3, embed_dim);
+    if (fused_x) {
+        /* Q4_K / Q6_K: q8 of the input inside the one projection launch,
+         * which also clears the ticket counters of the partial kernel */
+        const GemvJobs jobs = {{all[0], all[1], all[2]}};
+        launch_gemv_q8x(fmts, jobs, 3, embed_dim, input, ctr, n_kv, st);
+    } else {
+        /* q8 once, then one launch per distinct format */
+        Q8Rows xq = q8_view(scratch + L.xq, 1, embed_dim, input);
+        if (fmt_q != TG_FMT_F16 || fmt_k != TG_FMT_F16 || fmt_v != TG_FMT_F16)
+            launch_quantize(input, embed_dim, 1, embed_dim, xq, st);
+        for (int i = 0; i < 3; i++) {
+            bool first = true;
+            for (int j = 0; j < i; j++) first &= fmts[j] != fmts[i];
+            if (!first) continue;
+            GemvJobs jobs;
+            int nj = 0;
+            for (int j = i; j < 3; j++)
+                if (fmts[j] == fmts[i]) jobs.j[nj++] = all[j];
+            launch_gemv_multi(fmts[i], jobs, nj, embed_dim, xq, 1, st);
+        }
     }
     float *att = (float *)(scratch + L.att);
     Q8Rows aq = q8_view(scratch + L.aq, 1, q_dim, att);
     /* attention; q8 of its output fused into the combine where the block
-     * layout allows */
+     * layout allows, and the combine into the partial kernel for short spans
+     * (its counters are cleared by the fused projection launch) */
     const bool fuse_q8 = fmt_o != TG_FMT_F16 && attention_combine_q8_ok(n_heads, head_dim);
     launch_attention_core(qkv, q_norm_w, k_norm_w, sinks, kv_k, kv_v, kv_len, kv_max, window, rope_cos_row,
                           rope_sin_row, n_heads, n_kv, head_dim, eps, (float *)(scratch + L.part), att,
-                          fuse_q8 ? &aq : nullptr, st);
+                          fuse_q8 ? &aq : nullptr, st, fused_x ? ctr : nullptr);
     if (fmt_o != TG_FMT_F16 && !fuse_q8) launch_quantize(att, q_dim, 1, q_dim, aq, st);
     launch_gemv(fmt_o, (const uint8_t *)wo, embed_dim, q_dim, bo, aq, 1, output, embed_dim, st);
     if (att_out) HIPCHECK(hipMemcpyAsync(att_out, att, (size_t)q_dim * 4, hipMemcpyDeviceToDevice, st));

@@ -60,6 +60,10 @@ __device__ inline u32x2 ld8(Buf b, uint32_t off) {
 __device__ inline uint32_t ld4(Buf b, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)off, 0, 0);
 }
+/* the same loads from a q8 row staged in LDS (offsets aligned to the size) */
+__device__ inline u32x4 ld16(const uint8_t *p, uint32_t off) { return *reinterpret_cast<const u32x4 *>(p + off); }
+__device__ inline u32x2 ld8(const uint8_t *p, uint32_t off) { return *reinterpret_cast<const u32x2 *>(p + off); }
+__device__ inline uint32_t ld4(const uint8_t *p, uint32_t off) { return *reinterpret_cast<const uint32_t *>(p + off); }
 __device__ inline uint32_t ld2(Buf b, uint32_t off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(b.r, (int)off, 0, 0);
 }
@@ -177,38 +181,58 @@ struct Q8Row {
     Buf qs, d, s32, s16, f;
 };
 
+/* One q8 row staged in LDS (no f32 copy): qs int8[nb*256], d f32[nb],
+ * s32 int32[nb*8], s16 int32[nb*16], as byte pointers into shared memory. */
+struct Q8Lds {
+    const uint8_t *qs, *d, *s32, *s16;
+};
+
 /* q8 of one 256-value block held by a wave, lane l owning values 4l..4l+3
  * (quantize_q8, csrc/libtinygiant.c:169-208): scale amax/127, quants
- * rint(v * 127/amax), 16- and 32-element sums and the block total, written to
- * block b of row r. */
-__device__ inline void q8_block_store(float v0, float v1, float v2, float v3, int lane, const Q8Rows &out, int r,
-                                      int b) {
+ * rint(v * 127/amax) packed four to a word, the lane's 16- and 32-element
+ * sums (valid in lanes l % 4 == 0 and l % 8 == 0) and the block total. */
+struct Q8Quant {
+    uint32_t packed;
+    int s16, s32, tot;
+    float sc;
+};
+__device__ inline Q8Quant q8_block_quant(float v0, float v1, float v2, float v3) {
     float amax = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    const float sc = amax / 127.f;                  /* correctly rounded */
+    Q8Quant r;
+    r.sc = amax / 127.f;                  /* correctly rounded */
     const float inv = amax > 0.f ? 127.f / amax : 0.f;
     int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
     int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
-    uint32_t packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
-                      ((uint32_t)(q3 & 0xFF) << 24);
-    const int nb = out.nb;
-    int8_t *qrow = out.qs + ((size_t)r * nb + b) * 256;
-    reinterpret_cast<uint32_t *>(qrow)[lane] = packed;
+    r.packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+               ((uint32_t)(q3 & 0xFF) << 24);
     int s = q0 + q1 + q2 + q3;
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);            /* 16-element sum */
-    int s32 = s + __shfl_xor(s, 4, 64);   /* 32-element sum */
-    int tot = s32;
+    r.s16 = s;
+    r.s32 = s + __shfl_xor(s, 4, 64);     /* 32-element sum */
+    int tot = r.s32;
     tot += __shfl_xor(tot, 8, 64);
     tot += __shfl_xor(tot, 16, 64);
     tot += __shfl_xor(tot, 32, 64);
+    r.tot = tot;
+    return r;
+}
+
+/* q8_block_quant of the wave's block, written to block b of row r */
+__device__ inline void q8_block_store(float v0, float v1, float v2, float v3, int lane, const Q8Rows &out, int r,
+                                      int b) {
+    const Q8Quant q = q8_block_quant(v0, v1, v2, v3);
+    const int nb = out.nb;
+    int8_t *qrow = out.qs + ((size_t)r * nb + b) * 256;
+    reinterpret_cast<uint32_t *>(qrow)[lane] = q.packed;
     const size_t rb = (size_t)r * nb + b;
-    if ((lane & 3) == 0) out.s16[rb * 16 + (lane >> 2)] = s;
-    if ((lane & 7) == 0) out.s32[rb * 8 + (lane >> 3)] = s32;
+    if ((lane & 3) == 0) out.s16[rb * 16 + (lane >> 2)] = q.s16;
+    if ((lane & 7) == 0) out.s32[rb * 8 + (lane >> 3)] = q.s32;
     if (lane == 0) {
-        out.d[rb] = sc;
-        out.sum[rb] = tot;
+        out.d[rb] = q.sc;
+        out.sum[rb] = q.tot;
     }
 }
 
@@ -241,7 +265,8 @@ struct FQ4K {
         r.q1 = ld16(w, p + 32 + 32 * g);
         return r;
     }
-    __device__ static inline X load_x(const Q8Row &x, int item) {
+    template <class R>   /* Q8Row (global) or Q8Lds */
+    __device__ static inline X load_x(const R &x, int item) {
         uint32_t b = item >> 2, g = item & 3;
         uint32_t o = b * 256 + 64 * g;
         X r;
@@ -320,7 +345,8 @@ struct FQ6K {
         r.d = ld4(w, p + 206);   /* sc[14], sc[15], d: d is the high half */
         return r;
     }
-    __device__ static inline X load_x(const Q8Row &x, int item) {
+    template <class R>   /* Q8Row (global) or Q8Lds */
+    __device__ static inline X load_x(const R &x, int item) {
         uint32_t b = item >> 2, u = item & 3, h = u >> 1, l0 = (u & 1) * 16;
         uint32_t o = b * 256 + 128 * h + l0;
         X r;

@@ -62,6 +62,19 @@ struct GemvJobs {
     GemvJob j[3];
 };
 void launch_gemv_multi(int fmt, const GemvJobs &jobs, int njobs, int ncols, const Q8Rows &x, int k, hipStream_t st);
+/* q8 of one f32 row (ncols % 256 == 0, at most Q8X_MAX_BLOCKS blocks) and
+ * up to three Q4_K / Q6_K GEMVs of it in one launch (fmts[j] per job); the
+ * same bits as launch_quantize + launch_gemv_multi.  Also clears n_zero
+ * (<= 256) words at `zero` with device-scope stores. */
+#define Q8X_MAX_BLOCKS 32
+struct GemvQ8xMap {
+    int wg0[4];     /* first workgroup of each job, then the total */
+    int fmt[3];
+    uint32_t rb[3];
+};
+bool gemv_q8x_ok(const int *fmts, int njobs, int ncols);
+void launch_gemv_q8x(const int *fmts, const GemvJobs &jobs, int njobs, int ncols, const float *x, unsigned *zero,
+                     int n_zero, hipStream_t st);
 void launch_isums(int fmt, const uint8_t *W, int nrows, int ncols, const Q8Rows &x, int nsums_row, int32_t *out,
                   hipStream_t st);
 /* `mark`, when given, is called after each kernel with its class:

@@ -105,8 +105,8 @@ constexpr uint32_t ROW_OOB = 0x80000000u;   /* past every weight buffer: reads z
  * items before any is used, so a row costs ceil(T / TB) memory round trips
  * instead of T.  An invalid row (rv false) or an item past the row is read
  * at an out-of-range offset and adds nothing. */
-template <class F, int S, int TB, int NM>
-__device__ inline void row_dots(const Buf (&w)[NM], uint32_t roff, bool rv, const Q8Row &xr, int sl, int nitems,
+template <class F, int S, int TB, int NM, class R>
+__device__ inline void row_dots(const Buf (&w)[NM], uint32_t roff, bool rv, const R &xr, int sl, int nitems,
                                 int T, float (&acc)[NM]) {
     for (int t0 = 0; t0 < T; t0 += TB) {
         typename F::X xs[TB];
@@ -172,6 +172,108 @@ __global__ __launch_bounds__(256) void k_gemv_multi(GemvJobs jobs, uint32_t rb, 
                                                     int rows_per_wave) {
     const GemvJob &jb = jobs.j[blockIdx.y];
     gemv_rows<F, S, TB>(jb.W, rb, jb.nrows, jb.bias, x, k, jb.y, jb.ystride, nitems, T, rows_per_wave);
+}
+
+/* q8 of one f32 row of ncols (a multiple of 256) values into LDS by the
+ * workgroup's 4 waves, block b by wave b % 4: the arithmetic of
+ * k_quantize_q8 */
+__device__ inline void q8_row_lds(const float *__restrict__ x, int ncols, uint8_t *xq, float *xd, int32_t *xs32,
+                                  int32_t *xs16) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nb = ncols / 256;
+    for (int b = wave; b < nb; b += 4) {
+        Buf xb = make_buf(x + (size_t)b * 256, 1024u);
+        const u32x4 raw = ld16(xb, (uint32_t)lane * 16u);
+        const Q8Quant q = q8_block_quant(__uint_as_float(raw.x), __uint_as_float(raw.y), __uint_as_float(raw.z),
+                                         __uint_as_float(raw.w));
+        reinterpret_cast<uint32_t *>(xq + b * 256)[lane] = q.packed;
+        if ((lane & 3) == 0) xs16[b * 16 + (lane >> 2)] = q.s16;
+        if ((lane & 7) == 0) xs32[b * 8 + (lane >> 3)] = q.s32;
+        if (lane == 0) xd[b] = q.sc;
+    }
+}
+
+constexpr int Q8X_MAXP = 4;   /* row passes per wave whose weights are loaded before the q8 */
+
+/* One job's share of k_gemv_q8x: the rows of gemv_rows for wave `wave` of
+ * the job, against the q8 row the workgroup builds in LDS.  When each lane
+ * holds one item of a row (T == 1), the wave's weights are requested before
+ * the q8 is built, so the two latencies overlap; the dots are the same
+ * operations in the same order as gemv_rows. */
+template <class F, int S, int TB>
+__device__ inline void q8x_job(const GemvJob &jb, uint32_t rb, const float *__restrict__ x, int ncols, int nitems,
+                               int T, int rows_per_wave, int wave, uint8_t *xq, float *xd, int32_t *xs32,
+                               int32_t *xs16) {
+    constexpr int G = 64 / S;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int row0 = wave * rows_per_wave;
+    const int nrw = max(0, min(rows_per_wave, jb.nrows - row0));   /* this wave's rows (0 past the job) */
+    const Buf wb = make_buf(jb.W + (size_t)min(row0, jb.nrows) * rb, (uint32_t)((size_t)nrw * rb));
+    const int P = (rows_per_wave + G - 1) / G;
+    const bool pre = T == 1 && P <= Q8X_MAXP;
+    typename F::W wp[Q8X_MAXP];
+    if (pre) {
+#pragma unroll
+        for (int p = 0; p < Q8X_MAXP; p++) {
+            const int rl = p * G + seg;
+            const bool iv = p < P && rl < nrw && sl < nitems;
+            wp[p] = F::load_w(wb, iv ? (uint32_t)rl * rb : ROW_OOB, iv ? sl : 0);
+        }
+    }
+    q8_row_lds(x, ncols, xq, xd, xs32, xs16);
+    __syncthreads();
+    if (nrw == 0) return;
+    const Q8Lds xr = {xq, reinterpret_cast<const uint8_t *>(xd), reinterpret_cast<const uint8_t *>(xs32),
+                      reinterpret_cast<const uint8_t *>(xs16)};
+    if (pre) {
+#pragma unroll
+        for (int p = 0; p < Q8X_MAXP; p++) {
+            const int rl = p * G + seg, r = row0 + rl;
+            if (p >= P) break;
+            const bool rv = rl < nrw;
+            float acc = 0.f;
+            if (rv && sl < nitems) acc += F::value(wp[p], F::load_x(xr, sl), sl);
+            const float v = seg_sum<S>(acc);
+            if (rv && sl == 0) jb.y[r] = v + (jb.bias ? jb.bias[r] : 0.f);
+        }
+    } else {
+        for (int rs = 0; rs < rows_per_wave; rs += G) {
+            const int rl = rs + seg, r = row0 + rl;
+            const bool rv = rl < nrw;
+            float acc[1] = {0.f};
+            const Buf ws[1] = {wb};
+            row_dots<F, S, TB, 1>(ws, (uint32_t)rl * rb, rv, xr, sl, nitems, T, acc);
+            const float v = seg_sum<S>(acc[0]);
+            if (rv && sl == 0) jb.y[r] = v + (jb.bias ? jb.bias[r] : 0.f);
+        }
+    }
+}
+
+/* q8 of one f32 row and the GEMVs of up to three Q4_K / Q6_K matrices of
+ * its width in one launch (decode attention's Q, K and V projections).
+ * Every workgroup quantizes the row into LDS itself, with the arithmetic of
+ * k_quantize_q8, then runs its rows as k_gemv_multi does, so the results are
+ * the same bits.  The grid is flat: job j owns workgroups
+ * [map.wg0[j], map.wg0[j + 1]).  Workgroup 0 also clears n_zero words at
+ * `zero` (the counters of a kernel that follows). */
+template <int S, int TB>
+__global__ __launch_bounds__(256) void k_gemv_q8x(GemvJobs jobs, GemvQ8xMap map, const float *__restrict__ x,
+                                                  int ncols, int nitems, int T, int rows_per_wave, unsigned *zero,
+                                                  int n_zero) {
+    __shared__ __attribute__((aligned(16))) uint8_t xq[Q8X_MAX_BLOCKS * 256];
+    __shared__ __attribute__((aligned(16))) float xd[Q8X_MAX_BLOCKS];
+    __shared__ __attribute__((aligned(16))) int32_t xs32[Q8X_MAX_BLOCKS * 8];
+    __shared__ __attribute__((aligned(16))) int32_t xs16[Q8X_MAX_BLOCKS * 16];
+    if (blockIdx.x == 0 && (int)threadIdx.x < n_zero)
+        __hip_atomic_store(zero + threadIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    int j = 0;
+    while (j < 2 && (int)blockIdx.x >= map.wg0[j + 1]) j++;
+    const int jw = ((int)blockIdx.x - map.wg0[j]) * 4 + (int)(threadIdx.x >> 6);
+    if (map.fmt[j] == TG_FMT_Q6K)
+        q8x_job<FQ6K, S, TB>(jobs.j[j], map.rb[j], x, ncols, nitems, T, rows_per_wave, jw, xq, xd, xs32, xs16);
+    else
+        q8x_job<FQ4K, S, TB>(jobs.j[j], map.rb[j], x, ncols, nitems, T, rows_per_wave, jw, xq, xd, xs32, xs16);
 }
 
 /* ======================= MoE phases ======================= */
@@ -410,6 +512,41 @@ void launch_gemv_multi(int fmt, const GemvJobs &jobs, int njobs, int ncols, cons
 #define CALL(S_, TB_) \
     hipLaunchKernelGGL((k_gemv_multi<F, S_, TB_>), grid, dim3(256), 0, st, jobs, rb, x, k, nitems, T, rpw)
     TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
+#undef CALL
+}
+
+bool gemv_q8x_ok(const int *fmts, int njobs, int ncols) {
+    if (njobs < 1 || njobs > 3 || ncols <= 0 || ncols % 256 || ncols > Q8X_MAX_BLOCKS * 256) return false;
+    for (int i = 0; i < njobs; i++)
+        if (fmts[i] != TG_FMT_Q4K && fmts[i] != TG_FMT_Q6K) return false;
+    return true;
+}
+
+void launch_gemv_q8x(const int *fmts, const GemvJobs &jobs, int njobs, int ncols, const float *x, unsigned *zero,
+                     int n_zero, hipStream_t st) {
+    int T;
+    const int nitems = items_per_row(TG_FMT_Q4K, ncols);   /* Q6_K rows have as many items */
+    const int S = pick_S(nitems, &T);
+    const int rpw = (64 / S) * 2;
+    GemvQ8xMap m;
+    int wg = 0;
+    for (int i = 0; i < 3; i++) {
+        m.wg0[i] = wg;
+        if (i < njobs) {
+            m.fmt[i] = fmts[i];
+            m.rb[i] = row_bytes(fmts[i], ncols);
+            const int waves = (jobs.j[i].nrows + rpw - 1) / rpw;
+            wg += (waves + 3) / 4;
+        } else {
+            m.fmt[i] = TG_FMT_Q4K;
+            m.rb[i] = 0;
+        }
+    }
+    m.wg0[3] = wg;
+    const int TB = pick_TB(T);
+#define CALL(S_, TB_) \
+    hipLaunchKernelGGL((k_gemv_q8x<S_, TB_>), dim3(wg), dim3(256), 0, st, jobs, m, x, ncols, nitems, T, rpw, zero, n_zero)
+    TG_DISPATCH_ST(S, TB, CALL)
 #undef CALL
 }
 
