@@ -79,6 +79,10 @@ struct Ctx {
     size_t arena_cap = 0;
     uint8_t *pin = nullptr;
     size_t pin_cap = 0;
+    /* coherent (uncached on the device) pinned rows that kernels read and
+     * write in place: the input and output rows of the host-pointer MoE call */
+    uint8_t *io = nullptr;
+    size_t io_cap = 0;
 };
 Ctx g;
 
@@ -113,6 +117,19 @@ uint8_t *pinned(size_t n) {
         g.pin_cap = cap;
     }
     return g.pin;
+}
+
+uint8_t *io_rows(size_t n) {
+    if (n > g.io_cap) {
+        if (g.io) {
+            HIPCHECK(hipStreamSynchronize(g.st));
+            HIPCHECK(hipHostFree(g.io));
+        }
+        size_t cap = std::max(n, (size_t)1 << 20);
+        HIPCHECK(hipHostMalloc(&g.io, cap, hipHostMallocCoherent));
+        g.io_cap = cap;
+    }
+    return g.io;
 }
 
 /* Bump allocator over a byte range, 256-byte aligned pieces. */
@@ -486,20 +503,25 @@ void moe_host(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs, co
     uint8_t *dev = arena(bump.off);
     for (auto &f : fixes) (*f.vec)[f.idx] += (uint64_t)(uintptr_t)dev;
 
+    /* the tables go over in one copy; the input rows are read and the output
+     * rows accumulated in place in coherent pinned memory (the q8 kernel and
+     * the combine reach them over the host link), which saves three copy
+     * launches per call */
     const size_t io_len = (size_t)k * D * 4;
-    uint8_t *img = pinned(L.tables_len + 2 * io_len);
+    uint8_t *img = pinned(L.tables_len);
+    uint8_t *io = io_rows(2 * io_len);
     MoeArgs a = plan_args(h, L, dev, img);
-    memcpy(img + L.tables_len, inputs, io_len);
-    memcpy(img + L.tables_len + io_len, output, io_len);
+    memcpy(io, inputs, io_len);
+    memcpy(io + io_len, output, io_len);
+    a.xin = (const float *)io;
+    a.xq.f = a.xin;
+    a.out = (float *)(io + io_len);
     HIPCHECK(hipMemcpyAsync(dev + L.tables, img, L.tables_len, hipMemcpyHostToDevice, g.st));
-    HIPCHECK(hipMemcpyAsync(dev + L.xin, img + L.tables_len, io_len, hipMemcpyHostToDevice, g.st));
-    HIPCHECK(hipMemcpyAsync(dev + L.out, img + L.tables_len + io_len, io_len, hipMemcpyHostToDevice, g.st));
     for (auto &it : sg.items) HIPCHECK(hipMemcpyAsync(dev + it.off, it.host, it.n, hipMemcpyHostToDevice, g.st));
     launch_moe(a, h.fmts_present.data(), (int)h.fmts_present.size(), g.st);
     HIPCHECK(hipGetLastError());
-    HIPCHECK(hipMemcpyAsync(img, dev + L.out, io_len, hipMemcpyDeviceToHost, g.st));
     HIPCHECK(hipStreamSynchronize(g.st));
-    memcpy(output, img, io_len);
+    memcpy(output, io + io_len, io_len);
     if (dbg_hidden)
         HIPCHECK(hipMemcpy(dbg_hidden, a.hidden, (size_t)h.P * I * 4, hipMemcpyDeviceToHost));
     if (dbg_hq) q8_to_blocks(a.hq, h.P, dbg_hq);
