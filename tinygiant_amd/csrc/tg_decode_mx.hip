@@ -33,9 +33,11 @@
  * (four blocks inside an MFMA, then per 128 values, per half and per wave),
  * which the f32 bar covers.
  *
- * Weights load into registers ahead of use: this layer's down blocks during
- * the hidden exchange (4), the next layer's gate/up blocks and RMSNorm weight
- * during the hop (7), while the compute waves would otherwise wait.  Two
+ * Weights load ahead of use: the next layer's gate/up blocks and RMSNorm
+ * weight into registers during the hop (7), while the compute waves would
+ * otherwise wait; this layer's down rows, one contiguous range per slice,
+ * straight into LDS right after the h gather (1), so the copy drains during
+ * RMSNorm and gate/up instead of ahead of the hidden exchange's polls.  Two
  * communication waves per workgroup do the polling and publishing.
  */
 #include <hip/hip_runtime.h>
@@ -81,6 +83,10 @@ constexpr int NTS = 24;               /* timing words per layer */
 constexpr int FMT_FP8 = 0, FMT_FP4 = 4, SCALE_1 = 127, SCALE_16 = 131;
 constexpr uint32_t OOB = 0x80000000u;  /* past every buffer: reads zeros, touches no memory */
 constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units between the compute waves' prefetch issue */
+constexpr int NDMA = 68;               /* 1 KiB direct-to-LDS copy steps per layer (16 bytes a lane) */
+constexpr int DZERO = NDMA * 1024;     /* 32 zero bytes after the copy, read by off-slice lanes */
+constexpr int DWS = DZERO + 32;        /* LDS copy of the slice's down rows */
+static_assert(RS * RB + 15 <= DZERO, "the slice's down rows fit the LDS copy");
 static_assert(NE * 2 == NX, "two XCDs per expert");
 static_assert(NRK * RS == D && RS % VPS == 0 && NG * 16 >= RS && RS <= 64, "slices");
 static_assert(NW * CPW >= NCH && (NW - 1) * CPW < NCH, "chunks per wave");
@@ -210,6 +216,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     __shared__ float ssq[NRK];                                /* sum of h^2 of each 45-row slice */
     __shared__ float red[NW][2 * NG][2][16];                  /* per-wave partial row sums: hi and lo columns */
     __shared__ float pp[NX][RS];                              /* weighted down values of the 8 XCDs */
+    __shared__ __attribute__((aligned(16))) uint8_t dws[DWS]; /* this layer's down rows of the slice */
     __shared__ int lds_fail;
     __shared__ DecodeLayerMx lys[MAX_LAYERS];
 
@@ -225,7 +232,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     const int sb = (lane & 15) == 0 ? SCALE_16 : SCALE_1;   /* B scale of this lane's column */
 
     MxBlk wa[CPW][2 * NG];   /* gate (units 0..2) and up (3..5) blocks of the wave's chunks */
-    MxBlk wb[CPW][NG];       /* down blocks */
+    MxBlk wb[CPW][NG];       /* down blocks, gathered from dws during the hidden exchange */
     u32x4 nw0, nw1;          /* next layer's RMSNorm weight (compute lanes) */
 
     /* block offset of unit row group gr, chunk i of this wave, or OOB */
@@ -249,13 +256,40 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 wa[i][NG + gr] = load_blk(ub, o);
             }
     };
-    auto load_d = [&](const DecodeLayerMx &ly) {
-        const bool cw = wave < NW;
-        Buf db = make_buf_uniform(cw ? ly.down[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
-#pragma unroll
-        for (int i = 0; i < CPW; i++)
-#pragma unroll
-            for (int gr = 0; gr < NG; gr++) wb[i][gr] = load_blk(db, blk_off(gr, i));
+    /* The slice's down rows are one contiguous 45-row range of the expert's
+     * down matrix.  The compute waves copy it into dws with direct-to-LDS
+     * loads, 1 KiB an instruction and 16 bytes a lane, from the 16-byte
+     * boundary at or below its start (dsh bytes earlier); the buffer range
+     * returns zeros past the matrix.  Issued right after the h gather, the
+     * copy drains during RMSNorm and gate/up, not ahead of the hidden
+     * exchange's polls, and takes no registers. */
+    const uint32_t dsh = (uint32_t)(RS * R * RB) & 15u;
+    auto fetch_down = [&](const DecodeLayerMx &ly) {
+        Buf db = make_buf_uniform(ly.down[xe], (uint32_t)D * RB);
+        const uint32_t a0 = (uint32_t)(RS * R * RB) - dsh;
+        for (int k = wave; k < NDMA; k += NW)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(db.r, (__attribute__((address_space(3))) void *)(dws + 1024 * k),
+                                                     16, a0 + 1024u * (uint32_t)k + 16u * (uint32_t)lane, 0, 0, 0);
+    };
+    /* down block (gr, i) of this lane from dws: the e8m0 byte at the block's
+     * offset, and the 16 code bytes after it from the five aligned dwords
+     * that start with the first code byte (the bytes load_blk would read
+     * from memory).  Off-slice lanes read the zero pad. */
+    auto lds_blk = [&](int gr, int i) -> MxBlk {
+        const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
+        const bool on = c < NCH && b < NBLK && sr < RS;
+        const uint32_t off = on ? dsh + (uint32_t)sr * RB + (uint32_t)b * 17u : (uint32_t)DZERO;
+        const uint32_t cs = off + (on ? 1u : 0u);   /* first code byte */
+        const uint32_t *p = reinterpret_cast<const uint32_t *>(dws + (cs & ~3u));
+        const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
+        const uint32_t sft = cs & 3u;
+        MxBlk r;
+        r.e = dws[off];
+        r.c.x = __builtin_amdgcn_alignbyte(w1, w0, sft);
+        r.c.y = __builtin_amdgcn_alignbyte(w2, w1, sft);
+        r.c.z = __builtin_amdgcn_alignbyte(w3, w2, sft);
+        r.c.w = __builtin_amdgcn_alignbyte(w4, w3, sft);
+        return r;
     };
     auto zero_a = [&]() {
         const u32x4 z = {0u, 0u, 0u, 0u};
@@ -264,13 +298,6 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         for (int i = 0; i < CPW; i++)
 #pragma unroll
             for (int u = 0; u < 2 * NG; u++) wa[i][u] = MxBlk{0u, z};
-    };
-    auto zero_d = [&]() {
-        const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int i = 0; i < CPW; i++)
-#pragma unroll
-            for (int gr = 0; gr < NG; gr++) wb[i][gr] = MxBlk{0u, z};
     };
     auto load_nw = [&](const DecodeLayerMx &ly, bool use) {
         const bool on = use && wave < NW && ly.norm_w != nullptr;
@@ -313,6 +340,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         for (int t = threadIdx.x; t < words; t += NT) dst[t] = src[t];
     }
     for (int t = threadIdx.x; t < D / 4; t += NT) reinterpret_cast<u32x4 *>(hx)[t] = reinterpret_cast<const u32x4 *>(h)[t];
+    if (threadIdx.x < (DWS - DZERO) / 4) reinterpret_cast<uint32_t *>(dws + DZERO)[threadIdx.x] = 0u;
     /* the fp8 block slots past the row stay zero (chunk 22 reads them) */
     for (int t = threadIdx.x; t < (NSB - NBLK) * 64 / 4; t += NT) {
         reinterpret_cast<uint32_t *>(&sx.sp[NBLK][0][0])[t] = 0u;
@@ -393,6 +421,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             dbv = __uint_as_float(ld4(make_buf_uniform(ly.db[xe], ly.db[xe] ? (uint32_t)D * 4u : 0u), o));
         }
         /* ---- 2: RMSNorm (weight or 1) + q8 + fp8 halves of x ---- */
+        if (cl < 0) fetch_down(ly);
         {
             const float tot = wave_sum(ssq[lane]);   /* the 64 slice sums, one per lane */
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
@@ -423,17 +452,26 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 for (int u = 0; u < 2 * NG; u++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) red[wave][u][lane & 15][4 * (lane >> 4) + v] = acc[u][v];
+            /* the down rows' copy has landed in dws before the barrier */
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         }
         __syncthreads();
         if (tw) tr[3] = wall_clock64();
         /* ---- 4: bias + activation, all-gather the expert's hidden vector ---- */
-        /* meanwhile the compute waves issue this layer's down blocks, one
-         * wave after another */
+        /* meanwhile the compute waves gather their down blocks from dws into
+         * registers; the communication waves zero theirs (both paths assign,
+         * so no old value stays live) */
         if (cl < 0) {
-            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
-            load_d(ly);
+#pragma unroll
+            for (int i = 0; i < CPW; i++)
+#pragma unroll
+                for (int u = 0; u < NG; u++) wb[i][u] = lds_blk(u, i);
         } else {
-            zero_d();   /* no loads ahead of the polls in these waves' queue */
+            const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < CPW; i++)
+#pragma unroll
+                for (int u = 0; u < NG; u++) wb[i][u] = MxBlk{0u, z};
         }
         if (cl >= 0) {
             /* row i of the slice: the six waves' partial sums in wave order */
