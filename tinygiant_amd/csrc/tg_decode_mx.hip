@@ -83,10 +83,14 @@ constexpr int NTS = 24;               /* timing words per layer */
 constexpr int FMT_FP8 = 0, FMT_FP4 = 4, SCALE_1 = 127, SCALE_16 = 131;
 constexpr uint32_t OOB = 0x80000000u;  /* past every buffer: reads zeros, touches no memory */
 constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units between the compute waves' prefetch issue */
-constexpr int NDMA = 68;               /* 1 KiB direct-to-LDS copy steps per layer (16 bytes a lane) */
-constexpr int DZERO = NDMA * 1024;     /* 32 zero bytes after the copy, read by off-slice lanes */
-constexpr int DWS = DZERO + 32;        /* LDS copy of the slice's down rows */
-static_assert(RS * RB + 15 <= DZERO, "the slice's down rows fit the LDS copy");
+constexpr int NDMA = 68;               /* 1 KiB direct-to-LDS copy steps of the down rows (16 bytes a lane) */
+constexpr int GSEG = 18;               /* 16-byte chunks of a wave's gate segment of one row (272 bytes + alignment) */
+constexpr int GINS = (RS * GSEG + 63) / 64;   /* copy steps per wave for its gate segments: 13 */
+constexpr int GREG = GINS * 1024;      /* LDS bytes of a wave's gate segments */
+constexpr int DZERO = NW * GREG;       /* 32 zero bytes after the copies, read by off-slice lanes */
+constexpr int DWS = DZERO + 32;        /* LDS staging of the slice's gate rows, then its down rows */
+static_assert(RS * RB + 15 <= NDMA * 1024 && NDMA * 1024 <= DZERO, "the slice's down rows fit the staging");
+static_assert(16 * 17 + 15 <= GSEG * 16, "a wave's 16 blocks of a row fit its gate segment");
 static_assert(NE * 2 == NX, "two XCDs per expert");
 static_assert(NRK * RS == D && RS % VPS == 0 && NG * 16 >= RS && RS <= 64, "slices");
 static_assert(NW * CPW >= NCH && (NW - 1) * CPW < NCH, "chunks per wave");
@@ -216,7 +220,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     __shared__ float ssq[NRK];                                /* sum of h^2 of each 45-row slice */
     __shared__ float red[NW][2 * NG][2][16];                  /* per-wave partial row sums: hi and lo columns */
     __shared__ float pp[NX][RS];                              /* weighted down values of the 8 XCDs */
-    __shared__ __attribute__((aligned(16))) uint8_t dws[DWS]; /* this layer's down rows of the slice */
+    __shared__ __attribute__((aligned(16))) uint8_t dws[DWS]; /* staged gate rows, then down rows, of the slice */
     __shared__ int lds_fail;
     __shared__ DecodeLayerMx lys[MAX_LAYERS];
 
@@ -241,20 +245,32 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         if (c >= NCH || b >= NBLK || sr >= RS) return OOB;
         return (uint32_t)(RS * R + sr) * (uint32_t)RB + (uint32_t)b * 17u;
     };
-    /* loads are unconditional so the registers' live ranges end at their
-     * use; an inactive step reads through an empty descriptor */
-    auto load_a = [&](const DecodeLayerMx &ly, bool on) {
+    /* up blocks into registers; loads are unconditional so the registers'
+     * live ranges end at their use; an inactive step reads through an empty
+     * descriptor */
+    auto load_up = [&](const DecodeLayerMx &ly, bool on) {
         const bool cw = on && wave < NW;
-        Buf gb = make_buf_uniform(cw ? ly.gate[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
         Buf ub = make_buf_uniform(cw ? ly.up[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
 #pragma unroll
         for (int i = 0; i < CPW; i++)
 #pragma unroll
-            for (int gr = 0; gr < NG; gr++) {
-                const uint32_t o = blk_off(gr, i);
-                wa[i][gr] = load_blk(gb, o);
-                wa[i][NG + gr] = load_blk(ub, o);
-            }
+            for (int gr = 0; gr < NG; gr++) wa[i][NG + gr] = load_blk(ub, blk_off(gr, i));
+    };
+    /* Gate rows: compute wave w uses blocks [16 w, 16 w + 16) of each of the
+     * slice's 45 rows, 272 bytes a row.  It copies those segments, from the
+     * 16-byte boundary at or below each start, into its own region of dws
+     * (row sr at 288 sr) with direct-to-LDS loads, and later gathers its
+     * blocks from there: no other wave touches the region, so only the
+     * wave's own copy has to have landed. */
+    auto fetch_gate = [&](const DecodeLayerMx &ly, bool on) {
+        Buf gbuf = make_buf_uniform(on ? ly.gate[xe] : nullptr, on ? (uint32_t)D * RB : 0u);
+        for (int k = 0; k < GINS; k++) {
+            const int sidx = 64 * k + lane, sr = sidx / GSEG, j = sidx - sr * GSEG;
+            const uint32_t a = ((uint32_t)(RS * R + sr) * (uint32_t)RB + 272u * (uint32_t)wave) & ~15u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                gbuf.r, (__attribute__((address_space(3))) void *)(dws + GREG * wave + 1024 * k), 16,
+                sr < RS ? a + 16u * (uint32_t)j : OOB, 0, 0, 0);
+        }
     };
     /* The slice's down rows are one contiguous 45-row range of the expert's
      * down matrix.  The compute waves copy it into dws with direct-to-LDS
@@ -271,14 +287,12 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             __builtin_amdgcn_raw_ptr_buffer_load_lds(db.r, (__attribute__((address_space(3))) void *)(dws + 1024 * k),
                                                      16, a0 + 1024u * (uint32_t)k + 16u * (uint32_t)lane, 0, 0, 0);
     };
-    /* down block (gr, i) of this lane from dws: the e8m0 byte at the block's
-     * offset, and the 16 code bytes after it from the five aligned dwords
-     * that start with the first code byte (the bytes load_blk would read
-     * from memory).  Off-slice lanes read the zero pad. */
-    auto lds_blk = [&](int gr, int i) -> MxBlk {
-        const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
-        const bool on = c < NCH && b < NBLK && sr < RS;
-        const uint32_t off = on ? dsh + (uint32_t)sr * RB + (uint32_t)b * 17u : (uint32_t)DZERO;
+    /* One MXFP4 block from dws at byte offset off: the e8m0 byte there and
+     * the 16 code bytes after it, from the five aligned dwords that start
+     * with the first code byte (the bytes load_blk reads from memory).
+     * Off-slice lanes pass on = false and read the zero pad. */
+    auto lds_blk_at = [&](uint32_t off, bool on) -> MxBlk {
+        off = on ? off : (uint32_t)DZERO;
         const uint32_t cs = off + (on ? 1u : 0u);   /* first code byte */
         const uint32_t *p = reinterpret_cast<const uint32_t *>(dws + (cs & ~3u));
         const uint32_t w0 = p[0], w1 = p[1], w2 = p[2], w3 = p[3], w4 = p[4];
@@ -291,13 +305,27 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         r.c.w = __builtin_amdgcn_alignbyte(w4, w3, sft);
         return r;
     };
-    auto zero_a = [&]() {
+    /* down block (gr, i) of this lane from the contiguous copy */
+    auto lds_blk = [&](int gr, int i) -> MxBlk {
+        const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
+        const bool on = c < NCH && b < NBLK && sr < RS;
+        return lds_blk_at(dsh + (uint32_t)sr * RB + (uint32_t)b * 17u, on);
+    };
+    /* gate block (gr, i) of this lane from the wave's own gate segments */
+    auto gate_blk = [&](int gr, int i) -> MxBlk {
+        const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
+        const bool on = c < NCH && b < NBLK && sr < RS;
+        const uint32_t s0 = (uint32_t)(RS * R + sr) * (uint32_t)RB + 272u * (uint32_t)wave;
+        return lds_blk_at((uint32_t)(GREG * wave + GSEG * 16 * sr) + (s0 & 15u) + (uint32_t)(b - 16 * wave) * 17u,
+                          on);
+    };
+    auto zero_up = [&]() {
         const u32x4 z = {0u, 0u, 0u, 0u};
         nw0 = nw1 = z;
 #pragma unroll
         for (int i = 0; i < CPW; i++)
 #pragma unroll
-            for (int u = 0; u < 2 * NG; u++) wa[i][u] = MxBlk{0u, z};
+            for (int u = NG; u < 2 * NG; u++) wa[i][u] = MxBlk{0u, z};
     };
     auto load_nw = [&](const DecodeLayerMx &ly, bool use) {
         const bool on = use && wave < NW && ly.norm_w != nullptr;
@@ -354,7 +382,12 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         if (lane == 0) ssq[s] = t;
     }
     load_nw(lys[0], true);
-    load_a(lys[0], true);
+    if (wave < NW) {
+        fetch_gate(lys[0], true);
+        load_up(lys[0], true);
+    } else {
+        zero_up();
+    }
     store_nw();
     __syncthreads();   /* layer 0's RMSNorm weight is in LDS before step 2 reads it */
 
@@ -371,6 +404,24 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
         uint8_t *rec = dbg ? dbg + (size_t)l * DecodeDebugMx::BYTES : nullptr;
         if (tw) tr[0] = wall_clock64();
+        /* this layer's gate blocks from the wave's own staged segments (copied
+         * during the previous layer's q8 of the hidden vector) into
+         * registers, while the communication waves gather h; the other waves
+         * zero theirs (both paths assign) */
+        if (cl < 0) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < CPW; i++)
+#pragma unroll
+                for (int gr = 0; gr < NG; gr++) wa[i][gr] = gate_blk(gr, i);
+        } else {
+            const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < CPW; i++)
+#pragma unroll
+                for (int gr = 0; gr < NG; gr++) wa[i][gr] = MxBlk{0u, z};
+        }
+        if (l == 0) __syncthreads();   /* every wave is done with dws before the down rows' copy */
         /* ---- 1: gather h: slices j' and 32 + j' from the other ranks of this XCD ---- */
         if (l > 0) {
             if (cl >= 0) {
@@ -407,7 +458,10 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 store_nw();
             }
             __syncthreads();
-            if (lds_fail) return;
+            if (lds_fail) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* no copy into LDS outlives the workgroup */
+            return;
+        }
         }
         if (tw) tr[1] = wall_clock64();
         /* the slice's gate, up and down biases (communication lanes, one row
@@ -517,12 +571,18 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             if (!ok) lds_fail = 1;
         }
         __syncthreads();
-        if (lds_fail) return;
+        if (lds_fail) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* no copy into LDS outlives the workgroup */
+            return;
+        }
         if (tw) tr[4] = wall_clock64();
         /* ---- 5: q8 + fp8 halves of the hidden vector ---- */
         if (rec && (xc & 1) == 0 && rk == 0)   /* workgroup 2e: expert slot e's record */
             for (int t = threadIdx.x; t < D; t += NT)
                 reinterpret_cast<float *>(rec + DecodeDebugMx::HID)[xe * D + t] = hid[t];
+        /* the next layer's gate segments into dws (free since the down blocks
+         * were gathered), draining during this q8, the down rows and the hop */
+        if (cl < 0 && l + 1 < L) fetch_gate(lys[l + 1], true);
         quantize(hid, false, 1.f, false, sh, nullptr);
         __syncthreads();
         if (tw) tr[5] = wall_clock64();
@@ -555,9 +615,9 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         if (cl < 0) {
             for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
             load_nw(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
-            load_a(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
+            load_up(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
         } else {
-            zero_a();
+            zero_up();
         }
         if (cl >= 0) {
             if (clv < RS) {
@@ -597,7 +657,10 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             if (!ok) lds_fail = 1;
         }
         __syncthreads();
-        if (lds_fail) return;
+        if (lds_fail) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* no copy into LDS outlives the workgroup */
+            return;
+        }
         if (tw) tr[7] = wall_clock64();
         /* ---- 8: combine slices rk (first communication wave) and 32 + rk
          * (second) in expert order, publish ---- */
