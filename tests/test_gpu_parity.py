@@ -271,6 +271,47 @@ def test_moe_prefill_64_rows(tg, orc):
                False, rw, x)
 
 
+@pytest.mark.parametrize("k,pool,top,mixed", [(1, 128, 8, False), (9, 32, 8, False), (6, 8, 3, True),
+                                               (64, 16, 4, False)])
+def test_moe_expert_major_equals_per_pair(tg, orc, k, pool, top, mixed):
+    """Q4_K / Q6_K phases run expert-major (each weight row read once for all
+    pairs of its expert, q8 rows staged eight at a time in LDS), with the q8
+    and the combine inside the phases or in launches of their own, or one
+    workgroup column per pair: the same operations per pair, so the same
+    bits in every mode, also past eight pairs per expert and with mixed down
+    formats."""
+    say("moe expert-major vs per-pair", k, pool, top, mixed)
+    import tinygiant_amd.synth as S
+    rng = np.random.default_rng(700 + k)
+    experts, rw = S.routing_rows(rng, k, pool, top)
+    n = len(experts)
+    fmts = [O.FMT_Q6K if (e % 2 or not mixed) else O.FMT_Q4K for e in range(n)]
+    g, u, d = _experts(n, 2048, 768, O.FMT_Q4K, fmts, 41)
+    x = rng.standard_normal((k, 2048)).astype(np.float32)
+    base = rng.standard_normal((k, 2048)).astype(np.float32)
+    P = int(np.count_nonzero(rw))
+    lib = tg.lib()
+    outs = []
+    prev = lib.tg_hip_set_moe_expert_major(7)
+    try:
+        for on in (7, 0, 1, 5, 3, 15):
+            lib.tg_hip_set_moe_expert_major(on)
+            h = np.zeros((P, 768), np.float32)
+            o = tg.moe_forward_rows_v2(g, u, d, O.FMT_Q4K, fmts, None, None, None, O.ACT_SILU, rw, x, base.copy(),
+                                       768, hidden_out=h)
+            outs.append((h, o))
+    finally:
+        lib.tg_hip_set_moe_expert_major(prev)
+    say("  pairs", P, "most per expert", int(np.count_nonzero(rw, axis=1).max()))
+    for h, o in outs[1:]:
+        assert h.tobytes() == outs[0][0].tobytes()
+        assert o.tobytes() == outs[0][1].tobytes()
+    ref = orc.moe_v2(g, u, d, O.FMT_Q4K, fmts, None, None, None, O.ACT_SILU, rw, x, base.copy(), 768,
+                     hidden_in=outs[0][0])
+    ok, rel = close(outs[0][1], ref)
+    assert ok, rel
+
+
 def test_moe_registered_equals_staged(tg, orc):
     """tg_mlock (HBM-resident weights) and the per-call staging path agree bit for bit."""
     say("moe registered vs staged")

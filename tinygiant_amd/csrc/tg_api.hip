@@ -83,6 +83,9 @@ struct Ctx {
      * write in place: the input and output rows of the host-pointer MoE call */
     uint8_t *io = nullptr;
     size_t io_cap = 0;
+    /* row-tile tickets of the host call's fused MoE combine (zero between calls) */
+    unsigned *tickets = nullptr;
+    int tickets_cap = 0;
 };
 Ctx g;
 
@@ -130,6 +133,22 @@ uint8_t *io_rows(size_t n) {
         g.io_cap = cap;
     }
     return g.io;
+}
+
+/* n zeroed ticket words on the device, queued on the library stream; every
+ * kernel that takes tickets leaves them zero again */
+unsigned *host_call_tickets(int n) {
+    if (n > g.tickets_cap) {
+        if (g.tickets) {
+            HIPCHECK(hipStreamSynchronize(g.st));
+            HIPCHECK(hipFree(g.tickets));
+        }
+        const int cap = std::max(n, 4096);
+        HIPCHECK(hipMalloc(&g.tickets, (size_t)cap * 4));
+        HIPCHECK(hipMemsetAsync(g.tickets, 0, (size_t)cap * 4, g.st));
+        g.tickets_cap = cap;
+    }
+    return g.tickets;
 }
 
 /* Bump allocator over a byte range, 256-byte aligned pieces. */
@@ -303,8 +322,11 @@ void build_pairs(HostPlan &h, const float *row_weights) {
 /* Lays out tables + scratch in `base` (device) and the table image in `img`
  * (host); returns MoeArgs pointing into base. */
 struct Layout {
-    size_t tables, tables_len, xin, xq, hidden, hq, part, out, xp, hp, total;
+    size_t tables, tables_len, xin, xq, hidden, hq, part, out, xp, hp, ctr, total;
 };
+
+/* row-tile tickets of the fused combine: at most one per 4 rows of D */
+static int moe_ctr_words(int D) { return D / 4 + 16; }
 
 Layout plan_layout(const HostPlan &h) {
     Layout L;
@@ -328,6 +350,7 @@ Layout plan_layout(const HostPlan &h) {
     L.xp = h.gate_fmt == TG_FMT_MXFP4 ? b.take((size_t)std::max(k, 1) * h.D * 2) : 0;
     L.hp = mx_down ? b.take((size_t)P * h.I * 2) : 0;
     L.out = b.take((size_t)k * h.D * 4);
+    L.ctr = b.take((size_t)moe_ctr_words(h.D) * 4);
     L.total = b.off;
     return L;
 }
@@ -370,6 +393,8 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     a.xp = L.xp ? dev + L.xp : nullptr;
     a.hp = L.hp ? dev + L.hp : nullptr;
     a.out = (float *)(dev + L.out);
+    a.ctr = (unsigned *)(dev + L.ctr);
+    a.ctr_n = moe_ctr_words(h.D);
     a.n = n;
     a.k = k;
     a.P = h.P;
@@ -515,7 +540,12 @@ void moe_host(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs, co
     memcpy(io + io_len, output, io_len);
     a.xin = (const float *)io;
     a.xq.f = a.xin;
+    a.xin_remote = 1;
     a.out = (float *)(io + io_len);
+    /* the arena is laid out afresh each call: the tickets live in a buffer
+     * of their own that every fused combine leaves zeroed */
+    a.ctr = host_call_tickets(moe_ctr_words(D));
+    a.ctr_n = a.ctr ? moe_ctr_words(D) : 0;
     HIPCHECK(hipMemcpyAsync(dev + L.tables, img, L.tables_len, hipMemcpyHostToDevice, g.st));
     for (auto &it : sg.items) HIPCHECK(hipMemcpyAsync(dev + it.off, it.host, it.n, hipMemcpyHostToDevice, g.st));
     launch_moe(a, h.fmts_present.data(), (int)h.fmts_present.size(), g.st);
@@ -903,6 +933,7 @@ TG_API tg_hip_moe_plan *tg_hip_moe_plan_create(const void *const *gate_dev, cons
     std::vector<uint8_t> img(p->L.tables_len);
     p->a = plan_args(h, p->L, p->dev, img.data());
     HIPCHECK(hipMemcpy(p->dev + p->L.tables, img.data(), img.size(), hipMemcpyHostToDevice));
+    HIPCHECK(hipMemset(p->dev + p->L.ctr, 0, (size_t)moe_ctr_words(h.D) * 4));
     return p;
 }
 
@@ -1677,6 +1708,16 @@ TG_API int tg_hip_set_moe_grouped_min_rows(int rows) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     const int prev = grouped_min_rows();
     set_grouped_min_rows(rows);
+    return prev;
+}
+
+/* Q4_K / Q6_K expert layers: expert-major phases (mode bits, default 7) or
+ * one workgroup column per pair (0); the same bits either way.  Returns the
+ * previous mode. */
+TG_API int tg_hip_set_moe_expert_major(int mode) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = expert_major();
+    set_expert_major(mode < 0 ? EM_DEFAULT : mode);
     return prev;
 }
 

@@ -41,6 +41,9 @@ struct MoeArgs {
     const int *mx_cum;                      /* cost prefix of each list (n_act + 1 entries each) */
     uint8_t *xp, *hp;                       /* fp8 halves of xq / hq rows in MFMA order, or null */
     int n_act_a, n_act_b;
+    unsigned *ctr;                          /* [ctr_n] row-tile tickets of the fused combine, zero between calls, or null */
+    int ctr_n;
+    int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */
 };
 
 int items_per_row(int fmt, int ncols);
@@ -93,6 +96,14 @@ void launch_moe_b_mx(const MoeArgs &a, hipStream_t st);
  * experts; 0 switches them off */
 void set_grouped_min_rows(int rows);
 int grouped_min_rows();
+/* Q4_K / Q6_K experts: one workgroup column per active expert, each weight
+ * row read once for all its pairs (EM_ON), or one per pair (0).  For layers
+ * with at most two pairs per expert: EM_FUSE_Q8, the phases quantize their
+ * rows themselves; EM_TICKETS, the down phase also combines (row-tile
+ * tickets).  EM_FUSE_ANY: those two whatever the pair count (for tests). */
+enum { EM_ON = 1, EM_FUSE_Q8 = 2, EM_TICKETS = 4, EM_FUSE_ANY = 8, EM_DEFAULT = 7, EM_ALL = 15 };
+void set_expert_major(int mode);
+int expert_major();
 /* RMSNorm rows of n <= 16384 values (rms_norm_fits); the _q8 form also
  * writes q8 of the result to q, bit-identical to launch_quantize over it */
 bool rms_norm_fits(int n);

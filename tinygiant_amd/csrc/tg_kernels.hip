@@ -347,6 +347,246 @@ __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, 
     }
 }
 
+/* ---- expert-major phases for Q4_K / Q6_K experts ----
+ * One workgroup column per active expert instead of per pair: each lane
+ * loads its weight items once and dots them with the q8 row of every pair of
+ * the expert, staged MOE_X_MAXP rows at a time in LDS.  Each pair's sums run
+ * over the same items in the same order as k_moe_a / k_moe_b, so the
+ * results are the same bits. */
+constexpr int MOE_X_MAXP = 8;
+
+/* LDS bytes of one staged q8 row of nb blocks: qs [nb*256], s32 [nb*8],
+ * s16 [nb*16], d [nb] */
+__host__ __device__ constexpr uint32_t q8_lds_stride(int nb) { return ((uint32_t)nb * 356u + 15u) & ~15u; }
+
+__device__ inline Q8Lds q8_lds_slot(const uint8_t *base, int nb, int s) {
+    const uint8_t *b = base + (size_t)s * q8_lds_stride(nb);
+    return Q8Lds{b, b + nb * 352, b + nb * 256, b + nb * 288};
+}
+
+/* q8 rows rows[0..n) of q into LDS slots 0..n-1 by the whole workgroup */
+__device__ inline void q8_rows_to_lds(const Q8Rows &q, const int *rows, int n, uint8_t *lds) {
+    const int nb = q.nb, per = nb * 22;   /* 16-byte units of qs, s32 and s16 */
+    for (int u = threadIdx.x; u < n * per; u += blockDim.x) {
+        const int s = u / per, v = u % per;
+        const size_t r = (size_t)rows[s];
+        const u32x4 *src;
+        uint32_t dst;
+        if (v < nb * 16) {
+            src = reinterpret_cast<const u32x4 *>(q.qs + r * nb * 256) + v;
+            dst = (uint32_t)v * 16;
+        } else if (v < nb * 18) {
+            src = reinterpret_cast<const u32x4 *>(q.s32 + r * nb * 8) + (v - nb * 16);
+            dst = nb * 256 + (uint32_t)(v - nb * 16) * 16;
+        } else {
+            src = reinterpret_cast<const u32x4 *>(q.s16 + r * nb * 16) + (v - nb * 18);
+            dst = nb * 288 + (uint32_t)(v - nb * 18) * 16;
+        }
+        *reinterpret_cast<u32x4 *>(lds + (size_t)s * q8_lds_stride(nb) + dst) = *src;
+    }
+    for (int u = threadIdx.x; u < n * nb; u += blockDim.x) {
+        const int s = u / nb, b = u % nb;
+        reinterpret_cast<float *>(lds + (size_t)s * q8_lds_stride(nb) + nb * 352)[b] = q.d[(size_t)rows[s] * nb + b];
+    }
+}
+
+/* q8 of f32 rows src[rows[s] * ld ..] (nb 256-value blocks each) into LDS
+ * slots 0..n-1, block per wave, with the arithmetic of k_quantize_q8 (the
+ * same bits).  With gw set, row s is also written to q8 row grows[s] of
+ * gout. */
+constexpr int Q8Q_BATCH = 8;   /* blocks per wave whose loads are in flight together */
+__device__ inline void q8_quant_rows_lds(const float *__restrict__ src, int ld, const int *rows, int n, int nb,
+                                         uint8_t *lds, bool gw, Q8Rows gout, const int *grows) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    for (int u0 = wave; u0 < n * nb; u0 += nw * Q8Q_BATCH) {
+        u32x4 raw[Q8Q_BATCH];
+#pragma unroll
+        for (int i = 0; i < Q8Q_BATCH; i++) {
+            const int u = u0 + i * nw;
+            const bool uv = u < n * nb;
+            const int s = uv ? u / nb : 0, b = uv ? u % nb : 0;
+            const Buf xb = make_buf(src + (size_t)rows[s] * ld + (size_t)b * 256, uv ? 1024u : 0u);
+            raw[i] = ld16(xb, (uint32_t)lane * 16u);
+        }
+#pragma unroll
+        for (int i = 0; i < Q8Q_BATCH; i++) {
+            const int u = u0 + i * nw;
+            if (u >= n * nb) continue;   /* uniform per wave */
+            const int s = u / nb, b = u % nb;
+            const float v0 = __uint_as_float(raw[i].x), v1 = __uint_as_float(raw[i].y);
+            const float v2 = __uint_as_float(raw[i].z), v3 = __uint_as_float(raw[i].w);
+            const Q8Quant q = q8_block_quant(v0, v1, v2, v3);
+            uint8_t *slot = lds + (size_t)s * q8_lds_stride(nb);
+            reinterpret_cast<uint32_t *>(slot + b * 256)[lane] = q.packed;
+            if ((lane & 3) == 0) reinterpret_cast<int32_t *>(slot + nb * 288)[b * 16 + (lane >> 2)] = q.s16;
+            if ((lane & 7) == 0) reinterpret_cast<int32_t *>(slot + nb * 256)[b * 8 + (lane >> 3)] = q.s32;
+            if (lane == 0) reinterpret_cast<float *>(slot + nb * 352)[b] = q.sc;
+            if (gw) q8_block_store(v0, v1, v2, v3, lane, gout, grows[s], b);
+        }
+    }
+}
+
+/* Phase A, expert-major: grid (x: wave groups over the I rows, y: active
+ * expert a.mx_act[y]).  Each wave owns 64/S rows with all T <= TB items of
+ * each in registers.  QX: the workgroup quantizes its pairs' input rows
+ * from a.xin itself (no q8 launch before it); otherwise it copies them from
+ * a.xq. */
+template <class F, int S, int TB, bool QX>
+__global__ __launch_bounds__(256) void k_moe_ax(MoeArgs a, int nitems, int T) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
+    __shared__ int srow[MOE_X_MAXP];
+    constexpr int G = 64 / S;
+    const int e = a.mx_act[blockIdx.y];
+    const int p0 = a.p_off[e], np = a.p_off[e + 1] - p0;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int r = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * G + seg;
+    const bool rv = r < a.I;
+    const uint32_t rb = a.gate_rb;
+    const size_t mbytes = (size_t)a.I * rb;
+    const Buf gw = make_buf((const void *)a.gate[e], (uint32_t)mbytes);
+    const Buf uw = make_buf((const void *)a.up[e], (uint32_t)mbytes);
+    typename F::W wg[TB], wu[TB];
+#pragma unroll
+    for (int u = 0; u < TB; u++) {
+        const int item = sl + u * S;
+        const bool iv = rv && u < T && item < nitems;
+        wg[u] = F::load_w(gw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+        wu[u] = F::load_w(uw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+    }
+    const float gb = rv && a.gbias ? ((const float *)a.gbias[e])[r] : 0.f;
+    const float ub = rv && a.ubias ? ((const float *)a.ubias[e])[r] : 0.f;
+    for (int c0 = 0; c0 < np; c0 += MOE_X_MAXP) {
+        const int nc = min(MOE_X_MAXP, np - c0);
+        __syncthreads();   /* the previous chunk's rows are no longer read */
+        if ((int)threadIdx.x < nc) srow[threadIdx.x] = a.p_row[p0 + c0 + threadIdx.x];
+        __syncthreads();
+        if (QX)
+            q8_quant_rows_lds(a.xin, a.D, srow, nc, a.xq.nb, xl, false, a.xq, srow);
+        else
+            q8_rows_to_lds(a.xq, srow, nc, xl);
+        __syncthreads();
+        for (int s = 0; s < nc; s++) {
+            const Q8Lds xr = q8_lds_slot(xl, a.xq.nb, s);
+            float ag = 0.f, au = 0.f;
+#pragma unroll
+            for (int u = 0; u < TB; u++) {
+                const int item = sl + u * S;
+                if (rv && u < T && item < nitems) {
+                    const typename F::X x = F::load_x(xr, item);
+                    ag += F::value(wg[u], x, item);
+                    au += F::value(wu[u], x, item);
+                }
+            }
+            float vg = seg_sum<S>(ag);
+            float vu = seg_sum<S>(au);
+            if (rv && sl == 0) {
+                if (a.gbias) vg += gb;
+                if (a.ubias) vu += ub;
+                a.hidden[(size_t)(p0 + c0 + s) * a.I + r] = act_fn(a.act, vg, vu);
+            }
+        }
+    }
+}
+
+/* Phase B, expert-major: grid (x: wave groups over the D rows, y: active
+ * expert).  Only experts whose down format is `fmt` run.  QH: each
+ * workgroup quantizes its pairs' hidden rows itself (column 0 also writes
+ * them to a.hq), so no q8 launch runs between the phases; otherwise it
+ * copies them from a.hq.
+ * CMB: the combine runs here too.  Partials are written through to memory;
+ * after its writes have completed, each workgroup takes a ticket on its row
+ * tile (a.ctr[blockIdx.x], system scope).  The workgroup with the last of
+ * the a.n_act_a tickets has every expert's partials for the tile's rows and
+ * adds them into a.out in expert order, as k_moe_combine does, then resets
+ * the counter to zero for the next call.  Nothing waits. */
+template <class F, int S, int TB, bool CMB, bool QH>
+__global__ __launch_bounds__(256) void k_moe_bx(MoeArgs a, int fmt, uint32_t rb, int nitems, int T) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
+    __shared__ int srow[MOE_X_MAXP];
+    constexpr int G = 64 / S;
+    const int e = a.mx_act[blockIdx.y];
+    if (a.down_fmt[e] != fmt) return;
+    const int p0 = a.p_off[e], np = a.p_off[e + 1] - p0;
+    const int lane = threadIdx.x & 63;
+    const int seg = lane / S, sl = lane % S;
+    const int r = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * G + seg;
+    const bool rv = r < a.D;
+    const Buf dw = make_buf((const void *)a.down[e], (uint32_t)((size_t)a.D * rb));
+    typename F::W wd[TB];
+#pragma unroll
+    for (int u = 0; u < TB; u++) {
+        const int item = sl + u * S;
+        const bool iv = rv && u < T && item < nitems;
+        wd[u] = F::load_w(dw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+    }
+    const float db = rv && a.dbias ? ((const float *)a.dbias[e])[r] : 0.f;
+    for (int c0 = 0; c0 < np; c0 += MOE_X_MAXP) {
+        const int nc = min(MOE_X_MAXP, np - c0);
+        __syncthreads();
+        if ((int)threadIdx.x < nc) srow[threadIdx.x] = p0 + c0 + threadIdx.x;
+        __syncthreads();
+        if (QH)
+            q8_quant_rows_lds(a.hidden, a.I, srow, nc, a.hq.nb, xl, blockIdx.x == 0, a.hq, srow);
+        else
+            q8_rows_to_lds(a.hq, srow, nc, xl);
+        __syncthreads();
+        for (int s = 0; s < nc; s++) {
+            const Q8Lds xr = q8_lds_slot(xl, a.hq.nb, s);
+            float acc = 0.f;
+#pragma unroll
+            for (int u = 0; u < TB; u++) {
+                const int item = sl + u * S;
+                if (rv && u < T && item < nitems) acc += F::value(wd[u], F::load_x(xr, item), item);
+            }
+            const float v = seg_sum<S>(acc);
+            const int p = p0 + c0 + s;
+            if (rv && sl == 0) {
+                const float o = a.p_w[p] * (v + (a.dbias ? db : 0.f));
+                if (CMB)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), make_buf(a.part, 0x7FFFFFFFu).r,
+                                                          (int)(((uint32_t)p * (uint32_t)a.D + (uint32_t)r) * 4u), 0,
+                                                          16 /* sc1 */);
+                else
+                    a.part[(size_t)p * a.D + r] = o;
+            }
+        }
+    }
+    if constexpr (CMB) {
+        __shared__ unsigned ticket;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            ticket = __hip_atomic_fetch_add(a.ctr + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __syncthreads();
+        if (ticket != (unsigned)(a.n_act_a - 1)) return;
+        const int tr = (blockDim.x >> 6) * G, r0 = blockIdx.x * tr;
+        const Buf pb = make_buf(a.part, 0x7FFFFFFFu);
+        for (int i = threadIdx.x; i < a.k * tr; i += blockDim.x) {
+            const int j = i / tr, c = r0 + i % tr;
+            if (c >= a.D) continue;
+            float o = a.out[(size_t)j * a.D + c];
+            /* the row's partials in batches of 8 loads, added in expert order */
+            for (int q0 = a.r_off[j]; q0 < a.r_off[j + 1]; q0 += 8) {
+                const int nq = min(8, a.r_off[j + 1] - q0);
+                float v[8];
+#pragma unroll
+                for (int t = 0; t < 8; t++) {
+                    const uint32_t pr = t < nq ? (uint32_t)a.r_pair[q0 + t] : 0u;
+                    v[t] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                        pb.r, t < nq ? (int)((pr * (uint32_t)a.D + (uint32_t)c) * 4u) : (int)ROW_OOB, 0,
+                        16 /* sc1 */));
+                }
+#pragma unroll
+                for (int t = 0; t < 8; t++)
+                    if (t < nq) o += v[t];
+            }
+            a.out[(size_t)j * a.D + c] = o;
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(a.ctr + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
 /* out[row][c] += part[p][c] for the pairs p of `row`, in expert order. */
 __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     const size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
@@ -569,6 +809,24 @@ static int g_grouped_min_rows = 4;
 void set_grouped_min_rows(int rows) { g_grouped_min_rows = rows < 0 ? 0 : rows; }
 int grouped_min_rows() { return g_grouped_min_rows; }
 
+static int g_expert_major = EM_DEFAULT;
+
+void set_expert_major(int mode) { g_expert_major = mode & EM_ALL; }
+int expert_major() { return g_expert_major; }
+
+/* the expert-major phases hold all T items of a row in registers and read
+ * Q4_K / Q6_K q8 items from LDS */
+static bool expert_major_ok(const MoeArgs &a, int fmt, int T) {
+    return (g_expert_major & EM_ON) && a.n_act_a > 0 && T <= 4 && (fmt == TG_FMT_Q4K || fmt == TG_FMT_Q6K);
+}
+/* Quantizing inside the phases repeats each row's q8 in every workgroup of
+ * its expert (~100 of them), and the ticket combine ends the down phase
+ * with a write-through and a read of every partial at memory latency: each
+ * beats the launch it saves only while the experts hold few pairs
+ * (measured on Qwen3-30B-A3B layers: 1 pair, 21.3 -> 17.5 us a layer; 5 to
+ * 16 rows, up to 4% slower). */
+constexpr int FUSE_MAX_ROWS = 2;
+
 /* the MFMA phases address each weight matrix and q8 table with one 31-bit
  * buffer range, copy 16-byte aligned slabs, and hold two slabs of a gate/up
  * row group in 64 KiB of LDS */
@@ -582,15 +840,33 @@ static bool grouped_fits(const MoeArgs &a) {
 
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
                 const std::function<void(int)> *mark, bool quantize_x) {
+    const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
+    const bool mx_a = mx_grouped && a.gate_fmt == TG_FMT_MXFP4 && a.xp;
+    int Ta;
+    pick_S(items_per_row(a.gate_fmt, a.D), &Ta);
+    /* expert-major phase A quantizes device-resident input rows itself */
+    const bool ax = !mx_a && expert_major_ok(a, a.gate_fmt, Ta);
+    const bool few = a.max_rows <= FUSE_MAX_ROWS || (g_expert_major & EM_FUSE_ANY);
+    const bool q8_fused = (g_expert_major & EM_FUSE_Q8) && few;
+    const bool qx_fused = quantize_x && ax && !a.xin_remote && q8_fused;
+    /* expert-major phase B (every down format Q4_K / Q6_K) quantizes the
+     * hidden rows itself and, given tile counters, also combines */
+    int Tb;
+    const int Sb = pick_S(items_per_row(TG_FMT_Q6K, a.I), &Tb);   /* Q4_K rows have as many items */
+    bool bx = n_down_fmts > 0;
+    for (int i = 0; i < n_down_fmts; i++) bx = bx && expert_major_ok(a, down_fmts_present[i], Tb);
+    const int tiles_b = ((a.D + 64 / Sb - 1) / (64 / Sb) + 3) / 4;
+    const bool qh_fused = bx && q8_fused;
+    const bool cmb = bx && (g_expert_major & EM_TICKETS) && few && a.ctr && tiles_b <= a.ctr_n &&
+                     (uint64_t)a.P * a.D * 4 < (1ull << 31);
     /* 1. quantize the k input rows */
-    if (quantize_x) {
+    if (quantize_x && !qx_fused) {
         launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
         if (mark) (*mark)(1);
     }
     /* 2. phase A: MXFP4 experts with many pairs take the MFMA kernel, which
      * reads each weight block once for up to 64 pairs */
-    const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
-    if (mx_grouped && a.gate_fmt == TG_FMT_MXFP4 && a.xp) {
+    if (mx_a) {
         launch_mx_split(a.xq, a.k, a.D, a.xp, st);
         launch_moe_a_mx(a, st);
     } else {
@@ -601,14 +877,34 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         const int waves = (a.I + rpw - 1) / rpw;
         dim3 grid((waves + 3) / 4, a.P);
         const int TB = pick_TB(T);
-#define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_a<F, S_, TB_>), grid, dim3(256), 0, st, a, nitems, T, rpw)
-        TG_DISPATCH_F(a.gate_fmt, TG_DISPATCH_ST(S, TB, CALL))
+        if (ax) {
+            const dim3 gx(grid.x, a.n_act_a);
+            const size_t lds = (size_t)std::min(a.max_rows, MOE_X_MAXP) * q8_lds_stride(a.xq.nb);
+#define CALL(S_, TB_)                                                                                   \
+    if (qx_fused)                                                                                       \
+        hipLaunchKernelGGL((k_moe_ax<F, S_, TB_, true>), gx, dim3(256), lds, st, a, nitems, T);         \
+    else                                                                                                \
+        hipLaunchKernelGGL((k_moe_ax<F, S_, TB_, false>), gx, dim3(256), lds, st, a, nitems, T)
+            if (a.gate_fmt == TG_FMT_Q4K) {
+                typedef FQ4K F;
+                TG_DISPATCH_ST(S, TB, CALL)
+            } else {
+                typedef FQ6K F;
+                TG_DISPATCH_ST(S, TB, CALL)
+            }
 #undef CALL
+        } else {
+#define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_a<F, S_, TB_>), grid, dim3(256), 0, st, a, nitems, T, rpw)
+            TG_DISPATCH_F(a.gate_fmt, TG_DISPATCH_ST(S, TB, CALL))
+#undef CALL
+        }
     }
     if (mark) (*mark)(2);
     /* 3. quantize the hidden rows */
-    launch_quantize(a.hidden, a.I, a.P, a.I, a.hq, st);
-    if (mark) (*mark)(3);
+    if (!qh_fused) {
+        launch_quantize(a.hidden, a.I, a.P, a.I, a.hq, st);
+        if (mark) (*mark)(3);
+    }
     /* 4. phase B, once per down format present */
     for (int i = 0; i < n_down_fmts; i++) {
         const int fmt = down_fmts_present[i];
@@ -625,11 +921,34 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         const uint32_t rb = row_bytes(fmt, a.I);
         dim3 grid((waves + 3) / 4, a.P);
         const int TB = pick_TB(T);
+        if (bx) {
+            const dim3 gx(grid.x, a.n_act_a);
+            const size_t lds = (size_t)std::min(a.max_rows, MOE_X_MAXP) * q8_lds_stride(a.hq.nb);
+#define CALL(S_, TB_)                                                                                          \
+    if (cmb && qh_fused)                                                                                       \
+        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, true, true>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T); \
+    else if (cmb)                                                                                              \
+        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, true, false>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T);\
+    else if (qh_fused)                                                                                         \
+        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, false, true>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T);\
+    else                                                                                                       \
+        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, false, false>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T)
+            if (fmt == TG_FMT_Q4K) {
+                typedef FQ4K F;
+                TG_DISPATCH_ST(S, TB, CALL)
+            } else {
+                typedef FQ6K F;
+                TG_DISPATCH_ST(S, TB, CALL)
+            }
+#undef CALL
+            continue;
+        }
 #define CALL(S_, TB_) hipLaunchKernelGGL((k_moe_b<F, S_, TB_>), grid, dim3(256), 0, st, a, fmt, rb, nitems, T, rpw)
         TG_DISPATCH_F(fmt, TG_DISPATCH_ST(S, TB, CALL))
 #undef CALL
     }
     if (mark) (*mark)(4);
+    if (cmb) return;
     /* 5. combine */
     const size_t n = (size_t)a.k * a.D;
     hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
