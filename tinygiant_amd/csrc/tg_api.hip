@@ -338,6 +338,7 @@ Layout plan_layout(const HostPlan &h) {
     t += (size_t)n * 4;                     /* down_fmt */
     t += (size_t)(n + 1) * 4 + (size_t)P * 4 * 4 + (size_t)(k + 1) * 4 + 8;   /* p_off, p_row, p_exp, p_w, r_off, r_pair */
     t += (size_t)4 * (n + 1) * 4 + 16;      /* active expert lists and their cost prefixes */
+    t += (size_t)n * sizeof(ExpDesc) + 16;  /* active expert descriptors */
     L.tables_len = t + 64;
     b.take(L.tables_len);
     L.xin = b.take((size_t)k * h.D * 4);
@@ -432,6 +433,21 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     };
     prefix(act_a, h.I, 10, 19);
     prefix(act_b, h.D, 5, 18);
+    std::vector<ExpDesc> ed(a.n_act_a);
+    for (int i = 0; i < a.n_act_a; i++) {
+        const int e = act_a[i];
+        ExpDesc &d = ed[i];
+        memset(&d, 0, sizeof d);
+        d.gate = h.gate[e];
+        d.up = h.up[e];
+        d.down = h.down[e];
+        d.e = e;
+        d.p0 = h.p_off[e];
+        d.np = h.p_off[e + 1] - h.p_off[e];
+        d.down_fmt = h.down_fmt[e];
+        for (int s = 0; s < std::min(d.np, EXP_ROWS); s++) d.row[s] = h.p_row[d.p0 + s];
+    }
+    a.ed = (const ExpDesc *)put(ed.data(), ed.size() * sizeof(ExpDesc));
     act_a.insert(act_a.end(), act_b.begin(), act_b.end());
     a.mx_act = (const int *)put(act_a.data(), act_a.size() * 4);
     a.mx_cum = (const int *)put(cum.data(), cum.size() * 4);

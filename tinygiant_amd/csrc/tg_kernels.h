@@ -14,6 +14,16 @@
 
 namespace tg {
 
+/* One active expert of a layer call, read by a workgroup of the
+ * expert-major phases in one scalar burst: weight addresses, its pairs
+ * [p0, p0 + np) and the input rows of the first EXP_ROWS of them. */
+#define EXP_ROWS 8
+struct ExpDesc {
+    uint64_t gate, up, down;
+    int e, p0, np, down_fmt;
+    int row[EXP_ROWS];
+};
+
 /* Everything one MoE layer call needs, all pointers on the device.
  * Pairs p = (expert e, active input row) are numbered expert-major, in the
  * order the reference gathers them (csrc/libtinygiant.c:1411-1423). */
@@ -41,6 +51,7 @@ struct MoeArgs {
     const int *mx_cum;                      /* cost prefix of each list (n_act + 1 entries each) */
     uint8_t *xp, *hp;                       /* fp8 halves of xq / hq rows in MFMA order, or null */
     int n_act_a, n_act_b;
+    const ExpDesc *ed;                      /* [n_act_a] active experts, the order of mx_act */
     unsigned *ctr;                          /* [ctr_n] row-tile tickets of the fused combine, zero between calls, or null */
     int ctr_n;
     int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */

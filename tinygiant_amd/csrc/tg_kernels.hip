@@ -354,6 +354,7 @@ __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, 
  * over the same items in the same order as k_moe_a / k_moe_b, so the
  * results are the same bits. */
 constexpr int MOE_X_MAXP = 8;
+static_assert(MOE_X_MAXP == EXP_ROWS, "the first chunk's rows come from the expert descriptor");
 
 /* LDS bytes of one staged q8 row of nb blocks: qs [nb*256], s32 [nb*8],
  * s16 [nb*16], d [nb] */
@@ -427,39 +428,44 @@ __device__ inline void q8_quant_rows_lds(const float *__restrict__ src, int ld, 
 }
 
 /* Phase A, expert-major: grid (x: wave groups over the I rows, y: active
- * expert a.mx_act[y]).  Each wave owns 64/S rows with all T <= TB items of
- * each in registers.  QX: the workgroup quantizes its pairs' input rows
- * from a.xin itself (no q8 launch before it); otherwise it copies them from
- * a.xq. */
-template <class F, int S, int TB, bool QX>
+ * expert a.mx_act[y]).  Each wave owns NP passes of 64/S rows, with all
+ * T <= TB items of each row in registers before any pair is dotted.  QX:
+ * the workgroup quantizes its pairs' input rows from a.xin itself (no q8
+ * launch before it); otherwise it copies them from a.xq. */
+template <class F, int S, int TB, int NP, bool QX>
 __global__ __launch_bounds__(256) void k_moe_ax(MoeArgs a, int nitems, int T) {
     extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
     __shared__ int srow[MOE_X_MAXP];
     constexpr int G = 64 / S;
-    const int e = a.mx_act[blockIdx.y];
-    const int p0 = a.p_off[e], np = a.p_off[e + 1] - p0;
+    const ExpDesc &d = a.ed[blockIdx.y];
+    const int e = d.e, p0 = d.p0, np = d.np;
     const int lane = threadIdx.x & 63;
     const int seg = lane / S, sl = lane % S;
-    const int r = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * G + seg;
-    const bool rv = r < a.I;
+    const int rw = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * NP * G + seg;
     const uint32_t rb = a.gate_rb;
     const size_t mbytes = (size_t)a.I * rb;
-    const Buf gw = make_buf((const void *)a.gate[e], (uint32_t)mbytes);
-    const Buf uw = make_buf((const void *)a.up[e], (uint32_t)mbytes);
-    typename F::W wg[TB], wu[TB];
+    const Buf gw = make_buf((const void *)d.gate, (uint32_t)mbytes);
+    const Buf uw = make_buf((const void *)d.up, (uint32_t)mbytes);
+    typename F::W wg[NP][TB], wu[NP][TB];
+    float gb[NP], ub[NP];
 #pragma unroll
-    for (int u = 0; u < TB; u++) {
-        const int item = sl + u * S;
-        const bool iv = rv && u < T && item < nitems;
-        wg[u] = F::load_w(gw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
-        wu[u] = F::load_w(uw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+    for (int i = 0; i < NP; i++) {
+        const int r = rw + i * G;
+        const bool rv = r < a.I;
+#pragma unroll
+        for (int u = 0; u < TB; u++) {
+            const int item = sl + u * S;
+            const bool iv = rv && u < T && item < nitems;
+            wg[i][u] = F::load_w(gw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+            wu[i][u] = F::load_w(uw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+        }
+        gb[i] = rv && a.gbias ? ((const float *)a.gbias[e])[r] : 0.f;
+        ub[i] = rv && a.ubias ? ((const float *)a.ubias[e])[r] : 0.f;
     }
-    const float gb = rv && a.gbias ? ((const float *)a.gbias[e])[r] : 0.f;
-    const float ub = rv && a.ubias ? ((const float *)a.ubias[e])[r] : 0.f;
     for (int c0 = 0; c0 < np; c0 += MOE_X_MAXP) {
         const int nc = min(MOE_X_MAXP, np - c0);
         __syncthreads();   /* the previous chunk's rows are no longer read */
-        if ((int)threadIdx.x < nc) srow[threadIdx.x] = a.p_row[p0 + c0 + threadIdx.x];
+        if ((int)threadIdx.x < nc) srow[threadIdx.x] = c0 == 0 ? d.row[threadIdx.x] : a.p_row[p0 + c0 + threadIdx.x];
         __syncthreads();
         if (QX)
             q8_quant_rows_lds(a.xin, a.D, srow, nc, a.xq.nb, xl, false, a.xq, srow);
@@ -468,59 +474,69 @@ __global__ __launch_bounds__(256) void k_moe_ax(MoeArgs a, int nitems, int T) {
         __syncthreads();
         for (int s = 0; s < nc; s++) {
             const Q8Lds xr = q8_lds_slot(xl, a.xq.nb, s);
-            float ag = 0.f, au = 0.f;
 #pragma unroll
-            for (int u = 0; u < TB; u++) {
-                const int item = sl + u * S;
-                if (rv && u < T && item < nitems) {
-                    const typename F::X x = F::load_x(xr, item);
-                    ag += F::value(wg[u], x, item);
-                    au += F::value(wu[u], x, item);
+            for (int i = 0; i < NP; i++) {
+                const int r = rw + i * G;
+                const bool rv = r < a.I;
+                float ag = 0.f, au = 0.f;
+#pragma unroll
+                for (int u = 0; u < TB; u++) {
+                    const int item = sl + u * S;
+                    if (rv && u < T && item < nitems) {
+                        const typename F::X x = F::load_x(xr, item);
+                        ag += F::value(wg[i][u], x, item);
+                        au += F::value(wu[i][u], x, item);
+                    }
                 }
-            }
-            float vg = seg_sum<S>(ag);
-            float vu = seg_sum<S>(au);
-            if (rv && sl == 0) {
-                if (a.gbias) vg += gb;
-                if (a.ubias) vu += ub;
-                a.hidden[(size_t)(p0 + c0 + s) * a.I + r] = act_fn(a.act, vg, vu);
+                float vg = seg_sum<S>(ag);
+                float vu = seg_sum<S>(au);
+                if (rv && sl == 0) {
+                    if (a.gbias) vg += gb[i];
+                    if (a.ubias) vu += ub[i];
+                    a.hidden[(size_t)(p0 + c0 + s) * a.I + r] = act_fn(a.act, vg, vu);
+                }
             }
         }
     }
 }
 
 /* Phase B, expert-major: grid (x: wave groups over the D rows, y: active
- * expert).  Only experts whose down format is `fmt` run.  QH: each
- * workgroup quantizes its pairs' hidden rows itself (column 0 also writes
- * them to a.hq), so no q8 launch runs between the phases; otherwise it
- * copies them from a.hq.
+ * expert), NP passes of 64/S rows per wave as in k_moe_ax.  Only experts
+ * whose down format is `fmt` run.  QH: each workgroup quantizes its pairs'
+ * hidden rows itself (column 0 also writes them to a.hq), so no q8 launch
+ * runs between the phases; otherwise it copies them from a.hq.
  * CMB: the combine runs here too.  Partials are written through to memory;
  * after its writes have completed, each workgroup takes a ticket on its row
  * tile (a.ctr[blockIdx.x], system scope).  The workgroup with the last of
  * the a.n_act_a tickets has every expert's partials for the tile's rows and
  * adds them into a.out in expert order, as k_moe_combine does, then resets
  * the counter to zero for the next call.  Nothing waits. */
-template <class F, int S, int TB, bool CMB, bool QH>
+template <class F, int S, int TB, int NP, bool CMB, bool QH>
 __global__ __launch_bounds__(256) void k_moe_bx(MoeArgs a, int fmt, uint32_t rb, int nitems, int T) {
     extern __shared__ __attribute__((aligned(16))) uint8_t xl[];
     __shared__ int srow[MOE_X_MAXP];
     constexpr int G = 64 / S;
-    const int e = a.mx_act[blockIdx.y];
-    if (a.down_fmt[e] != fmt) return;
-    const int p0 = a.p_off[e], np = a.p_off[e + 1] - p0;
+    const ExpDesc &d = a.ed[blockIdx.y];
+    if (d.down_fmt != fmt) return;
+    const int e = d.e, p0 = d.p0, np = d.np;
     const int lane = threadIdx.x & 63;
     const int seg = lane / S, sl = lane % S;
-    const int r = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * G + seg;
-    const bool rv = r < a.D;
-    const Buf dw = make_buf((const void *)a.down[e], (uint32_t)((size_t)a.D * rb));
-    typename F::W wd[TB];
+    const int rw = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * NP * G + seg;
+    const Buf dw = make_buf((const void *)d.down, (uint32_t)((size_t)a.D * rb));
+    typename F::W wd[NP][TB];
+    float db[NP];
 #pragma unroll
-    for (int u = 0; u < TB; u++) {
-        const int item = sl + u * S;
-        const bool iv = rv && u < T && item < nitems;
-        wd[u] = F::load_w(dw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+    for (int i = 0; i < NP; i++) {
+        const int r = rw + i * G;
+        const bool rv = r < a.D;
+#pragma unroll
+        for (int u = 0; u < TB; u++) {
+            const int item = sl + u * S;
+            const bool iv = rv && u < T && item < nitems;
+            wd[i][u] = F::load_w(dw, iv ? (uint32_t)r * rb : ROW_OOB, iv ? item : 0);
+        }
+        db[i] = rv && a.dbias ? ((const float *)a.dbias[e])[r] : 0.f;
     }
-    const float db = rv && a.dbias ? ((const float *)a.dbias[e])[r] : 0.f;
     for (int c0 = 0; c0 < np; c0 += MOE_X_MAXP) {
         const int nc = min(MOE_X_MAXP, np - c0);
         __syncthreads();
@@ -533,22 +549,27 @@ __global__ __launch_bounds__(256) void k_moe_bx(MoeArgs a, int fmt, uint32_t rb,
         __syncthreads();
         for (int s = 0; s < nc; s++) {
             const Q8Lds xr = q8_lds_slot(xl, a.hq.nb, s);
-            float acc = 0.f;
-#pragma unroll
-            for (int u = 0; u < TB; u++) {
-                const int item = sl + u * S;
-                if (rv && u < T && item < nitems) acc += F::value(wd[u], F::load_x(xr, item), item);
-            }
-            const float v = seg_sum<S>(acc);
             const int p = p0 + c0 + s;
-            if (rv && sl == 0) {
-                const float o = a.p_w[p] * (v + (a.dbias ? db : 0.f));
-                if (CMB)
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), make_buf(a.part, 0x7FFFFFFFu).r,
-                                                          (int)(((uint32_t)p * (uint32_t)a.D + (uint32_t)r) * 4u), 0,
-                                                          16 /* sc1 */);
-                else
-                    a.part[(size_t)p * a.D + r] = o;
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+                const int r = rw + i * G;
+                const bool rv = r < a.D;
+                float acc = 0.f;
+#pragma unroll
+                for (int u = 0; u < TB; u++) {
+                    const int item = sl + u * S;
+                    if (rv && u < T && item < nitems) acc += F::value(wd[i][u], F::load_x(xr, item), item);
+                }
+                const float v = seg_sum<S>(acc);
+                if (rv && sl == 0) {
+                    const float o = a.p_w[p] * (v + (a.dbias ? db[i] : 0.f));
+                    if (CMB)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o), make_buf(a.part, 0x7FFFFFFFu).r,
+                                                              (int)(((uint32_t)p * (uint32_t)a.D + (uint32_t)r) * 4u),
+                                                              0, 16 /* sc1 */);
+                    else
+                        a.part[(size_t)p * a.D + r] = o;
+                }
             }
         }
     }
@@ -560,7 +581,7 @@ __global__ __launch_bounds__(256) void k_moe_bx(MoeArgs a, int fmt, uint32_t rb,
             ticket = __hip_atomic_fetch_add(a.ctr + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         __syncthreads();
         if (ticket != (unsigned)(a.n_act_a - 1)) return;
-        const int tr = (blockDim.x >> 6) * G, r0 = blockIdx.x * tr;
+        const int tr = (blockDim.x >> 6) * NP * G, r0 = blockIdx.x * tr;
         const Buf pb = make_buf(a.part, 0x7FFFFFFFu);
         for (int i = threadIdx.x; i < a.k * tr; i += blockDim.x) {
             const int j = i / tr, c = r0 + i % tr;
@@ -838,6 +859,33 @@ static bool grouped_fits(const MoeArgs &a) {
     return a.mx_aligned && gu < lim && dn < lim && xq < lim && hq < lim && grouped_lds_ok(a.D, a.I);
 }
 
+/* The expert-major launches.  Each wave takes NP = 1 pass of 64/S rows:
+ * two or four passes per wave measured slower at every pair count
+ * (Qwen3-30B-A3B verify layers, k = 16: 67.6 -> 76.2 and 90.1 us). */
+template <class F, int S, int TB>
+static void launch_ax(const MoeArgs &a, int nitems, int T, bool qx, size_t lds, hipStream_t st) {
+    const int waves = (a.I + (64 / S) - 1) / (64 / S);
+    const dim3 g((waves + 3) / 4, a.n_act_a);
+    if (qx)
+        hipLaunchKernelGGL((k_moe_ax<F, S, TB, 1, true>), g, dim3(256), lds, st, a, nitems, T);
+    else
+        hipLaunchKernelGGL((k_moe_ax<F, S, TB, 1, false>), g, dim3(256), lds, st, a, nitems, T);
+}
+template <class F, int S, int TB>
+static void launch_bx(const MoeArgs &a, int fmt, uint32_t rb, int nitems, int T, bool cmb, bool qh, size_t lds,
+                      hipStream_t st) {
+    const int waves = (a.D + (64 / S) - 1) / (64 / S);
+    const dim3 g((waves + 3) / 4, a.n_act_a);
+    if (cmb && qh)
+        hipLaunchKernelGGL((k_moe_bx<F, S, TB, 1, true, true>), g, dim3(256), lds, st, a, fmt, rb, nitems, T);
+    else if (cmb)
+        hipLaunchKernelGGL((k_moe_bx<F, S, TB, 1, true, false>), g, dim3(256), lds, st, a, fmt, rb, nitems, T);
+    else if (qh)
+        hipLaunchKernelGGL((k_moe_bx<F, S, TB, 1, false, true>), g, dim3(256), lds, st, a, fmt, rb, nitems, T);
+    else
+        hipLaunchKernelGGL((k_moe_bx<F, S, TB, 1, false, false>), g, dim3(256), lds, st, a, fmt, rb, nitems, T);
+}
+
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
                 const std::function<void(int)> *mark, bool quantize_x) {
     const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
@@ -878,13 +926,8 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         dim3 grid((waves + 3) / 4, a.P);
         const int TB = pick_TB(T);
         if (ax) {
-            const dim3 gx(grid.x, a.n_act_a);
             const size_t lds = (size_t)std::min(a.max_rows, MOE_X_MAXP) * q8_lds_stride(a.xq.nb);
-#define CALL(S_, TB_)                                                                                   \
-    if (qx_fused)                                                                                       \
-        hipLaunchKernelGGL((k_moe_ax<F, S_, TB_, true>), gx, dim3(256), lds, st, a, nitems, T);         \
-    else                                                                                                \
-        hipLaunchKernelGGL((k_moe_ax<F, S_, TB_, false>), gx, dim3(256), lds, st, a, nitems, T)
+#define CALL(S_, TB_) launch_ax<F, S_, TB_>(a, nitems, T, qx_fused, lds, st)
             if (a.gate_fmt == TG_FMT_Q4K) {
                 typedef FQ4K F;
                 TG_DISPATCH_ST(S, TB, CALL)
@@ -922,17 +965,8 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         dim3 grid((waves + 3) / 4, a.P);
         const int TB = pick_TB(T);
         if (bx) {
-            const dim3 gx(grid.x, a.n_act_a);
             const size_t lds = (size_t)std::min(a.max_rows, MOE_X_MAXP) * q8_lds_stride(a.hq.nb);
-#define CALL(S_, TB_)                                                                                          \
-    if (cmb && qh_fused)                                                                                       \
-        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, true, true>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T); \
-    else if (cmb)                                                                                              \
-        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, true, false>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T);\
-    else if (qh_fused)                                                                                         \
-        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, false, true>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T);\
-    else                                                                                                       \
-        hipLaunchKernelGGL((k_moe_bx<F, S_, TB_, false, false>), gx, dim3(256), lds, st, a, fmt, rb, nitems, T)
+#define CALL(S_, TB_) launch_bx<F, S_, TB_>(a, fmt, rb, nitems, T, cmb, qh_fused, lds, st)
             if (fmt == TG_FMT_Q4K) {
                 typedef FQ4K F;
                 TG_DISPATCH_ST(S, TB, CALL)
