@@ -644,7 +644,7 @@ def main():
         names = ["rms_norm_q8", "quantize_x", "gate_up", "quantize_h", "down", "combine"]
         per_kernel = {names[i]: {"avg_us": round(kms[i] / max(kn[i], 1) * 1e3, 2), "launches": kn[i]}
                       for i in range(6)}
-        kernel_name = "k_moe_a<FQ4K,32> (gate+up+SiLU, 8 experts)"
+        kernel_name = "k_moe_ax<FQ4K,32> (gate+up+SiLU, expert-major, 8 experts)"
         k_us = kms[2] / max(kn[2], 1) * 1e3
         k_bytes = TOPK * 2 * GATE_B
         traffic = read_traffic("pmc_moe_gate_up_qwen_decode.txt")
