@@ -280,12 +280,13 @@ void tg_hip_device_name(char *buf, int n);
  * Default 4.  Returns the previous setting.  No counterpart in the
  * reference, which has one CPU kernel for every row count. */
 int tg_hip_set_moe_grouped_min_rows(int rows);
-/* Q4_K / Q6_K expert layers run expert-major (bit 1): each weight row is
+/* Q4_K / Q6_K expert layers, and MXFP4 ones below the MFMA threshold, run
+ * expert-major (bit 1): each weight row is
  * read once and dotted with the q8 row of every pair of its expert, as
  * moe_phase_a / moe_phase_b do with dot_fmt_x4 (csrc/libtinygiant.c:
  * 1279-1384, :622-628).  For a layer with at most two pairs per expert:
  * bit 2, the two phases quantize their rows themselves instead of q8
- * launches; bit 4, the down phase also adds the partials into the output
+ * launches (rows of at most 2048 values); bit 4, the down phase also adds the partials into the output
  * rows (the last workgroup of each row tile, in expert order) instead of a
  * combine launch.  Bit 8: bits 2 and 4 whatever the pair count.  0 runs one
  * workgroup column per pair with the q8 and combine launches.  Every mode

@@ -312,6 +312,47 @@ def test_moe_expert_major_equals_per_pair(tg, orc, k, pool, top, mixed):
     assert ok, rel
 
 
+@pytest.mark.parametrize("k", [1, 3])
+def test_moe_expert_major_mxfp4_equals_per_pair(tg, orc, k):
+    """gpt-oss shape (D = I = 2880: a partial last 256-block per row), MXFP4
+    gate/up/down with biases and the gpt-oss activation, at most 3 pairs per
+    expert (below the MFMA phases): expert-major phases in every mode give
+    the per-pair kernels' bits."""
+    say("moe expert-major mxfp4", k)
+    import tinygiant_amd.synth as S
+    rng = np.random.default_rng(900 + k)
+    experts, rw = S.routing_rows(rng, k, 8, 4)
+    n, D, I = len(experts), 2880, 2880
+    fmts = [O.FMT_MXFP4] * n
+    g, u, d = _experts(n, D, I, O.FMT_MXFP4, fmts, 43)
+    gb = [rng.uniform(-0.5, 0.5, I).astype(np.float32) for _ in range(n)]
+    ub = [rng.uniform(-0.5, 0.5, I).astype(np.float32) for _ in range(n)]
+    db = [rng.uniform(-0.05, 0.05, D).astype(np.float32) for _ in range(n)]
+    x = rng.uniform(-1, 1, (k, D)).astype(np.float32)
+    base = rng.standard_normal((k, D)).astype(np.float32)
+    P = int(np.count_nonzero(rw))
+    assert int(np.count_nonzero(rw, axis=1).max()) < 4
+    lib = tg.lib()
+    outs = []
+    prev = lib.tg_hip_set_moe_expert_major(7)
+    try:
+        for on in (7, 0, 1, 15):
+            lib.tg_hip_set_moe_expert_major(on)
+            h = np.zeros((P, I), np.float32)
+            o = tg.moe_forward_rows_v2(g, u, d, O.FMT_MXFP4, fmts, gb, ub, db, O.ACT_GPTOSS, rw, x, base.copy(), I,
+                                       hidden_out=h)
+            outs.append((h, o))
+    finally:
+        lib.tg_hip_set_moe_expert_major(prev)
+    for h, o in outs[1:]:
+        assert h.tobytes() == outs[0][0].tobytes()
+        assert o.tobytes() == outs[0][1].tobytes()
+    ref = orc.moe_v2(g, u, d, O.FMT_MXFP4, fmts, gb, ub, db, O.ACT_GPTOSS, rw, x, base.copy(), I,
+                     hidden_in=outs[0][0])
+    ok, rel = close(outs[0][1], ref)
+    assert ok, rel
+
+
 def test_moe_registered_equals_staged(tg, orc):
     """tg_mlock (HBM-resident weights) and the per-call staging path agree bit for bit."""
     say("moe registered vs staged")

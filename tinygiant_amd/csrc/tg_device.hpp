@@ -419,7 +419,8 @@ struct FMXFP4 {
         r.c = ld16(w, p + 1);
         return r;
     }
-    __device__ static inline X load_x(const Q8Row &x, int item) {
+    template <class R>   /* Q8Row (global) or Q8Lds */
+    __device__ static inline X load_x(const R &x, int item) {
         uint32_t o = (uint32_t)(item >> 3) * 256 + (item & 7) * 32;
         X r;
         r.a = ld16(x.qs, o);

@@ -406,7 +406,9 @@ __device__ inline void q8_quant_rows_lds(const float *__restrict__ src, int ld, 
             const int u = u0 + i * nw;
             const bool uv = u < n * nb;
             const int s = uv ? u / nb : 0, b = uv ? u % nb : 0;
-            const Buf xb = make_buf(src + (size_t)rows[s] * ld + (size_t)b * 256, uv ? 1024u : 0u);
+            /* a row's last block may be partial: zeros past its end, as k_quantize_q8 reads */
+            const Buf xb = make_buf(src + (size_t)rows[s] * ld + (size_t)b * 256,
+                                    uv ? (uint32_t)min(256, ld - b * 256) * 4u : 0u);
             raw[i] = ld16(xb, (uint32_t)lane * 16u);
         }
 #pragma unroll
@@ -836,9 +838,10 @@ void set_expert_major(int mode) { g_expert_major = mode & EM_ALL; }
 int expert_major() { return g_expert_major; }
 
 /* the expert-major phases hold all T items of a row in registers and read
- * Q4_K / Q6_K q8 items from LDS */
+ * Q4_K / Q6_K / MXFP4 q8 items from LDS */
 static bool expert_major_ok(const MoeArgs &a, int fmt, int T) {
-    return (g_expert_major & EM_ON) && a.n_act_a > 0 && T <= 4 && (fmt == TG_FMT_Q4K || fmt == TG_FMT_Q6K);
+    return (g_expert_major & EM_ON) && a.n_act_a > 0 && T <= 4 &&
+           (fmt == TG_FMT_Q4K || fmt == TG_FMT_Q6K || fmt == TG_FMT_MXFP4);
 }
 /* Quantizing inside the phases repeats each row's q8 in every workgroup of
  * its expert (~100 of them), and the ticket combine ends the down phase
@@ -847,6 +850,10 @@ static bool expert_major_ok(const MoeArgs &a, int fmt, int T) {
  * (measured on Qwen3-30B-A3B layers: 1 pair, 21.3 -> 17.5 us a layer; 5 to
  * 16 rows, up to 4% slower). */
 constexpr int FUSE_MAX_ROWS = 2;
+/* ... and the in-phase q8 only for rows of at most 8 blocks: for gpt-oss's
+ * 12-block rows (2880 values, ~360 workgroups per expert) it measured 11%
+ * slower than the q8 launch (36-layer graph step 1.60 against 1.40 ms) */
+constexpr int FUSE_MAX_BLOCKS = 8;
 
 /* the MFMA phases address each weight matrix and q8 table with one 31-bit
  * buffer range, copy 16-byte aligned slabs, and hold two slabs of a gate/up
@@ -896,15 +903,21 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
     const bool ax = !mx_a && expert_major_ok(a, a.gate_fmt, Ta);
     const bool few = a.max_rows <= FUSE_MAX_ROWS || (g_expert_major & EM_FUSE_ANY);
     const bool q8_fused = (g_expert_major & EM_FUSE_Q8) && few;
-    const bool qx_fused = quantize_x && ax && !a.xin_remote && q8_fused;
+    const bool any = g_expert_major & EM_FUSE_ANY;
+    const bool qx_fused = quantize_x && ax && !a.xin_remote && q8_fused && (a.xq.nb <= FUSE_MAX_BLOCKS || any);
     /* expert-major phase B (every down format Q4_K / Q6_K) quantizes the
      * hidden rows itself and, given tile counters, also combines */
-    int Tb;
-    const int Sb = pick_S(items_per_row(TG_FMT_Q6K, a.I), &Tb);   /* Q4_K rows have as many items */
+    int Tb = 0, Sb = 64;
     bool bx = n_down_fmts > 0;
-    for (int i = 0; i < n_down_fmts; i++) bx = bx && expert_major_ok(a, down_fmts_present[i], Tb);
+    if (bx) Sb = pick_S(items_per_row(down_fmts_present[0], a.I), &Tb);
+    for (int i = 0; i < n_down_fmts; i++) {
+        const int f = down_fmts_present[i];
+        /* one grid (and one set of row tiles) for every format present */
+        bx = bx && expert_major_ok(a, f, Tb) && items_per_row(f, a.I) == items_per_row(down_fmts_present[0], a.I) &&
+             !(mx_grouped && f == TG_FMT_MXFP4 && a.hp);
+    }
     const int tiles_b = ((a.D + 64 / Sb - 1) / (64 / Sb) + 3) / 4;
-    const bool qh_fused = bx && q8_fused;
+    const bool qh_fused = bx && q8_fused && (a.hq.nb <= FUSE_MAX_BLOCKS || any);
     const bool cmb = bx && (g_expert_major & EM_TICKETS) && few && a.ctr && tiles_b <= a.ctr_n &&
                      (uint64_t)a.P * a.D * 4 < (1ull << 31);
     /* 1. quantize the k input rows */
@@ -931,8 +944,11 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
             if (a.gate_fmt == TG_FMT_Q4K) {
                 typedef FQ4K F;
                 TG_DISPATCH_ST(S, TB, CALL)
-            } else {
+            } else if (a.gate_fmt == TG_FMT_Q6K) {
                 typedef FQ6K F;
+                TG_DISPATCH_ST(S, TB, CALL)
+            } else {
+                typedef FMXFP4 F;
                 TG_DISPATCH_ST(S, TB, CALL)
             }
 #undef CALL
@@ -970,8 +986,11 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
             if (fmt == TG_FMT_Q4K) {
                 typedef FQ4K F;
                 TG_DISPATCH_ST(S, TB, CALL)
-            } else {
+            } else if (fmt == TG_FMT_Q6K) {
                 typedef FQ6K F;
+                TG_DISPATCH_ST(S, TB, CALL)
+            } else {
+                typedef FMXFP4 F;
                 TG_DISPATCH_ST(S, TB, CALL)
             }
 #undef CALL
