@@ -288,8 +288,8 @@ def configs_probe(tg, iters=20, plain=False):
                         launch and no graph, for profilers (rocprofv3 fails
                         on cooperative launches and on graph replays)
       gptoss_prefill    64 tokens through one gpt-oss layer (top-4 each): the
-                        int8 MFMA expert phases, and for comparison the
-                        per-pair kernels"""
+                        block-scaled f8f6f4 MFMA expert phases, and for
+                        comparison the per-pair kernels"""
     import tinygiant_amd.synth as S
     lib = tg.lib()
     out = {}
@@ -398,7 +398,7 @@ def configs_probe(tg, iters=20, plain=False):
     lib.tg_hip_set_moe_grouped_min_rows(prev)
     ops = 2 * kp * GK * 3 * GD * GD
     out["gptoss_prefill"] = {"tokens": kp, "experts": n, "rows_per_expert_max": int((rw != 0).sum(axis=1).max()),
-                             "path": "int8 MFMA phases" if int((rw != 0).sum(axis=1).max()) >= prev else "per-pair",
+                             "path": "block-scaled f8f6f4 MFMA phases" if int((rw != 0).sum(axis=1).max()) >= prev else "per-pair",
                              "us": round(us, 2), "us_per_pair_kernels": round(us_pp, 2),
                              "weight_bytes": n * exp_b,
                              "weight_gbps": round(n * exp_b / (us * 1e-6) / 1e9, 1),

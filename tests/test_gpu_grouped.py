@@ -1,4 +1,5 @@
-"""GPU parity of the MXFP4 expert phases on int8 MFMA (tg_grouped.hip):
+"""GPU parity of the MXFP4 expert phases on block-scaled f8f6f4 MFMA
+(v_mfma_scale_f32_16x16x128_f8f6f4, tg_grouped.hip):
 moe_phase_a / moe_phase_b (csrc/libtinygiant.c:1279-1384) over many pairs
 per expert, as a prefill or a long verify batch routes them.
 

@@ -15,7 +15,8 @@ mistake fails one of them:
     x4 == x1 (Tests 5, 6), MoE == per-row expert composition (Test 7),
     MXFP4 + gpt-oss activation + biases vs float64 (Test 10), threaded ==
     serial (Test 8);
-  * the committed golden fixtures in tests/golden/ (regression of the above).
+  * the SiLU activation on exactly known gate/up values (closed forms) and
+    the Qwen3 expert path against a float64 dequantized model.
 """
 
 import numpy as np
@@ -335,6 +336,116 @@ def test_moe_v2_mxfp4_gptoss_biases_vs_float64(orc):
             h = g / (1 + np.exp(-1.702 * g)) * (u + 1)
             ref[r] += rw[e, r] * (Dn @ h + bd[e])
     assert np.max(np.abs(got - ref)) <= 0.03 * np.abs(ref).max()
+
+
+def _silu64(g, u):
+    """SiLU gating in float64: g * sigmoid(g) * u (csrc/libtinygiant.c:1256)."""
+    g = np.asarray(g, np.float64)
+    with np.errstate(over="ignore"):
+        return g / (1.0 + np.exp(-g)) * np.asarray(u, np.float64)
+
+
+def _q4k_one_hot_rows(rows, ncols, pos, nib):
+    """Q4_K rows with d = 1, dmin = 0, unit sub-scales and every nibble 0
+    except nibble nib[r] at column pos[r]: with an integer x of amax 127 the
+    row's dot is exactly nib[r] * x[pos[r]]."""
+    nb = ncols // 256
+    m = np.zeros((rows, nb, 144), np.uint8)
+    m[:, :, 0:2] = [0x00, 0x3C]
+    m[:, :, 4:16] = [1, 1, 1, 1, 0, 0, 0, 0, 1, 1, 1, 1]
+    for r in range(rows):
+        b, p = divmod(int(pos[r]), 256)
+        g, j = divmod(p, 64)
+        if j < 32:
+            m[r, b, 16 + 32 * g + j] |= np.uint8(nib[r])
+        else:
+            m[r, b, 16 + 32 * g + j - 32] |= np.uint8(nib[r] << 4)
+    return m.reshape(-1)
+
+
+def test_silu_activation_closed_form(orc):
+    """The SiLU gating h = g / (1 + exp(-g)) * u of both oracle copies
+    (act_fn of the MoE path and the inline one of tg_expert_forward_mixed,
+    csrc/libtinygiant.c:1256 and :1105-1110) on exactly known g and u.
+
+    Gate and up rows are one-hot Q4_K rows with unit scales and x is integer
+    with amax 127, so every gate and up dot is an exact integer (g in
+    [-150, 150], including 0).  The hidden values are read from the MoE
+    path's stage hook and, through an F16 identity down matrix, from the
+    single-expert path; both must equal the float64 formula to a few f32
+    ulps.  Closed forms: g = 0 or u = 0 gives 0, g >> 0 gives g * u,
+    g << 0 gives 0."""
+    D = I = 256
+    rng = np.random.default_rng(9)
+    x = rng.integers(-10, 11, D).astype(np.float32)
+    x[0] = 127.0
+    x[1:6] = [0, 1, -1, 10, -10]
+    pos_g = rng.integers(1, D, I)
+    pos_u = rng.integers(1, D, I)
+    nib_g = rng.integers(0, 16, I)
+    nib_u = rng.integers(0, 16, I)
+    # pinned rows: g = 0, u = 0, g = +150, g = -150, g = +-1
+    pos_g[:6], nib_g[:6] = [1, 4, 4, 5, 2, 3], [7, 15, 15, 15, 1, 1]
+    pos_u[:6], nib_u[:6] = [4, 1, 4, 2, 4, 4], [3, 9, 2, 5, 1, 1]
+    gate = _q4k_one_hot_rows(I, D, pos_g, nib_g)
+    up = _q4k_one_hot_rows(I, D, pos_u, nib_u)
+    g = nib_g * x[pos_g].astype(np.float64)
+    u = nib_u * x[pos_u].astype(np.float64)
+    assert g[0] == 0 and u[1] == 0 and g[2] == 150 and g[3] == -150
+    assert g.min() < -50 and g.max() > 50 and np.count_nonzero(np.abs(g) < 4) > 8
+    ref = _silu64(g, u)
+    down_q6 = _rand_row(O.FMT_Q6K, I)
+    down_q6 = np.concatenate([down_q6] * D)
+    hid = np.zeros((1, I), np.float32)
+    orc.moe_v2([gate], [up], [down_q6], O.FMT_Q4K, [O.FMT_Q6K], None, None, None, O.ACT_SILU,
+               np.ones((1, 1), np.float32), x.reshape(1, D), np.zeros((1, D), np.float32), I, hidden_out=hid)
+    tol = 4 * np.finfo(np.float32).eps * np.abs(ref) + 1e-30
+    assert np.all(np.abs(hid[0] - ref) <= tol)
+    assert hid[0, 0] == 0 and hid[0, 1] == 0 and hid[0, 2] == np.float32(150 * u[2])
+    assert abs(hid[0, 3]) < 1e-30
+    # the single-expert path's inline SiLU, read through an F16 identity down
+    eye = np.eye(D, I, dtype=np.float16).view(np.uint8).reshape(-1)
+    out = np.zeros(D, np.float32)
+    orc.expert_forward_mixed(gate, up, eye, 1, x, out, 1.0, D, I)
+    assert np.all(np.abs(out - ref) <= tol)
+    assert out[0] == 0 and out[1] == 0 and out[2] == np.float32(150 * u[2])
+
+
+def test_moe_v2_silu_q4k_q6k_vs_float64(orc):
+    """The Qwen3 expert path (q4_K gate/up, q6_K down, SiLU, router-weighted
+    combine; csrc/libtinygiant.c:1279-1437) against a float64 dequantized
+    model, within the q8 quantization error (the bound of reference Test 10).
+    The inputs are scaled so the gate values span the SiLU's curved range,
+    and the test checks that a sign error in the activation (g * sigmoid(-g))
+    or swapped gate and up operands would miss the bar."""
+    D, I, k, n = 512, 256, 3, 3
+    gates, ups, downs = _moe_weights(n, D, I, [O.FMT_Q6K] * n, 41)
+    rng = np.random.default_rng(42)
+    x = (rng.standard_normal((k, D)) * 0.04).astype(np.float32)
+    rw = np.array([[0.5, 0.0, 0.2], [0.3, 0.6, 0.0], [0.2, 0.4, 0.8]], np.float32)
+    got = orc.moe_v2(gates, ups, downs, O.FMT_Q4K, [O.FMT_Q6K] * n, None, None, None, O.ACT_SILU, rw, x,
+                     np.zeros((k, D), np.float32), I)
+    ref = np.zeros((k, D))
+    flip = np.zeros((k, D))
+    swap = np.zeros((k, D))
+    gs = []
+    for e in range(n):
+        G = F.dequant_row(O.FMT_Q4K, gates[e], I * D).reshape(I, D)
+        U = F.dequant_row(O.FMT_Q4K, ups[e], I * D).reshape(I, D)
+        Dn = F.dequant_row(O.FMT_Q6K, downs[e], D * I).reshape(D, I)
+        for r in range(k):
+            if rw[e, r] == 0:
+                continue
+            g, u = G @ x[r], U @ x[r]
+            gs.append(g)
+            ref[r] += rw[e, r] * (Dn @ _silu64(g, u))
+            flip[r] += rw[e, r] * (Dn @ (g / (1.0 + np.exp(g)) * u))
+            swap[r] += rw[e, r] * (Dn @ _silu64(u, g))
+    gs = np.concatenate(gs)
+    assert 1.0 < np.std(gs) < 20.0, np.std(gs)
+    bar = 0.03 * np.abs(ref).max()
+    assert np.max(np.abs(got - ref)) <= bar
+    assert np.max(np.abs(flip - ref)) > 5 * bar and np.max(np.abs(swap - ref)) > 5 * bar
 
 
 def test_moe_v2_skips_exact_zero_and_accumulates(orc):
