@@ -107,17 +107,21 @@ class Layers:
             b.free()
 
 
-def _run(tg, layers, mode, h0, steps=1, debug=None, norm=False):
+def _run(tg, layers, mode, h0, steps=1, debug=None, norm=False, policy=None, place=None):
     lib = tg.lib()
     h = tg.DeviceArray(D * 4)
     h.upload(h0)
     d = layers.decode(h.ptr, mode, norm)
     if debug is not None:
         lib.tg_hip_decode_set_debug(d, debug.ptr)
+    if policy is not None:
+        assert lib.tg_hip_decode_set_policy(d, policy) == 0
     for _ in range(steps):
         lib.tg_hip_decode_run(d, None)
     lib.tg_hip_synchronize()
     status = lib.tg_hip_decode_status(d)
+    if place is not None:
+        assert lib.tg_hip_decode_placement(d, place.ctypes.data) == 256
     lib.tg_hip_decode_destroy(d)
     out = h.download(np.float32, D)
     h.free()
@@ -227,3 +231,24 @@ def test_decode_plain_launch_equals_cooperative(tg, qwen3):
     b, s2 = _run(tg, qwen3, 3, h0, steps=2, norm=True)
     assert s1 == 0 and s2 == 0
     assert a.tobytes() == b.tobytes()
+
+
+def test_decode_placement_recorded_and_coherent_policy(tg, qwen3):
+    """Every launch records each workgroup's HW_REG_XCC_ID; the intra-XCD
+    exchanges of the default slot policy assume the workgroups g of each
+    class g % 8 share one XCD, which the status check verifies (cooperative
+    and plain launches).  Policy 1 stores every slot device-coherently
+    (correct under any placement) and gives the same bits."""
+    say("decode placement and slot policies")
+    h0 = np.random.default_rng(6).standard_normal(D).astype(np.float32)
+    for mode in (2, 3):
+        place = np.zeros(256, np.uint32)
+        a, s0 = _run(tg, qwen3, mode, h0, steps=2, norm=True, place=place)
+        say(f"  mode {mode}: XCC_ID of workgroups 0..15: {list(place[:16] & 0xF)}")
+        assert s0 == 0, "placement check or exchange wait failed"
+        grp = place.reshape(32, 8)
+        assert np.all(grp == grp[0]), "a class g % 8 spans several XCDs"
+        assert len(set((grp[0] & 0xF).tolist())) == 8, "two classes share an XCD"
+        b, s1 = _run(tg, qwen3, mode, h0, steps=2, norm=True, policy=1)
+        assert s1 == 0
+        assert a.tobytes() == b.tobytes()

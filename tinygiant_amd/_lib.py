@@ -113,6 +113,8 @@ def register_extensions(lib):
     _reg(lib.tg_hip_decode_kernel_times, [VP, VP, VP])
     _reg(lib.tg_hip_decode_destroy, [VP])
     _reg(lib.tg_hip_decode_status, [VP], CI)
+    _reg(lib.tg_hip_decode_set_policy, [VP, CI], CI)
+    _reg(lib.tg_hip_decode_placement, [VP, VP], CI)
     _reg(lib.tg_hip_decode_set_debug, [VP, VP])
     _reg(lib.tg_hip_decode_debug_bytes, [], SZ)
     _reg(lib.tg_hip_decode_record_bytes, [VP], SZ)

@@ -1394,6 +1394,10 @@ struct tg_hip_decode {
     int grid = 0;
     uint8_t *debug = nullptr;
     uint64_t *times = nullptr;
+    uint8_t *qdown = nullptr;    /* Qwen3 kernel: the layers' down matrices in the row-group layout */
+    unsigned *place = nullptr;   /* Qwen3 kernel: HW_REG_XCC_ID of each workgroup, last launch */
+    int pol = 0;                 /* Qwen3 kernel: 1 = every exchange slot stored device-coherently */
+    int placement_bad = 0;       /* a launch ran with workgroup g off XCD g % 8 */
 };
 
 /* the gpt-oss kernel covers k = 1 steps of 4 MXFP4 experts of 2880 x 2880
@@ -1554,8 +1558,22 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
             HIPCHECK(hipMalloc(&d->layers_mx, lm.size() * sizeof(DecodeLayerMx)));
             HIPCHECK(hipMemcpy(d->layers_mx, lm.data(), lm.size() * sizeof(DecodeLayerMx), hipMemcpyHostToDevice));
         } else {
+            /* the kernel reads each down matrix in the row-group layout: one
+             * rewritten copy per (layer, expert slot) */
+            const DecodeShape sh = decode_qwen_shape();
+            const size_t mb = (size_t)sh.D * row_bytes(TG_FMT_Q6K, sh.I);
+            HIPCHECK(hipMalloc(&d->qdown, ls.size() * DECODE_MAXE * mb));
+            for (size_t l = 0; l < ls.size(); l++)
+                for (int e = 0; e < DECODE_MAXE; e++) {
+                    uint8_t *dst = d->qdown + (l * DECODE_MAXE + e) * mb;
+                    HIPCHECK(launch_q6k_row_groups(ls[l].down[e], dst, sh.D, sh.I / 256, g.st));
+                    ls[l].down[e] = dst;
+                }
             HIPCHECK(hipMalloc(&d->layers, ls.size() * sizeof(DecodeLayer)));
             HIPCHECK(hipMemcpy(d->layers, ls.data(), ls.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice));
+            HIPCHECK(hipMalloc(&d->place, DECODE_GRID * sizeof(unsigned)));
+            HIPCHECK(hipMemset(d->place, 0xFF, DECODE_GRID * sizeof(unsigned)));
+            HIPCHECK(hipStreamSynchronize(g.st));
         }
         const size_t sb = d->kind == 1 ? decode_mx_slot_bytes() : decode_qwen_slot_bytes(d->grid);
         HIPCHECK(hipMalloc(&d->hidden, sb));   /* the exchange slots */
@@ -1586,7 +1604,7 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
         d->base += 2u * (unsigned)d->L;
     } else if (d->mode >= 2) {
         HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
-                                    d->grid, d->mode == 2, st));
+                                    d->place, d->pol, d->grid, d->mode == 2, st));
         d->base += 2u * (unsigned)d->L;
     } else if (d->exec) {
         HIPCHECK(hipGraphLaunch(d->exec, st));
@@ -1621,15 +1639,61 @@ TG_API void tg_hip_decode_set_timing(tg_hip_decode *d, void *times_dev) {
     if (d) d->times = (uint64_t *)times_dev;
 }
 
-/* 0 if every persistent step so far completed its grid barriers; 1 if a
- * barrier wait timed out (the results of that step are invalid). */
+/* Qwen3 step: true if, in the last launch, the workgroups g of each class
+ * g % 8 all ran on one XCD -- what its intra-XCD exchanges need under
+ * policy 0 (which XCD a class gets, and whether two classes share one, only
+ * affects speed: a plain launch may start the round robin on another XCD). */
+static bool placement_ok(tg_hip_decode *d) {
+    if (!d->place) return true;
+    unsigned x[DECODE_GRID];
+    HIPCHECK(hipMemcpy(x, d->place, sizeof x, hipMemcpyDeviceToHost));
+    for (int i = 8; i < DECODE_GRID; i++)
+        if (x[i] != x[i % 8]) return false;
+    return true;
+}
+
+/* 0 if every persistent step so far completed its exchange waits; 1 if a
+ * wait timed out (the results of that step are invalid).  For the Qwen3
+ * step, 2 if a launch split a class of workgroups g % 8 over several XCDs,
+ * which its intra-XCD exchanges do not allow under policy 0: the step then
+ * switches itself to storing every slot device-coherently
+ * (tg_hip_decode_set_policy 1); the launches before the switch are suspect
+ * (a wait that timed out among them also reports 1). */
 TG_API int tg_hip_decode_status(tg_hip_decode *d) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!d || d->mode < 2) return 0;
     unsigned w;
     HIPCHECK(hipStreamSynchronize(g.st));
     HIPCHECK(hipMemcpy(&w, d->sync, 4, hipMemcpyDeviceToHost));
-    return w ? 1 : 0;
+    if (w) return 1;
+    if (d->pol == 0 && !placement_ok(d)) {
+        d->placement_bad = 1;
+        d->pol = 1;
+    }
+    return d->placement_bad ? 2 : 0;
+}
+
+/* Exchange-slot policy of the Qwen3 persistent step: 0 keeps slots read only
+ * inside one XCD in that XCD's L2 (needs workgroup g on XCD g % 8; the
+ * default), 1 stores every slot device-coherently (correct under any
+ * placement, slower).  Both give the same bits.  Returns the previous
+ * policy, or -1 for a step that is not the Qwen3 persistent kernel. */
+TG_API int tg_hip_decode_set_policy(tg_hip_decode *d, int pol) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d || d->mode < 2 || d->kind != 0) return -1;
+    const int prev = d->pol;
+    d->pol = pol ? 1 : 0;
+    return prev;
+}
+
+/* HW_REG_XCC_ID of each of the Qwen3 persistent step's 256 workgroups in
+ * its last launch (out[256]); returns the number written (0 if none). */
+TG_API int tg_hip_decode_placement(tg_hip_decode *d, unsigned *out) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!d || !d->place || !out) return 0;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipMemcpy(out, d->place, DECODE_GRID * sizeof(unsigned), hipMemcpyDeviceToHost));
+    return DECODE_GRID;
 }
 
 TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
@@ -1643,6 +1707,8 @@ TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
     if (d->layers_mx) HIPCHECK(hipFree(d->layers_mx));
     if (d->hidden) HIPCHECK(hipFree(d->hidden));
     if (d->sync) HIPCHECK(hipFree(d->sync));
+    if (d->qdown) HIPCHECK(hipFree(d->qdown));
+    if (d->place) HIPCHECK(hipFree(d->place));
     delete d;
 }
 

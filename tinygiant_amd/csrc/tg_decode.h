@@ -76,10 +76,18 @@ DecodeShape decode_qwen_shape();
  * shows one workgroup fits per CU), and a workgroup that never starts only
  * makes the others' bounded waits time out.  Returns the launch status. */
 size_t decode_qwen_slot_bytes(int grid);
+/* place_dev (grid words, or null) receives each workgroup's HW_REG_XCC_ID;
+ * pol = 1 stores every exchange slot device-coherently (correct under any
+ * placement), pol = 0 keeps intra-XCD slots in the writer's L2 (needs
+ * workgroup g on XCD g % 8).  The down matrices of layers_dev are in the
+ * row-group layout of launch_q6k_row_groups. */
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
                               unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
-                              int grid, bool cooperative, hipStream_t st);
+                              unsigned *place_dev, int pol, int grid, bool cooperative, hipStream_t st);
 int decode_qwen_max_grid();
+/* Q6_K matrix (nrows x nb blocks, nrows % 8 == 0) -> row-group layout:
+ * per 8 rows {ql[8 nb][128] | qh[8 nb][64] | sc[8 nb][16] | d[8 nb]}. */
+hipError_t launch_q6k_row_groups(const void *src, void *dst, int nrows, int nb, hipStream_t st);
 
 }  // namespace tg
 #endif

@@ -22,22 +22,37 @@
  *   8  h[r] += w_e * out_e[r] in expert order (the reference's combine order,
  *      csrc/libtinygiant.c:1428-1434); all 8 XCDs compute the same bits for
  *      the slice and publish it for step 1 of the next layer.
- * Only step 7 crosses XCDs.  Each layer's weights are loaded into registers
- * one layer ahead: a compute lane holds one Q4_K block (gate or up) and one
- * Q6_K half-block (down).  The next layer's gate/up blocks are issued during
- * step 4 and its down half-blocks and RMSNorm weight during step 7, while the
- * compute waves would otherwise wait; the six compute waves issue one after
- * another so few weight requests sit in the CU's memory queue ahead of the
- * exchange polls.
+ * Only step 7 crosses XCDs; the placement the intra-XCD exchanges rely on
+ * is recorded by every launch (HW_REG_XCC_ID of each workgroup) for the host
+ * to check, and a launch with pol = 1 stores every slot device-coherently,
+ * which is correct wherever the workgroups run.
+ *
+ * Weights stream through LDS.  A CU returns the data of its vector loads in
+ * the order it issued them, so an exchange poll waits behind every weight
+ * load its CU issued before it.  The weights are therefore copied into LDS
+ * by direct-to-LDS loads (no registers) in three batches per layer, each
+ * issued right after an exchange and needed only after a later one:
+ *   D  this layer's down rows            at the start of RMSNorm (every wave)
+ *   A  the next layer's RMSNorm weight   at the start of q8(hidden) (every
+ *      and first 32 KiB of gate/up rows  wave)
+ *   B  the rest of its gate/up rows      at the start of the down dots (the
+ *                                        communication waves, idle there)
+ * so the exchange polls wait for little that is not needed anyway, and the
+ * weight stream runs while the chain of exchanges and dots runs (an issuing
+ * wave stalls once its CU's memory queue is full, so each batch is spread
+ * over waves that have time).  Each lane then reads its Q4_K block
+ * (gate/up) or Q6_K half-block (down) from LDS.
+ *
+ * Down matrices arrive in a row-group layout made once when the step is
+ * created (tg_api.hip): every 8 rows' Q6_K blocks become field-major
+ * {ql[24][128] | qh[24][64] | sc[24][16] | d[24]} (5040 bytes, the same
+ * bytes), so every field a lane reads is aligned in LDS.
  *
  * Exchanges use epoch-tagged 16-byte slots {tag, v0, v1, v2}, written and
- * polled with device-coherent (sc1) vector accesses so the tag and its values
- * arrive together.  Two communication waves per workgroup do the polling and
- * publishing, so a poll never waits behind the compute waves' outstanding
- * weight loads.  Every wait is bounded; a timed-out wait raises an abort flag
- * that releases every other waiter, so the grid always drains.  Placement
- * only affects speed: every exchange is device-coherent wherever the
- * workgroups run.
+ * polled as one vector access so the tag and its values arrive together.
+ * Two communication waves per workgroup do the polling and publishing.
+ * Every wait is bounded; a timed-out wait raises an abort flag that
+ * releases every other waiter, so the grid always drains.
  */
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -75,6 +90,32 @@ constexpr int GS = RA / VPS;          /* hidden slots per workgroup: 8 */
 constexpr int PS = (RB + VPS - 1) / VPS;   /* slots per 64-row slice: 22 */
 constexpr int MAX_LAYERS = 64;        /* layer descriptors staged in LDS */
 constexpr int NTS = 24;               /* timing words per layer */
+/* LDS weight regions and their direct-to-LDS copies (1 KiB an instruction) */
+constexpr int SEG = RA * GATE_RB;     /* one matrix's 24-row slice: 27,648 bytes */
+constexpr int WGB = 2 * SEG;          /* gate rows, then up rows */
+constexpr int G_INS = WGB / 1024;     /* 54 */
+constexpr int DGRP = 8 * DOWN_RB;     /* one 8-row group of the row-group layout: 5040 bytes */
+constexpr int WDB = RB / 8 * DGRP;    /* the 64-row down slice: 40,320 bytes */
+constexpr int D_INS = (WDB + 1023) / 1024;   /* 40 (the last one runs past the slice) */
+constexpr int N_INS = D * 4 / 1024;   /* RMSNorm weight: 8 */
+#ifndef TG_DECODE_G_SPLIT
+#define TG_DECODE_G_SPLIT 32
+#endif
+#ifndef TG_DECODE_B_AT_DOWN
+#define TG_DECODE_B_AT_DOWN 1
+#endif
+/* Copy batches (each wave issues its share; a wave that issues more than
+ * its CU's memory queue takes stalls until the queue drains):
+ *   D  this layer's down rows     every wave, at the start of RMSNorm
+ *      (after the h gather)       (done before the hidden gather ends)
+ *   A  RMSNorm weight and the     every wave, at the start of q8(hidden)
+ *      first G_SPLIT gate/up KiB  (after the hidden gather)
+ *   B  the other gate/up KiB      the communication waves at the start of
+ *                                 the down dots (they are idle there), or
+ *                                 every wave after the hop
+ * A and B are done before the next h gather ends. */
+constexpr int G_SPLIT = TG_DECODE_G_SPLIT;
+constexpr bool B_AT_DOWN = TG_DECODE_B_AT_DOWN != 0;
 static_assert(NE == NX, "one expert per XCD");
 static_assert(NR * RA == I && NR * RB == D && RA % VPS == 0, "row split");
 static_assert(2 * RA * NBD == NW * 64, "gate/up: one Q4_K block per compute lane");
@@ -83,16 +124,15 @@ static_assert((NR - 1) * PS <= 6 * CL && (NR - 1) * GS <= 2 * CL && (NX - 1) * P
 static_assert(NBI <= NA && NBD == NA, "q8 blocks per wave");
 static_assert(RB == VPS * (PS - 1) + 1, "the last slice slot holds one row and the slice's sum of h^2");
 static_assert(NR % NA == 0, "layer-0 slice sums: whole slices per wave");
+static_assert(WGB % 1024 == 0 && SEG % 1024 == 0 && DGRP % 16 == 0 && RB % 8 == 0, "copy granules");
+static_assert(G_SPLIT <= G_INS, "copy split");
+static_assert(G_SPLIT <= G_INS, "batch split");
 
-/* A slot is 16 bytes {tag, v0, v1, v2} written and read as one vector access,
- * so its tag and values arrive together.  Cross-XCD slots are stored and
- * loaded with device-scope coherence (sc1: the store writes through to
- * memory, the load does not allocate in the reader's L2, so it never sees a
- * stale line).  Slots read only inside the writer's XCD are stored plainly
+/* Slot policies: slots read only inside the writer's XCD are stored plainly
  * (the line stays in that XCD's L2) and loaded with sc1, which bypasses the
- * CU's L1 and reads the L2 line: measured coherent, and ~0.4 us faster per
- * exchange than writing through to memory. */
-constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units (64 cycles) between compute waves' prefetch issue */
+ * CU's L1 and reads the L2 line; cross-XCD slots are stored with sc1 (write
+ * through to memory) and loaded with sc1 (no stale line from the reader's
+ * L2).  With pol = 1 every slot is stored with sc1. */
 /* slot regions (u32x4 index), each double buffered by layer parity:
  *   h slices  [2][NWG][PS]   rows [64 j, 64 j + 64) of the layer output
  *   hidden    [2][NWG][GS]   the workgroup's 24 hidden values
@@ -116,10 +156,10 @@ struct __attribute__((aligned(16))) LdsH {   /* q8(hidden) of this XCD's expert 
 struct Q4Blk {
     u32x4 w[9];
 };
-__device__ inline Q4Blk load_q4blk(Buf b, uint32_t off) {
+__device__ inline Q4Blk lds_q4blk(const uint8_t *p) {
     Q4Blk r;
 #pragma unroll
-    for (int i = 0; i < 9; i++) r.w[i] = ld16(b, off + 16u * i);
+    for (int i = 0; i < 9; i++) r.w[i] = *reinterpret_cast<const u32x4 *>(p + 16 * i);
     return r;
 }
 /* dot_q4k_q8 of one block (csrc/libtinygiant.c:223-272): integer sums per
@@ -164,23 +204,26 @@ __device__ inline float dot_q4blk(const Q4Blk &q, const int8_t *xq, const int32_
 }
 
 /* One lane's half of a Q6_K block: 64 bytes of ql, 32 of qh, 8 int8
- * sub-scales and the f16 d. */
+ * sub-scales and the f16 d (low 16 bits). */
 struct Q6Half {
     u32x4 la0, la1, lb0, lb1, h0, h1;
     u32x2 sc;
-    uint32_t d;   /* d is the high 16 bits */
+    uint32_t d;
 };
-__device__ inline Q6Half load_q6half(Buf b, uint32_t blk, int h) {
+/* Half h of block j (0..23) of an 8-row group in the row-group layout. */
+__device__ inline Q6Half lds_q6half(const uint8_t *grp, int j, int h) {
     Q6Half r;
-    const uint32_t ql = blk + 64u * h, qh = blk + 128u + 32u * h;
-    r.la0 = ld16(b, ql);
-    r.la1 = ld16(b, ql + 16);
-    r.lb0 = ld16(b, ql + 32);
-    r.lb1 = ld16(b, ql + 48);
-    r.h0 = ld16(b, qh);
-    r.h1 = ld16(b, qh + 16);
-    r.sc = ld8(b, blk + 192u + 8u * h);
-    r.d = ld4(b, blk + 206u);
+    const uint8_t *ql = grp + 128 * j + 64 * h;
+    const uint8_t *qh = grp + 24 * 128 + 64 * j + 32 * h;
+    r.la0 = *reinterpret_cast<const u32x4 *>(ql);
+    r.la1 = *reinterpret_cast<const u32x4 *>(ql + 16);
+    r.lb0 = *reinterpret_cast<const u32x4 *>(ql + 32);
+    r.lb1 = *reinterpret_cast<const u32x4 *>(ql + 48);
+    r.h0 = *reinterpret_cast<const u32x4 *>(qh);
+    r.h1 = *reinterpret_cast<const u32x4 *>(qh + 16);
+    r.sc = *reinterpret_cast<const u32x2 *>(grp + 24 * 192 + 16 * j + 8 * h);
+    const uint32_t dw = *reinterpret_cast<const uint32_t *>(grp + 24 * 208 + 4 * (j >> 1));
+    r.d = (dw >> (16 * (j & 1))) & 0xFFFFu;
     return r;
 }
 /* dot_q6k_q8 over one 128-value half (csrc/libtinygiant.c:384-443):
@@ -225,7 +268,7 @@ __device__ inline float dot_q6half(const Q6Half &q, const int8_t *xq, const int3
         const int sc = (int)(int8_t)((i < 4 ? q.sc.x : q.sc.y) >> (8 * (i & 3)));
         A += __mul24(sc, S[i] - 32 * xs[i]);   /* |S - 32 xs| < 2^18: exact */
     }
-    return ref_f16(q.d >> 16) * xd * (float)A;
+    return ref_f16(q.d) * xd * (float)A;
 }
 
 /* q8 of 4 consecutive values per lane of one wave = one 256-block
@@ -251,6 +294,58 @@ __device__ inline uint32_t q8_block_wave(float v0, float v1, float v2, float v3,
 
 __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 
+/* One 1 KiB direct-to-LDS copy: lane l moves the 16 bytes at byte offset
+ * off + 16 l of the buffer `desc` to LDS address lds + 16 l (lds is
+ * wave-uniform).  Issued from inline assembly, so the compiler does not
+ * track it: it would otherwise make LDS reads of other arrays wait for the
+ * copies still in flight (it cannot tell the arrays apart), which is the
+ * overlap this kernel needs.  The waves that issue copies wait for them
+ * themselves (wait_copies) before the barrier that opens the phase reading
+ * them.  Vector-memory waits the compiler emits for its own loads stay
+ * correct: the counter completes in order, so untracked operations only
+ * make those waits stricter. */
+__device__ inline u32x4 buf_desc(const void *p, uint32_t nbytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    u32x4 d;
+    d.x = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    d.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xFFFFu;
+    d.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)nbytes);
+    d.w = 0x00020000u;
+    return d;
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p);
+}
+/* M0 holds the copy's LDS address.  M0 is a reserved register the
+ * compiler does not let inline assembly clobber; nothing else in this
+ * kernel uses it (its generated code sets M0 nowhere else). */
+__device__ inline void copy_1k(const u32x4 &desc, uint32_t off, uint32_t lds, int lane) {
+    const uint32_t voff = off + 16u * (uint32_t)lane;
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(desc)
+                 : "memory");
+}
+
+__device__ inline void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+/* wait until at most N of the wave's vector memory operations are in flight */
+template <int N>
+__device__ inline void wait_copies_but() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* Workgroup barrier for the layer loop: waits for the wave's LDS accesses
+ * (lgkmcnt) and meets the other waves; the memory clobber keeps the
+ * compiler from moving accesses across it.  __syncthreads() (and a release
+ * fence on LDS alone) would also wait for the wave's outstanding
+ * direct-to-LDS copies (they count as LDS writes), which must stay in
+ * flight across the phases they overlap.  A wave whose copies a phase
+ * reads waits for them itself (wait_copies) before the barrier that opens
+ * that phase; nothing the workgroup stores to global memory inside a layer
+ * is read back by the workgroup. */
+__device__ inline void bar_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 }  // namespace
 
 /* Tags are base + layer + 1 in every region, so a launch never mistakes a
@@ -259,66 +354,83 @@ __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g))
  * something the writer waited for in between. */
 __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restrict__ layers, int L, float *h,
                                                     u32x4 *slots, unsigned *abort_flag, unsigned base, float eps,
-                                                    uint8_t *dbg, uint64_t *times) {
-    __shared__ __attribute__((aligned(16))) float hx[D];          /* this layer's input h */
-    __shared__ __attribute__((aligned(16))) float nws[D];         /* this layer's RMSNorm weight */
-    __shared__ __attribute__((aligned(16))) float hid[I];         /* this XCD's expert hidden vector */
+                                                    uint8_t *dbg, uint64_t *times, unsigned *place, int pol) {
+    __shared__ __attribute__((aligned(16))) uint8_t wgs[WGB];          /* gate/up rows of the slice */
+    __shared__ __attribute__((aligned(16))) uint8_t wds[D_INS * 1024]; /* down rows of the slice (row groups) */
+    __shared__ __attribute__((aligned(16))) float nws[D];              /* this layer's RMSNorm weight */
+    __shared__ __attribute__((aligned(16))) float hx[D];               /* this layer's input h */
+    __shared__ __attribute__((aligned(16))) float hid[I];              /* this XCD's expert hidden vector */
     __shared__ LdsX sx;
     __shared__ LdsH sh;
-    __shared__ float ssq[NR];                                     /* sum of h^2 of each 64-row slice */
-    __shared__ float gu[2 * RA];                                  /* gate and up row sums */
-    __shared__ float part6[RB * HB];                              /* down half-block partial dots */
-    __shared__ float pp[NE][RB];                                  /* down values of every expert, own rows */
+    __shared__ float ssq[NR];                                          /* sum of h^2 of each 64-row slice */
+    __shared__ float gu[2 * RA];                                       /* gate and up row sums */
+    __shared__ float part6[RB * HB];                                   /* down half-block partial dots */
+    __shared__ float pp[NE][RB];                                       /* down values of every expert, own rows */
     __shared__ int lds_fail;
     __shared__ DecodeLayer lys[MAX_LAYERS];
 
     int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
-    const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid when >= 0 */
+    const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid in the communication waves */
     const int ct = (int)threadIdx.x;             /* compute lane, valid when < NW * 64 */
-    if (threadIdx.x == 0) lds_fail = 0;
+    if (threadIdx.x == 0) {
+        lds_fail = 0;
+        unsigned x;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+        if (place) place[blockIdx.x] = x;
+    }
     const int wg = blockIdx.x;
     const int xe = wg % NX, rk = wg / NX;        /* expert slot (= XCD) and rank */
     Buf sl = make_buf(slots, NSLOTS * 16u);
+    const bool sc1_all = pol != 0;
+    const bool comm = wave >= NW;
 
-    Q4Blk wa;                                    /* this lane's gate or up block */
-    Q6Half wb;                                   /* this lane's down half-block */
-    u32x4 nw0, nw1;                              /* next layer's RMSNorm weight (compute lanes) */
     /* gate/up: compute lane t owns block t % 8 of row-task t / 8 (tasks 0-23
      * gate rows, 24-47 up rows); down: compute lane t owns half-block t % 6
      * of down row t / 6 */
     const int ta = ct >> 3, ba = ct & 7;
     const int tb = ct / HB, hbb = ct % HB;
 
-    /* loads are unconditional so the registers' live ranges end at their
-     * use; an inactive step reads through an empty descriptor (zeros, no
-     * memory access) */
-    auto load_a = [&](const DecodeLayer &ly) {
-        /* waves 0-2 hold gate rows, waves 3-5 up rows (uniform per wave) */
-        const bool cw = wave < NW;
-        const uint8_t *m = wave < NW / 2 ? ly.gate[xe] : ly.up[xe];
-        Buf gb = make_buf_uniform(cw ? m : nullptr, cw ? (uint32_t)I * GATE_RB : 0u);
-        const uint32_t r = (uint32_t)(RA * rk + (ta % RA));
-        wa = load_q4blk(gb, r * GATE_RB + (uint32_t)ba * 144u);
+    /* copies into LDS: batch D (down rows), A (RMSNorm weight + the first
+     * G_SPLIT gate/up KiB), B (the rest of the gate/up rows).  The buffer
+     * descriptors are formed once per batch: the copies' memory clobber
+     * would otherwise make every copy re-read the layer table from LDS. */
+    struct Descs {
+        u32x4 g, u, n;
     };
-    auto load_b = [&](const DecodeLayer &ly) {
-        const bool cw = wave < NW;
-        Buf db = make_buf_uniform(cw ? ly.down[xe] : nullptr, cw ? (uint32_t)D * DOWN_RB : 0u);
-        const uint32_t r = (uint32_t)(RB * rk + tb);
-        wb = load_q6half(db, r * DOWN_RB + (uint32_t)(hbb >> 1) * 210u, hbb & 1);
+    auto descs = [&](const DecodeLayer &ly) {
+        Descs d;
+        d.g = buf_desc(ly.gate[xe], (uint32_t)I * GATE_RB);
+        d.u = buf_desc(ly.up[xe], (uint32_t)I * GATE_RB);
+        /* a layer without an RMSNorm weight still issues its copies, reading
+         * nothing, so every wave's copy count stays the same */
+        d.n = buf_desc(ly.norm_w, ly.norm_w != nullptr ? (uint32_t)D * 4u : 0u);
+        return d;
     };
-    /* RMSNorm weight: compute lane t holds float4 t and (t < 128) float4 384 + t */
-    auto load_nw = [&](const DecodeLayer &ly) {
-        const bool on = wave < NW && ly.norm_w != nullptr;
-        Buf nb = make_buf_uniform(on ? ly.norm_w : nullptr, on ? (uint32_t)D * 4u : 0u);
-        nw0 = ld16(nb, (uint32_t)ct * 16u);
-        nw1 = ld16(nb, (uint32_t)(NW * 64 + ct) * 16u);
+    const uint32_t goff = (uint32_t)(RA * rk) * GATE_RB;
+    auto copy_gate_up = [&](const Descs &d, int k) {
+        if (k < SEG / 1024) copy_1k(d.g, goff + 1024u * (uint32_t)k, lds_addr(wgs + 1024 * k), lane);
+        else copy_1k(d.u, goff + 1024u * (uint32_t)(k - SEG / 1024), lds_addr(wgs + 1024 * k), lane);
     };
-    auto store_nw = [&]() {
-        if (wave < NW) {
-            reinterpret_cast<u32x4 *>(nws)[ct] = nw0;
-            if (ct < D / 4 - NW * 64) reinterpret_cast<u32x4 *>(nws)[NW * 64 + ct] = nw1;
+    auto batch_d = [&](const DecodeLayer &ly) {   /* every wave */
+        const u32x4 b = buf_desc(ly.down[xe], (uint32_t)D * DOWN_RB);
+        for (int k = wave; k < D_INS; k += NA)
+            copy_1k(b, (uint32_t)(rk * WDB) + 1024u * (uint32_t)k, lds_addr(wds + 1024 * k), lane);
+    };
+    auto batch_a = [&](const DecodeLayer &ly) {   /* every wave */
+        const Descs d = descs(ly);
+        for (int i = wave; i < G_SPLIT + N_INS; i += NA) {
+            if (i < N_INS) copy_1k(d.n, 1024u * (uint32_t)i, lds_addr(nws + 256 * i), lane);
+            else copy_gate_up(d, i - N_INS);
         }
+    };
+    auto batch_b = [&](const DecodeLayer &ly, int w0, int nw) {   /* waves w0 .. w0 + nw - 1 */
+        const Descs d = descs(ly);
+        for (int k = G_SPLIT + wave - w0; k < G_INS; k += nw) copy_gate_up(d, k);
+    };
+    auto put = [&](uint32_t slot, unsigned tag, float a, float b, float c, bool cross) {
+        if (cross || sc1_all) put_slot<CPOL_SC1>(sl, slot, tag, a, b, c);
+        else put_slot<CPOL_PLAIN>(sl, slot, tag, a, b, c);
     };
 
     /* layer descriptors -> LDS (the loop then never chases pointers in
@@ -339,16 +451,17 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         const float ss = wave_sum(v * v);
         if (lane == 0) ssq[sl] = ss;
     }
-    load_nw(lys[0]);
-    load_a(lys[0]);
-    load_b(lys[0]);
-    store_nw();
+    batch_a(lys[0]);
+    batch_b(lys[0], 0, NA);
+    wait_copies();
+    __syncthreads();
 
     for (int l = 0; l < L; l++) {
         const DecodeLayer &ly = lys[l];
         const unsigned par = (unsigned)(l & 1);
         const unsigned tag = base + (unsigned)l + 1u;
         const bool has_nw = ly.norm_w != nullptr;
+        const bool more = l + 1 < L;
         /* an opaque copy of the lane keeps per-lane address arithmetic inside
          * the loop instead of hoisted (and live) across every layer */
         int clv = cl;
@@ -360,9 +473,10 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         const bool tc = times && clv == 0;
         uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
         if (tw) tr[0] = wall_clock64();
-        /* ---- 1: gather h from the other ranks of this XCD ---- */
+        /* ---- 1: gather h from the other ranks of this XCD (the copies of
+         * this layer's gate/up rows and RMSNorm weight are ahead of the polls) ---- */
         if (l > 0) {
-            if (cl >= 0) {
+            if (comm) {
                 unsigned rounds = 0;
                 if (tc) tr[15] = wall_clock64();
                 const bool ok = poll_slots<CL, 6>(
@@ -384,22 +498,23 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                             o[2] = __uint_as_float(v.w);
                         }
                     },
-                    tc ? &rounds : nullptr);
+                    &rounds);
                 if (tc) {
                     tr[16] = wall_clock64();
                     tr[17] = rounds;
                 }
                 if (!ok) lds_fail = 1;
-            } else {
-                store_nw();
             }
-            __syncthreads();
+            wait_copies();   /* this layer's gate/up rows and RMSNorm weight (batches A, B) */
+            bar_lds();
             if (lds_fail) return;
         }
         if (tw) tr[1] = wall_clock64();
+        /* this layer's down rows stream in during RMSNorm, gate/up and the
+         * hidden gather */
+        batch_d(ly);
         /* ---- 2: RMSNorm (weight norm_w or 1) then q8, in LDS; wave w owns block w.
          * sum h^2 = the 32 slice sums in rank order (each a fixed DPP tree) ---- */
-        if (l == 0) __syncthreads();
         {
             float tot = 0.f;
 #pragma unroll
@@ -430,7 +545,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                 reinterpret_cast<uint32_t *>(rec + DecodeDebug::XQ)[threadIdx.x] = q;
             }
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[2] = wall_clock64();
         if (dbg && wg == 0) {
             uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
@@ -440,28 +555,23 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         }
         /* ---- 3: gate/up rows [24 rk, 24 rk + 24) of expert xe, one block per lane ---- */
         if (wave < NW) {
+            const Q4Blk wa = lds_q4blk(wgs + (ta / RA) * SEG + (ta % RA) * GATE_RB + ba * 144);
             float v = dot_q4blk(wa, sx.qs + ba * XST, sx.s32 + ba * 8, sx.d[ba]);
             v = seg_sum_last<NBD>(v);
             if (ba == NBD - 1) gu[ta] = v;
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[3] = wall_clock64();
-        /* ---- 4: all-gather the expert's hidden vector within the XCD ---- */
-        /* meanwhile the compute waves issue the next layer's gate/up blocks,
-         * one wave after another, so the weight requests queued ahead of the
-         * polls stay short */
-        if (cl < 0 && l + 1 < L) {
-            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
-            load_a(lys[l + 1]);
-        }
-        if (cl >= 0) {
+        /* ---- 4: all-gather the expert's hidden vector within the XCD (the
+         * down rows' copies are ahead of the polls) ---- */
+        if (comm) {
             /* SwiGLU, one value per lane of the first communication wave; the
              * same wave then publishes them (its LDS accesses run in order) */
             if (clv < RA) hid[RA * rk + clv] = silu_mul(gu[clv], gu[RA + clv]);
             __builtin_amdgcn_wave_barrier();
             if (clv < GS) {
                 const float *a = hid + RA * rk + VPS * clv;
-                put_slot<CPOL_PLAIN>(sl, GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, a[0], a[1], a[2]);
+                put(GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, a[0], a[1], a[2], false);
             }
             if (tc) tr[9] = wall_clock64();
             unsigned rounds = 0;
@@ -481,16 +591,20 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                     o[1] = __uint_as_float(v.z);
                     o[2] = __uint_as_float(v.w);
                 },
-                tc ? &rounds : nullptr);
+                &rounds);
             if (tc) {
                 tr[13] = wall_clock64();
                 tr[14] = rounds;
             }
             if (!ok) lds_fail = 1;
         }
-        __syncthreads();
+        wait_copies();   /* this layer's down rows (batch D) */
+        bar_lds();
         if (lds_fail) return;
         if (tw) tr[4] = wall_clock64();
+        /* the next layer's RMSNorm weight and part of its gate/up rows stream
+         * in from here (the gate/up region and the norm weight are free) */
+        if (more) batch_a(lys[l + 1]);
         /* ---- 5: q8 of the hidden vector, one wave per 256-block ---- */
         if (wave < NBI) {
             const int b = wave;
@@ -504,7 +618,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                 reinterpret_cast<uint32_t *>(rec + DecodeDebug::HQ + xe * I + b * 256)[lane] = q;
             }
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[5] = wall_clock64();
         if (dbg && rk == 0) {
             uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
@@ -513,20 +627,16 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                 reinterpret_cast<int32_t *>(rec + DecodeDebug::HS16)[xe * NBI * 16 + threadIdx.x] = sh.s16[threadIdx.x];
         }
         /* ---- 6: down rows [64 rk, 64 rk + 64) of expert xe, one half-block per lane ---- */
+        if (B_AT_DOWN && more && comm) batch_b(lys[l + 1], NW, NC);
         if (wave < NW) {
             const int b = hbb >> 1;
+            const Q6Half wb = lds_q6half(wds + (tb >> 3) * DGRP, (tb & 7) * NBI + b, hbb & 1);
             part6[ct] = dot_q6half(wb, sh.qs + hbb * HST, sh.s16 + b * 16 + 8 * (hbb & 1), sh.d[b]);
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[6] = wall_clock64();
         /* ---- 7: cross-XCD hop: rank rk of every XCD trades its 64 down values ---- */
-        /* meanwhile the next layer's RMSNorm weight and down rows are issued */
-        if (cl < 0 && l + 1 < L) {
-            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
-            load_nw(lys[l + 1]);
-            load_b(lys[l + 1]);
-        }
-        if (cl >= 0) {
+        if (comm) {
             /* row sums of the six half-block dots, in half-block order, one row
              * per lane of the first communication wave, which then publishes */
             if (clv < RB) {
@@ -538,8 +648,8 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             __builtin_amdgcn_wave_barrier();
             if (clv < PS) {
                 const int r0 = VPS * clv;
-                put_slot<CPOL_SC1>(sl, PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, pp[xe][r0],
-                                   r0 + 1 < RB ? pp[xe][r0 + 1] : 0.f, r0 + 2 < RB ? pp[xe][r0 + 2] : 0.f);
+                put(PSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, pp[xe][r0],
+                    r0 + 1 < RB ? pp[xe][r0 + 1] : 0.f, r0 + 2 < RB ? pp[xe][r0 + 2] : 0.f, true);
             }
             if (tc) tr[10] = wall_clock64();
             unsigned rounds = 0;
@@ -558,20 +668,25 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                     if (VPS * t + 1 < RB) o[1] = __uint_as_float(v.z);
                     if (VPS * t + 2 < RB) o[2] = __uint_as_float(v.w);
                 },
-                tc ? &rounds : nullptr);
+                &rounds);
             if (tc) {
                 tr[18] = wall_clock64();
                 tr[19] = rounds;
             }
             if (!ok) lds_fail = 1;
         }
-        __syncthreads();
-        if (lds_fail) return;
+        bar_lds();
+        if (lds_fail) {
+            wait_copies();   /* no copy into LDS outlives the workgroup */
+            return;
+        }
         if (tw) tr[7] = wall_clock64();
+        /* the rest of the next layer's gate/up rows */
+        if (!B_AT_DOWN && more) batch_b(lys[l + 1], 0, NA);
         /* ---- 8: combine rows [64 rk, 64 rk + 64) in expert order, publish ---- */
         /* one row per lane of the first communication wave, which then
          * publishes the slice */
-        if (cl >= 0 && clv < RB) {
+        if (comm && clv < RB) {
             const int r = RB * rk + clv;
             float a = hx[r];
 #pragma unroll
@@ -581,16 +696,42 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             const float ss = wave_sum(a * a);   /* this slice's sum of h^2, for the next RMSNorm */
             if (clv == 0) ssq[rk] = ss;
             __builtin_amdgcn_wave_barrier();
-            if (l + 1 < L && clv < PS) {
+            if (more && clv < PS) {
                 const float *o = hx + RB * rk + VPS * clv;
                 const bool last = clv == PS - 1;   /* row 63 alone, plus the slice sum */
-                put_slot<CPOL_PLAIN>(sl, HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0],
-                                     last ? ss : o[1], last ? 0.f : o[2]);
+                put(HSL + (par * NWG + (uint32_t)wg) * PS + (uint32_t)clv, tag, o[0], last ? ss : o[1],
+                    last ? 0.f : o[2], false);
             }
             if (tc) tr[11] = wall_clock64();
         }
         if (tw) tr[8] = wall_clock64();
     }
+    wait_copies();
+}
+
+/* Rewrites a Q6_K matrix (nrows x nb 210-byte blocks, nrows a multiple of
+ * 8) into the row-group layout the persistent step reads: group g of rows
+ * [8 g, 8 g + 8) is {ql[8 nb][128] | qh[8 nb][64] | sc[8 nb][16] | d[8 nb]},
+ * block j = r * nb + b, the same 8 * nb * 210 bytes.  One thread per block. */
+__global__ void k_q6k_row_groups(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int nrows, int nb) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nrows * nb) return;
+    const int row = t / nb, b = t % nb, g = row >> 3, j = (row & 7) * nb + b;
+    const uint8_t *s = src + (size_t)t * 210;
+    uint8_t *o = dst + (size_t)g * 8 * nb * 210;
+    const int n8 = 8 * nb;
+    for (int i = 0; i < 128; i++) o[128 * j + i] = s[i];
+    for (int i = 0; i < 64; i++) o[128 * n8 + 64 * j + i] = s[128 + i];
+    for (int i = 0; i < 16; i++) o[192 * n8 + 16 * j + i] = s[192 + i];
+    o[208 * n8 + 2 * j] = s[208];
+    o[208 * n8 + 2 * j + 1] = s[209];
+}
+
+hipError_t launch_q6k_row_groups(const void *src, void *dst, int nrows, int nb, hipStream_t st) {
+    const int n = nrows * nb;
+    hipLaunchKernelGGL(k_q6k_row_groups, dim3((n + 255) / 256), dim3(256), 0, st, (const uint8_t *)src,
+                       (uint8_t *)dst, nrows, nb);
+    return hipGetLastError();
 }
 
 DecodeShape decode_qwen_shape() { return DecodeShape{D, I, TG_FMT_Q4K, TG_FMT_Q6K, DECODE_MAXE, NT}; }
@@ -608,9 +749,10 @@ size_t decode_qwen_slot_bytes(int) { return (size_t)NSLOTS * 16; }
 
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
                               unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
-                              int grid, bool cooperative, hipStream_t st) {
-    void *args[] = {(void *)&layers_dev, (void *)&L, (void *)&h_dev, (void *)&slots_dev, (void *)&abort_dev,
-                    (void *)&base, (void *)&eps, (void *)&debug_dev, (void *)&times_dev};
+                              unsigned *place_dev, int pol, int grid, bool cooperative, hipStream_t st) {
+    void *args[] = {(void *)&layers_dev, (void *)&L,         (void *)&h_dev,     (void *)&slots_dev,
+                    (void *)&abort_dev,  (void *)&base,      (void *)&eps,       (void *)&debug_dev,
+                    (void *)&times_dev,  (void *)&place_dev, (void *)&pol};
     if (cooperative) return hipLaunchCooperativeKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
     return hipLaunchKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
 }
