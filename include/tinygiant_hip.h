@@ -173,6 +173,18 @@ void tg_hip_moe_plan_destroy(tg_hip_moe_plan *plan);
 void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_dev, const float *inputs_dev,
                        float *outputs_dev, int nrows, int ncols, int k, void *scratch_dev, void *stream);
 size_t tg_hip_matmul_scratch_bytes(int k, int ncols);
+/* No counterpart in the reference.  For callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops): tg_hip_matmul_dev with the
+ * q8 rows of the inputs in the library's fixed device scratch instead of a
+ * workspace argument; allocates nothing.  tg_hip_init() must have run on the
+ * device first.  k * ceil(ncols / 256) * 360 bytes must fit in
+ * tg_hip_matmul_noalloc_max_bytes() (384 KiB), else it sets
+ * tg_hip_last_error() and leaves the outputs untouched.  Calls on one GPU
+ * share the scratch: calls that overlap in time on one GPU race. */
+void tg_hip_init(void);
+void tg_hip_matmul_dev_noalloc(int fmt, const void *mat_dev, const float *bias_dev, const float *inputs_dev,
+                               float *outputs_dev, int nrows, int ncols, int k, void *stream);
+size_t tg_hip_matmul_noalloc_max_bytes(void);
 void tg_hip_rms_norm_dev(const float *x_dev, const float *w_dev, float *out_dev, int nrows, int n,
                          float eps, void *stream);
 

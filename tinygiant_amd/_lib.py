@@ -91,6 +91,9 @@ def register_extensions(lib):
     _reg(lib.tg_hip_moe_plan_destroy, [VP])
     _reg(lib.tg_hip_matmul_dev, [CI, VP, VP, VP, VP, CI, CI, CI, VP, VP])
     _reg(lib.tg_hip_matmul_scratch_bytes, [CI, CI], SZ)
+    _reg(lib.tg_hip_init, [])
+    _reg(lib.tg_hip_matmul_dev_noalloc, [CI, VP, VP, VP, VP, CI, CI, CI, VP])
+    _reg(lib.tg_hip_matmul_noalloc_max_bytes, [], SZ)
     _reg(lib.tg_hip_head_argmax_dev, [CI, VP, VP, VP, CF, CI, CI, CI, VP, VP, VP, VP, VP])
     _reg(lib.tg_hip_head_scratch_bytes, [CI, CI, CI], SZ)
     _reg(lib.tg_hip_route_dev, [VP, VP, VP, CI, CI, CI, CI, VP, VP, VP, VP])

@@ -43,6 +43,13 @@
 
 using namespace tg;
 
+/* Fixed scratch of tg_hip_matmul_dev_noalloc: the q8 rows of its inputs.
+ * Every GPU the library runs on holds one copy until the process ends; in
+ * host code the name is only a handle, so the kernels get the device
+ * address hipGetSymbolAddress returns for it at set-up (Ctx::scratch). */
+constexpr size_t NOALLOC_SCRATCH_BYTES = 384 << 10;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 std::recursive_mutex g_mu;
@@ -86,6 +93,8 @@ struct Ctx {
     /* row-tile tickets of the host call's fused MoE combine (zero between calls) */
     unsigned *tickets = nullptr;
     int tickets_cap = 0;
+    /* device address of this GPU's copy of `scratch` (below) */
+    uint8_t *scratch = nullptr;
 };
 Ctx g;
 
@@ -93,6 +102,7 @@ void ensure_init() {
     if (g.ready) return;
     HIPCHECK(hipGetDevice(&g.dev));
     HIPCHECK(hipStreamCreateWithFlags(&g.st, hipStreamNonBlocking));
+    HIPCHECK(hipGetSymbolAddress((void **)&g.scratch, HIP_SYMBOL(scratch)));
     g.ready = true;
 }
 
@@ -995,6 +1005,46 @@ TG_API void tg_hip_matmul_dev(int fmt, const void *mat_dev, const float *bias_de
 }
 
 TG_API size_t tg_hip_matmul_scratch_bytes(int k, int ncols) { return q8_bytes(k, ncols); }
+
+/* Sets up the library on the current device (its stream and the device
+ * address of the fixed scratch); every other entry point does it on first
+ * use, tg_hip_matmul_dev_noalloc requires it. */
+TG_API void tg_hip_init(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    ensure_init();
+}
+
+/* tg_hip_matmul_dev without a workspace and without any allocation: the q8
+ * rows of the inputs go to the library's fixed device scratch, which holds
+ * tg_hip_matmul_noalloc_max_bytes() bytes (k * ceil(ncols/256) * 360 bytes
+ * are needed).  For callers that cannot allocate (HIP graph capture, serving
+ * loops).  Needs tg_hip_init() first.  Calls on one GPU share the scratch:
+ * calls that overlap in time on one GPU (other streams, other threads'
+ * queued work) race. */
+TG_API void tg_hip_matmul_dev_noalloc(int fmt, const void *mat_dev, const float *bias_dev, const float *inputs_dev,
+                                      float *outputs_dev, int nrows, int ncols, int k, void *stream) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!fmt_ok(fmt) || ncols <= 0 || ncols % 32 || nrows <= 0 || k <= 0) {
+        set_err("tg_hip_matmul_dev_noalloc: bad format or shape");
+        return;
+    }
+    if (!g.ready) {
+        set_err("tg_hip_matmul_dev_noalloc: call tg_hip_init() first");
+        return;
+    }
+    if (q8_bytes(k, ncols) > NOALLOC_SCRATCH_BYTES) {
+        set_err("tg_hip_matmul_dev_noalloc: %d rows of %d columns need %zu scratch bytes, the fixed scratch holds %zu",
+                k, ncols, q8_bytes(k, ncols), NOALLOC_SCRATCH_BYTES);
+        return;
+    }
+    hipStream_t st = stream ? (hipStream_t)stream : g.st;
+    Q8Rows q = q8_view(g.scratch, k, ncols, inputs_dev);
+    if (fmt != TG_FMT_F16) launch_quantize(inputs_dev, ncols, k, ncols, q, st);
+    launch_gemv(fmt, (const uint8_t *)mat_dev, nrows, ncols, bias_dev, q, k, outputs_dev, nrows, st);
+    HIPCHECK(hipGetLastError());
+}
+
+TG_API size_t tg_hip_matmul_noalloc_max_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
 
 /* ---- decode attention (tg_attention_v2, csrc/libtinygiant.c:939-983) ----
  * Scratch: q8 of the input | Q, K, V projections | chunk partials |
