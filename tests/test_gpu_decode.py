@@ -144,20 +144,18 @@ def test_decode_graph_equals_eager(tg, qwen3, norm):
     assert a.tobytes() == b.tobytes()
 
 
-@pytest.mark.parametrize("norm", [False, True])
-def test_decode_persistent_stagewise(tg, orc, qwen3, norm):
-    say(f"decode persistent stage-wise norm={norm}")
+def _stagewise(tg, orc, layers, norm, seed):
     off = _dbg_offsets()
     assert off["BYTES"] == tg.lib().tg_hip_decode_debug_bytes()
-    L = qwen3.L
+    L = layers.L
     dbg = tg.DeviceArray(L * off["BYTES"])
-    h0 = np.random.default_rng(2).standard_normal(D).astype(np.float32)
-    h_final, status = _run(tg, qwen3, 2, h0, debug=dbg, norm=norm)
-    assert status == 0, "grid barrier timed out"
+    h0 = np.random.default_rng(seed).standard_normal(D).astype(np.float32)
+    h_final, status = _run(tg, layers, 2, h0, debug=dbg, norm=norm)
+    assert status == 0, "an exchange wait timed out"
     raw = dbg.download(np.uint8, L * off["BYTES"]).reshape(L, off["BYTES"])
     dbg.free()
     for l in range(L):
-        nw = qwen3.norm_host[l] if norm else np.ones(D, np.float32)
+        nw = layers.norm_host[l] if norm else np.ones(D, np.float32)
         rec = raw[l]
         f32 = lambda o, n: rec[o:o + 4 * n].view(np.float32)
         hin = f32(off["HIN"], D)
@@ -173,9 +171,9 @@ def test_decode_persistent_stagewise(tg, orc, qwen3, norm):
         assert np.array_equal(f32(off["XD"], D // 256), q["scale"])
         assert np.array_equal(rec[off["XS32"]:off["XS32"] + D // 8].view(np.int32), q["bsums"].reshape(-1))
         # A
-        g, u, d = qwen3.host[l]
+        g, u, d = layers.host[l]
         n = len(g)
-        rw = qwen3.rw[l]
+        rw = layers.rw[l]
         hid = f32(off["HID"], 8 * I).reshape(8, I)[:n]
         h_ref = np.zeros((n, I), np.float32)
         orc.moe_v2(g, u, d, 0, [2] * n, None, None, None, 0, rw, x.reshape(1, D), np.zeros((1, D), np.float32), I,
@@ -186,13 +184,42 @@ def test_decode_persistent_stagewise(tg, orc, qwen3, norm):
         qh = orc.quantize_q8(hid)
         assert np.array_equal(rec[off["HQ"]:off["HQ"] + 8 * I].view(np.int8).reshape(8, I)[:n], qh["qs"].reshape(n, I))
         assert np.array_equal(f32(off["HD"], 8 * 3).reshape(8, 3)[:n], qh["scale"])
+        assert np.array_equal(rec[off["HS16"]:off["HS16"] + 8 * (I // 16) * 4].view(np.int32).reshape(8, I // 16)[:n],
+                              _sums16(qh).reshape(n, I // 16))
         # B
         out_ref = orc.moe_v2(g, u, d, 0, [2] * n, None, None, None, 0, rw, x.reshape(1, D), hin.reshape(1, D).copy(),
                              I, hidden_in=np.ascontiguousarray(hid))[0]
         h_out = h_final if l == L - 1 else raw[l + 1][off["HIN"]:off["HIN"] + 4 * D].view(np.float32)
         err = np.abs(h_out - out_ref).max() / np.abs(out_ref).max()
-        say(f"  layer {l}: output rel {err:.2e}")
+        if l < 3 or l == L - 1:
+            say(f"  layer {l}: output rel {err:.2e}")
         assert err <= 1e-5, (l, err)
+
+
+def _sums16(q):
+    """16-element sums of the quants of q8 blocks (what the Q6_K dots take
+    for their -32 offset)"""
+    qs = q["qs"].astype(np.int64)
+    return qs.reshape(*qs.shape[:-1], 16, 16).sum(-1).astype(np.int32)
+
+
+@pytest.mark.parametrize("norm", [False, True])
+def test_decode_persistent_stagewise(tg, orc, qwen3, norm):
+    say(f"decode persistent stage-wise norm={norm}")
+    _stagewise(tg, orc, qwen3, norm, 2)
+
+
+def test_decode_persistent_full_depth_stagewise(tg, orc):
+    """All 48 layers of the Qwen3-30B-A3B expert step (8 of 128 experts each,
+    RMSNorm weights), every layer checked stage by stage from the GPU's own
+    inputs: the chain of tinygiant/engine.py:281-282,335-341 over the model's
+    whole depth, which reuses every exchange slot 24 times."""
+    say("decode persistent 48 layers stage-wise")
+    ly = Layers(tg, 48, 4848)
+    try:
+        _stagewise(tg, orc, ly, True, 48)
+    finally:
+        ly.close()
 
 
 @pytest.mark.parametrize("norm", [False, True])

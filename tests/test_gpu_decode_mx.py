@@ -7,7 +7,9 @@ Checked stage by stage through the per-layer debug records against the
 oracle (the MXFP4 dots run on block-scaled MFMA: the reference's per-block
 integer sums, the f32 additions grouped differently):
   N  RMSNorm(h) vs the oracle's                        <= 2e-6 of max|x|
+  Q1 q8(x) quants and scales vs the oracle's q8 of the GPU's x   bit-exact
   A  hidden vs oracle (from the GPU's x)                <= 1e-4 per expert row
+  Q2 q8(hidden) vs the oracle's q8 of the GPU's hidden  bit-exact
   B  layer output vs oracle down+combine from the GPU's x and hidden
                                                          <= 1e-5 of max|h|
 and end to end against the graph of per-layer kernels (which differ only by
@@ -25,6 +27,16 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 D = 2880
 E = 4
+NQ = (D + 255) // 256
+# per-layer debug record (byte offsets): h_in f32[D] | x f32[D] | q8(x) i8[NQ*256] |
+# q8(x) scales f32[NQ] | hidden f32[E][D] | q8(hidden) i8[E][NQ*256] | scales f32[E][NQ]
+R_HIN, R_X = 0, 4 * D
+R_XQ = R_X + 4 * D
+R_XD = R_XQ + NQ * 256
+R_HID = R_XD + 4 * NQ
+R_HQ = R_HID + 4 * E * D
+R_HD = R_HQ + E * NQ * 256
+R_BYTES = R_HD + 4 * E * NQ
 
 
 def say(*a):
@@ -97,7 +109,7 @@ class MxLayers:
         dbg = None
         if debug:
             rb = lib.tg_hip_decode_record_bytes(d)
-            assert rb == 6 * D * 4
+            assert rb == R_BYTES
             dbg = self.tg.DeviceArray(self.L * rb)
             lib.tg_hip_decode_set_debug(d, dbg.ptr)
         for _ in range(steps):
@@ -109,7 +121,7 @@ class MxLayers:
         h.free()
         recs = None
         if dbg is not None:
-            recs = dbg.download(np.float32, self.L * 6 * D).reshape(self.L, 6, D)
+            recs = dbg.download(np.uint8, self.L * R_BYTES).reshape(self.L, R_BYTES)
             dbg.free()
         return out, status, recs
 
@@ -128,22 +140,24 @@ def gptoss(tg):
     ly.close()
 
 
-def test_decode_mx_stagewise(tg, orc, gptoss):
-    say("gpt-oss persistent step, stage-wise")
-    h0 = np.random.default_rng(5).standard_normal(D).astype(np.float32)
-    h_final, status, recs = gptoss.run(2, h0, debug=True)
-    assert status == 0, "an exchange wait timed out"
-    for l in range(gptoss.L):
-        hin, x = recs[l, 0], recs[l, 1]
-        hid = np.ascontiguousarray(recs[l, 2:6])
+def _stagewise(orc, layers, recs, h0, h_final):
+    f32 = lambda rec, o, n: rec[o:o + 4 * n].view(np.float32)
+    for l in range(layers.L):
+        rec = recs[l]
+        hin, x = f32(rec, R_HIN, D), f32(rec, R_X, D)
+        hid = np.ascontiguousarray(f32(rec, R_HID, E * D).reshape(E, D))
         if l == 0:
             assert np.array_equal(hin, h0)
         # N
-        x_ref = orc.rms_norm(hin, gptoss.norm_host[l], 1e-5)
+        x_ref = orc.rms_norm(hin, layers.norm_host[l], 1e-5)
         assert np.abs(x - x_ref).max() <= 2e-6 * np.abs(x_ref).max(), l
-        g, u, d = gptoss.host[l]
-        gb, ub, db = gptoss.bias_host[l]
-        rw = gptoss.rw[l]
+        # Q1
+        qx = orc.quantize_q8(x)
+        assert np.array_equal(rec[R_XQ:R_XQ + NQ * 256].view(np.int8), qx["qs"].reshape(-1)), l
+        assert np.array_equal(f32(rec, R_XD, NQ).view(np.uint32), qx["scale"].view(np.uint32)), l
+        g, u, d = layers.host[l]
+        gb, ub, db = layers.bias_host[l]
+        rw = layers.rw[l]
         # A
         h_ref = np.zeros((E, D), np.float32)
         orc.moe_v2(g, u, d, O.FMT_MXFP4, [O.FMT_MXFP4] * E, gb, ub, db, O.ACT_GPTOSS, rw, x.reshape(1, D),
@@ -151,13 +165,41 @@ def test_decode_mx_stagewise(tg, orc, gptoss):
         for e in range(E):
             rel = np.abs(hid[e] - h_ref[e]).max() / np.abs(h_ref[e]).max()
             assert rel <= 1e-4, (l, e, rel)
+        # Q2
+        qh = orc.quantize_q8(hid)
+        assert np.array_equal(rec[R_HQ:R_HQ + E * NQ * 256].view(np.int8), qh["qs"].reshape(-1)), l
+        assert np.array_equal(f32(rec, R_HD, E * NQ).view(np.uint32), qh["scale"].reshape(-1).view(np.uint32)), l
         # B
         out_ref = orc.moe_v2(g, u, d, O.FMT_MXFP4, [O.FMT_MXFP4] * E, gb, ub, db, O.ACT_GPTOSS, rw,
                              x.reshape(1, D), hin.reshape(1, D).copy(), D, hidden_in=hid)[0]
-        h_out = h_final if l == gptoss.L - 1 else recs[l + 1, 0]
+        h_out = h_final if l == layers.L - 1 else f32(recs[l + 1], R_HIN, D)
         err = np.abs(h_out - out_ref).max() / np.abs(out_ref).max()
-        say(f"  layer {l}: output rel {err:.2e}")
+        if l < 3 or l == layers.L - 1:
+            say(f"  layer {l}: output rel {err:.2e}")
         assert err <= 1e-5, (l, err)
+
+
+def test_decode_mx_stagewise(tg, orc, gptoss):
+    say("gpt-oss persistent step, stage-wise")
+    h0 = np.random.default_rng(5).standard_normal(D).astype(np.float32)
+    h_final, status, recs = gptoss.run(2, h0, debug=True)
+    assert status == 0, "an exchange wait timed out"
+    _stagewise(orc, gptoss, recs, h0, h_final)
+
+
+def test_decode_mx_full_depth_stagewise(tg, orc):
+    """All 36 layers of the gpt-oss-120b step (4 of 128 experts each), every
+    layer checked stage by stage from the GPU's own inputs: the chain of
+    tinygiant/engine.py:281-282,335-341 over the model's whole depth."""
+    say("gpt-oss persistent step, 36 layers stage-wise")
+    ly = MxLayers(tg, 36, 360)
+    try:
+        h0 = np.random.default_rng(36).standard_normal(D).astype(np.float32)
+        h_final, status, recs = ly.run(2, h0, debug=True)
+        assert status == 0, "an exchange wait timed out"
+        _stagewise(orc, ly, recs, h0, h_final)
+    finally:
+        ly.close()
 
 
 def test_decode_mx_matches_graph(tg, gptoss):

@@ -158,3 +158,21 @@ def test_head_ties_take_the_first_row(tg, orc):
     logits, am, _ = _head(tg, Q6K, mat, xs[:1], nrows, ncols)
     assert logits[0][317] == logits[0][701] > 0
     assert am[0] == 317
+
+
+@pytest.mark.parametrize("k", [1, 9])
+def test_head_q6k_full_vocabulary(tg, orc, k):
+    """The Qwen3-30B-A3B output head at its full size, 151936 x 2048 q6_K
+    (255,252,480 bytes; engine.py:347-354 with tg_matmul, csrc/libtinygiant.c:
+    925-931), with the RMSNorm weight applied, over a k-row verify batch:
+    every logit against the oracle and the fused argmax against the oracle's."""
+    import tinygiant_amd.synth as S
+    nrows, ncols = 151936, 2048
+    rng = np.random.default_rng(151936 + k)
+    mat = S.matrix_host(Q6K, S.tensor_seed(15, 0, 0, 3), nrows, ncols)
+    x = rng.standard_normal((k, ncols)).astype(np.float32)
+    norm = rng.uniform(0.5, 1.5, ncols).astype(np.float32)
+    say(f"head full vocabulary k={k}")
+    logits, am, mv = _head(tg, Q6K, mat, x, nrows, ncols, norm=norm)
+    ref = _oracle(orc, Q6K, mat, x, nrows, ncols, norm=norm)
+    _check(ref, logits, am, mv, 1e-5)

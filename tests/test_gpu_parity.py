@@ -85,6 +85,23 @@ def test_matmul_vs_oracle(tg, orc, fmt, ncols):
     assert ok, rel
 
 
+def test_matmul_q4k_768x2048(tg, orc):
+    """The single fused matvec of the smallest workload at its exact shape:
+    768 x 2048 q4_K (d, dmin U[1e-3, 2e-2], uniform scale and quant bytes),
+    x ~ N(0, 1), through tg_matmul (csrc/libtinygiant.c:908-931), and its
+    per-sub-block integer sums bit-exact."""
+    import tinygiant_amd.synth as S
+    say("matmul q4_K 768x2048")
+    nrows, ncols = 768, 2048
+    mat = S.matrix_host(O.FMT_Q4K, S.tensor_seed(20261201, 0, 0, 0), nrows, ncols)
+    x = np.random.default_rng(768).standard_normal(ncols).astype(np.float32)
+    got = tg.matmul(O.FMT_Q4K, mat, None, x, nrows, ncols)
+    ref = orc.matmul(O.FMT_Q4K, mat, None, x, nrows, ncols)
+    ok, rel = close(got, ref)
+    assert ok, rel
+    assert np.array_equal(tg.isums(O.FMT_Q4K, mat, nrows, ncols, x), orc.isums(O.FMT_Q4K, mat, nrows, ncols, x))
+
+
 @pytest.mark.parametrize("fmt,ncols", FMTS)
 def test_matmul_integer_cases_exact(tg, orc, fmt, ncols):
     say("matmul exact", fmt, ncols)

@@ -50,11 +50,14 @@ struct DecodeLayerMx {
     const float *norm_w;
     int n, pad;
 };
-/* Its per-layer debug record: h_in f32[D] | x f32[D] (workgroup 0) |
- * hidden f32[4][D] (expert slot e's by workgroup 2e) */
+/* Its per-layer debug record: h_in f32[D] | x f32[D] | q8(x) quants i8[NQ*256]
+ * (zero padded) | q8(x) scales f32[NQ] (workgroup 0) | hidden f32[4][D] |
+ * q8(hidden) quants i8[4][NQ*256] | q8(hidden) scales f32[4][NQ] (expert
+ * slot e's by workgroup 2e); NQ = 12 q8 blocks of 256 per row */
 struct DecodeDebugMx {
-    static constexpr int D = DECODE_MX_D, E = DECODE_MX_E;
-    static constexpr int HIN = 0, X = HIN + D * 4, HID = X + D * 4, BYTES = HID + E * D * 4;
+    static constexpr int D = DECODE_MX_D, E = DECODE_MX_E, NQ = (DECODE_MX_D + 255) / 256;
+    static constexpr int HIN = 0, X = HIN + D * 4, XQ = X + D * 4, XD = XQ + NQ * 256, HID = XD + NQ * 4,
+                         HQ = HID + E * D * 4, HD = HQ + E * NQ * 256, BYTES = HD + E * NQ * 4;
 };
 int decode_mx_max_grid();
 size_t decode_mx_slot_bytes();

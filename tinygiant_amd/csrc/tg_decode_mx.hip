@@ -147,7 +147,8 @@ struct __attribute__((aligned(16))) LdsQ {
  * of k_quantize_q8, written as fp8 halves into block slots 8b .. 8b + 7 of q.
  * Lanes l and l + 4 hold values t and 16 + t of the same 32-block, which the
  * MFMA K order interleaves; lane l (l % 8 < 4) writes both. */
-__device__ inline void q8_split_block(float v0, float v1, float v2, float v3, int lane, int b, LdsQ &q) {
+__device__ inline void q8_split_block(float v0, float v1, float v2, float v3, int lane, int b, LdsQ &q,
+                                      uint32_t *dbg_q = nullptr, float *dbg_d = nullptr) {
     const float amax = wave_max(fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3))));
     const float inv = amax > 0.f ? 127.f / amax : 0.f;
     const int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
@@ -174,6 +175,11 @@ __device__ inline void q8_split_block(float v0, float v1, float v2, float v3, in
         pl[1] = inter(lo, lo2, 1);
     }
     if (lane == 0) q.d[b] = amax / 127.f;
+    if (dbg_q) {   /* debug record: the block's quants, four per lane, and its scale */
+        dbg_q[64 * b + lane] = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+                               ((uint32_t)(q3 & 0xFF) << 24);
+        if (lane == 0) dbg_d[b] = amax / 127.f;
+    }
 }
 
 /* The B operand of chunk c for this lane: column 0 holds the fp8 hi halves of
@@ -341,7 +347,8 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     };
     /* q8 + fp8 halves of a D-value LDS vector (scaled by `scale` and the
      * RMSNorm weight when norm): wave w quantizes blocks w and w + 8 */
-    auto quantize = [&](const float *src, bool norm, float scale, bool has_nw, LdsQ &q, float *dbg_x) {
+    auto quantize = [&](const float *src, bool norm, float scale, bool has_nw, LdsQ &q, float *dbg_x,
+                        uint8_t *dbg_q, float *dbg_d) {
 #pragma unroll
         for (int k = 0; k < 2; k++) {
             const int b = wave + NA * k;
@@ -356,7 +363,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 v[c] = t;
                 if (dbg_x && i < D) dbg_x[i] = t;
             }
-            q8_split_block(v[0], v[1], v[2], v[3], lane, b, q);
+            q8_split_block(v[0], v[1], v[2], v[3], lane, b, q, reinterpret_cast<uint32_t *>(dbg_q), dbg_d);
         }
     };
 
@@ -481,8 +488,10 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
             if (rec && wg == 0)
                 for (int t = threadIdx.x; t < D; t += NT) reinterpret_cast<float *>(rec + DecodeDebugMx::HIN)[t] = hx[t];
-            quantize(hx, true, scale, has_nw, sx,
-                     rec && wg == 0 ? reinterpret_cast<float *>(rec + DecodeDebugMx::X) : nullptr);
+            const bool rx = rec && wg == 0;
+            quantize(hx, true, scale, has_nw, sx, rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::X) : nullptr,
+                     rx ? rec + DecodeDebugMx::XQ : nullptr,
+                     rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::XD) : nullptr);
         }
         __syncthreads();
         if (tw) tr[2] = wall_clock64();
@@ -583,7 +592,11 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         /* the next layer's gate segments into dws (free since the down blocks
          * were gathered), draining during this q8, the down rows and the hop */
         if (cl < 0 && l + 1 < L) fetch_gate(lys[l + 1], true);
-        quantize(hid, false, 1.f, false, sh, nullptr);
+        {
+            const bool rh = rec && (xc & 1) == 0 && rk == 0;
+            quantize(hid, false, 1.f, false, sh, nullptr, rh ? rec + DecodeDebugMx::HQ + xe * (NQ * 256) : nullptr,
+                     rh ? reinterpret_cast<float *>(rec + DecodeDebugMx::HD) + xe * NQ : nullptr);
+        }
         __syncthreads();
         if (tw) tr[5] = wall_clock64();
         /* ---- 6: down rows of the slice ---- */
