@@ -410,6 +410,52 @@ def configs_probe(tg, iters=20, plain=False):
     return out
 
 
+def prefill_probe(tg, iters=20, tokens=64):
+    """Only the gpt-oss 64-token prefill layer of configs_probe (one layer of
+    128 resident MXFP4 experts, top-4 Zipf routing, biases, clamped SwiGLU,
+    the block-scaled MFMA expert phases), for MFMA counter passes."""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    rng = np.random.default_rng(SEED + 23)
+    GD, GE, GK = 2880, 128, 4
+    mat_b = GD * (GD // 32) * 17
+    buf = tg.DeviceArray(GE * 3 * mat_b)
+    for e in range(GE):
+        for part in range(3):
+            lib.tg_hip_synth_fill(3, S.tensor_seed(SEED + 25, 0, e, part), buf.ptr + (e * 3 + part) * mat_b, mat_b,
+                                  None)
+    perm = rng.permutation(GE)
+    experts, rw = S.routing_rows(rng, tokens, GE, GK, 1.1, perm)
+    n = len(experts)
+    ptrs = [(ctypes.c_void_p * n)(*[buf.ptr + (int(e) * 3 + p) * mat_b for e in experts]) for p in range(3)]
+    bl = []
+    for p in range(3):
+        bb = tg.DeviceArray(n * GD * 4)
+        bb.upload((rng.standard_normal((n, GD)) * 0.05).astype(np.float32))
+        bl.append(bb)
+    bptr = [(ctypes.c_void_p * n)(*[bl[p].ptr + i * GD * 4 for i in range(n)]) for p in range(3)]
+    fm = np.full(n, tg.FMT_MXFP4, np.int32)
+    rwc = np.ascontiguousarray(rw, np.float32)
+    plan = lib.tg_hip_moe_plan_create(*[ctypes.addressof(q) for q in ptrs], tg.FMT_MXFP4, fm.ctypes.data,
+                                      *[ctypes.addressof(q) for q in bptr], tg.ACT_GPTOSS, n, rwc.ctypes.data,
+                                      tokens, GD, GD)
+    if not plan:
+        raise RuntimeError(tg.last_error())
+    xp = tg.DeviceArray(tokens * GD * 4)
+    xp.upload(rng.standard_normal((tokens, GD)).astype(np.float32))
+    yp = tg.DeviceArray(tokens * GD * 4)
+    us = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, xp.ptr, yp.ptr, None), iters)
+    lib.tg_hip_synchronize()
+    ops = 2 * tokens * GK * 3 * GD * GD
+    out = {"tokens": tokens, "experts": n, "rows_per_expert_max": int((rw != 0).sum(axis=1).max()), "us": round(us, 2),
+           "weight_bytes": n * 3 * mat_b, "weight_gbps": round(n * 3 * mat_b / (us * 1e-6) / 1e9, 1),
+           "useful_mfma_ops": ops, "mfma_tops": round(ops / (us * 1e-6) / 1e12, 2)}
+    lib.tg_hip_moe_plan_destroy(plan)
+    for a in bl + [buf, xp, yp]:
+        a.free()
+    return out
+
+
 def head_probe(tg, ks=(1, 5, 9), iters=20):
     """The q6_K output head of Qwen3-30B-A3B (151936 x 2048, 255,252,480 B) over
     k verify rows with the argmax fused in (tg_hip_head_argmax_dev, RMSNorm
@@ -545,16 +591,32 @@ def loader_probe(tg, n_layers=2):
         shutil.rmtree(d, ignore_errors=True)
 
 
+def source_sha256(rel):
+    """sha256 of a kernel source file of this tree (profiles are stamped with
+    the hash of the source they measured)."""
+    import hashlib
+    return hashlib.sha256((ROOT / rel).read_bytes()).hexdigest()
+
+
 def read_traffic(name):
     """HBM bytes per launch of the dominant kernel from the committed rocprofv3
-    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present."""
+    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if present
+    and measured on the kernel source this tree holds (its `source_sha256`
+    line matches the source file its `source:` line names); else None."""
     p = ROOT / "profiles" / name
     if not p.exists():
         return None
+    fields = {}
     for line in p.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        if ":" in line and not line.startswith(("|", " ", "#", "`")):
+            k, v = line.split(":", 1)
+            fields[k.strip()] = v.strip()
+    src, sha = fields.get("source"), fields.get("source_sha256")
+    if not src or not sha or not (ROOT / src).exists() or source_sha256(src) != sha:
+        log(f"profiles/{name}: measured on another version of its kernel source; traffic not reported")
+        return None
+    t = fields.get("traffic_bytes_per_launch")
+    return float(t) if t else None
 
 
 def main():
@@ -576,6 +638,8 @@ def main():
                          "a plain launch, for profilers); graph: per-layer kernels in a HIP graph")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only time a plain 1 GiB device copy (HBM reference / counter calibration)")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="only the gpt-oss 64-token prefill layer on the MFMA expert phases (counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the expert path is "
@@ -584,8 +648,10 @@ def main():
 
     import tinygiant_amd as tg
     lib = tg.lib()
-    if args.copy_probe:
-        print(json.dumps(copy_probe(tg)), flush=True)
+    if args.copy_probe or args.prefill_probe:
+        out = copy_probe(tg) if args.copy_probe else prefill_probe(tg)
+        lib.tg_hip_shutdown()
+        print(json.dumps(out), flush=True)
         return 0
     name = ctypes.create_string_buffer(256)
     lib.tg_hip_device_name(name, 256)
@@ -630,11 +696,33 @@ def main():
     if mode >= 2:
         phases = phase_breakdown(tg, step, layers)
         log(f"phase breakdown (us per layer, first/last workgroup): {json.dumps(phases)}")
+    launch_note = None
     if mode >= 2:
-        # the whole step is one kernel: its launch duration is the step time
-        per_kernel = {"k_decode_qwen": {"avg_us": round(ms_step * 1e3, 2), "launches": args.steps}}
+        # the whole step is one kernel.  A cooperative launch adds a fixed
+        # runtime dispatch cost (about 18 us, the same for any kernel length);
+        # the kernel's own duration is timed over plain launches of the same
+        # step, which is also the command the committed kernel trace runs
+        k_us = ms_step * 1e3
+        if mode == 2:
+            plain = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, ctypes.addressof(narr),
+                                             ctypes.c_float(1e-6), h.ptr, 3)
+            if not plain:
+                raise RuntimeError(tg.last_error())
+            for _ in range(args.warmup):
+                lib.tg_hip_decode_run(plain, None)
+            ms_plain = lib.tg_hip_decode_time(plain, args.steps)
+            lib.tg_hip_synchronize()
+            if lib.tg_hip_decode_status(plain) != 0:
+                raise RuntimeError("persistent decode (plain launch): a grid barrier timed out")
+            lib.tg_hip_decode_destroy(plain)
+            k_us = ms_plain / args.steps * 1e3
+            launch_note = {"cooperative_step_us": round(ms_step * 1e3, 2), "plain_launch_us": round(k_us, 2),
+                           "cooperative_dispatch_us": round(ms_step * 1e3 - k_us, 2)}
+            log(f"kernel duration over {args.steps} plain launches: {k_us:.2f} us "
+                f"(cooperative step {ms_step * 1e3:.2f} us)")
+        per_kernel = {"k_decode_qwen": {"avg_us": round(k_us, 2), "launches": args.steps}}
         kernel_name = "k_decode_qwen (persistent: 48 layers x (gate/up + down), one launch per token)"
-        k_bytes, k_us = bytes_step, ms_step * 1e3
+        k_bytes = bytes_step
         traffic = read_traffic("pmc_decode_qwen_step.txt")
     else:
         # per-kernel durations of one eager step (HIP events on the library stream)
@@ -682,7 +770,7 @@ def main():
             "kernel": kernel_name,
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "bytes_per_launch": k_bytes, "avg_us": round(k_us, 2),
+            "bytes_per_launch": k_bytes, "avg_us": round(k_us, 2), "launch": launch_note,
         },
         "kernels": per_kernel,
         "phases_us": phases,
@@ -694,7 +782,7 @@ def main():
         result["verify_layer"] = verify_probe(tg, bufs[0].ptr)
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
-    for b in bufs + nbufs:
+    for b in bufs + nbufs + [h]:
         b.free()
     if not args.no_boundary:
         log("boundary probe ...")
@@ -712,6 +800,7 @@ def main():
     if not args.no_cpu:
         log("cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(routes, min(args.cpu_layers, layers))
+    lib.tg_hip_shutdown()
     print(json.dumps(result), flush=True)
     return 0
 

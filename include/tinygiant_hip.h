@@ -137,6 +137,11 @@ void tg_hip_memcpy_h2d(void *dst_dev, const void *src, size_t n);   /* synchrono
 void tg_hip_memcpy_d2h(void *dst, const void *src_dev, size_t n);   /* synchronous */
 void tg_hip_memcpy_d2d(void *dst_dev, const void *src_dev, size_t n, void *stream);
 void tg_hip_synchronize(void);
+/* No counterpart in the reference (its CPU library holds no device state).
+ * Waits for the device, then releases the library's stream, arena, pinned
+ * rows, upload buffers and timing marks; a later call re-initialises.  Plans,
+ * decode steps and device arrays are the caller's to destroy first. */
+void tg_hip_shutdown(void);
 
 /* Seeded synthetic tensors: kind -1 raw bytes, 0 Q4_K, 2 Q6_K, 3 MXFP4, 4 Q8_0
  * (block scale fields drawn as documented in tg_synth.h). */

@@ -135,6 +135,21 @@ def test_matmul_run_to_run_identical(tg):
     assert a.tobytes() == b.tobytes()
 
 
+def test_shutdown_then_reinit(tg):
+    """tg_hip_shutdown releases the library's stream, arena and pinned rows;
+    the next call sets them up again and computes the same bits."""
+    say("shutdown + re-init")
+    nrows, ncols = 300, 2048
+    mat = np.concatenate([_rand_row(O.FMT_Q4K, ncols) for _ in range(nrows)])
+    x = RNG.standard_normal(ncols).astype(np.float32)
+    a = tg.matmul(O.FMT_Q4K, mat, None, x, nrows, ncols)
+    lib = tg.lib()
+    lib.tg_hip_shutdown()
+    lib.tg_hip_shutdown()          # a second call finds nothing to release
+    b = tg.matmul(O.FMT_Q4K, mat, None, x, nrows, ncols)
+    assert a.tobytes() == b.tobytes()
+
+
 def _experts(n, D, I, gate_fmt, down_fmts, seed):
     import tinygiant_amd.synth as S
     g, u, d = [], [], []

@@ -80,6 +80,7 @@ def register_extensions(lib):
     _reg(lib.tg_hip_memcpy_d2h, [VP, VP, SZ])
     _reg(lib.tg_hip_memcpy_d2d, [VP, VP, SZ, VP])
     _reg(lib.tg_hip_synchronize, [])
+    _reg(lib.tg_hip_shutdown, [])
     _reg(lib.tg_hip_synth_fill, [CI, U64, VP, U64, VP])
     _reg(lib.tg_hip_synth_fill_host, [CI, U64, VP, U64])
     _reg(lib.tg_hip_quantize_q8, [VP, CI, CI, VP])

@@ -1014,6 +1014,29 @@ TG_API void tg_hip_init(void) {
     ensure_init();
 }
 
+static void release_upload_buffers();
+static void release_marks();
+
+/* Waits for the device and releases everything the library holds: its
+ * stream, the device arena, the pinned and coherent host rows, the ticket
+ * words, the file-upload buffers and the timing marks.  Objects the caller
+ * created (plans, decode steps, device arrays) stay theirs to destroy first.
+ * A later call re-initialises the library. */
+TG_API void tg_hip_shutdown(void) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    if (!g.ready) return;
+    HIPCHECK(hipStreamSynchronize(g.st));
+    HIPCHECK(hipDeviceSynchronize());
+    release_upload_buffers();
+    release_marks();
+    if (g.arena) HIPCHECK(hipFree(g.arena));
+    if (g.tickets) HIPCHECK(hipFree(g.tickets));
+    if (g.pin) HIPCHECK(hipHostFree(g.pin));
+    if (g.io) HIPCHECK(hipHostFree(g.io));
+    HIPCHECK(hipStreamDestroy(g.st));
+    g = Ctx();
+}
+
 /* tg_hip_matmul_dev without a workspace and without any allocation: the q8
  * rows of the inputs go to the library's fixed device scratch, which holds
  * tg_hip_matmul_noalloc_max_bytes() bytes (k * ceil(ncols/256) * 360 bytes
@@ -1252,6 +1275,17 @@ static uint8_t *g_up_buf[2] = {nullptr, nullptr};
 static size_t g_up_cap = 0;
 static hipEvent_t g_up_ev[2];
 static const int UP_THREADS = 8;
+
+static void release_upload_buffers() {
+    for (int i = 0; i < 2; i++) {
+        if (!g_up_buf[i]) continue;
+        HIPCHECK(hipEventSynchronize(g_up_ev[i]));
+        HIPCHECK(hipEventDestroy(g_up_ev[i]));
+        HIPCHECK(hipHostFree(g_up_buf[i]));
+        g_up_buf[i] = nullptr;
+    }
+    g_up_cap = 0;
+}
 
 /* Reads n bytes at file offset off into dst; returns how many bytes were read
  * before the first share that ended early (n when none did). */
@@ -1856,6 +1890,12 @@ TG_API int tg_hip_set_moe_expert_major(int mode) {
 /* Event marks on the library stream, for timing queued device work. */
 static hipEvent_t g_marks[8];
 static bool g_marks_ready = false;
+
+static void release_marks() {
+    if (!g_marks_ready) return;
+    for (auto &e : g_marks) HIPCHECK(hipEventDestroy(e));
+    g_marks_ready = false;
+}
 
 TG_API void tg_hip_mark(int slot) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
