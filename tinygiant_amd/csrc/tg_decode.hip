@@ -50,7 +50,9 @@
  *
  * Exchanges use epoch-tagged 16-byte slots {tag, v0, v1, v2}, written and
  * polled as one vector access so the tag and its values arrive together.
- * Two communication waves per workgroup do the polling and publishing.
+ * Two communication waves per workgroup publish; the two intra-XCD gathers
+ * are polled by all eight waves (one or two slots a lane, so a round is one
+ * load latency), the cross-XCD hop by the communication waves alone.
  * Every wait is bounded; a timed-out wait raises an abort flag that
  * releases every other waiter, so the grid always drains.
  */
@@ -294,58 +296,6 @@ __device__ inline uint32_t q8_block_wave(float v0, float v1, float v2, float v3,
 
 __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g)) * u; }
 
-/* One 1 KiB direct-to-LDS copy: lane l moves the 16 bytes at byte offset
- * off + 16 l of the buffer `desc` to LDS address lds + 16 l (lds is
- * wave-uniform).  Issued from inline assembly, so the compiler does not
- * track it: it would otherwise make LDS reads of other arrays wait for the
- * copies still in flight (it cannot tell the arrays apart), which is the
- * overlap this kernel needs.  The waves that issue copies wait for them
- * themselves (wait_copies) before the barrier that opens the phase reading
- * them.  Vector-memory waits the compiler emits for its own loads stay
- * correct: the counter completes in order, so untracked operations only
- * make those waits stricter. */
-__device__ inline u32x4 buf_desc(const void *p, uint32_t nbytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)p;
-    u32x4 d;
-    d.x = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
-    d.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xFFFFu;
-    d.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)nbytes);
-    d.w = 0x00020000u;
-    return d;
-}
-__device__ inline uint32_t lds_addr(const void *p) {
-    return (uint32_t)__builtin_amdgcn_readfirstlane(
-        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p);
-}
-/* M0 holds the copy's LDS address.  M0 is a reserved register the
- * compiler does not let inline assembly clobber; nothing else in this
- * kernel uses it (its generated code sets M0 nowhere else). */
-__device__ inline void copy_1k(const u32x4 &desc, uint32_t off, uint32_t lds, int lane) {
-    const uint32_t voff = off + 16u * (uint32_t)lane;
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(lds), "v"(voff), "s"(desc)
-                 : "memory");
-}
-
-__device__ inline void wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-/* wait until at most N of the wave's vector memory operations are in flight */
-template <int N>
-__device__ inline void wait_copies_but() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-/* Workgroup barrier for the layer loop: waits for the wave's LDS accesses
- * (lgkmcnt) and meets the other waves; the memory clobber keeps the
- * compiler from moving accesses across it.  __syncthreads() (and a release
- * fence on LDS alone) would also wait for the wave's outstanding
- * direct-to-LDS copies (they count as LDS writes), which must stay in
- * flight across the phases they overlap.  A wave whose copies a phase
- * reads waits for them itself (wait_copies) before the barrier that opens
- * that phase; nothing the workgroup stores to global memory inside a layer
- * is read back by the workgroup. */
-__device__ inline void bar_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
 }  // namespace
 
 /* Tags are base + layer + 1 in every region, so a launch never mistakes a
@@ -476,11 +426,11 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         /* ---- 1: gather h from the other ranks of this XCD (the copies of
          * this layer's gate/up rows and RMSNorm weight are ahead of the polls) ---- */
         if (l > 0) {
-            if (comm) {
+            {   /* every wave polls: the compute waves are idle here */
                 unsigned rounds = 0;
                 if (tc) tr[15] = wall_clock64();
-                const bool ok = poll_slots<CL, 6>(
-                    sl, clv, (NR - 1) * PS, base + (unsigned)l, abort_flag,
+                const bool ok = poll_slots<NT, ((NR - 1) * PS + NT - 1) / NT>(
+                    sl, (int)threadIdx.x, (NR - 1) * PS, base + (unsigned)l, abort_flag,
                     [&](int f) {
                         const int jj = f / PS, t = f % PS;
                         const int j = jj + (jj >= rk);
@@ -574,10 +524,13 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                 put(GSL + (par * NWG + (uint32_t)wg) * GS + (uint32_t)clv, tag, a[0], a[1], a[2], false);
             }
             if (tc) tr[9] = wall_clock64();
+        }
+        {   /* every wave polls the other ranks' slots while the first
+             * communication wave publishes this rank's */
             unsigned rounds = 0;
             if (tc) tr[12] = wall_clock64();
-            const bool ok = poll_slots<CL, 2>(
-                sl, clv, (NR - 1) * GS, tag, abort_flag,
+            const bool ok = poll_slots<NT, ((NR - 1) * GS + NT - 1) / NT>(
+                sl, (int)threadIdx.x, (NR - 1) * GS, tag, abort_flag,
                 [&](int f) {
                     const int jj = f / GS, t = f % GS;
                     const int j = jj + (jj >= rk);
@@ -652,8 +605,11 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                     r0 + 1 < RB ? pp[xe][r0 + 1] : 0.f, r0 + 2 < RB ? pp[xe][r0 + 2] : 0.f, true);
             }
             if (tc) tr[10] = wall_clock64();
+        }
+        if (comm) {   /* the hop is polled by the communication waves alone (every
+                       * wave polling it measured slower) */
             unsigned rounds = 0;
-            const bool ok = poll_slots<CL, 2>(
+            const bool ok = poll_slots<CL, ((NX - 1) * PS + CL - 1) / CL>(
                 sl, clv, (NX - 1) * PS, tag, abort_flag,
                 [&](int f) {
                     const int xx = f / PS, t = f % PS;

@@ -33,12 +33,20 @@
  * (four blocks inside an MFMA, then per 128 values, per half and per wave),
  * which the f32 bar covers.
  *
- * Weights load ahead of use: the next layer's gate/up blocks and RMSNorm
- * weight into registers during the hop (7), while the compute waves would
- * otherwise wait; this layer's down rows, one contiguous range per slice,
- * straight into LDS right after the h gather (1), so the copy drains during
- * RMSNorm and gate/up instead of ahead of the hidden exchange's polls.  Two
- * communication waves per workgroup do the polling and publishing.
+ * Every weight byte streams through one LDS region by direct-to-LDS copies
+ * (1 KiB an instruction, aligned 16-byte pieces): a CU returns its vector
+ * loads in issue order, so each batch is issued right after an exchange and
+ * drains during the compute that follows, not ahead of the next poll:
+ *   this layer's down rows (one contiguous 45-row range) after the h gather
+ *   (1), gathered into registers during the hidden exchange (4);
+ *   the next layer's gate segments (each compute wave the 272-byte pieces of
+ *   its own K range, into its own part of the region) at q8 of the hidden
+ *   vector (5), moved into registers at the hop (7);
+ *   the next layer's up segments, the same way, at the hop (7), moved into
+ *   registers at the next layer's start.
+ * Two communication waves per workgroup publish; the two gathers are polled
+ * by all eight waves (one or two slots a lane), the hop by the communication
+ * waves.
  */
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -82,7 +90,6 @@ constexpr int MAX_LAYERS = 64;
 constexpr int NTS = 24;               /* timing words per layer */
 constexpr int FMT_FP8 = 0, FMT_FP4 = 4, SCALE_1 = 127, SCALE_16 = 131;
 constexpr uint32_t OOB = 0x80000000u;  /* past every buffer: reads zeros, touches no memory */
-constexpr int PREFETCH_STAGGER = 16;   /* s_sleep units between the compute waves' prefetch issue */
 constexpr int NDMA = 68;               /* 1 KiB direct-to-LDS copy steps of the down rows (16 bytes a lane) */
 constexpr int GSEG = 18;               /* 16-byte chunks of a wave's gate segment of one row (272 bytes + alignment) */
 constexpr int GINS = (RS * GSEG + 63) / 64;   /* copy steps per wave for its gate segments: 13 */
@@ -127,12 +134,6 @@ struct MxBlk {
     uint32_t e;
     u32x4 c;
 };
-__device__ inline MxBlk load_blk(Buf w, uint32_t off) {
-    MxBlk b;
-    b.e = ld4(w, off);
-    b.c = ld16(w, off == OOB ? OOB : off + 1u);
-    return b;
-}
 
 /* LDS image of one q8 row for the MFMA: per 32-value block, the fp8 codes of
  * hi = x >> 4 and lo = x & 15 in MFMA K order (byte 2t holds value t, byte
@@ -224,7 +225,9 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     __shared__ __attribute__((aligned(16))) float hid[D];     /* the expert's hidden vector */
     __shared__ LdsQ sx, sh;                                   /* fp8 images of q8(x) and q8(hidden) */
     __shared__ float ssq[NRK];                                /* sum of h^2 of each 45-row slice */
-    __shared__ float red[NW][2 * NG][2][16];                  /* per-wave partial row sums: hi and lo columns */
+    /* per-wave partial row sums, hi and lo columns: red[unit][row][wave][column],
+     * so a row's twelve partials are three 16-byte LDS reads */
+    __shared__ __attribute__((aligned(16))) float red[2 * NG][16][NW][2];
     __shared__ float pp[NX][RS];                              /* weighted down values of the 8 XCDs */
     __shared__ __attribute__((aligned(16))) uint8_t dws[DWS]; /* staged gate rows, then down rows, of the slice */
     __shared__ int lds_fail;
@@ -245,37 +248,21 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     MxBlk wb[CPW][NG];       /* down blocks, gathered from dws during the hidden exchange */
     u32x4 nw0, nw1;          /* next layer's RMSNorm weight (compute lanes) */
 
-    /* block offset of unit row group gr, chunk i of this wave, or OOB */
-    auto blk_off = [&](int gr, int i) -> uint32_t {
-        const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
-        if (c >= NCH || b >= NBLK || sr >= RS) return OOB;
-        return (uint32_t)(RS * R + sr) * (uint32_t)RB + (uint32_t)b * 17u;
-    };
-    /* up blocks into registers; loads are unconditional so the registers'
-     * live ranges end at their use; an inactive step reads through an empty
-     * descriptor */
-    auto load_up = [&](const DecodeLayerMx &ly, bool on) {
-        const bool cw = on && wave < NW;
-        Buf ub = make_buf_uniform(cw ? ly.up[xe] : nullptr, cw ? (uint32_t)D * RB : 0u);
-#pragma unroll
-        for (int i = 0; i < CPW; i++)
-#pragma unroll
-            for (int gr = 0; gr < NG; gr++) wa[i][NG + gr] = load_blk(ub, blk_off(gr, i));
-    };
-    /* Gate rows: compute wave w uses blocks [16 w, 16 w + 16) of each of the
-     * slice's 45 rows, 272 bytes a row.  It copies those segments, from the
-     * 16-byte boundary at or below each start, into its own region of dws
-     * (row sr at 288 sr) with direct-to-LDS loads, and later gathers its
-     * blocks from there: no other wave touches the region, so only the
-     * wave's own copy has to have landed. */
-    auto fetch_gate = [&](const DecodeLayerMx &ly, bool on) {
-        Buf gbuf = make_buf_uniform(on ? ly.gate[xe] : nullptr, on ? (uint32_t)D * RB : 0u);
+    /* Gate and up rows: compute wave w uses blocks [16 w, 16 w + 16) of each
+     * of the slice's 45 rows, 272 bytes a row.  It copies those segments of
+     * the matrix `mat`, from the 16-byte boundary at or below each start,
+     * into its own region of dws (row sr at 288 sr) with direct-to-LDS
+     * loads, and later gathers its blocks from there into registers: no
+     * other wave touches the region, so only the wave's own copy has to have
+     * landed, and the wave can copy the next matrix in as soon as it has
+     * gathered the last one.  An inactive call reads through an empty
+     * descriptor (zeros). */
+    auto fetch_seg = [&](const uint8_t *mat, bool on) {
+        const u32x4 desc = buf_desc(on ? mat : nullptr, on ? (uint32_t)D * RB : 0u);
         for (int k = 0; k < GINS; k++) {
             const int sidx = 64 * k + lane, sr = sidx / GSEG, j = sidx - sr * GSEG;
             const uint32_t a = ((uint32_t)(RS * R + sr) * (uint32_t)RB + 272u * (uint32_t)wave) & ~15u;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                gbuf.r, (__attribute__((address_space(3))) void *)(dws + GREG * wave + 1024 * k), 16,
-                sr < RS ? a + 16u * (uint32_t)j : OOB, 0, 0, 0);
+            copy_lanes(desc, sr < RS ? a + 16u * (uint32_t)j : OOB, lds_addr(dws + GREG * wave + 1024 * k));
         }
     };
     /* The slice's down rows are one contiguous 45-row range of the expert's
@@ -287,15 +274,13 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
      * exchange's polls, and takes no registers. */
     const uint32_t dsh = (uint32_t)(RS * R * RB) & 15u;
     auto fetch_down = [&](const DecodeLayerMx &ly) {
-        Buf db = make_buf_uniform(ly.down[xe], (uint32_t)D * RB);
+        const u32x4 desc = buf_desc(ly.down[xe], (uint32_t)D * RB);
         const uint32_t a0 = (uint32_t)(RS * R * RB) - dsh;
-        for (int k = wave; k < NDMA; k += NW)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(db.r, (__attribute__((address_space(3))) void *)(dws + 1024 * k),
-                                                     16, a0 + 1024u * (uint32_t)k + 16u * (uint32_t)lane, 0, 0, 0);
+        for (int k = wave; k < NDMA; k += NW) copy_1k(desc, a0 + 1024u * (uint32_t)k, lds_addr(dws + 1024 * k), lane);
     };
     /* One MXFP4 block from dws at byte offset off: the e8m0 byte there and
      * the 16 code bytes after it, from the five aligned dwords that start
-     * with the first code byte (the bytes load_blk reads from memory).
+     * with the first code byte.
      * Off-slice lanes pass on = false and read the zero pad. */
     auto lds_blk_at = [&](uint32_t off, bool on) -> MxBlk {
         off = on ? off : (uint32_t)DZERO;
@@ -317,21 +302,22 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         const bool on = c < NCH && b < NBLK && sr < RS;
         return lds_blk_at(dsh + (uint32_t)sr * RB + (uint32_t)b * 17u, on);
     };
-    /* gate block (gr, i) of this lane from the wave's own gate segments */
-    auto gate_blk = [&](int gr, int i) -> MxBlk {
+    /* gate or up block (gr, i) of this lane from the wave's own segments */
+    auto seg_blk = [&](int gr, int i) -> MxBlk {
         const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
         const bool on = c < NCH && b < NBLK && sr < RS;
         const uint32_t s0 = (uint32_t)(RS * R + sr) * (uint32_t)RB + 272u * (uint32_t)wave;
         return lds_blk_at((uint32_t)(GREG * wave + GSEG * 16 * sr) + (s0 & 15u) + (uint32_t)(b - 16 * wave) * 17u,
                           on);
     };
-    auto zero_up = [&]() {
+    /* the communication waves hold no weights: they zero the registers the
+     * compute waves fill, so both paths assign them */
+    auto zero_units = [&](int u0) {
         const u32x4 z = {0u, 0u, 0u, 0u};
-        nw0 = nw1 = z;
 #pragma unroll
         for (int i = 0; i < CPW; i++)
 #pragma unroll
-            for (int u = NG; u < 2 * NG; u++) wa[i][u] = MxBlk{0u, z};
+            for (int u = u0; u < u0 + NG; u++) wa[i][u] = MxBlk{0u, z};
     };
     auto load_nw = [&](const DecodeLayerMx &ly, bool use) {
         const bool on = use && wave < NW && ly.norm_w != nullptr;
@@ -390,13 +376,21 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     }
     load_nw(lys[0], true);
     if (wave < NW) {
-        fetch_gate(lys[0], true);
-        load_up(lys[0], true);
+        fetch_seg(lys[0].gate[xe], true);
+        wait_copies();
+#pragma unroll
+        for (int i = 0; i < CPW; i++)
+#pragma unroll
+            for (int gr = 0; gr < NG; gr++) wa[i][gr] = seg_blk(gr, i);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        fetch_seg(lys[0].up[xe], true);
     } else {
-        zero_up();
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        nw0 = nw1 = z;
+        zero_units(0);
     }
     store_nw();
-    __syncthreads();   /* layer 0's RMSNorm weight is in LDS before step 2 reads it */
+    bar_lds();   /* layer 0's RMSNorm weight is in LDS before step 2 reads it */
 
     for (int l = 0; l < L; l++) {
         const DecodeLayerMx &ly = lys[l];
@@ -411,31 +405,37 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
         uint8_t *rec = dbg ? dbg + (size_t)l * DecodeDebugMx::BYTES : nullptr;
         if (tw) tr[0] = wall_clock64();
-        /* this layer's gate blocks from the wave's own staged segments (copied
-         * during the previous layer's q8 of the hidden vector) into
-         * registers, while the communication waves gather h; the other waves
-         * zero theirs (both paths assign) */
+        /* this layer's up blocks from the wave's own staged segments (copied
+         * during the previous layer's hop) into registers; its gate blocks
+         * arrived there during that hop */
         if (cl < 0) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            wait_copies();
 #pragma unroll
             for (int i = 0; i < CPW; i++)
 #pragma unroll
-                for (int gr = 0; gr < NG; gr++) wa[i][gr] = gate_blk(gr, i);
+                for (int gr = 0; gr < NG; gr++) wa[i][NG + gr] = seg_blk(gr, i);
         } else {
-            const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-            for (int i = 0; i < CPW; i++)
-#pragma unroll
-                for (int gr = 0; gr < NG; gr++) wa[i][gr] = MxBlk{0u, z};
+            zero_units(NG);
         }
-        if (l == 0) __syncthreads();   /* every wave is done with dws before the down rows' copy */
+        if (l == 0) bar_lds();   /* every wave is done with dws before the down rows' copy */
+        /* the slice's gate, up and down biases (communication lanes, one row
+         * each): issued ahead of the h polls, behind no weight copies */
+        float gbv = 0.f, ubv = 0.f, dbv = 0.f;
+        if (cl >= 0) {
+            const bool on = clv < RS;
+            const uint32_t o = on ? (uint32_t)(RS * R + clv) * 4u : OOB;
+            gbv = __uint_as_float(ld4(make_buf_uniform(ly.gb[xe], ly.gb[xe] ? (uint32_t)D * 4u : 0u), o));
+            ubv = __uint_as_float(ld4(make_buf_uniform(ly.ub[xe], ly.ub[xe] ? (uint32_t)D * 4u : 0u), o));
+            dbv = __uint_as_float(ld4(make_buf_uniform(ly.db[xe], ly.db[xe] ? (uint32_t)D * 4u : 0u), o));
+        }
         /* ---- 1: gather h: slices j' and 32 + j' from the other ranks of this XCD ---- */
         if (l > 0) {
-            if (cl >= 0) {
+            if (cl < 0) store_nw();
+            {   /* every wave polls (one or two slots a lane) */
                 unsigned rounds = 0;
                 if (tc) tr[15] = wall_clock64();
-                const bool ok = poll_slots<CL, 8>(
-                    sl, clv, (NR - 1) * HS, base + (unsigned)l, abort_flag,
+                const bool ok = poll_slots<NT, ((NR - 1) * HS + NT - 1) / NT>(
+                    sl, (int)threadIdx.x, (NR - 1) * HS, base + (unsigned)l, abort_flag,
                     [&](int f) {
                         const int jj = f / HS, t = f % HS;
                         const int j = jj + (jj >= rk);
@@ -461,28 +461,17 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                     tr[17] = rounds;
                 }
                 if (!ok) lds_fail = 1;
-            } else {
-                store_nw();
             }
-            __syncthreads();
+            bar_lds();
             if (lds_fail) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* no copy into LDS outlives the workgroup */
+            wait_copies();   /* no copy into LDS outlives the workgroup */
             return;
         }
         }
         if (tw) tr[1] = wall_clock64();
-        /* the slice's gate, up and down biases (communication lanes, one row
-         * each): issued after the h polls so none waits behind them */
-        float gbv = 0.f, ubv = 0.f, dbv = 0.f;
-        if (cl >= 0) {
-            const bool on = clv < RS;
-            const uint32_t o = on ? (uint32_t)(RS * R + clv) * 4u : OOB;
-            gbv = __uint_as_float(ld4(make_buf_uniform(ly.gb[xe], ly.gb[xe] ? (uint32_t)D * 4u : 0u), o));
-            ubv = __uint_as_float(ld4(make_buf_uniform(ly.ub[xe], ly.ub[xe] ? (uint32_t)D * 4u : 0u), o));
-            dbv = __uint_as_float(ld4(make_buf_uniform(ly.db[xe], ly.db[xe] ? (uint32_t)D * 4u : 0u), o));
-        }
         /* ---- 2: RMSNorm (weight or 1) + q8 + fp8 halves of x ---- */
         if (cl < 0) fetch_down(ly);
+        if (tw) tr[20] = wall_clock64();
         {
             const float tot = wave_sum(ssq[lane]);   /* the 64 slice sums, one per lane */
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
@@ -493,7 +482,9 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                      rx ? rec + DecodeDebugMx::XQ : nullptr,
                      rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::XD) : nullptr);
         }
-        __syncthreads();
+        if (tw) tr[21] = wall_clock64();
+        if (tc) tr[22] = wall_clock64();
+        bar_lds();
         if (tw) tr[2] = wall_clock64();
         /* ---- 3: gate/up rows of the slice, chunks [4 w, 4 w + 4) of wave w ---- */
         if (wave < NW) {
@@ -514,11 +505,11 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
 #pragma unroll
                 for (int u = 0; u < 2 * NG; u++)
 #pragma unroll
-                    for (int v = 0; v < 4; v++) red[wave][u][lane & 15][4 * (lane >> 4) + v] = acc[u][v];
+                    for (int v = 0; v < 4; v++) red[u][4 * (lane >> 4) + v][wave][lane & 15] = acc[u][v];
             /* the down rows' copy has landed in dws before the barrier */
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            wait_copies();
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[3] = wall_clock64();
         /* ---- 4: bias + activation, all-gather the expert's hidden vector ---- */
         /* meanwhile the compute waves gather their down blocks from dws into
@@ -540,11 +531,19 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             /* row i of the slice: the six waves' partial sums in wave order */
             if (clv < RS) {
                 const int gi = clv >> 4, ri = clv & 15, row = RS * R + clv;
+                float pg[2 * NW], pu[2 * NW];
+#pragma unroll
+                for (int k = 0; k < NW / 2; k++) {
+                    const float4 a = reinterpret_cast<const float4 *>(&red[gi][ri][0][0])[k];
+                    const float4 b = reinterpret_cast<const float4 *>(&red[NG + gi][ri][0][0])[k];
+                    pg[4 * k] = a.x, pg[4 * k + 1] = a.y, pg[4 * k + 2] = a.z, pg[4 * k + 3] = a.w;
+                    pu[4 * k] = b.x, pu[4 * k + 1] = b.y, pu[4 * k + 2] = b.z, pu[4 * k + 3] = b.w;
+                }
                 float g = 0.f, u = 0.f;
 #pragma unroll
                 for (int w = 0; w < NW; w++) {
-                    g += red[w][gi][0][ri] + red[w][gi][1][ri];
-                    u += red[w][NG + gi][0][ri] + red[w][NG + gi][1][ri];
+                    g += pg[2 * w] + pg[2 * w + 1];
+                    u += pu[2 * w] + pu[2 * w + 1];
                 }
                 hid[row] = act_fn(TG_ACT_GPTOSS, g + gbv, u + ubv);
             }
@@ -554,10 +553,12 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 put_slot<CPOL_SC1>(sl, GSL + (par * NWG + (uint32_t)wg) * SS + (uint32_t)clv, tag, a[0], a[1], a[2]);
             }
             if (tc) tr[9] = wall_clock64();
+        }
+        {   /* every wave polls the expert's other ranks (one or two slots a lane) */
             unsigned rounds = 0;
             if (tc) tr[12] = wall_clock64();
-            const bool ok = poll_slots<CL, 8>(
-                sl, clv, (NRK - 1) * SS, tag, abort_flag,
+            const bool ok = poll_slots<NT, ((NRK - 1) * SS + NT - 1) / NT>(
+                sl, (int)threadIdx.x, (NRK - 1) * SS, tag, abort_flag,
                 [&](int f) {
                     const int rr = f / SS, t = f % SS;
                     const int r2 = rr + (rr >= R);
@@ -579,9 +580,9 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             }
             if (!ok) lds_fail = 1;
         }
-        __syncthreads();
+        bar_lds();
         if (lds_fail) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* no copy into LDS outlives the workgroup */
+            wait_copies();   /* no copy into LDS outlives the workgroup */
             return;
         }
         if (tw) tr[4] = wall_clock64();
@@ -591,13 +592,13 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 reinterpret_cast<float *>(rec + DecodeDebugMx::HID)[xe * D + t] = hid[t];
         /* the next layer's gate segments into dws (free since the down blocks
          * were gathered), draining during this q8, the down rows and the hop */
-        if (cl < 0 && l + 1 < L) fetch_gate(lys[l + 1], true);
+        if (cl < 0 && l + 1 < L) fetch_seg(lys[l + 1].gate[xe], true);
         {
             const bool rh = rec && (xc & 1) == 0 && rk == 0;
             quantize(hid, false, 1.f, false, sh, nullptr, rh ? rec + DecodeDebugMx::HQ + xe * (NQ * 256) : nullptr,
                      rh ? reinterpret_cast<float *>(rec + DecodeDebugMx::HD) + xe * NQ : nullptr);
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[5] = wall_clock64();
         /* ---- 6: down rows of the slice ---- */
         if (wave < NW) {
@@ -617,27 +618,41 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
 #pragma unroll
                 for (int u = 0; u < NG; u++)
 #pragma unroll
-                    for (int v = 0; v < 4; v++) red[wave][u][lane & 15][4 * (lane >> 4) + v] = acc[u][v];
+                    for (int v = 0; v < 4; v++) red[u][4 * (lane >> 4) + v][wave][lane & 15] = acc[u][v];
         }
-        __syncthreads();
+        bar_lds();
         if (tw) tr[6] = wall_clock64();
         /* ---- 7: cross-XCD hop: rank rk of every XCD trades its 45 weighted down values ---- */
-        /* meanwhile the next layer's RMSNorm weight and gate/up blocks are issued */
-        /* both paths assign the registers (empty loads past the last layer),
-         * so this layer's blocks are free once they are used */
+        /* meanwhile each compute wave moves the next layer's gate blocks (its
+         * segments landed during q8(hidden) and the down dots) into
+         * registers, then copies the next layer's up segments into the same
+         * region and loads the next RMSNorm weight; both paths assign the
+         * registers (empty loads past the last layer) */
         if (cl < 0) {
-            for (int z = 0; z < wave; z++) __builtin_amdgcn_s_sleep(PREFETCH_STAGGER);
-            load_nw(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
-            load_up(lys[l + 1 < L ? l + 1 : l], l + 1 < L);
+            const bool more = l + 1 < L;
+            wait_copies();
+#pragma unroll
+            for (int i = 0; i < CPW; i++)
+#pragma unroll
+                for (int gr = 0; gr < NG; gr++) wa[i][gr] = seg_blk(gr, i);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   /* read before the copy overwrites */
+            fetch_seg(more ? lys[l + 1].up[xe] : nullptr, more);
+            load_nw(lys[more ? l + 1 : l], more);
         } else {
-            zero_up();
+            const u32x4 z = {0u, 0u, 0u, 0u};
+            nw0 = nw1 = z;
+            zero_units(0);
         }
         if (cl >= 0) {
             if (clv < RS) {
                 const int gi = clv >> 4, ri = clv & 15;
                 float v = 0.f;
 #pragma unroll
-                for (int w = 0; w < NW; w++) v += red[w][gi][0][ri] + red[w][gi][1][ri];
+                for (int k = 0; k < NW / 2; k++) {
+                    const float4 a = reinterpret_cast<const float4 *>(&red[gi][ri][0][0])[k];
+                    v += a.x + a.y;
+                    v += a.z + a.w;
+                }
                 pp[xc][clv] = ly.w[xe] * (v + dbv);
             }
             __builtin_amdgcn_wave_barrier();
@@ -669,9 +684,9 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             }
             if (!ok) lds_fail = 1;
         }
-        __syncthreads();
+        bar_lds();
         if (lds_fail) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* no copy into LDS outlives the workgroup */
+            wait_copies();   /* no copy into LDS outlives the workgroup */
             return;
         }
         if (tw) tr[7] = wall_clock64();

@@ -44,6 +44,7 @@ __device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsig
     for (int i = 0; i < MAXP; i++)
         if (cl + CL * i < total) pending |= 1u << i;
     unsigned spins = 0;
+    bool ok = true;
     while (pending) {
         u32x4 v[MAXP];
 #pragma unroll
@@ -57,18 +58,93 @@ __device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsig
                 pending &= ~(1u << i);
             }
         if (!pending) break;
-        if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
-            return false;
+        if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+            ok = false;
+            break;
+        }
         if (rounds) *rounds = spins;
         if (spins > SPIN_LIMIT) {
             __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            return false;
+            ok = false;
+            break;
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    return true;
+    /* Every load the loop issued has returned (each round waits for its
+     * own), but the compiler cannot prove it for the loads of rounds a lane
+     * skipped, and would otherwise wait for them (vmcnt(0), which also waits
+     * for every untracked copy issued later) before it reuses their
+     * registers.  A wait it can see, on the one exit, ends that; it costs
+     * nothing here. */
+    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0), expcnt and lgkmcnt unchanged */
+    return ok;
 }
 
+
+/* ---- weight streams into LDS (persistent kernels) ----
+ *
+ * One 1 KiB direct-to-LDS copy: lane l moves the 16 bytes at byte offset
+ * voff (its own) of the buffer `desc` to LDS address lds + 16 l (lds is
+ * wave-uniform).  Issued from inline assembly, so the compiler does not
+ * track it: it would otherwise make LDS reads of other arrays wait for the
+ * copies still in flight (it cannot tell the arrays apart), which is the
+ * overlap these kernels need.  The waves that issue copies wait for them
+ * themselves (wait_copies) before the barrier that opens the phase reading
+ * them.  Vector-memory waits the compiler emits for its own loads stay
+ * correct: the counter completes in order, so untracked operations only
+ * make those waits stricter. */
+__device__ inline u32x4 buf_desc(const void *p, uint32_t nbytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)p;
+    u32x4 d;
+    d.x = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    d.y = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(a >> 32)) & 0xFFFFu;
+    d.z = (uint32_t)__builtin_amdgcn_readfirstlane((int)nbytes);
+    d.w = 0x00020000u;
+    return d;
+}
+__device__ inline uint32_t lds_addr(const void *p) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane(
+        (int)(uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void *)p);
+}
+/* M0 holds the copy's LDS address.  M0 is a reserved register the compiler
+ * does not let inline assembly clobber; the kernels that use these copies
+ * set M0 nowhere else (their generated code has no other M0 write). */
+__device__ inline void copy_lanes(const u32x4 &desc, uint32_t voff, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(desc)
+                 : "memory");
+}
+/* the 1 KiB at byte offset off: lane l copies bytes off + 16 l .. + 15 */
+__device__ inline void copy_1k(const u32x4 &desc, uint32_t off, uint32_t lds, int lane) {
+    copy_lanes(desc, off + 16u * (uint32_t)lane, lds);
+}
+
+/* A wait the compiler sees (the intrinsic, not inline assembly), so its
+ * own bookkeeping of outstanding loads is cleared too: otherwise it keeps
+ * loads of paths a wave never takes as pending and later waits for them,
+ * with vmcnt(0), in the middle of a phase whose copies should stay in
+ * flight.  It keeps such a wait as written. */
+__device__ inline void wait_copies() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0); expcnt and lgkmcnt unchanged */
+    asm volatile("" ::: "memory");
+}
+/* wait until at most N of the wave's vector memory operations are in flight */
+template <int N>
+__device__ inline void wait_copies_but() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+/* Workgroup barrier for the layer loops: waits for the wave's LDS accesses
+ * (lgkmcnt) and meets the other waves; the memory clobber keeps the
+ * compiler from moving accesses across it.  __syncthreads() (and a release
+ * fence on LDS alone) would also wait for the wave's outstanding
+ * direct-to-LDS copies (they count as vector memory operations), which must
+ * stay in flight across the phases they overlap.  A wave whose copies a
+ * phase reads waits for them itself (wait_copies) before the barrier that
+ * opens that phase; nothing a workgroup stores to global memory inside a
+ * layer is read back by that workgroup. */
+__device__ inline void bar_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 }  // namespace tg
 #endif
