@@ -271,17 +271,17 @@ typedef struct tg_hip_decode tg_hip_decode;
 tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers,
                                     const float *const *norm_w_dev, float eps, float *h_dev,
                                     int mode);
-/* 0 ok; 1 if a persistent step's exchange wait timed out; 2 (Qwen3 step) if a
- * launch split a class of workgroups g % 8 over several XCDs, which its
- * intra-XCD exchanges assume they share -- the step then stores every slot
+/* 0 ok; 1 if a persistent step's exchange wait timed out; 2 if a launch split
+ * a class of workgroups g % 8 over several XCDs, which its intra-XCD
+ * exchanges assume they share -- the step then stores every slot
  * device-coherently from the next launch on */
 int tg_hip_decode_status(tg_hip_decode *step);
-/* Qwen3 persistent step: exchange-slot policy 0 (intra-XCD slots stay in the
+/* Persistent steps: exchange-slot policy 0 (intra-XCD slots stay in the
  * writer's L2; the default) or 1 (every slot device-coherent, correct under
  * any placement; same bits).  Returns the previous policy, -1 otherwise. */
 int tg_hip_decode_set_policy(tg_hip_decode *step, int policy);
-/* Qwen3 persistent step: HW_REG_XCC_ID of each of its 256 workgroups in the
- * last launch into out[256]; returns the count written (0 if none). */
+/* Persistent steps: HW_REG_XCC_ID of each of its 256 workgroups in the last
+ * launch into out[256]; returns the count written (0 if none). */
 int tg_hip_decode_placement(tg_hip_decode *step, unsigned *out);
 /* Stage-wise parity probe of the persistent step: while set, each layer
  * writes a record of tg_hip_decode_record_bytes(step) bytes into

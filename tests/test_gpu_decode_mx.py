@@ -97,7 +97,7 @@ class MxLayers:
             self.plans.append(plan)
         lib.tg_hip_synchronize()
 
-    def run(self, mode, h0, steps=1, debug=False):
+    def run(self, mode, h0, steps=1, debug=False, policy=None, place=None):
         lib = self.tg.lib()
         h = self.tg.DeviceArray(D * 4)
         h.upload(h0)
@@ -112,10 +112,14 @@ class MxLayers:
             assert rb == R_BYTES
             dbg = self.tg.DeviceArray(self.L * rb)
             lib.tg_hip_decode_set_debug(d, dbg.ptr)
+        if policy is not None:
+            assert lib.tg_hip_decode_set_policy(d, policy) == 0
         for _ in range(steps):
             lib.tg_hip_decode_run(d, None)
         lib.tg_hip_synchronize()
         status = lib.tg_hip_decode_status(d)
+        if place is not None:
+            assert lib.tg_hip_decode_placement(d, place.ctypes.data) == 256
         lib.tg_hip_decode_destroy(d)
         out = h.download(np.float32, D)
         h.free()
@@ -222,3 +226,23 @@ def test_decode_mx_repeatable(tg, gptoss):
     b, s2, _ = gptoss.run(2, h0, steps=3)
     assert s1 == 0 and s2 == 0
     assert a.tobytes() == b.tobytes()
+
+
+def test_decode_mx_placement_recorded_and_coherent_policy(tg, gptoss):
+    """Every launch records each workgroup's HW_REG_XCC_ID; the h gather's
+    slots stay in the writer's L2 under the default policy, which needs the
+    workgroups g of each class g % 8 on one XCD -- the status check verifies
+    it (cooperative and plain launches).  Policy 1 stores every slot
+    device-coherently and gives the same bits."""
+    say("gpt-oss placement and slot policies")
+    h0 = np.random.default_rng(8).standard_normal(D).astype(np.float32)
+    for mode in (2, 3):
+        place = np.zeros(256, np.uint32)
+        a, s0, _ = gptoss.run(mode, h0, steps=2, place=place)
+        say(f"  mode {mode}: XCC_ID of workgroups 0..15: {list(place[:16] & 0xF)}")
+        assert s0 == 0, "placement check or exchange wait failed"
+        grp = place.reshape(32, 8)
+        assert np.all(grp == grp[0]), "a class g % 8 spans several XCDs"
+        b, s1, _ = gptoss.run(mode, h0, steps=2, policy=1)
+        assert s1 == 0
+        assert a.tobytes() == b.tobytes()

@@ -1480,7 +1480,7 @@ struct tg_hip_decode {
     uint64_t *times = nullptr;
     uint8_t *qdown = nullptr;    /* Qwen3 kernel: the layers' down matrices in the row-group layout */
     unsigned *place = nullptr;   /* Qwen3 kernel: HW_REG_XCC_ID of each workgroup, last launch */
-    int pol = 0;                 /* Qwen3 kernel: 1 = every exchange slot stored device-coherently */
+    int pol = 0;                 /* persistent kernels: 1 = every exchange slot stored device-coherently */
     int placement_bad = 0;       /* a launch ran with workgroup g off XCD g % 8 */
 };
 
@@ -1638,6 +1638,8 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
             return nullptr;
         }
         d->grid = DECODE_GRID;
+        HIPCHECK(hipMalloc(&d->place, DECODE_GRID * sizeof(unsigned)));
+        HIPCHECK(hipMemset(d->place, 0xFF, DECODE_GRID * sizeof(unsigned)));
         if (d->kind == 1) {
             HIPCHECK(hipMalloc(&d->layers_mx, lm.size() * sizeof(DecodeLayerMx)));
             HIPCHECK(hipMemcpy(d->layers_mx, lm.data(), lm.size() * sizeof(DecodeLayerMx), hipMemcpyHostToDevice));
@@ -1655,8 +1657,6 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
                 }
             HIPCHECK(hipMalloc(&d->layers, ls.size() * sizeof(DecodeLayer)));
             HIPCHECK(hipMemcpy(d->layers, ls.data(), ls.size() * sizeof(DecodeLayer), hipMemcpyHostToDevice));
-            HIPCHECK(hipMalloc(&d->place, DECODE_GRID * sizeof(unsigned)));
-            HIPCHECK(hipMemset(d->place, 0xFF, DECODE_GRID * sizeof(unsigned)));
             HIPCHECK(hipStreamSynchronize(g.st));
         }
         const size_t sb = d->kind == 1 ? decode_mx_slot_bytes() : decode_qwen_slot_bytes(d->grid);
@@ -1684,7 +1684,7 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
     hipStream_t st = stream ? (hipStream_t)stream : g.st;
     if (d->mode >= 2 && d->kind == 1) {
         HIPCHECK(launch_decode_mx(d->layers_mx, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
-                                  d->mode == 2, st));
+                                  d->place, d->pol, d->mode == 2, st));
         d->base += 2u * (unsigned)d->L;
     } else if (d->mode >= 2) {
         HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
@@ -1723,8 +1723,8 @@ TG_API void tg_hip_decode_set_timing(tg_hip_decode *d, void *times_dev) {
     if (d) d->times = (uint64_t *)times_dev;
 }
 
-/* Qwen3 step: true if, in the last launch, the workgroups g of each class
- * g % 8 all ran on one XCD -- what its intra-XCD exchanges need under
+/* Persistent steps: true if, in the last launch, the workgroups g of each
+ * class g % 8 all ran on one XCD -- what their intra-XCD exchanges need under
  * policy 0 (which XCD a class gets, and whether two classes share one, only
  * affects speed: a plain launch may start the round robin on another XCD). */
 static bool placement_ok(tg_hip_decode *d) {
@@ -1737,8 +1737,8 @@ static bool placement_ok(tg_hip_decode *d) {
 }
 
 /* 0 if every persistent step so far completed its exchange waits; 1 if a
- * wait timed out (the results of that step are invalid).  For the Qwen3
- * step, 2 if a launch split a class of workgroups g % 8 over several XCDs,
+ * wait timed out (the results of that step are invalid).  2 if a launch
+ * split a class of workgroups g % 8 over several XCDs,
  * which its intra-XCD exchanges do not allow under policy 0: the step then
  * switches itself to storing every slot device-coherently
  * (tg_hip_decode_set_policy 1); the launches before the switch are suspect
@@ -1757,21 +1757,21 @@ TG_API int tg_hip_decode_status(tg_hip_decode *d) {
     return d->placement_bad ? 2 : 0;
 }
 
-/* Exchange-slot policy of the Qwen3 persistent step: 0 keeps slots read only
+/* Exchange-slot policy of the persistent steps: 0 keeps slots read only
  * inside one XCD in that XCD's L2 (needs workgroup g on XCD g % 8; the
  * default), 1 stores every slot device-coherently (correct under any
  * placement, slower).  Both give the same bits.  Returns the previous
- * policy, or -1 for a step that is not the Qwen3 persistent kernel. */
+ * policy, or -1 for a step that is not a persistent kernel. */
 TG_API int tg_hip_decode_set_policy(tg_hip_decode *d, int pol) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (!d || d->mode < 2 || d->kind != 0) return -1;
+    if (!d || d->mode < 2) return -1;
     const int prev = d->pol;
     d->pol = pol ? 1 : 0;
     return prev;
 }
 
-/* HW_REG_XCC_ID of each of the Qwen3 persistent step's 256 workgroups in
- * its last launch (out[256]); returns the number written (0 if none). */
+/* HW_REG_XCC_ID of each of the persistent step's 256 workgroups in its last
+ * launch (out[256]); returns the number written (0 if none). */
 TG_API int tg_hip_decode_placement(tg_hip_decode *d, unsigned *out) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!d || !d->place || !out) return 0;

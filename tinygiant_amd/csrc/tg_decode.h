@@ -62,8 +62,8 @@ struct DecodeDebugMx {
 int decode_mx_max_grid();
 size_t decode_mx_slot_bytes();
 hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
-                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, bool cooperative,
-                            hipStream_t st);
+                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev,
+                            int pol, bool cooperative, hipStream_t st);
 
 /* Shape the persistent kernel is built for; the host checks a step against it. */
 struct DecodeShape {

@@ -118,6 +118,7 @@ constexpr int N_INS = D * 4 / 1024;   /* RMSNorm weight: 8 */
  * A and B are done before the next h gather ends. */
 constexpr int G_SPLIT = TG_DECODE_G_SPLIT;
 constexpr bool B_AT_DOWN = TG_DECODE_B_AT_DOWN != 0;
+
 static_assert(NE == NX, "one expert per XCD");
 static_assert(NR * RA == I && NR * RB == D && RA % VPS == 0, "row split");
 static_assert(2 * RA * NBD == NW * 64, "gate/up: one Q4_K block per compute lane");
@@ -470,30 +471,34 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
 #pragma unroll
             for (int i = 0; i < NR; i++) tot += ssq[i];
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
-            const u32x4 hv = reinterpret_cast<const u32x4 *>(hx)[threadIdx.x];
-            u32x4 wv;
-            if (has_nw) {
-                wv = reinterpret_cast<const u32x4 *>(nws)[threadIdx.x];
-            } else {
-                wv.x = wv.y = wv.z = wv.w = __float_as_uint(1.f);
-            }
-            const float v0 = (__uint_as_float(hv.x) * scale) * __uint_as_float(wv.x);
-            const float v1 = (__uint_as_float(hv.y) * scale) * __uint_as_float(wv.y);
-            const float v2 = (__uint_as_float(hv.z) * scale) * __uint_as_float(wv.z);
-            const float v3 = (__uint_as_float(hv.w) * scale) * __uint_as_float(wv.w);
-            const uint32_t q = q8_block_wave(v0, v1, v2, v3, lane, &sx.d[wave], &sx.s32[wave * 8], nullptr);
-            reinterpret_cast<uint32_t *>(sx.qs + wave * XST)[lane] = q;
-            if (dbg && wg == 0) {
-                uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
-                reinterpret_cast<u32x4 *>(rec + DecodeDebug::HIN)[threadIdx.x] = hv;
-                u32x4 xv;
-                xv.x = __float_as_uint(v0);
-                xv.y = __float_as_uint(v1);
-                xv.z = __float_as_uint(v2);
-                xv.w = __float_as_uint(v3);
-                reinterpret_cast<u32x4 *>(rec + DecodeDebug::X)[threadIdx.x] = xv;
-                reinterpret_cast<uint32_t *>(rec + DecodeDebug::XQ)[threadIdx.x] = q;
-            }
+            auto norm_block = [&](int b) {
+                const int t = 64 * b + lane;   /* values 4 t .. 4 t + 3 */
+                const u32x4 hv = reinterpret_cast<const u32x4 *>(hx)[t];
+                u32x4 wv;
+                if (has_nw) {
+                    wv = reinterpret_cast<const u32x4 *>(nws)[t];
+                } else {
+                    wv.x = wv.y = wv.z = wv.w = __float_as_uint(1.f);
+                }
+                const float v0 = (__uint_as_float(hv.x) * scale) * __uint_as_float(wv.x);
+                const float v1 = (__uint_as_float(hv.y) * scale) * __uint_as_float(wv.y);
+                const float v2 = (__uint_as_float(hv.z) * scale) * __uint_as_float(wv.z);
+                const float v3 = (__uint_as_float(hv.w) * scale) * __uint_as_float(wv.w);
+                const uint32_t q = q8_block_wave(v0, v1, v2, v3, lane, &sx.d[b], &sx.s32[b * 8], nullptr);
+                reinterpret_cast<uint32_t *>(sx.qs + b * XST)[lane] = q;
+                if (dbg && wg == 0) {
+                    uint8_t *rec = dbg + (size_t)l * DecodeDebug::BYTES;
+                    reinterpret_cast<u32x4 *>(rec + DecodeDebug::HIN)[t] = hv;
+                    u32x4 xv;
+                    xv.x = __float_as_uint(v0);
+                    xv.y = __float_as_uint(v1);
+                    xv.z = __float_as_uint(v2);
+                    xv.w = __float_as_uint(v3);
+                    reinterpret_cast<u32x4 *>(rec + DecodeDebug::X)[t] = xv;
+                    reinterpret_cast<uint32_t *>(rec + DecodeDebug::XQ)[t] = q;
+                }
+            };
+            norm_block(wave);
         }
         bar_lds();
         if (tw) tr[2] = wall_clock64();

@@ -219,7 +219,7 @@ __device__ inline void mma_chunk(const MxBlk &a, const v8i &bx, int sb, float d,
  * something the writer waited for in between. */
 __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restrict__ layers, int L, float *h,
                                                   u32x4 *slots, unsigned *abort_flag, unsigned base, float eps,
-                                                  uint8_t *dbg, uint64_t *times) {
+                                                  uint8_t *dbg, uint64_t *times, unsigned *place, int pol) {
     __shared__ __attribute__((aligned(16))) float hx[D];      /* this layer's h */
     __shared__ __attribute__((aligned(16))) float nws[D];     /* this layer's RMSNorm weight */
     __shared__ __attribute__((aligned(16))) float hid[D];     /* the expert's hidden vector */
@@ -237,7 +237,12 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid when >= 0 */
     const int ct = (int)threadIdx.x;             /* compute lane, valid when < NW * 64 */
-    if (threadIdx.x == 0) lds_fail = 0;
+    if (threadIdx.x == 0) {
+        lds_fail = 0;
+        unsigned x;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+        if (place) place[blockIdx.x] = x;
+    }
     const int wg = blockIdx.x;
     const int xc = wg % NX, rk = wg / NX;        /* XCD and rank in it */
     const int xe = xc >> 1, R = NR * (xc & 1) + rk;   /* expert slot and rank in the expert */
@@ -273,10 +278,10 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
      * copy drains during RMSNorm and gate/up, not ahead of the hidden
      * exchange's polls, and takes no registers. */
     const uint32_t dsh = (uint32_t)(RS * R * RB) & 15u;
-    auto fetch_down = [&](const DecodeLayerMx &ly) {
+    auto fetch_down = [&](const DecodeLayerMx &ly) {   /* the communication waves */
         const u32x4 desc = buf_desc(ly.down[xe], (uint32_t)D * RB);
         const uint32_t a0 = (uint32_t)(RS * R * RB) - dsh;
-        for (int k = wave; k < NDMA; k += NW) copy_1k(desc, a0 + 1024u * (uint32_t)k, lds_addr(dws + 1024 * k), lane);
+        for (int k = wave - NW; k < NDMA; k += NC) copy_1k(desc, a0 + 1024u * (uint32_t)k, lds_addr(dws + 1024 * k), lane);
     };
     /* One MXFP4 block from dws at byte offset off: the e8m0 byte there and
      * the 16 code bytes after it, from the five aligned dwords that start
@@ -333,21 +338,48 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     };
     /* q8 + fp8 halves of a D-value LDS vector (scaled by `scale` and the
      * RMSNorm weight when norm): wave w quantizes blocks w and w + 8 */
-    auto quantize = [&](const float *src, bool norm, float scale, bool has_nw, LdsQ &q, float *dbg_x,
+    /* blocks[phase][wave][k]: the q8 blocks each wave quantizes, -1 = none.
+     * Phase 0 (q8 of x): the communication waves issue the down rows' copies
+     * meanwhile, so the six compute waves take all twelve blocks, three per
+     * SIMD (waves w and w + 4 share SIMD w % 4).  Phase 1 (q8 of the hidden
+     * vector): every wave, blocks w and w + 8. */
+    auto qblock = [&](int phase, int k) -> int {
+        if (phase == 0) {
+            switch (wave) {
+                case 0: return k == 0 ? 0 : k == 1 ? 6 : -1;
+                case 1: return k == 0 ? 1 : k == 1 ? 7 : -1;
+                case 2: return k == 0 ? 2 : k == 1 ? 8 : 10;
+                case 3: return k == 0 ? 3 : k == 1 ? 9 : 11;
+                case 4: return k == 0 ? 4 : -1;
+                case 5: return k == 0 ? 5 : -1;
+                default: return -1;
+            }
+        }
+        const int b = wave + NA * k;   /* waves 0-3: blocks w and w + 8; waves 4-7: block w */
+        return k < 2 && b < NQ ? b : -1;
+    };
+    static_assert(NQ == 12 && NW == 6 && NA == 8, "q8 block assignment");
+    auto quantize = [&](int phase, const float *src, bool norm, float scale, bool has_nw, LdsQ &q, float *dbg_x,
                         uint8_t *dbg_q, float *dbg_d) {
 #pragma unroll
-        for (int k = 0; k < 2; k++) {
-            const int b = wave + NA * k;
-            if (b >= NQ) break;   /* uniform */
+        for (int k = 0; k < 3; k++) {
+            const int b = qblock(phase, k);
+            if (b < 0) break;   /* uniform */
+            /* lane l: values 4l .. 4l + 3 of the block, all inside the row
+             * or all past it (D is a multiple of 4): one 16-byte LDS read of
+             * each operand, from a clamped address, then zeros past the row */
             const int i0 = 256 * b + 4 * lane;
-            float v[4];
+            const bool in = i0 < D;
+            float4 h4 = *reinterpret_cast<const float4 *>(src + (in ? i0 : 0));
+            float4 w4 = *reinterpret_cast<const float4 *>(nws + (in ? i0 : 0));
+            if (!in) h4 = float4{0.f, 0.f, 0.f, 0.f};
+            if (!(norm && has_nw && in)) w4 = float4{1.f, 1.f, 1.f, 1.f};
+            float v[4] = {h4.x, h4.y, h4.z, h4.w};
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
             for (int c = 0; c < 4; c++) {
-                const int i = i0 + c;
-                float t = i < D ? src[i] : 0.f;
-                if (norm) t = (t * scale) * (has_nw && i < D ? nws[i] : 1.f);
-                v[c] = t;
-                if (dbg_x && i < D) dbg_x[i] = t;
+                if (norm) v[c] = (v[c] * scale) * wv[c];
+                if (dbg_x && in) dbg_x[i0 + c] = v[c];
             }
             q8_split_block(v[0], v[1], v[2], v[3], lane, b, q, reinterpret_cast<uint32_t *>(dbg_q), dbg_d);
         }
@@ -470,7 +502,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         }
         if (tw) tr[1] = wall_clock64();
         /* ---- 2: RMSNorm (weight or 1) + q8 + fp8 halves of x ---- */
-        if (cl < 0) fetch_down(ly);
+        if (cl >= 0) fetch_down(ly);
         if (tw) tr[20] = wall_clock64();
         {
             const float tot = wave_sum(ssq[lane]);   /* the 64 slice sums, one per lane */
@@ -478,7 +510,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             if (rec && wg == 0)
                 for (int t = threadIdx.x; t < D; t += NT) reinterpret_cast<float *>(rec + DecodeDebugMx::HIN)[t] = hx[t];
             const bool rx = rec && wg == 0;
-            quantize(hx, true, scale, has_nw, sx, rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::X) : nullptr,
+            quantize(0, hx, true, scale, has_nw, sx, rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::X) : nullptr,
                      rx ? rec + DecodeDebugMx::XQ : nullptr,
                      rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::XD) : nullptr);
         }
@@ -506,27 +538,31 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                 for (int u = 0; u < 2 * NG; u++)
 #pragma unroll
                     for (int v = 0; v < 4; v++) red[u][4 * (lane >> 4) + v][wave][lane & 15] = acc[u][v];
-            /* the down rows' copy has landed in dws before the barrier */
-            wait_copies();
         }
+        /* the down rows' copy (issued by the communication waves) has landed
+         * in dws before the barrier */
+        wait_copies();
         bar_lds();
         if (tw) tr[3] = wall_clock64();
         /* ---- 4: bias + activation, all-gather the expert's hidden vector ---- */
         /* meanwhile the compute waves gather their down blocks from dws into
          * registers; the communication waves zero theirs (both paths assign,
          * so no old value stays live) */
-        if (cl < 0) {
+        auto gather_down = [&]() {
+            if (cl < 0) {
 #pragma unroll
-            for (int i = 0; i < CPW; i++)
+                for (int i = 0; i < CPW; i++)
 #pragma unroll
-                for (int u = 0; u < NG; u++) wb[i][u] = lds_blk(u, i);
-        } else {
-            const u32x4 z = {0u, 0u, 0u, 0u};
+                    for (int u = 0; u < NG; u++) wb[i][u] = lds_blk(u, i);
+            } else {
+                const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
-            for (int i = 0; i < CPW; i++)
+                for (int i = 0; i < CPW; i++)
 #pragma unroll
-                for (int u = 0; u < NG; u++) wb[i][u] = MxBlk{0u, z};
-        }
+                    for (int u = 0; u < NG; u++) wb[i][u] = MxBlk{0u, z};
+            }
+        };
+        gather_down();
         if (cl >= 0) {
             /* row i of the slice: the six waves' partial sums in wave order */
             if (clv < RS) {
@@ -595,7 +631,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         if (cl < 0 && l + 1 < L) fetch_seg(lys[l + 1].gate[xe], true);
         {
             const bool rh = rec && (xc & 1) == 0 && rk == 0;
-            quantize(hid, false, 1.f, false, sh, nullptr, rh ? rec + DecodeDebugMx::HQ + xe * (NQ * 256) : nullptr,
+            quantize(1, hid, false, 1.f, false, sh, nullptr, rh ? rec + DecodeDebugMx::HQ + xe * (NQ * 256) : nullptr,
                      rh ? reinterpret_cast<float *>(rec + DecodeDebugMx::HD) + xe * NQ : nullptr);
         }
         bar_lds();
@@ -708,12 +744,17 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             __builtin_amdgcn_wave_barrier();
             if (l + 1 < L && ri <= SS) {
                 const uint32_t slot = HSL + (par * NWG + (uint32_t)wg) * HS + (uint32_t)((SS + 1) * half + ri);
+                /* read only inside this XCD: kept in its L2 (policy 0), or
+                 * stored device-coherently like every other slot (policy 1) */
+                float a0 = sq, a1 = 0.f, a2 = 0.f;   /* the slot after the slice: its sum of h^2 */
                 if (ri < SS) {
                     const float *o = hx + RS * s + VPS * ri;
-                    put_slot<CPOL_PLAIN>(sl, slot, tag, o[0], o[1], o[2]);
-                } else {
-                    put_slot<CPOL_PLAIN>(sl, slot, tag, sq, 0.f, 0.f);
+                    a0 = o[0];
+                    a1 = o[1];
+                    a2 = o[2];
                 }
+                if (pol) put_slot<CPOL_SC1>(sl, slot, tag, a0, a1, a2);
+                else put_slot<CPOL_PLAIN>(sl, slot, tag, a0, a1, a2);
             }
             if (tc) tr[11] = wall_clock64();
         }
@@ -733,10 +774,11 @@ int decode_mx_max_grid() {
 size_t decode_mx_slot_bytes() { return (size_t)NSLOTS * 16; }
 
 hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
-                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, bool cooperative,
-                            hipStream_t st) {
-    void *args[] = {(void *)&layers_dev, (void *)&L, (void *)&h_dev, (void *)&slots_dev, (void *)&abort_dev,
-                    (void *)&base, (void *)&eps, (void *)&debug_dev, (void *)&times_dev};
+                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev,
+                            int pol, bool cooperative, hipStream_t st) {
+    void *args[] = {(void *)&layers_dev, (void *)&L,         (void *)&h_dev,     (void *)&slots_dev,
+                    (void *)&abort_dev,  (void *)&base,      (void *)&eps,       (void *)&debug_dev,
+                    (void *)&times_dev,  (void *)&place_dev, (void *)&pol};
     if (cooperative)
         return hipLaunchCooperativeKernel((const void *)k_decode_mx, dim3(DECODE_GRID), dim3(NT), args, 0, st);
     return hipLaunchKernel((const void *)k_decode_mx, dim3(DECODE_GRID), dim3(NT), args, 0, st);
