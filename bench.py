@@ -747,11 +747,17 @@ def loader_probe(tg, n_layers=2):
         shutil.rmtree(d, ignore_errors=True)
 
 
-def source_sha256(rel):
-    """sha256 of a kernel source file of this tree (profiles are stamped with
-    the hash of the source they measured)."""
+def source_sha256(rels):
+    """sha256 over the kernel source files of this tree named in `rels`
+    (space separated: the kernel's file and the headers it includes; each
+    file contributes its path, a NUL and its bytes).  Profiles are stamped
+    with the hash of the sources they measured."""
     import hashlib
-    return hashlib.sha256((ROOT / rel).read_bytes()).hexdigest()
+    h = hashlib.sha256()
+    for rel in rels.split():
+        h.update(rel.encode() + b"\0")
+        h.update((ROOT / rel).read_bytes())
+    return h.hexdigest()
 
 
 def read_traffic(name):
@@ -768,7 +774,7 @@ def read_traffic(name):
             k, v = line.split(":", 1)
             fields[k.strip()] = v.strip()
     src, sha = fields.get("source"), fields.get("source_sha256")
-    if not src or not sha or not (ROOT / src).exists() or source_sha256(src) != sha:
+    if not src or not sha or not all((ROOT / r).exists() for r in src.split()) or source_sha256(src) != sha:
         log(f"profiles/{name}: measured on another version of its kernel source; traffic not reported")
         return None
     t = fields.get("traffic_bytes_per_launch")
