@@ -248,6 +248,17 @@ def test_moe_mixed_down_formats(tg, orc):
     _check_moe(tg, orc, n, k, 2048, 768, O.FMT_Q4K, fmts, O.ACT_SILU, False, rw, x)
 
 
+def test_moe_wide_rows_fall_back(tg, orc):
+    """Rows too wide for the expert-major phases' LDS staging (8 q8 rows of
+    16384 values: 178 KiB against the device's 160 KiB) take the per-pair
+    kernels instead of failing the launch."""
+    say("moe wide rows")
+    n, k, D, I = 2, 8, 16384, 256
+    rw = np.full((n, k), 0.5, np.float32)
+    x = (RNG.standard_normal((k, D)) * 0.1).astype(np.float32)
+    _check_moe(tg, orc, n, k, D, I, O.FMT_Q4K, [O.FMT_Q6K] * n, O.ACT_SILU, False, rw, x)
+
+
 def test_moe_f16_down(tg, orc):
     say("moe f16 down")
     n, k, D, I = 2, 2, 512, 256

@@ -839,8 +839,22 @@ int expert_major() { return g_expert_major; }
 
 /* the expert-major phases hold all T items of a row in registers and read
  * Q4_K / Q6_K / MXFP4 q8 items from LDS */
-static bool expert_major_ok(const MoeArgs &a, int fmt, int T) {
-    return (g_expert_major & EM_ON) && a.n_act_a > 0 && T <= 4 &&
+/* the expert-major phases stage up to MOE_X_MAXP q8 rows of nb blocks in
+ * dynamic LDS; wider rows than the device allows fall back to the per-pair
+ * kernels */
+static size_t device_max_lds() {
+    static int max_lds = -1;
+    if (max_lds < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            max_lds = 0;
+    }
+    return (size_t)max_lds;
+}
+static bool expert_major_ok(const MoeArgs &a, int fmt, int T, int nb) {
+    const size_t lds = (size_t)std::min(a.max_rows, MOE_X_MAXP) * q8_lds_stride(nb);
+    return (g_expert_major & EM_ON) && a.n_act_a > 0 && T <= 4 && lds <= device_max_lds() &&
            (fmt == TG_FMT_Q4K || fmt == TG_FMT_Q6K || fmt == TG_FMT_MXFP4);
 }
 /* Quantizing inside the phases repeats each row's q8 in every workgroup of
@@ -900,20 +914,21 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
     int Ta;
     pick_S(items_per_row(a.gate_fmt, a.D), &Ta);
     /* expert-major phase A quantizes device-resident input rows itself */
-    const bool ax = !mx_a && expert_major_ok(a, a.gate_fmt, Ta);
+    const bool ax = !mx_a && expert_major_ok(a, a.gate_fmt, Ta, a.xq.nb);
     const bool few = a.max_rows <= FUSE_MAX_ROWS || (g_expert_major & EM_FUSE_ANY);
     const bool q8_fused = (g_expert_major & EM_FUSE_Q8) && few;
     const bool any = g_expert_major & EM_FUSE_ANY;
     const bool qx_fused = quantize_x && ax && !a.xin_remote && q8_fused && (a.xq.nb <= FUSE_MAX_BLOCKS || any);
-    /* expert-major phase B (every down format Q4_K / Q6_K) quantizes the
-     * hidden rows itself and, given tile counters, also combines */
+    /* expert-major phase B (every down format present Q4_K, Q6_K or MXFP4,
+     * with one item count per row) quantizes the hidden rows itself when the
+     * experts hold few pairs and, given tile counters, also combines */
     int Tb = 0, Sb = 64;
     bool bx = n_down_fmts > 0;
     if (bx) Sb = pick_S(items_per_row(down_fmts_present[0], a.I), &Tb);
     for (int i = 0; i < n_down_fmts; i++) {
         const int f = down_fmts_present[i];
         /* one grid (and one set of row tiles) for every format present */
-        bx = bx && expert_major_ok(a, f, Tb) && items_per_row(f, a.I) == items_per_row(down_fmts_present[0], a.I) &&
+        bx = bx && expert_major_ok(a, f, Tb, a.hq.nb) && items_per_row(f, a.I) == items_per_row(down_fmts_present[0], a.I) &&
              !(mx_grouped && f == TG_FMT_MXFP4 && a.hp);
     }
     const int tiles_b = ((a.D + 64 / Sb - 1) / (64 / Sb) + 3) / 4;
