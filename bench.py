@@ -860,10 +860,11 @@ def main():
         log(f"phase breakdown (us per layer, first/last workgroup): {json.dumps(phases)}")
     launch_note = None
     if mode >= 2:
-        # the whole step is one kernel.  A cooperative launch adds a fixed
-        # runtime dispatch cost (about 18 us, the same for any kernel length);
-        # the kernel's own duration is timed over plain launches of the same
-        # step, which is also the command the committed kernel trace runs
+        # the whole step is one kernel.  Its cooperative dispatch (a graph
+        # node) adds a fixed runtime cost of a few us, the same for any
+        # kernel length; the kernel's own duration is timed over plain
+        # launches of the same step, which is also the command the committed
+        # kernel trace runs
         k_us = ms_step * 1e3
         if mode == 2:
             plain = lib.tg_hip_decode_create(ctypes.addressof(parr), layers, ctypes.addressof(narr),

@@ -264,9 +264,13 @@ size_t tg_hip_head_scratch_bytes(int k, int nrows, int ncols);
  *     optional biases, exactly 4 active experts per layer (MXFP4 dots on
  *     block-scaled MFMA: the reference's per-block integer sums, f32
  *     additions grouped differently);
+ * (mode 2 launches it as the one cooperative node of a HIP graph, rebuilt
+ * when a setter below changes its arguments);
  * 3 launches the same kernel with a plain launch (for tools that do not
  * follow cooperative launches; needs an otherwise idle device, and a step
- * whose workgroups are not all resident ends with status 1). */
+ * whose workgroups are not all resident ends with status 1).  The persistent
+ * kernels keep their launch epoch on the device, so a caller may capture a
+ * mode-3 tg_hip_decode_run into a graph of its own and replay it. */
 typedef struct tg_hip_decode tg_hip_decode;
 tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers,
                                     const float *const *norm_w_dev, float eps, float *h_dev,

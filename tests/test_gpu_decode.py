@@ -279,3 +279,95 @@ def test_decode_placement_recorded_and_coherent_policy(tg, qwen3):
         b, s1 = _run(tg, qwen3, mode, h0, steps=2, norm=True, policy=1)
         assert s1 == 0
         assert a.tobytes() == b.tobytes()
+
+
+def _hip_runtime():
+    """The HIP runtime the library itself loaded (its path from the process's
+    mappings), for the stream-capture calls of the test below."""
+    import tinygiant_amd._lib  # noqa: F401  (loads the library and its runtime)
+    with open("/proc/self/maps") as f:
+        paths = {ln.split()[-1] for ln in f if "libamdhip64" in ln}
+    assert paths, "HIP runtime not mapped"
+    hip = ctypes.CDLL(sorted(paths)[0])
+    VP = ctypes.c_void_p
+    for name, args in (("hipStreamCreate", [VP]), ("hipStreamDestroy", [VP]), ("hipStreamSynchronize", [VP]),
+                       ("hipStreamBeginCapture", [VP, ctypes.c_int]), ("hipStreamEndCapture", [VP, VP]),
+                       ("hipGraphInstantiate", [VP, VP, VP, VP, ctypes.c_size_t]), ("hipGraphLaunch", [VP, VP]),
+                       ("hipGraphExecDestroy", [VP]), ("hipGraphDestroy", [VP])):
+        fn = getattr(hip, name)
+        fn.argtypes, fn.restype = args, ctypes.c_int
+    return hip
+
+
+def test_decode_persistent_rebuilds_after_setters(tg, qwen3):
+    """Mode 2 launches the kernel as a cooperative graph node whose arguments
+    are fixed at build; the slot policy and debug setters mark it stale and
+    the next run rebuilds it.  The launch epoch (tag base of the exchange
+    slots) lives on the device, so four steps with rebuilds in between give
+    the bits of four plain launches."""
+    say("decode persistent graph node rebuilt by setters")
+    lib = tg.lib()
+    h0 = np.random.default_rng(8).standard_normal(D).astype(np.float32)
+    a, s0 = _run(tg, qwen3, 3, h0, steps=4, norm=True)
+    assert s0 == 0
+    h = tg.DeviceArray(D * 4)
+    h.upload(h0)
+    dbg = tg.DeviceArray(qwen3.L * lib.tg_hip_decode_debug_bytes())
+    d = qwen3.decode(h.ptr, 2, True)
+    try:
+        lib.tg_hip_decode_run(d, None)
+        assert lib.tg_hip_decode_set_policy(d, 1) == 0
+        lib.tg_hip_decode_run(d, None)
+        assert lib.tg_hip_decode_set_policy(d, 0) == 1
+        lib.tg_hip_decode_run(d, None)
+        lib.tg_hip_decode_set_debug(d, dbg.ptr)
+        lib.tg_hip_decode_run(d, None)
+        lib.tg_hip_synchronize()
+        assert lib.tg_hip_decode_status(d) == 0
+    finally:
+        lib.tg_hip_decode_destroy(d)
+    b = h.download(np.float32, D)
+    # the debug record of the last step holds that step's input h
+    hin3 = dbg.download(np.uint8, 4 * D).view(np.float32)
+    c, _ = _run(tg, qwen3, 3, h0, steps=3, norm=True)
+    h.free()
+    dbg.free()
+    assert a.tobytes() == b.tobytes()
+    assert hin3.tobytes() == c.tobytes()
+
+
+def test_decode_plain_step_replays_in_caller_graph(tg, qwen3):
+    """A caller may capture a mode-3 step (one plain launch) into a graph of
+    its own: nothing in the launch depends on host state that changes from
+    step to step.  Three replays, with downloads and status reads between
+    them, match one, two and three eager steps bit for bit."""
+    say("decode plain step captured in a caller graph")
+    lib = tg.lib()
+    hip = _hip_runtime()
+    h0 = np.random.default_rng(9).standard_normal(D).astype(np.float32)
+    refs = [_run(tg, qwen3, 3, h0, steps=n, norm=True)[0] for n in (1, 2, 3)]
+    h = tg.DeviceArray(D * 4)
+    h.upload(h0)
+    d = qwen3.decode(h.ptr, 3, True)
+    s, graph, exe = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(s)) == 0
+    try:
+        assert hip.hipStreamBeginCapture(s, 1) == 0          # thread-local capture
+        lib.tg_hip_decode_run(d, s)
+        assert hip.hipStreamEndCapture(s, ctypes.byref(graph)) == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, 0) == 0
+        for n in range(3):
+            assert hip.hipGraphLaunch(exe, s) == 0
+            assert hip.hipStreamSynchronize(s) == 0
+            assert lib.tg_hip_decode_status(d) == 0
+            got = h.download(np.float32, D)
+            say(f"  replay {n + 1}: max |diff| vs eager {np.abs(got - refs[n]).max():.1e}")
+            assert got.tobytes() == refs[n].tobytes(), n
+    finally:
+        lib.tg_hip_decode_destroy(d)
+        if exe.value:
+            hip.hipGraphExecDestroy(exe)
+        if graph.value:
+            hip.hipGraphDestroy(graph)
+        hip.hipStreamDestroy(s)
+        h.free()

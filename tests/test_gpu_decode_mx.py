@@ -246,3 +246,34 @@ def test_decode_mx_placement_recorded_and_coherent_policy(tg, gptoss):
         b, s1, _ = gptoss.run(mode, h0, steps=2, policy=1)
         assert s1 == 0
         assert a.tobytes() == b.tobytes()
+
+
+def test_decode_mx_graph_node_equals_plain_across_rebuilds(tg, gptoss):
+    """Mode 2 launches the kernel as a cooperative graph node; a policy change
+    rebuilds the node between steps, and the device-side launch epoch keeps
+    the slot tags advancing: three steps give the bits of three plain
+    launches."""
+    say("gpt-oss graph node across rebuilds vs plain launches")
+    lib = tg.lib()
+    h0 = np.random.default_rng(9).standard_normal(D).astype(np.float32)
+    a, s0, _ = gptoss.run(3, h0, steps=3)
+    assert s0 == 0
+    h = tg.DeviceArray(D * 4)
+    h.upload(h0)
+    arr = (ctypes.c_void_p * gptoss.L)(*gptoss.plans)
+    nw = (ctypes.c_void_p * gptoss.L)(*[x.ptr for x in gptoss.norm])
+    d = lib.tg_hip_decode_create(ctypes.addressof(arr), gptoss.L, ctypes.addressof(nw), ctypes.c_float(1e-5), h.ptr, 2)
+    assert d, tg.last_error()
+    try:
+        lib.tg_hip_decode_run(d, None)
+        assert lib.tg_hip_decode_set_policy(d, 1) == 0
+        lib.tg_hip_decode_run(d, None)
+        assert lib.tg_hip_decode_set_policy(d, 0) == 1
+        lib.tg_hip_decode_run(d, None)
+        lib.tg_hip_synchronize()
+        assert lib.tg_hip_decode_status(d) == 0
+    finally:
+        lib.tg_hip_decode_destroy(d)
+    b = h.download(np.float32, D)
+    h.free()
+    assert a.tobytes() == b.tobytes()

@@ -1473,9 +1473,14 @@ struct tg_hip_decode {
     DecodeLayer *layers = nullptr;
     DecodeLayerMx *layers_mx = nullptr;
     float *hidden = nullptr;
-    unsigned *sync = nullptr;
-    unsigned base = 0;
+    unsigned *sync = nullptr;    /* word 0: abort flag; word 1: the kernels' launch epoch */
     int grid = 0;
+    /* mode 2: the persistent kernel as one cooperative graph node (a graph
+     * launch costs ~6 us against ~19 us for a cooperative launch); its
+     * arguments are fixed, and a setter that changes one marks it stale */
+    hipGraph_t cgraph = nullptr;
+    hipGraphExec_t cexec = nullptr;
+    bool cstale = false;
     uint8_t *debug = nullptr;
     uint64_t *times = nullptr;
     uint8_t *qdown = nullptr;    /* Qwen3 kernel: the layers' down matrices in the row-group layout */
@@ -1575,6 +1580,57 @@ static void decode_enqueue(tg_hip_decode *d, hipStream_t st) {
     }
 }
 
+/* Mode 2: the persistent kernel as the one cooperative node of a graph,
+ * built from the step's current arguments (debug, timing and slot policy
+ * included; a setter that changes one marks the graph stale and the next run
+ * rebuilds it).  Where the runtime refuses the node, cexec stays null and the
+ * run falls back to hipLaunchCooperativeKernel. */
+static void coop_graph_drop(tg_hip_decode *d) {
+    if (d->cexec) HIPCHECK(hipDeviceSynchronize());   /* no launch of it may be pending */
+    if (d->cexec) HIPCHECK(hipGraphExecDestroy(d->cexec));
+    if (d->cgraph) HIPCHECK(hipGraphDestroy(d->cgraph));
+    d->cexec = nullptr;
+    d->cgraph = nullptr;
+}
+
+static void coop_graph_build(tg_hip_decode *d) {
+    coop_graph_drop(d);
+    d->cstale = false;
+    const void *layers = d->kind == 1 ? (const void *)d->layers_mx : (const void *)d->layers;
+    int L = d->L, pol = d->pol;
+    float *h = d->h;
+    void *slots = d->hidden;
+    unsigned *sync = d->sync, *place = d->place;
+    float eps = d->eps;
+    uint8_t *debug = d->debug;
+    uint64_t *times = d->times;
+    /* both kernels take (layers, L, h, slots, abort/epoch, eps, debug, times,
+     * place, pol); the node copies the values at creation */
+    void *args[] = {(void *)&layers, (void *)&L,     (void *)&h,     (void *)&slots, (void *)&sync,
+                    (void *)&eps,    (void *)&debug, (void *)&times, (void *)&place, (void *)&pol};
+    hipKernelNodeParams kp;
+    memset(&kp, 0, sizeof kp);
+    kp.func = (void *)(d->kind == 1 ? decode_mx_fn() : decode_qwen_fn());
+    kp.gridDim = dim3(d->grid);
+    kp.blockDim = dim3(d->kind == 1 ? decode_mx_threads() : decode_threads());
+    kp.sharedMemBytes = 0;
+    kp.kernelParams = args;
+    kp.extra = nullptr;
+    hipGraphNode_t node;
+    hipKernelNodeAttrValue v;
+    memset(&v, 0, sizeof v);
+    v.cooperative = 1;
+    if (hipGraphCreate(&d->cgraph, 0) != hipSuccess || hipGraphAddKernelNode(&node, d->cgraph, nullptr, 0, &kp) != hipSuccess ||
+        hipGraphKernelNodeSetAttribute(node, hipKernelNodeAttributeCooperative, &v) != hipSuccess ||
+        hipGraphInstantiate(&d->cexec, d->cgraph, nullptr, nullptr, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        if (d->cexec) (void)hipGraphExecDestroy(d->cexec);
+        if (d->cgraph) (void)hipGraphDestroy(d->cgraph);
+        d->cexec = nullptr;
+        d->cgraph = nullptr;
+    }
+}
+
 TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers, const float *const *norm_w_dev,
                                            float eps, float *h_dev, int use_graph) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
@@ -1664,6 +1720,7 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
         HIPCHECK(hipMemset(d->hidden, 0, sb));
         HIPCHECK(hipMalloc(&d->sync, 256));
         HIPCHECK(hipMemset(d->sync, 0, 256));
+        if (d->mode == 2) coop_graph_build(d);
         return d;
     }
     if (use_graph) {
@@ -1682,14 +1739,15 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!d) return;
     hipStream_t st = stream ? (hipStream_t)stream : g.st;
-    if (d->mode >= 2 && d->kind == 1) {
-        HIPCHECK(launch_decode_mx(d->layers_mx, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
-                                  d->place, d->pol, d->mode == 2, st));
-        d->base += 2u * (unsigned)d->L;
+    if (d->mode == 2 && d->cstale) coop_graph_build(d);
+    if (d->mode == 2 && d->cexec) {
+        HIPCHECK(hipGraphLaunch(d->cexec, st));
+    } else if (d->mode >= 2 && d->kind == 1) {
+        HIPCHECK(launch_decode_mx(d->layers_mx, d->L, d->h, d->hidden, d->sync, d->eps, d->debug, d->times, d->place,
+                                  d->pol, d->mode == 2, st));
     } else if (d->mode >= 2) {
-        HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->base, d->eps, d->debug, d->times,
-                                    d->place, d->pol, d->grid, d->mode == 2, st));
-        d->base += 2u * (unsigned)d->L;
+        HIPCHECK(launch_decode_qwen(d->layers, d->L, d->h, d->hidden, d->sync, d->eps, d->debug, d->times, d->place,
+                                    d->pol, d->grid, d->mode == 2, st));
     } else if (d->exec) {
         HIPCHECK(hipGraphLaunch(d->exec, st));
     } else {
@@ -1702,7 +1760,9 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
  * (tg_hip_decode_debug_bytes() each) while it is set; NULL turns it off. */
 TG_API void tg_hip_decode_set_debug(tg_hip_decode *d, void *debug_dev) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (d) d->debug = (uint8_t *)debug_dev;
+    if (!d) return;
+    d->cstale |= d->debug != (uint8_t *)debug_dev;
+    d->debug = (uint8_t *)debug_dev;
 }
 
 TG_API size_t tg_hip_decode_debug_bytes(void) { return (size_t)DecodeDebug::BYTES; }
@@ -1720,7 +1780,9 @@ TG_API size_t tg_hip_decode_record_bytes(tg_hip_decode *d) {
  * times_dev [256][L][24] (uint64) while it is set; NULL turns it off. */
 TG_API void tg_hip_decode_set_timing(tg_hip_decode *d, void *times_dev) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
-    if (d) d->times = (uint64_t *)times_dev;
+    if (!d) return;
+    d->cstale |= d->times != (uint64_t *)times_dev;
+    d->times = (uint64_t *)times_dev;
 }
 
 /* Persistent steps: true if, in the last launch, the workgroups g of each
@@ -1753,6 +1815,7 @@ TG_API int tg_hip_decode_status(tg_hip_decode *d) {
     if (d->pol == 0 && !placement_ok(d)) {
         d->placement_bad = 1;
         d->pol = 1;
+        d->cstale = true;
     }
     return d->placement_bad ? 2 : 0;
 }
@@ -1767,6 +1830,7 @@ TG_API int tg_hip_decode_set_policy(tg_hip_decode *d, int pol) {
     if (!d || d->mode < 2) return -1;
     const int prev = d->pol;
     d->pol = pol ? 1 : 0;
+    d->cstale |= d->pol != prev;
     return prev;
 }
 
@@ -1786,6 +1850,7 @@ TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
     HIPCHECK(hipStreamSynchronize(g.st));
     if (d->exec) HIPCHECK(hipGraphExecDestroy(d->exec));
     if (d->graph) HIPCHECK(hipGraphDestroy(d->graph));
+    coop_graph_drop(d);
     HIPCHECK(hipFree(d->x));
     if (d->layers) HIPCHECK(hipFree(d->layers));
     if (d->layers_mx) HIPCHECK(hipFree(d->layers_mx));

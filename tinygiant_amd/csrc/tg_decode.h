@@ -62,8 +62,13 @@ struct DecodeDebugMx {
 int decode_mx_max_grid();
 size_t decode_mx_slot_bytes();
 hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
-                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev,
-                            int pol, bool cooperative, hipStream_t st);
+                            float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, int pol,
+                            bool cooperative, hipStream_t st);
+/* the persistent kernels' entry points and block size, for graph nodes */
+const void *decode_mx_fn();
+int decode_mx_threads();
+const void *decode_qwen_fn();
+int decode_threads();
 
 /* Shape the persistent kernel is built for; the host checks a step against it. */
 struct DecodeShape {
@@ -85,7 +90,7 @@ size_t decode_qwen_slot_bytes(int grid);
  * workgroup g on XCD g % 8).  The down matrices of layers_dev are in the
  * row-group layout of launch_q6k_row_groups. */
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
-                              unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
+                              unsigned *abort_dev, float eps, uint8_t *debug_dev, uint64_t *times_dev,
                               unsigned *place_dev, int pol, int grid, bool cooperative, hipStream_t st);
 int decode_qwen_max_grid();
 /* Q6_K matrix (nrows x nb blocks, nrows % 8 == 0) -> row-group layout:

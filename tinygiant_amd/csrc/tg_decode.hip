@@ -304,7 +304,7 @@ __device__ inline float silu_mul(float g, float u) { return g / (1.f + expf(-g))
  * rewritten two layers later only after every reader of it has published
  * something the writer waited for in between. */
 __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restrict__ layers, int L, float *h,
-                                                    u32x4 *slots, unsigned *abort_flag, unsigned base, float eps,
+                                                    u32x4 *slots, unsigned *abort_flag, float eps,
                                                     uint8_t *dbg, uint64_t *times, unsigned *place, int pol) {
     __shared__ __attribute__((aligned(16))) uint8_t wgs[WGB];          /* gate/up rows of the slice */
     __shared__ __attribute__((aligned(16))) uint8_t wds[D_INS * 1024]; /* down rows of the slice (row groups) */
@@ -324,8 +324,10 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid in the communication waves */
     const int ct = (int)threadIdx.x;             /* compute lane, valid when < NW * 64 */
+    __shared__ unsigned epoch_s;
     if (threadIdx.x == 0) {
         lds_fail = 0;
+        epoch_s = read_epoch(abort_flag);
         unsigned x;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
         if (place) place[blockIdx.x] = x;
@@ -407,6 +409,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     wait_copies();
     __syncthreads();
 
+    const unsigned base = epoch_s;   /* read after the prologue barrier */
     for (int l = 0; l < L; l++) {
         const DecodeLayer &ly = lys[l];
         const unsigned par = (unsigned)(l & 1);
@@ -458,7 +461,10 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             }
             wait_copies();   /* this layer's gate/up rows and RMSNorm weight (batches A, B) */
             bar_lds();
-            if (lds_fail) return;
+            if (lds_fail) {
+                advance_epoch(abort_flag, base, L);
+                return;
+            }
         }
         if (tw) tr[1] = wall_clock64();
         /* this layer's down rows stream in during RMSNorm, gate/up and the
@@ -558,7 +564,10 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         }
         wait_copies();   /* this layer's down rows (batch D) */
         bar_lds();
-        if (lds_fail) return;
+        if (lds_fail) {
+            advance_epoch(abort_flag, base, L);
+            return;
+        }
         if (tw) tr[4] = wall_clock64();
         /* the next layer's RMSNorm weight and part of its gate/up rows stream
          * in from here (the gate/up region and the norm weight are free) */
@@ -639,6 +648,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         bar_lds();
         if (lds_fail) {
             wait_copies();   /* no copy into LDS outlives the workgroup */
+            advance_epoch(abort_flag, base, L);
             return;
         }
         if (tw) tr[7] = wall_clock64();
@@ -668,6 +678,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
         if (tw) tr[8] = wall_clock64();
     }
     wait_copies();
+    advance_epoch(abort_flag, base, L);
 }
 
 /* Rewrites a Q6_K matrix (nrows x nb 210-byte blocks, nrows a multiple of
@@ -709,13 +720,16 @@ int decode_qwen_max_grid() {
 size_t decode_qwen_slot_bytes(int) { return (size_t)NSLOTS * 16; }
 
 hipError_t launch_decode_qwen(const DecodeLayer *layers_dev, int L, float *h_dev, void *slots_dev,
-                              unsigned *abort_dev, unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev,
+                              unsigned *abort_dev, float eps, uint8_t *debug_dev, uint64_t *times_dev,
                               unsigned *place_dev, int pol, int grid, bool cooperative, hipStream_t st) {
     void *args[] = {(void *)&layers_dev, (void *)&L,         (void *)&h_dev,     (void *)&slots_dev,
-                    (void *)&abort_dev,  (void *)&base,      (void *)&eps,       (void *)&debug_dev,
-                    (void *)&times_dev,  (void *)&place_dev, (void *)&pol};
+                    (void *)&abort_dev,  (void *)&eps,       (void *)&debug_dev, (void *)&times_dev,
+                    (void *)&place_dev,  (void *)&pol};
     if (cooperative) return hipLaunchCooperativeKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
     return hipLaunchKernel((const void *)k_decode_qwen, dim3(grid), dim3(NT), args, 0, st);
 }
+
+const void *decode_qwen_fn() { return (const void *)k_decode_qwen; }
+int decode_threads() { return NT; }
 
 }  // namespace tg

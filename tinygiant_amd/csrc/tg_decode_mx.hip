@@ -218,7 +218,7 @@ __device__ inline void mma_chunk(const MxBlk &a, const v8i &bx, int sb, float d,
  * rewritten two layers later only after every reader of it has published
  * something the writer waited for in between. */
 __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restrict__ layers, int L, float *h,
-                                                  u32x4 *slots, unsigned *abort_flag, unsigned base, float eps,
+                                                  u32x4 *slots, unsigned *abort_flag, float eps,
                                                   uint8_t *dbg, uint64_t *times, unsigned *place, int pol) {
     __shared__ __attribute__((aligned(16))) float hx[D];      /* this layer's h */
     __shared__ __attribute__((aligned(16))) float nws[D];     /* this layer's RMSNorm weight */
@@ -237,8 +237,10 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
     const int cl = (int)threadIdx.x - NW * 64;   /* communication lane, valid when >= 0 */
     const int ct = (int)threadIdx.x;             /* compute lane, valid when < NW * 64 */
+    __shared__ unsigned epoch_s;
     if (threadIdx.x == 0) {
         lds_fail = 0;
+        epoch_s = read_epoch(abort_flag);
         unsigned x;
         asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
         if (place) place[blockIdx.x] = x;
@@ -424,6 +426,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     store_nw();
     bar_lds();   /* layer 0's RMSNorm weight is in LDS before step 2 reads it */
 
+    const unsigned base = epoch_s;   /* read after the prologue barrier */
     for (int l = 0; l < L; l++) {
         const DecodeLayerMx &ly = lys[l];
         const unsigned par = (unsigned)(l & 1);
@@ -497,13 +500,13 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
             bar_lds();
             if (lds_fail) {
             wait_copies();   /* no copy into LDS outlives the workgroup */
+            advance_epoch(abort_flag, base, L);
             return;
         }
         }
         if (tw) tr[1] = wall_clock64();
         /* ---- 2: RMSNorm (weight or 1) + q8 + fp8 halves of x ---- */
         if (cl >= 0) fetch_down(ly);
-        if (tw) tr[20] = wall_clock64();
         {
             const float tot = wave_sum(ssq[lane]);   /* the 64 slice sums, one per lane */
             const float scale = 1.f / sqrtf(tot / (float)D + eps);
@@ -514,8 +517,6 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
                      rx ? rec + DecodeDebugMx::XQ : nullptr,
                      rx ? reinterpret_cast<float *>(rec + DecodeDebugMx::XD) : nullptr);
         }
-        if (tw) tr[21] = wall_clock64();
-        if (tc) tr[22] = wall_clock64();
         bar_lds();
         if (tw) tr[2] = wall_clock64();
         /* ---- 3: gate/up rows of the slice, chunks [4 w, 4 w + 4) of wave w ---- */
@@ -619,6 +620,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         bar_lds();
         if (lds_fail) {
             wait_copies();   /* no copy into LDS outlives the workgroup */
+            advance_epoch(abort_flag, base, L);
             return;
         }
         if (tw) tr[4] = wall_clock64();
@@ -723,6 +725,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         bar_lds();
         if (lds_fail) {
             wait_copies();   /* no copy into LDS outlives the workgroup */
+            advance_epoch(abort_flag, base, L);
             return;
         }
         if (tw) tr[7] = wall_clock64();
@@ -760,6 +763,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
         }
         if (tw) tr[8] = wall_clock64();
     }
+    advance_epoch(abort_flag, base, L);
 }
 
 int decode_mx_max_grid() {
@@ -774,14 +778,17 @@ int decode_mx_max_grid() {
 size_t decode_mx_slot_bytes() { return (size_t)NSLOTS * 16; }
 
 hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
-                            unsigned base, float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev,
-                            int pol, bool cooperative, hipStream_t st) {
+                            float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, int pol,
+                            bool cooperative, hipStream_t st) {
     void *args[] = {(void *)&layers_dev, (void *)&L,         (void *)&h_dev,     (void *)&slots_dev,
-                    (void *)&abort_dev,  (void *)&base,      (void *)&eps,       (void *)&debug_dev,
-                    (void *)&times_dev,  (void *)&place_dev, (void *)&pol};
+                    (void *)&abort_dev,  (void *)&eps,       (void *)&debug_dev, (void *)&times_dev,
+                    (void *)&place_dev,  (void *)&pol};
     if (cooperative)
         return hipLaunchCooperativeKernel((const void *)k_decode_mx, dim3(DECODE_GRID), dim3(NT), args, 0, st);
     return hipLaunchKernel((const void *)k_decode_mx, dim3(DECODE_GRID), dim3(NT), args, 0, st);
 }
+
+const void *decode_mx_fn() { return (const void *)k_decode_mx; }
+int decode_mx_threads() { return NT; }
 
 }  // namespace tg

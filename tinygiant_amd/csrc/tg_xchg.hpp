@@ -81,6 +81,24 @@ __device__ inline bool poll_slots(Buf sl, int cl, int total, unsigned tag, unsig
 }
 
 
+/* ---- launch epochs (persistent kernels) ----
+ *
+ * Exchange tags are epoch + layer + 1; the epoch lives in word 1 of the
+ * kernel's sync buffer (word 0 is the abort flag), so a launch needs no
+ * per-launch argument and can be replayed from a graph.  Thread 0 of every
+ * workgroup reads it before the workgroup's first barrier; thread 0 of
+ * workgroup 0 advances it by 2 L when its workgroup leaves.  Workgroup 0
+ * cannot leave before every workgroup has published its first layer, so
+ * every workgroup has read the old value by then; the next launch on the
+ * stream sees the new one. */
+__device__ inline unsigned read_epoch(unsigned *sync) {
+    return __hip_atomic_load(sync + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline void advance_epoch(unsigned *sync, unsigned epoch, int L) {
+    if (blockIdx.x == 0 && threadIdx.x == 0)
+        __hip_atomic_store(sync + 1, epoch + 2u * (unsigned)L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 /* ---- weight streams into LDS (persistent kernels) ----
  *
  * One 1 KiB direct-to-LDS copy: lane l moves the 16 bytes at byte offset
