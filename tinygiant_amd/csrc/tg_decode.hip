@@ -30,13 +30,16 @@
  * Weights stream through LDS.  A CU returns the data of its vector loads in
  * the order it issued them, so an exchange poll waits behind every weight
  * load its CU issued before it.  The weights are therefore copied into LDS
- * by direct-to-LDS loads (no registers) in three batches per layer, each
- * issued right after an exchange and needed only after a later one:
+ * by direct-to-LDS loads (no registers) in four batches per layer, each
+ * issued right after an exchange or a phase that frees its region, and
+ * needed only after a later exchange:
  *   D  this layer's down rows            at the start of RMSNorm (every wave)
- *   A  the next layer's RMSNorm weight   at the start of q8(hidden) (every
- *      and first 32 KiB of gate/up rows  wave)
- *   B  the rest of its gate/up rows      at the start of the down dots (the
+ *   N  the next layer's RMSNorm weight   at the start of gate/up (the
  *                                        communication waves, idle there)
+ *   A  the first 24 KiB of the next      at the start of q8(hidden) (every
+ *      layer's gate/up rows              wave)
+ *   B  the rest of its gate/up rows      at the start of the down dots (the
+ *                                        communication waves)
  * so the exchange polls wait for little that is not needed anyway, and the
  * weight stream runs while the chain of exchanges and dots runs (an issuing
  * wave stalls once its CU's memory queue is full, so each batch is spread
@@ -101,7 +104,7 @@ constexpr int WDB = RB / 8 * DGRP;    /* the 64-row down slice: 40,320 bytes */
 constexpr int D_INS = (WDB + 1023) / 1024;   /* 40 (the last one runs past the slice) */
 constexpr int N_INS = D * 4 / 1024;   /* RMSNorm weight: 8 */
 #ifndef TG_DECODE_G_SPLIT
-#define TG_DECODE_G_SPLIT 32
+#define TG_DECODE_G_SPLIT 24
 #endif
 #ifndef TG_DECODE_B_AT_DOWN
 #define TG_DECODE_B_AT_DOWN 1
@@ -110,12 +113,17 @@ constexpr int N_INS = D * 4 / 1024;   /* RMSNorm weight: 8 */
  * its CU's memory queue takes stalls until the queue drains):
  *   D  this layer's down rows     every wave, at the start of RMSNorm
  *      (after the h gather)       (done before the hidden gather ends)
- *   A  RMSNorm weight and the     every wave, at the start of q8(hidden)
- *      first G_SPLIT gate/up KiB  (after the hidden gather)
+ *   N  the next layer's RMSNorm   the communication waves, at the start of
+ *      weight (8 KiB)             gate/up (the region is free after RMSNorm;
+ *                                 done before the hidden gather ends)
+ *   A  the first G_SPLIT gate/up  every wave, at the start of q8(hidden)
+ *      KiB of the next layer      (after the hidden gather)
  *   B  the other gate/up KiB      the communication waves at the start of
  *                                 the down dots (they are idle there), or
  *                                 every wave after the hop
- * A and B are done before the next h gather ends. */
+ * A and B are done before the next h gather ends.  The copies that drain
+ * between the hidden gather and the hop (A, B) set how long the hop's polls
+ * wait, so N moves what it can into the gap before the hidden gather. */
 constexpr int G_SPLIT = TG_DECODE_G_SPLIT;
 constexpr bool B_AT_DOWN = TG_DECODE_B_AT_DOWN != 0;
 
@@ -344,20 +352,17 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     const int ta = ct >> 3, ba = ct & 7;
     const int tb = ct / HB, hbb = ct % HB;
 
-    /* copies into LDS: batch D (down rows), A (RMSNorm weight + the first
+    /* copies into LDS: batch D (down rows), N (RMSNorm weight), A (the first
      * G_SPLIT gate/up KiB), B (the rest of the gate/up rows).  The buffer
      * descriptors are formed once per batch: the copies' memory clobber
      * would otherwise make every copy re-read the layer table from LDS. */
     struct Descs {
-        u32x4 g, u, n;
+        u32x4 g, u;
     };
     auto descs = [&](const DecodeLayer &ly) {
         Descs d;
         d.g = buf_desc(ly.gate[xe], (uint32_t)I * GATE_RB);
         d.u = buf_desc(ly.up[xe], (uint32_t)I * GATE_RB);
-        /* a layer without an RMSNorm weight still issues its copies, reading
-         * nothing, so every wave's copy count stays the same */
-        d.n = buf_desc(ly.norm_w, ly.norm_w != nullptr ? (uint32_t)D * 4u : 0u);
         return d;
     };
     const uint32_t goff = (uint32_t)(RA * rk) * GATE_RB;
@@ -372,10 +377,14 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     };
     auto batch_a = [&](const DecodeLayer &ly) {   /* every wave */
         const Descs d = descs(ly);
-        for (int i = wave; i < G_SPLIT + N_INS; i += NA) {
-            if (i < N_INS) copy_1k(d.n, 1024u * (uint32_t)i, lds_addr(nws + 256 * i), lane);
-            else copy_gate_up(d, i - N_INS);
-        }
+        for (int i = wave; i < G_SPLIT; i += NA) copy_gate_up(d, i);
+    };
+    auto batch_n = [&](const DecodeLayer &ly, int w0, int nw) {   /* RMSNorm weight: waves w0 .. w0 + nw - 1 */
+        if (wave < w0) return;
+        /* a layer without an RMSNorm weight still issues its copies, reading
+         * nothing, so every wave's copy count stays the same */
+        const u32x4 n = buf_desc(ly.norm_w, ly.norm_w != nullptr ? (uint32_t)D * 4u : 0u);
+        for (int i = wave - w0; i < N_INS; i += nw) copy_1k(n, 1024u * (uint32_t)i, lds_addr(nws + 256 * i), lane);
     };
     auto batch_b = [&](const DecodeLayer &ly, int w0, int nw) {   /* waves w0 .. w0 + nw - 1 */
         const Descs d = descs(ly);
@@ -406,6 +415,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
     }
     batch_a(lys[0]);
     batch_b(lys[0], 0, NA);
+    batch_n(lys[0], 0, NA);
     wait_copies();
     __syncthreads();
 
@@ -459,7 +469,7 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
                 }
                 if (!ok) lds_fail = 1;
             }
-            wait_copies();   /* this layer's gate/up rows and RMSNorm weight (batches A, B) */
+            wait_copies();   /* this layer's gate/up rows and RMSNorm weight (batches N, A, B) */
             bar_lds();
             if (lds_fail) {
                 advance_epoch(abort_flag, base, L);
@@ -514,6 +524,9 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             if (threadIdx.x < NBD * 8)
                 reinterpret_cast<int32_t *>(rec + DecodeDebug::XS32)[threadIdx.x] = sx.s32[threadIdx.x];
         }
+        /* the next layer's RMSNorm weight streams in during gate/up, issued by
+         * the communication waves (idle there) */
+        if (more && comm) batch_n(lys[l + 1], NW, NC);
         /* ---- 3: gate/up rows [24 rk, 24 rk + 24) of expert xe, one block per lane ---- */
         if (wave < NW) {
             const Q4Blk wa = lds_q4blk(wgs + (ta / RA) * SEG + (ta % RA) * GATE_RB + ba * 144);
@@ -569,8 +582,8 @@ __global__ __launch_bounds__(NT) void k_decode_qwen(const DecodeLayer *__restric
             return;
         }
         if (tw) tr[4] = wall_clock64();
-        /* the next layer's RMSNorm weight and part of its gate/up rows stream
-         * in from here (the gate/up region and the norm weight are free) */
+        /* part of the next layer's gate/up rows streams in from here (the
+         * gate/up region is free) */
         if (more) batch_a(lys[l + 1]);
         /* ---- 5: q8 of the hidden vector, one wave per 256-block ---- */
         if (wave < NBI) {
