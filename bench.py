@@ -423,6 +423,55 @@ def verify_probe(tg, base, ks=(5, 9, 1), iters=20):
     return out
 
 
+def qwen_prefill_probe(tg, base, tokens=(64, 128), iters=20):
+    """Prefill tokens through layer 0 of the step (128 resident Qwen3 experts,
+    q4_K gate/up, q6_K down, each token its own Zipf top-8): the int8 MFMA
+    expert phases (tg_grouped_k.hip; the busiest expert holds 16+ pairs), and
+    for comparison the v_dot4 expert-major phases.  Weight bytes = every
+    expert of the union, read once; ops = 2 x pairs x 3 x D x I."""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    rng = np.random.default_rng(SEED + 43)
+    perm = rng.permutation(E)
+    out = {}
+    for kp in tokens:
+        experts, rw = S.routing_rows(rng, kp, E, TOPK, 1.1, perm)
+        n = len(experts)
+        gp = (ctypes.c_void_p * n)(*[base + int(e) * GATE_B for e in experts])
+        up = (ctypes.c_void_p * n)(*[base + E * GATE_B + int(e) * GATE_B for e in experts])
+        dp = (ctypes.c_void_p * n)(*[base + 2 * E * GATE_B + int(e) * DOWN_B for e in experts])
+        fm = np.full(n, tg.FMT_Q6K, np.int32)
+        rwc = np.ascontiguousarray(rw, np.float32)
+        plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
+                                          tg.FMT_Q4K, fm.ctypes.data, None, None, None, tg.ACT_SILU, n,
+                                          rwc.ctypes.data, kp, D, I)
+        if not plan:
+            raise RuntimeError(tg.last_error())
+        x = tg.DeviceArray(kp * D * 4)
+        x.upload(rng.standard_normal((kp, D)).astype(np.float32))
+        y = tg.DeviceArray(kp * D * 4)
+        most = int((rw != 0).sum(axis=1).max())
+        prev = lib.tg_hip_set_moe_qk_min_rows(1)
+        us = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None), iters)
+        lib.tg_hip_set_moe_qk_min_rows(0)
+        us_dot4 = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None), iters)
+        lib.tg_hip_set_moe_qk_min_rows(prev)
+        nbytes = n * EXPERT_B
+        pairs = int((rw != 0).sum())
+        ops = 2 * pairs * 3 * D * I
+        out[str(kp)] = {"experts": n, "pairs": pairs, "rows_per_expert_max": most,
+                        "path": "int8 MFMA phases" if most >= prev > 0 else "v_dot4 expert-major phases",
+                        "us": round(us, 2), "us_dot4_phases": round(us_dot4, 2), "weight_bytes": nbytes,
+                        "weight_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        "int8_tops": round(ops / (us * 1e-6) / 1e12, 2),
+                        "frac_of_int8_mfma_peak": round(ops / (us * 1e-6) / 5.0e15, 5)}
+        lib.tg_hip_moe_plan_destroy(plan)
+        x.free()
+        y.free()
+    return out
+
+
 def _time_calls(lib, fn, iters):
     for _ in range(3):
         fn()
@@ -943,6 +992,8 @@ def main():
     if not args.no_verify:
         log("verify batch probe ...")
         result["verify_layer"] = verify_probe(tg, bufs[0].ptr)
+        log("qwen3 prefill probe ...")
+        result["qwen_prefill"] = qwen_prefill_probe(tg, bufs[0].ptr)
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
     for b in bufs + nbufs + [h]:

@@ -312,6 +312,13 @@ void tg_hip_device_name(char *buf, int n);
  * Default 4.  Returns the previous setting.  No counterpart in the
  * reference, which has one CPU kernel for every row count. */
 int tg_hip_set_moe_grouped_min_rows(int rows);
+/* Q4_K gate/up + Q6_K down expert layers whose busiest expert holds at
+ * least `rows` pairs run both phases on int8 MFMA (each weight byte read
+ * once per 16 pairs; the integer sums of dot_q4k_q8 / dot_q6k_q8,
+ * csrc/libtinygiant.c:223-272, :384-443, with the f32 additions grouped
+ * differently); 0 keeps every such layer on the v_dot4 phases.  Default 64.
+ * Returns the previous setting.  No counterpart in the reference. */
+int tg_hip_set_moe_qk_min_rows(int rows);
 /* Q4_K / Q6_K expert layers, and MXFP4 ones below the MFMA threshold, run
  * expert-major (bit 1): each weight row is
  * read once and dotted with the q8 row of every pair of its expert, as

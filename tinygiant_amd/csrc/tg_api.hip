@@ -1397,7 +1397,7 @@ static size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
 TG_API size_t tg_hip_head_scratch_bytes(int k, int nrows, int ncols) {
     if (k <= 0 || nrows <= 0 || ncols <= 0) return 0;
-    return align256(q8_bytes(k, ncols)) + align256(16 * 8) + align256((size_t)k * ncols * 4) +
+    return align256(q8_bytes(k, ncols)) + align256(HEAD_KEY_WORDS * 8) + align256((size_t)k * ncols * 4) +
            align256((size_t)k * nrows * 4);
 }
 
@@ -1415,28 +1415,32 @@ TG_API void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *in
     uint8_t *sp = (uint8_t *)scratch_dev;
     uint8_t *q8p = sp;
     unsigned long long *keys = (unsigned long long *)(sp + align256(q8_bytes(k, ncols)));
-    float *normed = (float *)((uint8_t *)keys + align256(16 * 8));
+    float *normed = (float *)((uint8_t *)keys + align256(HEAD_KEY_WORDS * 8));
     float *lg_scratch = (float *)((uint8_t *)normed + align256((size_t)k * ncols * 4));
     const float *xin = norm_w_dev ? normed : inputs_dev;
     Q8Rows q = q8_view(q8p, k, ncols, xin);
+    /* the fused kernel's keys and finish counter start at zero: the q8
+     * kernel before it clears them */
+    const bool fast = head_fast_ok(fmt, ncols, k);
+    unsigned long long *clr = fast ? keys : nullptr;
     if (norm_w_dev) {
         /* RMSNorm fused with q8 of the normed rows */
         if (fmt != TG_FMT_F16) {
-            launch_rms_norm_q8(inputs_dev, norm_w_dev, normed, k, ncols, eps, q, st);
+            launch_rms_norm_q8(inputs_dev, norm_w_dev, normed, k, ncols, eps, q, st, clr, HEAD_KEY_WORDS);
         } else {
             launch_rms_norm(inputs_dev, norm_w_dev, normed, k, ncols, eps, st);
         }
     } else if (fmt != TG_FMT_F16) {
-        launch_quantize(xin, ncols, k, ncols, q, st);
+        launch_quantize(xin, ncols, k, ncols, q, st, clr, HEAD_KEY_WORDS);
     }
-    if (head_fast_ok(fmt, ncols, k)) {
-        launch_head_q6k((const uint8_t *)mat_dev, nrows, q, k, logits_dev, keys, st);
+    if (fast) {
+        launch_head_q6k((const uint8_t *)mat_dev, nrows, q, k, logits_dev, keys, argmax_dev, maxval_dev, st);
     } else {
         float *lg = logits_dev ? logits_dev : lg_scratch;
         launch_gemv(fmt, (const uint8_t *)mat_dev, nrows, ncols, nullptr, q, k, lg, nrows, st);
         launch_argmax_rows(lg, nrows, k, keys, st);
+        launch_argmax_finish(keys, k, argmax_dev, maxval_dev, st);
     }
-    launch_argmax_finish(keys, k, argmax_dev, maxval_dev, st);
     HIPCHECK(hipGetLastError());
 }
 
@@ -1939,6 +1943,15 @@ TG_API int tg_hip_set_moe_grouped_min_rows(int rows) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     const int prev = grouped_min_rows();
     set_grouped_min_rows(rows);
+    return prev;
+}
+
+/* Pairs per expert from which Q4_K gate/up + Q6_K down expert layers take
+ * the int8 MFMA phases (0: never); returns the previous setting. */
+TG_API int tg_hip_set_moe_qk_min_rows(int rows) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    const int prev = qk_min_rows();
+    set_qk_min_rows(rows);
     return prev;
 }
 

@@ -1,0 +1,415 @@
+/*
+ * tg_grouped_k.hip -- Q4_K gate/up and Q6_K down expert phases on int8 MFMA
+ * for layers whose experts hold many pairs (a prefill, a long verify batch):
+ * moe_phase_a / moe_phase_b of csrc/libtinygiant.c:1279-1384 with the
+ * per-block dots of dot_q4k_q8 (:223-272) and dot_q6k_q8 (:384-443), the
+ * contraction the reference groups four rows at a time (dot_q4k_q8_x4
+ * :276-337, dot_q6k_q8_x4 :445-487) done sixteen pairs at a time.
+ *
+ * Arithmetic.  v_mfma_i32_16x16x32_i8 sums 32 int8 products exactly.  A
+ * Q4_K sub-block is 32 values under one 6-bit scale and min, so one MFMA per
+ * sub-block gives the reference's integer sums idot for 16 weight rows x 16
+ * pairs, and the scale work is the reference's per group g of two
+ * sub-blocks, summed here over the block: d * sum_s sc_s idot_s - dmin *
+ * sum_s m_s bs_s, both sums exact (int32, and the min sums, a 16 x 16
+ * product of 8-long integer vectors, on two f32 MFMAs of K = 4 whose
+ * products and sums stay integers below 2^24).  A Q6_K sub-block is 16
+ * values under one int8 scale: each 32-value chunk of a half-block runs
+ * twice, the pair operand zero in one half of K each time, so the two
+ * sub-block sums come out apart; the 6-bit codes enter unshifted and the
+ * -32 offset is folded in with the pair's 16-value sums (sum (c - 32) x sc =
+ * sum c x sc - 32 sum sc sum x, the last on two f32 MFMAs), exact in int32
+ * per half-block.  Only the f32 additions (per block or half-block, then
+ * across waves) are associated differently from the reference's
+ * sub-block-by-sub-block sum.
+ *
+ * Operand layout of v_mfma_i32_16x16x32_i8 (measured on gfx950): A lane l =
+ * weight row l % 16, K = 8 (l / 16) + byte; B lane l = pair l % 16, the same
+ * K; D lane l, register v = weight row 4 (l / 16) + v, pair l % 16.
+ *
+ * Work: one workgroup per (16-row slab, active expert).  The slab is staged
+ * in LDS (Q6_K blocks re-spaced to 224 bytes so every field is aligned, each
+ * load inside its block, since a buffer load that runs past the matrix end
+ * reads zero as a whole); the
+ * eight waves split the row's blocks (Q4_K) or half-blocks (Q6_K); each pass
+ * runs 16 pairs of the expert against the resident slab, their q8 operands
+ * read from the q8 rows in global memory; 256 threads add the waves' partial
+ * sums in wave order and write one result each.  HBM sees each weight byte
+ * once however many pairs the expert holds.
+ */
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "tg_device.hpp"
+#include "tg_kernels.h"
+#include "tg_xchg.hpp"
+
+namespace tg {
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int NW = 8;                    /* waves per workgroup */
+constexpr int NT = 64 * NW;
+constexpr uint32_t OOB = 0x80000000u;    /* past every buffer: the load reads zero */
+constexpr uint32_t Q4B = 144, Q6B = 210; /* bytes per 256-value block */
+constexpr uint32_t Q6S = 224;            /* LDS stride of a staged Q6_K block */
+
+__device__ inline long as_long(u32x2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
+
+__device__ inline v4i mma(long a, long b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+
+/* LDS bytes: the gate and up slabs (rows 16 bytes apart more than their
+ * length, so the 16 lanes reading one sub-block of 16 rows hit distinct
+ * banks; each slab rounded up to whole 1 KiB copies), then the waves'
+ * partial sums.  Q6_K slabs likewise pad each row of blocks by 16 bytes. */
+__host__ __device__ inline uint32_t qa_row_stride(int D) { return (uint32_t)(D / 256) * Q4B + 16u; }
+__host__ __device__ inline uint32_t qa_slab_region(int D) { return (16u * qa_row_stride(D) + 1023u) & ~1023u; }
+__host__ __device__ inline uint32_t qb_row_stride(int I) { return (uint32_t)(I / 256) * Q6S + 16u; }
+__host__ __device__ inline size_t qa_lds_bytes(int D) {
+    return 2u * (size_t)qa_slab_region(D) + (size_t)NW * 2 * 4 * 64 * 4;
+}
+__host__ __device__ inline size_t qb_lds_bytes(int I) {
+    return 16u * (size_t)qb_row_stride(I) + (size_t)NW * 4 * 64 * 4;
+}
+
+/* 6-bit scales and mins of a Q4_K block header (get_scale_min_k4,
+ * csrc/libtinygiant.c:146-155), four bytes at a time: sc of sub-blocks 0-3,
+ * 4-7, then the mins */
+struct Q4Hdr {
+    float d, dmin;
+    uint32_t scl, sch, mnl, mnh;
+};
+__device__ inline Q4Hdr q4_hdr(u32x4 h) {
+    Q4Hdr r;
+    const uint32_t m4 = 0x0F0F0F0Fu;
+    r.d = ref_f16(h.x & 0xFFFFu);
+    r.dmin = ref_f16(h.x >> 16);
+    r.scl = h.y & 0x3F3F3F3Fu;
+    r.mnl = h.z & 0x3F3F3F3Fu;
+    r.sch = (h.w & m4) | ((h.y >> 2) & 0x30303030u);
+    r.mnh = ((h.w >> 4) & m4) | ((h.z >> 2) & 0x30303030u);
+    return r;
+}
+__device__ inline int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFFu); }
+
+}  // namespace
+
+/* Phase A: hidden[p][r] = act(gate_r . xq_p + bg[r], up_r . xq_p + bu[r])
+ * for rows r of slab blockIdx.x and every pair p of active expert
+ * a.ed[blockIdx.y]; Q4_K gate and up matrices of D = 256 nb columns.  The
+ * slabs arrive by direct-to-LDS copies, while the first pass's q8 operands
+ * load into registers. */
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_qa(MoeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const ExpDesc &ex = a.ed[blockIdx.y];
+    const int e = ex.e, p0 = ex.p0, np = ex.np;
+    const int nb = a.D / 256;
+    const uint32_t rb = (uint32_t)nb * Q4B, rs = qa_row_stride(a.D), sreg = qa_slab_region(a.D);
+    float *red = (float *)(lds + 2 * sreg);   /* [NW][2][4][64] */
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int r0 = blockIdx.x * 16;
+
+    /* the slabs, 1 KiB of LDS a copy: lane l of copy k fills LDS bytes
+     * 1024 k + 16 l, i.e. row (1024 k + 16 l) / rs at that column (the row
+     * padding and rows past 16 or past I read zero) */
+    {
+        const uint32_t mbytes = (uint32_t)a.I * rb, base = (uint32_t)r0 * rb, nins = sreg / 1024u;
+        const u32x4 gd = buf_desc((const void *)(uintptr_t)ex.gate, mbytes);
+        const u32x4 ud = buf_desc((const void *)(uintptr_t)ex.up, mbytes);
+        for (uint32_t k = (uint32_t)w; k < nins; k += NW) {
+            const uint32_t P = 1024u * k + 16u * (uint32_t)lane, row = P / rs, col = P - row * rs;
+            const uint32_t src = row < 16u && col < rb ? base + row * rb + col : OOB;
+            copy_lanes(gd, src, lds_addr(lds + 1024u * k));
+            copy_lanes(ud, src, lds_addr(lds + sreg + 1024u * k));
+        }
+    }
+    const Q8Rows &q = a.xq;
+    const Buf qs_b = make_buf(q.qs, (uint32_t)((size_t)a.k * nb * 256));
+    const Buf s32_b = make_buf(q.s32, (uint32_t)((size_t)a.k * nb * 32));
+    const Buf d_b = make_buf(q.d, (uint32_t)((size_t)a.k * nb * 4));
+    const Buf prow_b = make_buf(a.p_row, (uint32_t)a.P * 4u);
+    const float *gbias = a.gbias ? (const float *)(uintptr_t)a.gbias[e] : nullptr;
+    const float *ubias = a.ubias ? (const float *)(uintptr_t)a.ubias[e] : nullptr;
+
+    /* pair c16's q8 operands of block b: sub-block s = 2 jg + half covers
+     * x[64 jg + 32 half ...], this lane's K slice 8 g .. 8 g + 7 */
+    long xb[8];
+    int bs[8];
+    float xd;
+    auto load_x = [&](uint32_t prow, bool pv, int b) {
+        const uint32_t qb = prow * (uint32_t)nb + (uint32_t)b;
+#pragma unroll
+        for (int s = 0; s < 8; s++)
+            xb[s] = as_long(ld8(qs_b, pv ? qb * 256u + 64u * (s >> 1) + 32u * (s & 1) + 8u * g : OOB));
+        const u32x4 bs0 = ld16(s32_b, pv ? qb * 32u : OOB), bs1 = ld16(s32_b, pv ? qb * 32u + 16u : OOB);
+        bs[0] = (int)bs0.x, bs[1] = (int)bs0.y, bs[2] = (int)bs0.z, bs[3] = (int)bs0.w;
+        bs[4] = (int)bs1.x, bs[5] = (int)bs1.y, bs[6] = (int)bs1.z, bs[7] = (int)bs1.w;
+        xd = __uint_as_float(ld4(d_b, pv ? qb * 4u : OOB));
+    };
+    int t0 = 0;
+    bool pv = c16 < np;
+    uint32_t prow = pv ? ld4(prow_b, (uint32_t)(p0 + c16) * 4u) : 0u;
+    if (w < nb) load_x(prow, pv, w);
+    wait_copies();
+    __syncthreads();
+
+    for (;;) {
+        float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+        for (int b = w; b < nb; b += NW) {
+            if (b != w) load_x(prow, pv, b);
+#pragma unroll 1
+            for (int m = 0; m < 2; m++) {
+                const uint8_t *sb = lds + m * sreg;
+                Q4Hdr hd[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) hd[v] = q4_hdr(*(const u32x4 *)(sb + (4 * g + v) * rs + b * Q4B));
+                /* the min terms sum_s m[row][s] bs[pair][s] of the 16 rows x 16
+                 * pairs: two f32 MFMAs of K = 4 (sub-blocks g and 4 + g of this
+                 * lane group; products and sums are integers below 2^24, exact) */
+                const Q4Hdr hr = q4_hdr(*(const u32x4 *)(sb + c16 * rs + b * Q4B));
+                v4f im = {0.f, 0.f, 0.f, 0.f};
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnl, g), (float)bs[g], im, 0, 0, 0);
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnh, g), (float)bs[4 + g], im, 0, 0, 0);
+                /* the scale terms sum_s sc[row][s] idot[row][pair][s]: one int8
+                 * MFMA per sub-block, summed exactly in int32 */
+                const uint8_t *ab = sb + c16 * rs + b * Q4B + 16 + 8 * g;   /* row c16's codes */
+                int isc[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int jg = 0; jg < 4; jg++) {
+                    const u32x2 qq = *(const u32x2 *)(ab + 32 * jg);
+                    u32x2 lo, hi;
+                    lo.x = qq.x & 0x0F0F0F0Fu;
+                    lo.y = qq.y & 0x0F0F0F0Fu;
+                    hi.x = (qq.x >> 4) & 0x0F0F0F0Fu;
+                    hi.y = (qq.y >> 4) & 0x0F0F0F0Fu;
+                    const v4i dl = mma(as_long(lo), xb[2 * jg]);
+                    const v4i dh = mma(as_long(hi), xb[2 * jg + 1]);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const uint32_t scw = jg < 2 ? hd[v].scl : hd[v].sch;
+                        const int i0 = 2 * (jg & 1);
+                        isc[v] += __mul24(byte_of(scw, i0), dl[v]) + __mul24(byte_of(scw, i0 + 1), dh[v]);
+                    }
+                }
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[m][v] += xd * (hd[v].d * (float)isc[v] - hd[v].dmin * im[v]);
+            }
+        }
+        /* the waves' partial sums (block order), then one result per thread */
+#pragma unroll
+        for (int m = 0; m < 2; m++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[((w * 2 + m) * 4 + v) * 64 + lane] = acc[m][v];
+        /* the next pass's q8 operands load while this one is written out */
+        const int t1 = t0 + 16;
+        if (t1 < np) {
+            pv = t1 + c16 < np;
+            prow = pv ? ld4(prow_b, (uint32_t)(p0 + t1 + c16) * 4u) : 0u;
+            if (w < nb) load_x(prow, pv, w);
+        }
+        __syncthreads();
+        if (tid < 256) {
+            const int ev = tid >> 6, el = tid & 63;
+            const int jj = t0 + (el & 15), r = r0 + 4 * (el >> 4) + ev;
+            if (jj < np && r < a.I) {
+                float gv = 0.f, uv = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < NW; ww++) {
+                    gv += red[((ww * 2 + 0) * 4 + ev) * 64 + el];
+                    uv += red[((ww * 2 + 1) * 4 + ev) * 64 + el];
+                }
+                if (gbias) gv += gbias[r];
+                if (ubias) uv += ubias[r];
+                a.hidden[(size_t)(p0 + jj) * a.I + r] = act_fn(a.act, gv, uv);
+            }
+        }
+        if (t1 >= np) break;
+        t0 = t1;
+        __syncthreads();   /* red is rewritten by the next pass */
+    }
+}
+
+/* Phase B: part[p][r] = w_p * (down_r . hq_p + bd[r]) for rows r of slab
+ * blockIdx.x and every pair p of active expert a.ed[blockIdx.y]; Q6_K down
+ * matrix of I = 256 nbi columns.  The slab's loads go out first, then the
+ * first pass's q8 operands, then the slab is stored to LDS. */
+constexpr int QB_PIECES = 13;   /* 16-byte pieces of a block's bytes 0-207 */
+constexpr int QB_NPC = 2;       /* pieces per thread loaded ahead of the q8 operands */
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_qb(MoeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const ExpDesc &ex = a.ed[blockIdx.y];
+    const int e = ex.e, p0 = ex.p0, np = ex.np;
+    const int nbi = a.I / 256;
+    const uint32_t rb = (uint32_t)nbi * Q6B, rs = qb_row_stride(a.I);
+    float *red = (float *)(lds + 16 * rs);   /* [NW][4][64] */
+    /* LDS offset of block blk of slab row row */
+    auto blk_at = [&](int row, int blk) { return (uint32_t)row * rs + (uint32_t)blk * Q6S; };
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    const int r0 = blockIdx.x * 16;
+
+    /* the slab, each block at a 224-byte stride: bytes 0-207 as 13 pieces,
+     * then d at 208 (a load that ran past byte 209 would read zero in the
+     * matrix's last block; rows past D read zero) */
+    const Buf dw = make_buf_uniform((const void *)(uintptr_t)ex.down, (uint32_t)a.D * rb);
+    const int nch = 16 * nbi * QB_PIECES;
+    auto piece_src = [&](int c) {
+        const int piece = c % QB_PIECES, rbk = c / QB_PIECES, row = rbk / nbi, blk = rbk % nbi;
+        return (uint32_t)(r0 + row) * rb + (uint32_t)blk * Q6B + 16u * piece;
+    };
+    u32x4 pc[QB_NPC];
+#pragma unroll
+    for (int i = 0; i < QB_NPC; i++) {
+        const int c = tid + NT * i;
+        pc[i] = ld16(dw, c < nch ? piece_src(c) : OOB);
+    }
+
+    const Q8Rows &q = a.hq;
+    const Buf qs_b = make_buf(q.qs, (uint32_t)((size_t)a.P * nbi * 256));
+    const Buf s16_b = make_buf(q.s16, (uint32_t)((size_t)a.P * nbi * 64));
+    const Buf d_b = make_buf(q.d, (uint32_t)((size_t)a.P * nbi * 4));
+    const Buf pw_b = make_buf(a.p_w, (uint32_t)a.P * 4u);
+    const float *dbias = a.dbias ? (const float *)(uintptr_t)a.dbias[e] : nullptr;
+    /* pair c16's q8 operands of half h of block bi: chunk m covers
+     * x[128 h + 32 m ...], this lane's K slice 8 g .. 8 g + 7; the 16-value
+     * sums of sub-blocks 8 h .. 8 h + 7 */
+    long xb[4];
+    int s16[8];
+    float xd;
+    auto load_x = [&](uint32_t prow, bool pv, int hb) {
+        const int bi = hb >> 1, h = hb & 1;
+        const uint32_t qb = prow * (uint32_t)nbi + (uint32_t)bi;
+#pragma unroll
+        for (int m = 0; m < 4; m++) xb[m] = as_long(ld8(qs_b, pv ? qb * 256u + 128u * h + 32u * m + 8u * g : OOB));
+        const u32x4 s0 = ld16(s16_b, pv ? qb * 64u + 32u * h : OOB);
+        const u32x4 s1 = ld16(s16_b, pv ? qb * 64u + 32u * h + 16u : OOB);
+        s16[0] = (int)s0.x, s16[1] = (int)s0.y, s16[2] = (int)s0.z, s16[3] = (int)s0.w;
+        s16[4] = (int)s1.x, s16[5] = (int)s1.y, s16[6] = (int)s1.z, s16[7] = (int)s1.w;
+        xd = __uint_as_float(ld4(d_b, pv ? qb * 4u : OOB));
+    };
+    int t0 = 0;
+    bool pv = c16 < np;
+    uint32_t prow = (uint32_t)(pv ? p0 + c16 : 0);
+    if (w < 2 * nbi) load_x(prow, pv, w);
+#pragma unroll
+    for (int i = 0; i < QB_NPC; i++) {
+        const int c = tid + NT * i;
+        if (c < nch) *(u32x4 *)(lds + blk_at(c / QB_PIECES / nbi, c / QB_PIECES % nbi) + 16 * (c % QB_PIECES)) = pc[i];
+    }
+    for (int c = tid + NT * QB_NPC; c < nch; c += NT)   /* rows of more than 2 blocks */
+        *(u32x4 *)(lds + blk_at(c / QB_PIECES / nbi, c / QB_PIECES % nbi) + 16 * (c % QB_PIECES)) =
+            ld16(dw, piece_src(c));
+    for (int rbk = tid; rbk < 16 * nbi; rbk += NT)
+        *(uint32_t *)(lds + blk_at(rbk / nbi, rbk % nbi) + 208) =
+            ld2(dw, (uint32_t)(r0 + rbk / nbi) * rb + (uint32_t)(rbk % nbi) * Q6B + 208u);
+    __syncthreads();
+
+    for (;;) {
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int hb = w; hb < 2 * nbi; hb += NW) {
+            if (hb != w) load_x(prow, pv, hb);
+            const int bi = hb >> 1, h = hb & 1;
+            /* row c16's codes: ql bytes 64 h + 32 (m & 1) + 8 g, qh bytes 32 h + 8 g */
+            const uint8_t *ab = lds + blk_at(c16, bi);
+            const u32x2 ql0 = *(const u32x2 *)(ab + 64 * h + 8 * g);
+            const u32x2 ql1 = *(const u32x2 *)(ab + 64 * h + 32 + 8 * g);
+            const u32x2 qh = *(const u32x2 *)(ab + 128 + 32 * h + 8 * g);
+            /* rows 4 g + v: sub-block scales 8 h .. 8 h + 7 and d */
+            u32x2 sc[4];
+            float dv[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const uint8_t *rbk = lds + blk_at(4 * g + v, bi);
+                sc[v] = *(const u32x2 *)(rbk + 192 + 8 * h);
+                dv[v] = ref_f16(*(const uint32_t *)(rbk + 208) & 0xFFFFu);
+            }
+            /* the -32 offset terms sum_s sc[row][s] s16[pair][s] over the
+             * half's 8 sub-blocks: two f32 MFMAs of K = 4 (sub-blocks g and
+             * 4 + g; integers below 2^24, exact) */
+            const u32x2 scr = *(const u32x2 *)(lds + blk_at(c16, bi) + 192 + 8 * h);   /* row c16 */
+            v4f cf = {0.f, 0.f, 0.f, 0.f};
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.x >> (8 * g)), (float)s16[g], cf, 0, 0, 0);
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.y >> (8 * g)), (float)s16[4 + g], cf, 0, 0, 0);
+            int ai[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const u32x2 ql = (m & 1) ? ql1 : ql0;
+                const int sl = 4 * (m >> 1), sh = 2 * m;
+                u32x2 c;
+                c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
+                c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
+                /* K slots 0-15 (lane groups 0, 1) are sub-block 2 m, 16-31 sub-block 2 m + 1 */
+                const long x0 = g < 2 ? xb[m] : 0l, x1 = g < 2 ? 0l : xb[m];
+                const v4i d0 = mma(as_long(c), x0), d1 = mma(as_long(c), x1);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const uint32_t sw = (m < 2 ? sc[v].x : sc[v].y);
+                    const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))), sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
+                    ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 per term */
+                }
+            }
+            /* sum (c - 32) x sc, exact in int32 */
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] += dv[v] * xd * (float)(ai[v] - 32 * (int)cf[v]);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[(w * 4 + v) * 64 + lane] = acc[v];
+        const int t1 = t0 + 16;
+        if (t1 < np) {
+            pv = t1 + c16 < np;
+            prow = (uint32_t)(pv ? p0 + t1 + c16 : 0);
+            if (w < 2 * nbi) load_x(prow, pv, w);
+        }
+        __syncthreads();
+        if (tid < 256) {
+            const int ev = tid >> 6, el = tid & 63;
+            const int jj = t0 + (el & 15), r = r0 + 4 * (el >> 4) + ev;
+            if (jj < np && r < a.D) {
+                float s = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < NW; ww++) s += red[(ww * 4 + ev) * 64 + el];
+                if (dbias) s += dbias[r];
+                const int p = p0 + jj;
+                a.part[(size_t)p * a.D + r] = __uint_as_float(ld4(pw_b, (uint32_t)p * 4u)) * s;
+            }
+        }
+        if (t1 >= np) break;
+        t0 = t1;
+        __syncthreads();
+    }
+}
+
+/* The MFMA phases need Q4_K gate/up and Q6_K down matrices of whole blocks,
+ * slabs within the device's LDS, and 31-bit buffer ranges. */
+bool qk_grouped_fits(const MoeArgs &a) {
+    static int max_lds = -1;
+    if (max_lds < 0) {
+        int dev = 0;
+        max_lds = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&max_lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            max_lds = 0;
+    }
+    if (a.gate_fmt != TG_FMT_Q4K || a.D % 256 || a.I % 256 || a.n_act_a <= 0) return false;
+    const uint64_t lim = 1ull << 31;
+    return qa_lds_bytes(a.D) <= (size_t)max_lds && qb_lds_bytes(a.I) <= (size_t)max_lds &&
+           (uint64_t)a.I * (a.D / 256) * Q4B < lim && (uint64_t)a.D * (a.I / 256) * Q6B < lim &&
+           (uint64_t)a.P * a.I < lim && (uint64_t)a.k * a.D < lim && (uint64_t)a.P * (a.I / 256) * 64 < lim;
+}
+
+void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_moe_qa, dim3((a.I + 15) / 16, a.n_act_a), dim3(NT), qa_lds_bytes(a.D), st, a);
+}
+
+void launch_moe_b_qk(const MoeArgs &a, hipStream_t st) {
+    hipLaunchKernelGGL(k_moe_qb, dim3((a.D + 15) / 16, a.n_act_a), dim3(NT), qb_lds_bytes(a.I), st, a);
+}
+
+}  // namespace tg

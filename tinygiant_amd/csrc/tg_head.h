@@ -12,9 +12,13 @@ namespace tg {
 
 /* The fused kernel covers Q6_K heads of 2048 columns and 1..16 rows. */
 bool head_fast_ok(int fmt, int ncols, int k);
-/* best[k] receives packed argmax keys (reset first); logits may be null. */
+/* best[0..k) receive packed argmax keys and best[16] counts finished
+ * workgroups: all 17 words must be zero at launch (launch_rms_norm_q8 and
+ * launch_quantize clear them); the last workgroup writes idx[k] and val[k]
+ * (val may be null); logits may be null. */
+constexpr int HEAD_KEY_WORDS = 17;
 void launch_head_q6k(const uint8_t *W, int nrows, const Q8Rows &x, int k, float *logits, unsigned long long *best,
-                     hipStream_t st);
+                     int32_t *idx, float *val, hipStream_t st);
 /* argmax keys of materialized logits [k][nrows] */
 void launch_argmax_rows(const float *logits, int nrows, int k, unsigned long long *best, hipStream_t st);
 /* keys -> row index and logit */

@@ -60,7 +60,10 @@ struct MoeArgs {
 int items_per_row(int fmt, int ncols);
 uint32_t row_bytes(int fmt, int ncols);
 
-void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st);
+/* q8 of nrows rows; clear[0 .. nclear) (nclear <= 64) are zeroed on the way,
+ * for a consumer launched next (the fused head's argmax keys) */
+void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st,
+                     unsigned long long *clear = nullptr, int nclear = 0);
 void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *bias, const Q8Rows &x, int k,
                  float *y, long ystride, hipStream_t st);
 /* up to three matrices of one format and width (ncols) against the same q8
@@ -107,6 +110,14 @@ void launch_moe_b_mx(const MoeArgs &a, hipStream_t st);
  * experts; 0 switches them off */
 void set_grouped_min_rows(int rows);
 int grouped_min_rows();
+/* Q4_K gate/up and Q6_K down phases on int8 MFMA with LDS-resident weight
+ * slabs (tg_grouped_k.hip), taken by launch_moe for layers whose experts
+ * hold at least qk_min_rows() pairs (0: never) */
+bool qk_grouped_fits(const MoeArgs &a);
+void launch_moe_a_qk(const MoeArgs &a, hipStream_t st);
+void launch_moe_b_qk(const MoeArgs &a, hipStream_t st);
+void set_qk_min_rows(int rows);
+int qk_min_rows();
 /* Q4_K / Q6_K experts: one workgroup column per active expert, each weight
  * row read once for all its pairs (EM_ON), or one per pair (0).  For layers
  * with at most two pairs per expert: EM_FUSE_Q8, the phases quantize their
@@ -120,7 +131,7 @@ int expert_major();
 bool rms_norm_fits(int n);
 void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st);
 void launch_rms_norm_q8(const float *x, const float *w, float *out, int nrows, int n, float eps, const Q8Rows &q,
-                        hipStream_t st);
+                        hipStream_t st, unsigned long long *clear = nullptr, int nclear = 0);
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st);
 void launch_copy(const void *src, void *dst, uint64_t nbytes, hipStream_t st);
 

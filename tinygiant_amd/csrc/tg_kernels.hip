@@ -32,8 +32,9 @@ namespace tg {
 
 /* One wave per 256-value block: lane l owns values 4l..4l+3. */
 __global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x, int ncols, int nrows,
-                                                     long xstride, Q8Rows out) {
+                                                     long xstride, Q8Rows out, unsigned long long *clear, int nclear) {
     const int lane = threadIdx.x & 63;
+    if (blockIdx.x == 0 && (int)threadIdx.x < nclear) clear[threadIdx.x] = 0;
     const int wave = (int)((blockIdx.x * (size_t)blockDim.x + threadIdx.x) >> 6);
     const int nb = out.nb;
     if (wave >= nrows * nb) return;   /* uniform per wave */
@@ -53,8 +54,10 @@ __global__ __launch_bounds__(256) void k_quantize_q8(const float *__restrict__ x
  * y is quantized in place of a separate k_quantize_q8 over it (same bits). */
 constexpr int RMS_WAVES = 16, RMS_BPW = 4;
 __global__ __launch_bounds__(RMS_WAVES * 64) void k_rms_norm_q8(const float *__restrict__ x, const float *__restrict__ w,
-                                                                float *__restrict__ y, int n, float eps, Q8Rows q) {
+                                                                float *__restrict__ y, int n, float eps, Q8Rows q,
+                                                                unsigned long long *clear, int nclear) {
     __shared__ float red[RMS_WAVES];
+    if (blockIdx.x == 0 && (int)threadIdx.x < nclear) clear[threadIdx.x] = 0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int r = blockIdx.x;
     Buf xb = make_buf(x + (size_t)r * n, (uint32_t)n * 4u);
@@ -738,10 +741,12 @@ static int pick_TB(int T) { return T >= 3 ? 4 : T; }
         default: { typedef FF16 F; BODY; } break;   \
     }
 
-void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st) {
+void launch_quantize(const float *x, int ncols, int nrows, long xstride, const Q8Rows &out, hipStream_t st,
+                     unsigned long long *clear, int nclear) {
     const int waves = nrows * out.nb;
     if (waves <= 0) return;
-    hipLaunchKernelGGL(k_quantize_q8, dim3((waves + 3) / 4), dim3(256), 0, st, x, ncols, nrows, xstride, out);
+    hipLaunchKernelGGL(k_quantize_q8, dim3((waves + 3) / 4), dim3(256), 0, st, x, ncols, nrows, xstride, out, clear,
+                       clear ? nclear : 0);
 }
 
 void launch_gemv(int fmt, const uint8_t *W, int nrows, int ncols, const float *bias, const Q8Rows &x, int k,
@@ -831,6 +836,9 @@ static int g_grouped_min_rows = 4;
 
 void set_grouped_min_rows(int rows) { g_grouped_min_rows = rows < 0 ? 0 : rows; }
 int grouped_min_rows() { return g_grouped_min_rows; }
+static int g_qk_min_rows = 64;
+void set_qk_min_rows(int rows) { g_qk_min_rows = rows < 0 ? 0 : rows; }
+int qk_min_rows() { return g_qk_min_rows; }
 
 static int g_expert_major = EM_DEFAULT;
 
@@ -909,6 +917,24 @@ static void launch_bx(const MoeArgs &a, int fmt, uint32_t rb, int nitems, int T,
 
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
                 const std::function<void(int)> *mark, bool quantize_x) {
+    /* Q4_K / Q6_K experts with many pairs: the int8 MFMA phases */
+    if (g_qk_min_rows > 0 && a.max_rows >= g_qk_min_rows && n_down_fmts == 1 && down_fmts_present[0] == TG_FMT_Q6K &&
+        qk_grouped_fits(a)) {
+        if (quantize_x) {
+            launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
+            if (mark) (*mark)(1);
+        }
+        launch_moe_a_qk(a, st);
+        if (mark) (*mark)(2);
+        launch_quantize(a.hidden, a.I, a.P, a.I, a.hq, st);
+        if (mark) (*mark)(3);
+        launch_moe_b_qk(a, st);
+        if (mark) (*mark)(4);
+        const size_t n = (size_t)a.k * a.D;
+        hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a);
+        if (mark) (*mark)(5);
+        return;
+    }
     const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
     const bool mx_a = mx_grouped && a.gate_fmt == TG_FMT_MXFP4 && a.xp;
     int Ta;
@@ -1029,12 +1055,14 @@ bool rms_norm_fits(int n) { return n > 0 && n <= RMS_WAVES * RMS_BPW * 256; }
 
 void launch_rms_norm(const float *x, const float *w, float *out, int nrows, int n, float eps, hipStream_t st) {
     Q8Rows none = {};
-    hipLaunchKernelGGL(k_rms_norm_q8, dim3(nrows), dim3(64 * rms_waves(n)), 0, st, x, w, out, n, eps, none);
+    hipLaunchKernelGGL(k_rms_norm_q8, dim3(nrows), dim3(64 * rms_waves(n)), 0, st, x, w, out, n, eps, none,
+                       (unsigned long long *)nullptr, 0);
 }
 
 void launch_rms_norm_q8(const float *x, const float *w, float *out, int nrows, int n, float eps, const Q8Rows &q,
-                        hipStream_t st) {
-    hipLaunchKernelGGL(k_rms_norm_q8, dim3(nrows), dim3(64 * rms_waves(n)), 0, st, x, w, out, n, eps, q);
+                        hipStream_t st, unsigned long long *clear, int nclear) {
+    hipLaunchKernelGGL(k_rms_norm_q8, dim3(nrows), dim3(64 * rms_waves(n)), 0, st, x, w, out, n, eps, q, clear,
+                       clear ? nclear : 0);
 }
 
 void launch_synth_fill(int kind, uint64_t seed, void *dst, uint64_t nbytes, hipStream_t st) {
