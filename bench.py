@@ -452,16 +452,19 @@ def qwen_prefill_probe(tg, base, tokens=(64, 128), iters=20):
         y = tg.DeviceArray(kp * D * 4)
         most = int((rw != 0).sum(axis=1).max())
         prev = lib.tg_hip_set_moe_qk_min_rows(1)
-        us = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None), iters)
+        us_mfma = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None), iters)
         lib.tg_hip_set_moe_qk_min_rows(0)
         us_dot4 = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None), iters)
         lib.tg_hip_set_moe_qk_min_rows(prev)
+        mfma = 0 < prev <= most   # the path the default threshold takes
+        us = us_mfma if mfma else us_dot4
         nbytes = n * EXPERT_B
         pairs = int((rw != 0).sum())
         ops = 2 * pairs * 3 * D * I
         out[str(kp)] = {"experts": n, "pairs": pairs, "rows_per_expert_max": most,
-                        "path": "int8 MFMA phases" if most >= prev > 0 else "v_dot4 expert-major phases",
-                        "us": round(us, 2), "us_dot4_phases": round(us_dot4, 2), "weight_bytes": nbytes,
+                        "path": "int8 MFMA phases" if mfma else "v_dot4 expert-major phases",
+                        "us": round(us, 2), "us_mfma_phases": round(us_mfma, 2), "us_dot4_phases": round(us_dot4, 2),
+                        "weight_bytes": nbytes,
                         "weight_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                         "int8_tops": round(ops / (us * 1e-6) / 1e12, 2),
