@@ -176,3 +176,52 @@ def test_head_q6k_full_vocabulary(tg, orc, k):
     logits, am, mv = _head(tg, Q6K, mat, x, nrows, ncols, norm=norm)
     ref = _oracle(orc, Q6K, mat, x, nrows, ncols, norm=norm)
     _check(ref, logits, am, mv, 1e-5)
+
+
+@pytest.mark.parametrize("k", [3, 7, 12])
+def test_head_q6k_padded_row_counts(tg, orc, k):
+    """Row counts between the kernel's instantiations (3 -> 4, 7 -> 8,
+    12 -> 16): the unused input slots take part in the reduce-scatter as
+    zeros and never reach the argmax."""
+    import tinygiant_amd.synth as S
+    nrows, ncols = 2501, 2048
+    mat = S.matrix_host(Q6K, S.tensor_seed(16, 0, 0, 3), nrows, ncols)
+    x = np.random.default_rng(100 + k).standard_normal((k, ncols)).astype(np.float32)
+    logits, am, mv = _head(tg, Q6K, mat, x, nrows, ncols)
+    ref = _oracle(orc, Q6K, mat, x, nrows, ncols)
+    _check(ref, logits, am, mv, 1e-5)
+
+
+def test_head_q6k_scratch_reused_across_calls(tg, orc):
+    """Two calls on one scratch buffer: the argmax keys and the finish
+    counter the kernel leaves behind are cleared by the next call."""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    nrows, ncols, k = 1999, 2048, 5
+    mat = S.matrix_host(Q6K, S.tensor_seed(17, 0, 0, 3), nrows, ncols)
+    md = tg.DeviceArray(mat.nbytes)
+    md.upload(mat)
+    sd = tg.DeviceArray(lib.tg_hip_head_scratch_bytes(k, nrows, ncols))
+    ad = tg.DeviceArray(k * 4)
+    vd = tg.DeviceArray(k * 4)
+    xd = tg.DeviceArray(k * ncols * 4)
+    try:
+        for seed in (1, 2):
+            x = np.random.default_rng(seed).standard_normal((k, ncols)).astype(np.float32)
+            if seed == 2:
+                x = -x   # a different winner per row
+            xd.upload(x)
+            lib.tg_hip_head_argmax_dev(Q6K, md.ptr, xd.ptr, None, ctypes.c_float(1e-6), k, nrows, ncols, None,
+                                       ad.ptr, vd.ptr, sd.ptr, None)
+            lib.tg_hip_synchronize()
+            am = ad.download(np.int32, k)
+            mv = vd.download(np.float32, k)
+            ref = _oracle(orc, Q6K, mat, x, nrows, ncols)
+            for j in range(k):
+                top2 = np.sort(ref[j])[-2:]
+                if am[j] != int(np.argmax(ref[j])):
+                    assert top2[1] - top2[0] <= 2e-5 * np.abs(ref).max(), (seed, j)
+                assert abs(mv[j] - ref[j][am[j]]) <= 1e-5 * np.abs(ref).max(), (seed, j)
+    finally:
+        for a in (md, sd, ad, vd, xd):
+            a.free()
