@@ -316,7 +316,7 @@ int tg_hip_set_moe_grouped_min_rows(int rows);
  * least `rows` pairs run both phases on int8 MFMA (each weight byte read
  * once per 16 pairs; the integer sums of dot_q4k_q8 / dot_q6k_q8,
  * csrc/libtinygiant.c:223-272, :384-443, with the f32 additions grouped
- * differently); 0 keeps every such layer on the v_dot4 phases.  Default 64.
+ * differently); 0 keeps every such layer on the v_dot4 phases.  Default 40.
  * Returns the previous setting.  No counterpart in the reference. */
 int tg_hip_set_moe_qk_min_rows(int rows);
 /* Q4_K / Q6_K expert layers, and MXFP4 ones below the MFMA threshold, run

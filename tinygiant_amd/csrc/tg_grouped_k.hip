@@ -31,7 +31,7 @@
  * in LDS (Q6_K blocks re-spaced to 224 bytes so every field is aligned, each
  * load inside its block, since a buffer load that runs past the matrix end
  * reads zero as a whole); the
- * eight waves split the row's blocks (Q4_K) or half-blocks (Q6_K); each pass
+ * four waves split the row's blocks (Q4_K) or half-blocks (Q6_K); each pass
  * runs 16 pairs of the expert against the resident slab, their q8 operands
  * read from the q8 rows in global memory; 256 threads add the waves' partial
  * sums in wave order and write one result each.  HBM sees each weight byte
@@ -53,7 +53,10 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int NW = 8;                    /* waves per workgroup */
+/* four waves a workgroup: three workgroups (twelve waves, three slabs in
+ * flight) share a CU, within its LDS; eight waves a workgroup measured 16%
+ * slower (two workgroups a CU) */
+constexpr int NW = 4;                    /* waves per workgroup */
 constexpr int NT = 64 * NW;
 constexpr uint32_t OOB = 0x80000000u;    /* past every buffer: the load reads zero */
 constexpr uint32_t Q4B = 144, Q6B = 210; /* bytes per 256-value block */
@@ -107,7 +110,7 @@ __device__ inline int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) &
  * a.ed[blockIdx.y]; Q4_K gate and up matrices of D = 256 nb columns.  The
  * slabs arrive by direct-to-LDS copies, while the first pass's q8 operands
  * load into registers. */
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_qa(MoeArgs a) {
+__global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const ExpDesc &ex = a.ed[blockIdx.y];
     const int e = ex.e, p0 = ex.p0, np = ex.np;
@@ -142,16 +145,15 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
     /* pair c16's q8 operands of block b: sub-block s = 2 jg + half covers
      * x[64 jg + 32 half ...], this lane's K slice 8 g .. 8 g + 7 */
     long xb[8];
-    int bs[8];
+    float bsg0, bsg1;   /* the pair's 32-value sums of sub-blocks g and 4 + g */
     float xd;
     auto load_x = [&](uint32_t prow, bool pv, int b) {
         const uint32_t qb = prow * (uint32_t)nb + (uint32_t)b;
 #pragma unroll
         for (int s = 0; s < 8; s++)
             xb[s] = as_long(ld8(qs_b, pv ? qb * 256u + 64u * (s >> 1) + 32u * (s & 1) + 8u * g : OOB));
-        const u32x4 bs0 = ld16(s32_b, pv ? qb * 32u : OOB), bs1 = ld16(s32_b, pv ? qb * 32u + 16u : OOB);
-        bs[0] = (int)bs0.x, bs[1] = (int)bs0.y, bs[2] = (int)bs0.z, bs[3] = (int)bs0.w;
-        bs[4] = (int)bs1.x, bs[5] = (int)bs1.y, bs[6] = (int)bs1.z, bs[7] = (int)bs1.w;
+        bsg0 = (float)(int)ld4(s32_b, pv ? qb * 32u + 4u * g : OOB);
+        bsg1 = (float)(int)ld4(s32_b, pv ? qb * 32u + 16u + 4u * g : OOB);
         xd = __uint_as_float(ld4(d_b, pv ? qb * 4u : OOB));
     };
     int t0 = 0;
@@ -176,8 +178,8 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
                  * lane group; products and sums are integers below 2^24, exact) */
                 const Q4Hdr hr = q4_hdr(*(const u32x4 *)(sb + c16 * rs + b * Q4B));
                 v4f im = {0.f, 0.f, 0.f, 0.f};
-                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnl, g), (float)bs[g], im, 0, 0, 0);
-                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnh, g), (float)bs[4 + g], im, 0, 0, 0);
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnl, g), bsg0, im, 0, 0, 0);
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnh, g), bsg1, im, 0, 0, 0);
                 /* the scale terms sum_s sc[row][s] idot[row][pair][s]: one int8
                  * MFMA per sub-block, summed exactly in int32 */
                 const uint8_t *ab = sb + c16 * rs + b * Q4B + 16 + 8 * g;   /* row c16's codes */
@@ -200,7 +202,12 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
                     }
                 }
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[m][v] += xd * (hd[v].d * (float)isc[v] - hd[v].dmin * im[v]);
+                for (int v = 0; v < 4; v++) {
+                    /* acc indexed with constants only (m is a loop variable) */
+                    const float t = xd * (hd[v].d * (float)isc[v] - hd[v].dmin * im[v]);
+                    if (m == 0) acc[0][v] += t;
+                    else acc[1][v] += t;
+                }
             }
         }
         /* the waves' partial sums (block order), then one result per thread */
@@ -243,7 +250,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_
  * first pass's q8 operands, then the slab is stored to LDS. */
 constexpr int QB_PIECES = 13;   /* 16-byte pieces of a block's bytes 0-207 */
 constexpr int QB_NPC = 2;       /* pieces per thread loaded ahead of the q8 operands */
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4))) void k_moe_qb(MoeArgs a) {
+__global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const ExpDesc &ex = a.ed[blockIdx.y];
     const int e = ex.e, p0 = ex.p0, np = ex.np;

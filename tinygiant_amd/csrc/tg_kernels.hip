@@ -836,7 +836,7 @@ static int g_grouped_min_rows = 4;
 
 void set_grouped_min_rows(int rows) { g_grouped_min_rows = rows < 0 ? 0 : rows; }
 int grouped_min_rows() { return g_grouped_min_rows; }
-static int g_qk_min_rows = 64;
+static int g_qk_min_rows = 40;
 void set_qk_min_rows(int rows) { g_qk_min_rows = rows < 0 ? 0 : rows; }
 int qk_min_rows() { return g_qk_min_rows; }
 
