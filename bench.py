@@ -854,6 +854,8 @@ def main():
                     help="only time a plain 1 GiB device copy (HBM reference / counter calibration)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only the gpt-oss 64-token prefill layer on the MFMA expert phases (counter passes)")
+    ap.add_argument("--qk-prefill-probe", action="store_true",
+                    help="only the Qwen3 128-token prefill layer (int8 MFMA and v_dot4 expert phases; counter passes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the expert path is "
@@ -864,6 +866,16 @@ def main():
     lib = tg.lib()
     if args.copy_probe or args.prefill_probe:
         out = copy_probe(tg) if args.copy_probe else prefill_probe(tg)
+        lib.tg_hip_shutdown()
+        print(json.dumps(out), flush=True)
+        return 0
+    if args.qk_prefill_probe:
+        qbufs, qplans = setup_gpu(tg, 1, routing(1))
+        out = qwen_prefill_probe(tg, qbufs[0].ptr, tokens=(128,), iters=10)
+        for p in qplans:
+            lib.tg_hip_moe_plan_destroy(p)
+        for b in qbufs:
+            b.free()
         lib.tg_hip_shutdown()
         print(json.dumps(out), flush=True)
         return 0
