@@ -619,7 +619,20 @@ __global__ __launch_bounds__(256) void k_moe_combine(MoeArgs a) {
     if (idx >= (size_t)a.k * a.D) return;
     const int row = (int)(idx / a.D), c = (int)(idx % a.D);
     float o = a.out[idx];
-    for (int q = a.r_off[row]; q < a.r_off[row + 1]; q++) o += a.part[(size_t)a.r_pair[q] * a.D + c];
+    /* eight pairs at a time: their indices, then their partials, each group
+     * of loads in flight together; the additions stay in expert order */
+    const int q0 = a.r_off[row], q1 = a.r_off[row + 1];
+    for (int qb = q0; qb < q1; qb += 8) {
+        int pr[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) pr[i] = qb + i < q1 ? a.r_pair[qb + i] : 0;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = qb + i < q1 ? a.part[(size_t)pr[i] * a.D + c] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+            if (qb + i < q1) o += v[i];
+    }
     a.out[idx] = o;
 }
 
