@@ -64,6 +64,14 @@ constexpr int FMT_FP8 = 0, FMT_FP4 = 4; /* MFMA operand formats */
 constexpr int NPRE = 4;                 /* passes whose pair rows and weights are fetched with the expert */
 constexpr int SCALE_1 = 127, SCALE_16 = 131;
 
+/* Slab bytes are read once per call: nontemporal loads (measured 3-6%
+ * faster on a 64-token gpt-oss prefill than regular ones; the Q4_K / Q6_K
+ * phases, whose lanes share 16-byte pieces of a line, lose with them). */
+constexpr int CPOL_NT = 2;
+__device__ inline u32x4 ld16_nt(Buf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, CPOL_NT);
+}
+
 /* Read-only tables through explicit address spaces: wave-uniform reads of
  * the constant space become scalar loads (counted apart from the vector
  * loads), per-lane reads of the global space in-order vector loads. */
@@ -282,7 +290,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
 #pragma unroll
             for (int c = 0; c < CH; c++) {
                 const uint32_t i = (uint32_t)(tid + NT * c) * 16u;
-                v[m][c] = ld16(iss_w[m], i < slab ? off + i : OOB);
+                v[m][c] = ld16_nt(iss_w[m], i < slab ? off + i : OOB);
             }
     };
 
