@@ -664,7 +664,7 @@ def prefill_probe(tg, iters=20, tokens=64):
     return out
 
 
-def head_probe(tg, ks=(1, 5, 9), iters=20):
+def head_probe(tg, ks=(1, 5, 9, 16), iters=20):
     """The q6_K output head of Qwen3-30B-A3B (151936 x 2048, 255,252,480 B) over
     k verify rows with the argmax fused in (tg_hip_head_argmax_dev, RMSNorm
     weight applied): time per call from HIP events, weight bytes read once."""

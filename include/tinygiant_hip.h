@@ -319,6 +319,14 @@ int tg_hip_set_moe_grouped_min_rows(int rows);
  * differently); 0 keeps every such layer on the v_dot4 phases.  Default 40.
  * Returns the previous setting.  No counterpart in the reference. */
 int tg_hip_set_moe_qk_min_rows(int rows);
+/* The fused q6_K head (tg_hip_head_argmax_dev) reads the head on int8 MFMA
+ * from `k` input rows on: each block's integer sum is exact and its term
+ * d * d_x * sum is added in block order, as dot_q6k_q8 does
+ * (csrc/libtinygiant.c:403-443); below `k` the v_dot4 kernel runs (its work
+ * grows with the row count); 0 keeps every call on the v_dot4 kernel.
+ * Default 14.  Returns the previous setting.  No counterpart in the
+ * reference. */
+int tg_hip_set_head_mfma_min_k(int k);
 /* Q4_K / Q6_K expert layers, and MXFP4 ones below the MFMA threshold, run
  * expert-major (bit 1): each weight row is
  * read once and dotted with the q8 row of every pair of its expert, as

@@ -225,3 +225,75 @@ def test_head_q6k_scratch_reused_across_calls(tg, orc):
     finally:
         for a in (md, sd, ad, vd, xd):
             a.free()
+
+
+class _head_kernel:
+    """Sets the input-row count from which the head runs on int8 MFMA."""
+
+    def __init__(self, tg, k):
+        self.lib, self.k = tg.lib(), k
+
+    def __enter__(self):
+        self.prev = self.lib.tg_hip_set_head_mfma_min_k(self.k)
+
+    def __exit__(self, *exc):
+        self.lib.tg_hip_set_head_mfma_min_k(self.prev)
+
+
+@pytest.mark.parametrize("k", [1, 2, 5, 9, 16])
+def test_head_q6k_mfma_logits_bit_exact(tg, orc, k):
+    """The int8 MFMA head (every k, forced on): each block's integer sum is
+    exact and its term d * d_x * sum is added in block order, the oracle's
+    row loop, so the logits equal the oracle's tg_matmul bit for bit (the
+    oracle's float block sums stay below 2^24 here, where they are exact);
+    3001 rows end in a partial 16-row item."""
+    import tinygiant_amd.synth as S
+    nrows, ncols = 3001, 2048
+    say(f"head q6k mfma k={k}")
+    mat = S.matrix_host(Q6K, S.tensor_seed(18, 0, 0, 3), nrows, ncols)
+    x = np.random.default_rng(200 + k).standard_normal((k, ncols)).astype(np.float32)
+    with _head_kernel(tg, 1):
+        logits, am, mv = _head(tg, Q6K, mat, x, nrows, ncols)
+    ref = _oracle(orc, Q6K, mat, x, nrows, ncols)
+    assert logits.tobytes() == ref.tobytes(), np.abs(logits - ref).max() / np.abs(ref).max()
+    _check(ref, logits, am, mv, 0.0)
+
+
+def test_head_q6k_mfma_equals_dot4(tg, orc):
+    """The same 9-row batch through both kernels: logits within the f32 bar
+    of each other, the same argmax (no near tie in this batch)."""
+    import tinygiant_amd.synth as S
+    nrows, ncols, k = 4099, 2048, 9
+    mat = S.matrix_host(Q6K, S.tensor_seed(19, 0, 0, 3), nrows, ncols)
+    x = np.random.default_rng(9).standard_normal((k, ncols)).astype(np.float32)
+    out = {}
+    for name, kk in (("mfma", 1), ("dot4", 0)):
+        with _head_kernel(tg, kk):
+            out[name] = _head(tg, Q6K, mat, x, nrows, ncols)
+    lm, am_m, _ = out["mfma"]
+    ld, am_d, _ = out["dot4"]
+    assert np.abs(lm - ld).max() <= 1e-5 * np.abs(ld).max()
+    assert list(am_m) == list(am_d)
+
+
+def test_head_q6k_mfma_ties_and_zero_rows(tg, orc):
+    """numpy.argmax's rule on the MFMA kernel: an all-zero head gives row 0
+    for every input row; two identical winning rows give the first."""
+    import tinygiant_amd.synth as S
+    nrows, ncols, rb, k = 1040, 2048, 8 * 210, 6
+    x = np.random.default_rng(3).standard_normal((k, ncols)).astype(np.float32)
+    zero = np.zeros(nrows * rb, np.uint8)
+    with _head_kernel(tg, 1):
+        _, am, mv = _head(tg, Q6K, zero, x, nrows, ncols)
+        assert list(am) == [0] * k and list(mv) == [0.0] * k
+        src = S.matrix_host(Q6K, S.tensor_seed(20, 0, 0, 3), 1, ncols)
+        mat = zero.copy()
+        mat[333 * rb:334 * rb] = src
+        mat[1001 * rb:1002 * rb] = src
+        logits, am, _ = _head(tg, Q6K, mat, x, nrows, ncols)
+    for j in range(k):
+        assert logits[j][333] == logits[j][1001]
+        if logits[j][333] > 0:
+            assert am[j] == 333
+        else:
+            assert logits[j][am[j]] == 0.0 and am[j] == 0

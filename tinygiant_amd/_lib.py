@@ -107,6 +107,7 @@ def register_extensions(lib):
     _reg(lib.tg_hip_mark, [CI])
     _reg(lib.tg_hip_set_moe_grouped_min_rows, [CI], CI)
     _reg(lib.tg_hip_set_moe_qk_min_rows, [CI], CI)
+    _reg(lib.tg_hip_set_head_mfma_min_k, [CI], CI)
     _reg(lib.tg_hip_set_moe_expert_major, [CI], CI)
     _reg(lib.tg_hip_marks_ms, [CI, CI], CF)
     _reg(lib.tg_hip_rms_norm_dev, [VP, VP, VP, CI, CI, CF, VP])

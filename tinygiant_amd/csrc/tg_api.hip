@@ -1955,6 +1955,13 @@ TG_API int tg_hip_set_moe_qk_min_rows(int rows) {
     return prev;
 }
 
+/* Input-row count from which the fused q6_K head runs on int8 MFMA (0:
+ * never); returns the previous setting. */
+TG_API int tg_hip_set_head_mfma_min_k(int k) {
+    std::lock_guard<std::recursive_mutex> lk(g_mu);
+    return set_head_mfma_min_k(k);
+}
+
 /* Q4_K / Q6_K expert layers: expert-major phases (mode bits, default 7) or
  * one workgroup column per pair (0); the same bits either way.  Returns the
  * previous mode. */

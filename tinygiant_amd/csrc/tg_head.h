@@ -19,6 +19,9 @@ bool head_fast_ok(int fmt, int ncols, int k);
 constexpr int HEAD_KEY_WORDS = 17;
 void launch_head_q6k(const uint8_t *W, int nrows, const Q8Rows &x, int k, float *logits, unsigned long long *best,
                      int32_t *idx, float *val, hipStream_t st);
+/* k at which launch_head_q6k switches to the int8 MFMA kernel (0: never);
+ * returns the previous setting */
+int set_head_mfma_min_k(int k);
 /* argmax keys of materialized logits [k][nrows] */
 void launch_argmax_rows(const float *logits, int nrows, int k, unsigned long long *best, hipStream_t st);
 /* keys -> row index and logit */

@@ -17,6 +17,10 @@
  *                   the best (logit, row) per input row, commits it with one
  *                   64-bit atomic max, and the last workgroup to finish
  *                   writes the argmax.
+ *   k_head_q6k_mfma the same head on int8 MFMA for 14 or more rows: 16 vocab
+ *                   rows an item, one 256-block per wave, logits formed and
+ *                   added block by block as the reference does (bit-equal
+ *                   to it where its float block sums are exact).
  *   k_argmax_rows   argmax of materialized logits (any format, via k_gemv).
  *
  * Argmax keys pack an order-preserving image of the f32 logit above the
@@ -31,6 +35,7 @@
 #include "tg_common.h"
 #include "tg_device.hpp"
 #include "tg_head.h"
+#include "tg_xchg.hpp"
 
 namespace tg {
 
@@ -223,6 +228,245 @@ __global__ __launch_bounds__(HT) void k_head_q6k(const uint8_t *__restrict__ W, 
     }
 }
 
+/* ---- the same head on int8 MFMA (v_mfma_i32_16x16x32_i8) ----
+ * A work item is 16 vocab rows; the eight waves of a workgroup take one
+ * 256-block each.  Operand layout (gfx950): A lane l = row l % 16 with
+ * K = 8 (l / 16) + byte, B lane l = input row l % 16 with the same K,
+ * D lane l register v = row 4 (l / 16) + v, input row l % 16.  A 32-value
+ * run of a half-block is one MFMA K; its two 16-value sub-blocks come apart
+ * by running it twice with the B operand zeroed in one half of K, and each
+ * sub-block's sum takes its int8 sub-scale in integer.  The -32 offset of
+ * the codes enters as 32 x sum_s sc[s] * xsum[s] over a half's 8
+ * sub-blocks (two f32 MFMAs of K = 4; integers below 2^24, exact).  So a
+ * block's integer sum is exact and its term d * d_x * sum is formed as the
+ * reference forms it; the workgroup adds the eight blocks' terms in block
+ * order, as the reference's row loop does (dot_q6k_q8, csrc/libtinygiant.c
+ * :403-443). */
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+constexpr int MW = 8;            /* waves: one 256-block each */
+constexpr int MT = 64 * MW;
+
+__device__ inline long as_long(u32x2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
+__device__ inline v4i mma_i8(long a, long b) {
+    const v4i z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, z, 0, 0, 0);
+}
+
+/* One lane's share of a 16-row item in block w: its A row's codes (both
+ * halves), the row's 16 sub-scales and d (the other lanes' D rows take
+ * theirs from the lanes that hold them) */
+struct MItem {
+    u32x2 ql[2][2];   /* [half h][run parity p]: 8 bytes at 64 h + 32 p + 8 g */
+    u32x2 qh[2];      /* [half h]: 8 bytes at 128 + 32 h + 8 g */
+    u32x4 sc;         /* the block's 16 sub-scales */
+    uint32_t dd;      /* bytes 206..209: d in the high half */
+};
+/* The item loads are issued from inline assembly, untracked by the
+ * compiler: across the rotation of five register sets below its wait
+ * analysis lost count and waited for every prefetched item before each
+ * compute.  The loop waits itself (wait_item): an item is MLOADS loads,
+ * items are issued in order and the counter completes in order, so with
+ * PF later items issued, vmcnt(PF * MLOADS) leaves exactly those in
+ * flight. */
+constexpr int MLOADS = 8;
+template <int OFF>
+__device__ inline u32x2 ldw8(const u32x4 &d, uint32_t v) {
+    u32x2 r;
+    asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ inline u32x4 ldw16(const u32x4 &d, uint32_t v) {
+    u32x4 r;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ inline uint32_t ldw4(const u32x4 &d, uint32_t v) {
+    uint32_t r;
+    asm volatile("buffer_load_dword %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    return r;
+}
+__device__ inline MItem load_mitem(const u32x4 &d, uint32_t r0, int w, int c16, int g) {
+    MItem it;
+    const uint32_t ba = (r0 + (uint32_t)c16) * HRB + 210u * (uint32_t)w, bq = ba + 8u * (uint32_t)g;
+    it.ql[0][0] = ldw8<0>(d, bq);
+    it.ql[0][1] = ldw8<32>(d, bq);
+    it.ql[1][0] = ldw8<64>(d, bq);
+    it.ql[1][1] = ldw8<96>(d, bq);
+    it.qh[0] = ldw8<128>(d, bq);
+    it.qh[1] = ldw8<160>(d, bq);
+    it.sc = ldw16<192>(d, ba);
+    it.dd = ldw4<206>(d, ba);
+    return it;
+}
+/* the item's loads have completed once at most N later loads are in flight;
+ * the operands tie its registers to the wait */
+template <int N>
+__device__ inline void wait_item(MItem &it) {
+    asm volatile("s_waitcnt vmcnt(%8)"
+                 : "+v"(it.ql[0][0]), "+v"(it.ql[0][1]), "+v"(it.ql[1][0]), "+v"(it.ql[1][1]), "+v"(it.qh[0]),
+                   "+v"(it.qh[1]), "+v"(it.sc), "+v"(it.dd)
+                 : "n"(N));
+}
+
+}  // namespace
+
+/* Q6_K head, 2048 columns, k <= 16 input rows: the contract of k_head_q6k. */
+__global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
+                                                     float *logits, unsigned long long *best, int32_t *idx,
+                                                     float *val) {
+    __shared__ __attribute__((aligned(16))) float red[2][MW][4][64];
+    __shared__ unsigned long long wb_best[16][16];
+    __shared__ int last_wg;
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+
+    /* input row c16's operands of block w, for the whole kernel: run m of
+     * half h at K slice 8 g .. 8 g + 7, zeroed outside the sub-block each
+     * MFMA of a pair keeps; the 16-value sums this lane's K of the offset
+     * MFMAs needs; the block scale.  Rows c16 >= k read zeros (the buffers
+     * end at row k). */
+    long x0[2][4], x1[2][4];
+    float s16a[2], s16b[2];
+    float xd;
+    {
+        const Buf qs_b = make_buf(x.qs, (uint32_t)k * NBH * 256u);
+        const Buf s16_b = make_buf(x.s16, (uint32_t)k * NBH * 64u);
+        const uint32_t qo = ((uint32_t)c16 * NBH + (uint32_t)w) * 256u;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const long xb = as_long(ld8(qs_b, qo + 128u * h + 32u * m + 8u * (uint32_t)g));   /* 0 past k */
+                x0[h][m] = g < 2 ? xb : 0l;
+                x1[h][m] = g < 2 ? 0l : xb;
+            }
+            const uint32_t so = ((uint32_t)c16 * NBH + (uint32_t)w) * 64u + 32u * h;
+            s16a[h] = (float)(int)ld4(s16_b, so + 4u * (uint32_t)g);
+            s16b[h] = (float)(int)ld4(s16_b, so + 16u + 4u * (uint32_t)g);
+        }
+        const Buf d_b = make_buf(x.d, (uint32_t)k * NBH * 4u);
+        xd = __uint_as_float(ld4(d_b, ((uint32_t)c16 * NBH + (uint32_t)w) * 4u));
+    }
+
+    const int nq = (nrows + 15) / 16;
+    const u32x4 wd = buf_desc(W, (uint32_t)((size_t)nrows * HRB));   /* rows past nrows read zeros */
+    /* the operand loads above complete before any untracked item load goes out */
+    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
+    /* epilogue thread (tid < 256): D register ev of lane el */
+    const int ev = tid >> 6, el = tid & 63, ej = el & 15;
+    uint64_t mybest = 0;
+    int q = blockIdx.x, it = 0;
+    /* one item: the loads of the item PF ahead go out first (PF + 1 register
+     * sets take turns, so no copy waits for them), then this item is
+     * computed */
+    constexpr int PF = 4;
+    auto item = [&](MItem &cur, MItem &nxt) {
+        nxt = load_mitem(wd, 16u * (uint32_t)(q + PF * (int)gridDim.x), w, c16, g);
+        wait_item<PF * MLOADS>(cur);
+        /* the sub-scales and d of D rows 4 g + v, from the lanes holding those rows */
+        u32x4 sc[4];
+        float dv[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) {
+            const int src = 4 * g + v;
+            sc[v].x = (uint32_t)__shfl((int)cur.sc.x, src, 64);
+            sc[v].y = (uint32_t)__shfl((int)cur.sc.y, src, 64);
+            sc[v].z = (uint32_t)__shfl((int)cur.sc.z, src, 64);
+            sc[v].w = (uint32_t)__shfl((int)cur.sc.w, src, 64);
+            dv[v] = ref_f16((uint32_t)__shfl((int)cur.dd, src, 64) >> 16);
+        }
+        int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t sw0 = h ? cur.sc.z : cur.sc.x, sw1 = h ? cur.sc.w : cur.sc.y;
+            v4f cf = {0.f, 0.f, 0.f, 0.f};
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(sw0 >> (8 * g)), s16a[h], cf, 0, 0, 0);
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(sw1 >> (8 * g)), s16b[h], cf, 0, 0, 0);
+            int ai[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const u32x2 ql = cur.ql[h][m & 1], qh = cur.qh[h];
+                const int sl = 4 * (m >> 1), sh = 2 * m;
+                u32x2 c;
+                c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
+                c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
+                const v4i d0 = mma_i8(as_long(c), x0[h][m]), d1 = mma_i8(as_long(c), x1[h][m]);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const u32x4 &s = sc[v];
+                    const uint32_t sw = (m >> 1) ? (h ? s.w : s.y) : (h ? s.z : s.x);
+                    const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))), sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
+                    ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 per term */
+                }
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) isum[v] += ai[v] - 32 * (int)cf[v];
+        }
+        /* the block's term d * d_x * sum, as the reference forms it */
+        float (&rb)[MW][4][64] = red[it & 1];
+#pragma unroll
+        for (int v = 0; v < 4; v++) rb[w][v][lane] = __fmul_rn(__fmul_rn(dv[v], xd), (float)isum[v]);
+        bar_lds();   /* LDS only: the prefetched items stay in flight */
+        if (tid < 256) {
+            const uint32_t row = 16u * (uint32_t)q + 4u * (uint32_t)(el >> 4) + (uint32_t)ev;
+            float s = 0.f;
+#pragma unroll
+            for (int b = 0; b < MW; b++) s = __fadd_rn(s, rb[b][ev][el]);
+            if (ej < k && row < (uint32_t)nrows) {
+                if (logits) logits[(size_t)ej * nrows + row] = s;
+                const uint64_t key = argmax_key(s, row);
+                mybest = key > mybest ? key : mybest;
+            }
+        }
+        q += gridDim.x;
+        it++;
+    };
+    const int G = (int)gridDim.x;
+    MItem s0 = load_mitem(wd, 16u * (uint32_t)q, w, c16, g);
+    MItem s1 = load_mitem(wd, 16u * (uint32_t)(q + G), w, c16, g);
+    MItem s2 = load_mitem(wd, 16u * (uint32_t)(q + 2 * G), w, c16, g);
+    MItem s3 = load_mitem(wd, 16u * (uint32_t)(q + 3 * G), w, c16, g);
+    MItem s4;
+    static_assert(PF == 4, "five register sets below");
+    for (;;) {
+        if (q >= nq) break;
+        item(s0, s4);
+        if (q >= nq) break;
+        item(s1, s0);
+        if (q >= nq) break;
+        item(s2, s1);
+        if (q >= nq) break;
+        item(s3, s2);
+        if (q >= nq) break;
+        item(s4, s3);
+    }
+    /* the prefetched items past the end land before the wave ends */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    /* workgroup best per input row (16 epilogue threads each), then one
+     * atomic max each; the last workgroup writes the result */
+    if (tid < 256) wb_best[ej][ev * 4 + (el >> 4)] = mybest;
+    __syncthreads();
+    if (tid < k) {
+        uint64_t m = 0;
+        for (int i = 0; i < 16; i++) m = wb_best[tid][i] > m ? wb_best[tid][i] : m;
+        /* the returned value is stored (to a slot already read), so the max
+         * has been performed before this thread reaches the barrier below */
+        wb_best[tid][0] = atomicMax(&best[tid], (unsigned long long)m);
+    }
+    __syncthreads();
+    if (tid == 0) last_wg = atomicAdd(&best[16], 1ull) == (unsigned long long)(gridDim.x - 1);
+    __syncthreads();
+    if (last_wg == 1 && tid < k) {
+        const uint64_t key = __hip_atomic_load(&best[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        idx[tid] = (int32_t)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFu));
+        if (val) val[tid] = key_value(key);
+    }
+}
+
 /* argmax of logits [k][nrows] (one workgroup per input row) */
 __global__ __launch_bounds__(256) void k_argmax_rows(const float *__restrict__ logits, int nrows,
                                                      unsigned long long *best) {
@@ -252,11 +496,34 @@ __global__ void k_argmax_finish(const unsigned long long *best, int k, int32_t *
 
 bool head_fast_ok(int fmt, int ncols, int k) { return fmt == TG_FMT_Q6K && ncols == NBH * 256 && k >= 1 && k <= 16; }
 
+/* From this many input rows the int8 MFMA kernel reads the head: its work
+ * does not grow with k (151936 x 2048: 92-96 us for every k), the v_dot4
+ * kernel's does (73 us at k = 9, 99 at 14, 109 at 16). */
+#ifndef TG_HEAD_MFMA_MIN_K
+#define TG_HEAD_MFMA_MIN_K 14
+#endif
+static int g_head_mfma_min_k = TG_HEAD_MFMA_MIN_K;
+int set_head_mfma_min_k(int k) {
+    const int prev = g_head_mfma_min_k;
+    g_head_mfma_min_k = k < 0 ? 0 : k;
+    return prev;
+}
+
 void launch_head_q6k(const uint8_t *W, int nrows, const Q8Rows &x, int k, float *logits, unsigned long long *best,
                      int32_t *idx, float *val, hipStream_t st) {
     int dev = 0, cus = 0;
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (g_head_mfma_min_k > 0 && k >= g_head_mfma_min_k) {
+        static int occ = -1;
+        if (occ < 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_head_q6k_mfma, MT, 0) != hipSuccess ||
+                        occ < 1))
+            occ = 1;
+        const int nq = (nrows + 15) / 16;
+        const int grid = std::max(1, std::min(std::max(cus, 1) * occ, nq));
+        hipLaunchKernelGGL(k_head_q6k_mfma, dim3(grid), dim3(MT), 0, st, W, nrows, x, k, logits, best, idx, val);
+        return;
+    }
     const int nq = (nrows + RPW - 1) / RPW;
     const int grid = std::max(1, std::min(cus * 4, (nq + HW - 1) / HW));
 /* k is rounded up to an instantiated K; rows j >= k skip their dots */
