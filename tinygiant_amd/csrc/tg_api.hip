@@ -1488,6 +1488,7 @@ struct tg_hip_decode {
     uint8_t *debug = nullptr;
     uint64_t *times = nullptr;
     uint8_t *qdown = nullptr;    /* Qwen3 kernel: the layers' down matrices in the row-group layout */
+    uint8_t *mxgu = nullptr;     /* gpt-oss kernel: the layers' gate and up matrices in the wave-segment layout */
     unsigned *place = nullptr;   /* Qwen3 kernel: HW_REG_XCC_ID of each workgroup, last launch */
     int pol = 0;                 /* persistent kernels: 1 = every exchange slot stored device-coherently */
     int placement_bad = 0;       /* a launch ran with workgroup g off XCD g % 8 */
@@ -1701,8 +1702,21 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
         HIPCHECK(hipMalloc(&d->place, DECODE_GRID * sizeof(unsigned)));
         HIPCHECK(hipMemset(d->place, 0xFF, DECODE_GRID * sizeof(unsigned)));
         if (d->kind == 1) {
+            /* the kernel reads each gate and up matrix in the wave-segment
+             * layout: one rewritten copy per (layer, expert slot, matrix) */
+            const size_t mb = decode_mx_seg_bytes();
+            HIPCHECK(hipMalloc(&d->mxgu, lm.size() * DECODE_MX_E * 2 * mb));
+            for (size_t l = 0; l < lm.size(); l++)
+                for (int e = 0; e < DECODE_MX_E; e++) {
+                    uint8_t *dg = d->mxgu + ((l * DECODE_MX_E + e) * 2) * mb, *du = dg + mb;
+                    HIPCHECK(launch_mx_wave_segments(lm[l].gate[e], dg, g.st));
+                    HIPCHECK(launch_mx_wave_segments(lm[l].up[e], du, g.st));
+                    lm[l].gate[e] = dg;
+                    lm[l].up[e] = du;
+                }
             HIPCHECK(hipMalloc(&d->layers_mx, lm.size() * sizeof(DecodeLayerMx)));
             HIPCHECK(hipMemcpy(d->layers_mx, lm.data(), lm.size() * sizeof(DecodeLayerMx), hipMemcpyHostToDevice));
+            HIPCHECK(hipStreamSynchronize(g.st));
         } else {
             /* the kernel reads each down matrix in the row-group layout: one
              * rewritten copy per (layer, expert slot) */
@@ -1861,6 +1875,7 @@ TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
     if (d->hidden) HIPCHECK(hipFree(d->hidden));
     if (d->sync) HIPCHECK(hipFree(d->sync));
     if (d->qdown) HIPCHECK(hipFree(d->qdown));
+    if (d->mxgu) HIPCHECK(hipFree(d->mxgu));
     if (d->place) HIPCHECK(hipFree(d->place));
     delete d;
 }

@@ -40,8 +40,9 @@
  *   this layer's down rows (one contiguous 45-row range) after the h gather
  *   (1), gathered into registers during the hidden exchange (4);
  *   the next layer's gate segments (each compute wave the 272-byte pieces of
- *   its own K range, into its own part of the region) at q8 of the hidden
- *   vector (5), moved into registers at the hop (7);
+ *   its own K range, one contiguous range of the wave-segment layout made
+ *   when the step is created, into its own part of the region) at q8 of the
+ *   hidden vector (5), moved into registers at the hop (7);
  *   the next layer's up segments, the same way, at the hop (7), moved into
  *   registers at the next layer's start.
  * Two communication waves per workgroup publish; the two gathers are polled
@@ -91,13 +92,24 @@ constexpr int NTS = 24;               /* timing words per layer */
 constexpr int FMT_FP8 = 0, FMT_FP4 = 4, SCALE_1 = 127, SCALE_16 = 131;
 constexpr uint32_t OOB = 0x80000000u;  /* past every buffer: reads zeros, touches no memory */
 constexpr int NDMA = 68;               /* 1 KiB direct-to-LDS copy steps of the down rows (16 bytes a lane) */
-constexpr int GSEG = 18;               /* 16-byte chunks of a wave's gate segment of one row (272 bytes + alignment) */
-constexpr int GINS = (RS * GSEG + 63) / 64;   /* copy steps per wave for its gate segments: 13 */
-constexpr int GREG = GINS * 1024;      /* LDS bytes of a wave's gate segments */
+/* Gate and up matrices arrive in a wave-segment layout made when the step
+ * is created (launch_mx_wave_segments): for each 45-row rank slice, compute
+ * wave w's 16 blocks [16 w, 16 w + 16) of every row (272 bytes; the last
+ * wave's 10 blocks, 170 bytes, at a 176-byte stride) lie contiguous and
+ * 16-byte aligned, so a wave copies its segments as one range. */
+constexpr int SEGB = 16 * 17;                          /* a wave's segment of one row: 272 bytes */
+constexpr int SEGL = (NBLK - 16 * (NW - 1)) * 17;      /* the last wave's: 170 bytes */
+constexpr int SEGLS = (SEGL + 15) & ~15;               /* its stride: 176 */
+constexpr int WSB = RS * SEGB;                         /* a wave's range of one slice: 12,240 bytes */
+constexpr int SLB = (NW - 1) * WSB + RS * SEGLS;       /* one slice: 69,120 bytes */
+constexpr uint32_t MXSEG_BYTES = (uint32_t)NRK * SLB;  /* one rewritten matrix: 4,423,680 bytes */
+constexpr int GINS = (WSB + 1023) / 1024;              /* copy steps of a wave's segments: 12 */
+constexpr int GINSL = (RS * SEGLS + 1023) / 1024;      /* the last wave's: 8 */
+constexpr int GREG = GINS * 1024;                      /* LDS bytes of a wave's segments */
 constexpr int DZERO = NW * GREG;       /* 32 zero bytes after the copies, read by off-slice lanes */
 constexpr int DWS = DZERO + 32;        /* LDS staging of the slice's gate rows, then its down rows */
 static_assert(RS * RB + 15 <= NDMA * 1024 && NDMA * 1024 <= DZERO, "the slice's down rows fit the staging");
-static_assert(16 * 17 + 15 <= GSEG * 16, "a wave's 16 blocks of a row fit its gate segment");
+static_assert(NBLK > 16 * (NW - 1) && NBLK <= 16 * NW && WSB % 16 == 0 && SLB % 16 == 0, "wave segments");
 static_assert(NE * 2 == NX, "two XCDs per expert");
 static_assert(NRK * RS == D && RS % VPS == 0 && NG * 16 >= RS && RS <= 64, "slices");
 static_assert(NW * CPW >= NCH && (NW - 1) * CPW < NCH, "chunks per wave");
@@ -256,21 +268,19 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     u32x4 nw0, nw1;          /* next layer's RMSNorm weight (compute lanes) */
 
     /* Gate and up rows: compute wave w uses blocks [16 w, 16 w + 16) of each
-     * of the slice's 45 rows, 272 bytes a row.  It copies those segments of
-     * the matrix `mat`, from the 16-byte boundary at or below each start,
-     * into its own region of dws (row sr at 288 sr) with direct-to-LDS
-     * loads, and later gathers its blocks from there into registers: no
-     * other wave touches the region, so only the wave's own copy has to have
-     * landed, and the wave can copy the next matrix in as soon as it has
-     * gathered the last one.  An inactive call reads through an empty
-     * descriptor (zeros). */
+     * of the slice's 45 rows.  In the wave-segment layout they are one
+     * aligned range, which the wave copies into its own region of dws with
+     * direct-to-LDS loads and later gathers into registers: no other wave
+     * touches the region, so only the wave's own copy has to have landed,
+     * and the wave can copy the next matrix in as soon as it has gathered
+     * the last one.  An inactive call reads through an empty descriptor
+     * (zeros). */
+    const int ginsw = wave == NW - 1 ? GINSL : GINS;
+    const uint32_t segst = wave == NW - 1 ? (uint32_t)SEGLS : (uint32_t)SEGB;
     auto fetch_seg = [&](const uint8_t *mat, bool on) {
-        const u32x4 desc = buf_desc(on ? mat : nullptr, on ? (uint32_t)D * RB : 0u);
-        for (int k = 0; k < GINS; k++) {
-            const int sidx = 64 * k + lane, sr = sidx / GSEG, j = sidx - sr * GSEG;
-            const uint32_t a = ((uint32_t)(RS * R + sr) * (uint32_t)RB + 272u * (uint32_t)wave) & ~15u;
-            copy_lanes(desc, sr < RS ? a + 16u * (uint32_t)j : OOB, lds_addr(dws + GREG * wave + 1024 * k));
-        }
+        const u32x4 desc = buf_desc(on ? mat : nullptr, on ? MXSEG_BYTES : 0u);
+        const uint32_t a0 = (uint32_t)R * SLB + (uint32_t)wave * WSB;
+        for (int k = 0; k < ginsw; k++) copy_1k(desc, a0 + 1024u * (uint32_t)k, lds_addr(dws + GREG * wave + 1024 * k), lane);
     };
     /* The slice's down rows are one contiguous 45-row range of the expert's
      * down matrix.  The compute waves copy it into dws with direct-to-LDS
@@ -313,9 +323,7 @@ __global__ __launch_bounds__(NT) void k_decode_mx(const DecodeLayerMx *__restric
     auto seg_blk = [&](int gr, int i) -> MxBlk {
         const int c = CPW * wave + i, b = 4 * c + (lane >> 4), sr = 16 * gr + (lane & 15);
         const bool on = c < NCH && b < NBLK && sr < RS;
-        const uint32_t s0 = (uint32_t)(RS * R + sr) * (uint32_t)RB + 272u * (uint32_t)wave;
-        return lds_blk_at((uint32_t)(GREG * wave + GSEG * 16 * sr) + (s0 & 15u) + (uint32_t)(b - 16 * wave) * 17u,
-                          on);
+        return lds_blk_at((uint32_t)(GREG * wave) + segst * (uint32_t)sr + (uint32_t)(b - 16 * wave) * 17u, on);
     };
     /* the communication waves hold no weights: they zero the registers the
      * compute waves fill, so both paths assign them */
@@ -776,6 +784,30 @@ int decode_mx_max_grid() {
 }
 
 size_t decode_mx_slot_bytes() { return (size_t)NSLOTS * 16; }
+
+/* Rewrites a 2880 x 2880 MXFP4 matrix into the wave-segment layout: slice R
+ * (rows 45 R ..), wave w, row sr at R * SLB + w * WSB + sr * stride(w), the
+ * wave's bytes [272 w, 272 w + len(w)) of the row (the same bytes; the 6
+ * bytes after each last-wave segment are zero).  One thread per (slice,
+ * wave, row), two bytes at a time (every offset is even). */
+__global__ void k_mx_wave_segments(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= NRK * NW * RS) return;
+    const int sr = t % RS, w = (t / RS) % NW, R = t / (RS * NW);
+    const int len = w == NW - 1 ? SEGL : SEGB, st = w == NW - 1 ? SEGLS : SEGB;
+    const uint16_t *s16 = reinterpret_cast<const uint16_t *>(src + (size_t)(RS * R + sr) * RB + (size_t)SEGB * w);
+    uint16_t *d16 = reinterpret_cast<uint16_t *>(dst + (size_t)R * SLB + (size_t)w * WSB + (size_t)sr * st);
+    for (int i = 0; i < st / 2; i++) d16[i] = 2 * i < len ? s16[i] : (uint16_t)0;
+}
+
+size_t decode_mx_seg_bytes() { return MXSEG_BYTES; }
+
+hipError_t launch_mx_wave_segments(const void *src, void *dst, hipStream_t st) {
+    const int n = NRK * NW * RS;
+    hipLaunchKernelGGL(k_mx_wave_segments, dim3((n + 255) / 256), dim3(256), 0, st, (const uint8_t *)src,
+                       (uint8_t *)dst);
+    return hipGetLastError();
+}
 
 hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
                             float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, int pol,
