@@ -41,6 +41,13 @@
 
 #define TG_API extern "C" __attribute__((visibility("default")))
 
+namespace tg {
+/* tg_decode_mx.hip: the gpt-oss step's gate and up matrices in its
+ * wave-segment layout (bytes of one rewritten matrix, and the rewrite) */
+size_t decode_mx_seg_bytes();
+hipError_t launch_mx_wave_segments(const void *src, void *dst, hipStream_t st);
+}  // namespace tg
+
 using namespace tg;
 
 /* Fixed scratch of tg_hip_matmul_dev_noalloc: the q8 rows of its inputs.

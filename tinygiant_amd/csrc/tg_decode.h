@@ -61,10 +61,6 @@ struct DecodeDebugMx {
 };
 int decode_mx_max_grid();
 size_t decode_mx_slot_bytes();
-/* the gate and up matrices of the gpt-oss step in its wave-segment layout:
- * bytes of one rewritten matrix, and the rewrite */
-size_t decode_mx_seg_bytes();
-hipError_t launch_mx_wave_segments(const void *src, void *dst, hipStream_t st);
 hipError_t launch_decode_mx(const DecodeLayerMx *layers_dev, int L, float *h_dev, void *slots_dev, unsigned *abort_dev,
                             float eps, uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, int pol,
                             bool cooperative, hipStream_t st);
