@@ -82,6 +82,51 @@ __device__ inline HHalf load_hhalf(Buf b, uint32_t blk, int h) {
 
 __device__ inline uint32_t pick(const u32x4 &v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
 
+/* Weight loads issued from inline assembly, which the compiler does not
+ * track: the kernels below wait for them themselves (s_waitcnt vmcnt(N) with
+ * N = the loads issued after the ones waited for; the counter completes in
+ * order).  Across register sets that take turns, the compiler's own wait
+ * analysis lost count and waited for every prefetched load. */
+template <int OFF>
+__device__ inline u32x2 ldw8(const u32x4 &d, uint32_t v) {
+    u32x2 r;
+    asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ inline u32x4 ldw16(const u32x4 &d, uint32_t v) {
+    u32x4 r;
+    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    return r;
+}
+template <int OFF>
+__device__ inline uint32_t ldw4(const u32x4 &d, uint32_t v) {
+    uint32_t r;
+    asm volatile("buffer_load_dword %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    return r;
+}
+/* one lane's half-block for k_head_q6k through those loads */
+constexpr int HLOADS = 8;
+__device__ inline HHalf load_hhalf_asm(const u32x4 &d, uint32_t blk, int h) {
+    HHalf r;
+    const uint32_t ql = blk + 64u * (uint32_t)h, qh = blk + 32u * (uint32_t)h;
+    r.la0 = ldw16<0>(d, ql);
+    r.la1 = ldw16<16>(d, ql);
+    r.lb0 = ldw16<32>(d, ql);
+    r.lb1 = ldw16<48>(d, ql);
+    r.h0 = ldw16<128>(d, qh);
+    r.h1 = ldw16<144>(d, qh);
+    r.sc = ldw8<192>(d, blk + 8u * (uint32_t)h);
+    r.d = ldw4<206>(d, blk);
+    return r;
+}
+template <int N>
+__device__ inline void wait_hhalf(HHalf &r) {
+    asm volatile("s_waitcnt vmcnt(%8)"
+                 : "+v"(r.la0), "+v"(r.la1), "+v"(r.lb0), "+v"(r.lb1), "+v"(r.h0), "+v"(r.h1), "+v"(r.sc), "+v"(r.d)
+                 : "n"(N));
+}
+
 }  // namespace
 
 /* One step of the segment reduce-scatter below: the lanes of each pair
@@ -122,7 +167,7 @@ constexpr int log2_of(int n) { return n <= 1 ? 0 : n == 2 ? 1 : n == 4 ? 2 : n =
  * start at zero (cleared by the kernel that quantizes x).  The last
  * workgroup to finish writes idx[j] / val[j]. */
 template <int K>
-__global__ __launch_bounds__(HT) void k_head_q6k(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
+__global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
                                                  float *logits, unsigned long long *best, int32_t *idx, float *val) {
     constexpr int N = pow2_at_least(K);
     __shared__ __attribute__((aligned(16))) int8_t xq[K][HPR * XST];
@@ -149,13 +194,23 @@ __global__ __launch_bounds__(HT) void k_head_q6k(const uint8_t *__restrict__ W, 
     const bool owner = (hb & (16 / N - 1)) == 0 && slot < k;
     const int gw = blockIdx.x * HW + (threadIdx.x >> 6), nw = gridDim.x * HW;
     const int nq = (nrows + RPW - 1) / RPW;
-    Buf wb = make_buf(W, (uint32_t)((size_t)nrows * HRB));   /* rows past nrows read zeros */
     uint64_t mybest = 0;
 
-    HHalf cur = load_hhalf(wb, (uint32_t)(RPW * gw + rsub) * HRB + (uint32_t)b * 210u, h);
-    for (int q = gw; q < nq; q += nw) {
-        /* the next row group loads while this one is computed */
-        HHalf nxt = load_hhalf(wb, (uint32_t)(RPW * (q + nw) + rsub) * HRB + (uint32_t)b * 210u, h);
+#ifndef TG_HEAD_PF
+#define TG_HEAD_PF 1
+#endif
+    /* row group q of this lane: its half-block; PF + 1 register sets take
+     * turns, the loads of the group PF ahead go out before each group is
+     * computed */
+    constexpr int PF = TG_HEAD_PF;
+    const u32x4 wd = buf_desc(W, (uint32_t)((size_t)nrows * HRB));
+    auto group_at = [&](int qq) {
+        return load_hhalf_asm(wd, (uint32_t)(RPW * qq + rsub) * HRB + (uint32_t)b * 210u, h);
+    };
+    int q = gw;
+    auto step = [&](HHalf &cur, HHalf &nxt) {
+        nxt = group_at(q + PF * nw);
+        wait_hhalf<PF * HLOADS>(cur);
         const uint32_t row = (uint32_t)(RPW * q + rsub);
         /* 6-bit codes of the half (q = ql nibble | qh pair << 4), decoded once */
         const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
@@ -206,8 +261,28 @@ __global__ __launch_bounds__(HT) void k_head_q6k(const uint8_t *__restrict__ W, 
             const uint64_t key = argmax_key(v, row);
             mybest = key > mybest ? key : mybest;
         }
-        cur = nxt;
+        q += nw;
+    };
+    HHalf s0 = group_at(q), s1, s2;
+    if (PF == 1) {
+        for (;;) {
+            if (q >= nq) break;
+            step(s0, s1);
+            if (q >= nq) break;
+            step(s1, s0);
+        }
+    } else {
+        s1 = group_at(q + nw);
+        for (;;) {
+            if (q >= nq) break;
+            step(s0, s2);
+            if (q >= nq) break;
+            step(s1, s0);
+            if (q >= nq) break;
+            step(s2, s1);
+        }
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* the prefetch past the last group */
     /* workgroup best per input row, then one atomic max each */
     if (owner && slot < K) wb_best[slot][(threadIdx.x >> 6) * RPW + rsub] = mybest;
     __syncthreads();
@@ -264,32 +339,11 @@ struct MItem {
     u32x4 sc;         /* the block's 16 sub-scales */
     uint32_t dd;      /* bytes 206..209: d in the high half */
 };
-/* The item loads are issued from inline assembly, untracked by the
- * compiler: across the rotation of five register sets below its wait
- * analysis lost count and waited for every prefetched item before each
- * compute.  The loop waits itself (wait_item): an item is MLOADS loads,
- * items are issued in order and the counter completes in order, so with
- * PF later items issued, vmcnt(PF * MLOADS) leaves exactly those in
+/* The item loads go through the untracked loads above; the loop waits
+ * itself (wait_item): an item is MLOADS loads, items are issued in order,
+ * so with PF later items issued vmcnt(PF * MLOADS) leaves exactly those in
  * flight. */
 constexpr int MLOADS = 8;
-template <int OFF>
-__device__ inline u32x2 ldw8(const u32x4 &d, uint32_t v) {
-    u32x2 r;
-    asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
-    return r;
-}
-template <int OFF>
-__device__ inline u32x4 ldw16(const u32x4 &d, uint32_t v) {
-    u32x4 r;
-    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
-    return r;
-}
-template <int OFF>
-__device__ inline uint32_t ldw4(const u32x4 &d, uint32_t v) {
-    uint32_t r;
-    asm volatile("buffer_load_dword %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
-    return r;
-}
 __device__ inline MItem load_mitem(const u32x4 &d, uint32_t r0, int w, int c16, int g) {
     MItem it;
     const uint32_t ba = (r0 + (uint32_t)c16) * HRB + 210u * (uint32_t)w, bq = ba + 8u * (uint32_t)g;
