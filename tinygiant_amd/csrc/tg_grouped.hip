@@ -43,6 +43,7 @@
 
 #include "tg_device.hpp"
 #include "tg_kernels.h"
+#include "tg_xchg.hpp"
 
 namespace tg {
 
@@ -70,6 +71,45 @@ constexpr int SCALE_1 = 127, SCALE_16 = 131;
 constexpr int CPOL_NT = 2;
 __device__ inline u32x4 ld16_nt(Buf b, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, CPOL_NT);
+}
+
+/* Loads issued from inline assembly, which the compiler does not track.
+ * Merging the paths of k_moe_mx's item loop (an item that keeps its q8
+ * operands, the last items), its wait analysis took the slab just issued for
+ * a later item as the newest load and waited for it before the current
+ * item's compute: no slab was in flight while an item computed.  k_moe_mx
+ * waits for these loads itself, s_waitcnt vmcnt(N) with N = the vector
+ * memory operations issued after the ones waited for (the counter completes
+ * in order; operations left out of N only make a wait stricter), and pins
+ * the registers behind the wait.
+ * A vector memory instruction may read an SGPR only 5 wait states after a
+ * VALU instruction wrote it (v_readlane restoring a spilled descriptor, for
+ * one).  The compiler pads its own loads but not inline assembly, so each
+ * load here carries the padding itself (s_nop 4). */
+__device__ inline u32x4 ldu16(const u32x4 &d, uint32_t off) {
+    u32x4 r;
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(r) : "v"(off), "s"(d));
+    return r;
+}
+__device__ inline u32x4 ldu16_nt(const u32x4 &d, uint32_t off) {
+    u32x4 r;
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(r) : "v"(off), "s"(d));
+    return r;
+}
+__device__ inline uint32_t ldu4(const u32x4 &d, uint32_t off) {
+    uint32_t r;
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen" : "=v"(r) : "v"(off), "s"(d));
+    return r;
+}
+template <int N>
+__device__ inline void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+/* after a wait: the value may not be read before it (volatile statements
+ * keep their order) */
+template <class T>
+__device__ inline void pin(T &v) {
+    asm volatile("" : "+v"(v));
 }
 
 /* Read-only tables through explicit address spaces: wave-uniform reads of
@@ -134,10 +174,15 @@ struct XBatch {
 struct XSrc {
     Buf sp;           /* fp8 halves, [rows][nblk][2][32] */
     Buf d;            /* q8 scales */
+    u32x4 spd, dd;    /* the same as descriptors for the untracked loads */
     int nblk, nb8;
 };
 
-template <int MT>
+/* vector loads of one batch with one tile */
+constexpr int XLOADS = NG * 5;
+
+/* U: through the untracked loads */
+template <int MT, bool U = false>
 __device__ inline void load_batch(XBatch<MT> &s, const XSrc &o, int b0, int b1, int nt, const int *xrow, int g) {
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -150,12 +195,14 @@ __device__ inline void load_batch(XBatch<MT> &s, const XSrc &o, int b0, int b1, 
             const int ba = b0 + GB * q + (g >> 1), bb = ba + 2;   /* blocks of bytes 0..15 and 16..31 */
             const uint32_t oa = ok && ba < b1 ? rbase + (uint32_t)ba * 64u : OOB;
             const uint32_t ob = ok && bb < b1 ? rbase + (uint32_t)bb * 64u : OOB;
-            const u32x4 h0 = ld16(o.sp, oa), h1 = ld16(o.sp, ob);
-            const u32x4 l0 = ld16(o.sp, oa == OOB ? OOB : oa + 32u), l1 = ld16(o.sp, ob == OOB ? OOB : ob + 32u);
+            const uint32_t oa2 = oa == OOB ? OOB : oa + 32u, ob2 = ob == OOB ? OOB : ob + 32u;
+            const u32x4 h0 = U ? ldu16(o.spd, oa) : ld16(o.sp, oa), h1 = U ? ldu16(o.spd, ob) : ld16(o.sp, ob);
+            const u32x4 l0 = U ? ldu16(o.spd, oa2) : ld16(o.sp, oa2), l1 = U ? ldu16(o.spd, ob2) : ld16(o.sp, ob2);
             s.hi[t][q] = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
             s.lo[t][q] = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
             const int bq = b0 + GB * q;
-            s.d[t][q] = __uint_as_float(ld4(o.d, ok && bq < b1 ? (row * o.nb8 + (uint32_t)(bq >> 3)) * 4u : OOB));
+            const uint32_t od = ok && bq < b1 ? (row * o.nb8 + (uint32_t)(bq >> 3)) * 4u : OOB;
+            s.d[t][q] = __uint_as_float(U ? ldu4(o.dd, od) : ld4(o.d, od));
         }
     }
 }
@@ -268,10 +315,12 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     xs.nb8 = q.nb;
     xs.sp = make_buf(DOWN ? a.hp : a.xp, (uint32_t)((size_t)qrows * nblk * 64));
     xs.d = make_buf(q.d, (uint32_t)((size_t)qrows * q.nb * 4));
+    xs.spd = buf_desc(DOWN ? a.hp : a.xp, (uint32_t)((size_t)qrows * nblk * 64));
+    xs.dd = buf_desc(q.d, (uint32_t)((size_t)qrows * q.nb * 4));
 
     /* the expert of the item being issued, and its matrices */
     int iss_ai = -1;
-    Buf iss_w[NM];
+    u32x4 iss_w[NM];
     u32x4 vA[NM][CH], vB[NM][CH];   /* slabs of two items ahead, alternating */
     auto set_issuer = [&](int ai) {
         iss_ai = ai;
@@ -279,7 +328,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const uint64_t base = DOWN ? ldc(a.down, e) : (m ? ldc(a.up, e) : ldc(a.gate, e));
-            iss_w[m] = make_buf_uniform((const void *)(uintptr_t)base, mbytes);
+            iss_w[m] = buf_desc((const void *)(uintptr_t)base, mbytes);
         }
     };
     auto issue = [&](u32x4 (&v)[NM][CH], int item) {
@@ -290,7 +339,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
 #pragma unroll
             for (int c = 0; c < CH; c++) {
                 const uint32_t i = (uint32_t)(tid + NT * c) * 16u;
-                v[m][c] = ld16_nt(iss_w[m], i < slab ? off + i : OOB);
+                v[m][c] = ldu16_nt(iss_w[m], i < slab ? off + i : OOB);
             }
     };
 
@@ -318,7 +367,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     struct Expert {
         int ai, p0, ne;
         bool has0, has1;
-        Buf bias[2];
+        u32x4 bias[2];
     };
     const Buf prow_buf = make_buf(a.p_row, (uint32_t)a.P * 4u), pw_buf = make_buf(a.p_w, (uint32_t)a.P * 4u);
     auto expert = [&](int ai) {
@@ -332,15 +381,19 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
         const float *b1p = DOWN ? nullptr : (a.ubias ? (const float *)(uintptr_t)ldc(a.ubias, e) : nullptr);
         x.has0 = b0p != nullptr;
         x.has1 = b1p != nullptr;
-        x.bias[0] = make_buf_uniform(b0p, b0p ? (uint32_t)rows * 4u : 0u);
-        x.bias[1] = make_buf_uniform(b1p, b1p ? (uint32_t)rows * 4u : 0u);
+        x.bias[0] = buf_desc(b0p, b0p ? (uint32_t)rows * 4u : 0u);
+        x.bias[1] = buf_desc(b1p, b1p ? (uint32_t)rows * 4u : 0u);
         return x;
     };
     /* input row of pair j of an expert (phase A: its q8 row, phase B: the
-     * pair itself), -1 past the expert's pairs; the pair's router weight */
+     * pair itself), unmasked (zero past the expert's pairs) and with -1
+     * there; the pair's router weight */
+    auto pair_row_raw = [&](const Expert &x, int j) -> int {
+        if (DOWN) return x.p0 + j;
+        return (int)ld4(prow_buf, j < x.ne ? (uint32_t)(x.p0 + j) * 4u : OOB);
+    };
     auto pair_row = [&](const Expert &x, int j) -> int {
-        if (DOWN) return j < x.ne ? x.p0 + j : -1;
-        const int r = (int)ld4(prow_buf, j < x.ne ? (uint32_t)(x.p0 + j) * 4u : OOB);
+        const int r = pair_row_raw(x, j);
         return j < x.ne ? r : -1;
     };
     auto pair_w = [&](const Expert &x, int j) -> float {
@@ -349,13 +402,15 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     /* epilogue thread (tid < 256) row of an item's slab */
     auto ep_row = [&](int item) { return (item % nslab) * 16 + 4 * (el >> 4) + ev; };
 
-    /* pair rows and (phase B) weights of an expert's first NPRE passes */
+    /* pair rows (unmasked: the mask is applied where a pass takes them, so
+     * the load is not waited for at once) and (phase B) weights of an
+     * expert's first NPRE passes */
     int xrows[NPRE], nxrows[NPRE];
     float wts[NPRE], nwts[NPRE];
     auto fetch_pairs = [&](const Expert &x, int (&rr)[NPRE], float (&ww)[NPRE]) {
 #pragma unroll
         for (int k = 0; k < NPRE; k++) {
-            rr[k] = pair_row(x, 16 * k + c16);
+            rr[k] = pair_row_raw(x, 16 * k + c16);
             ww[k] = DOWN ? pair_w(x, 16 * k + (el & 15)) : 0.f;
         }
     };
@@ -364,21 +419,28 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
      * second item's slabs */
     Expert cur = expert(it / nslab), nxt = cur;
     fetch_pairs(cur, xrows, wts);
-    xrow[0] = xrows[0];
+    wait_copies();   /* a wait the compiler sees: the pair loads are not pending in the item loop */
+    xrow[0] = c16 < cur.ne ? xrows[0] : -1;
     issue(vA, it);
-    load_batch(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
+    load_batch<MT, true>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
+    bool xnew = true;   /* this item's first q8 batch was loaded for it (not kept) */
     int er = ep_row(it);
-    float bias0 = __uint_as_float(ld4(cur.bias[0], (uint32_t)er * 4u));
-    float bias1 = __uint_as_float(ld4(cur.bias[1], (uint32_t)er * 4u));
+    float bias0 = __uint_as_float(ldu4(cur.bias[0], (uint32_t)er * 4u));
+    float bias1 = __uint_as_float(ldu4(cur.bias[1], (uint32_t)er * 4u));
     float wt = wts[0];
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < it_end) issue(vB, it + 1);
 
     /* Per item, loads are issued in one fixed order: the next expert's pair
      * rows (when it changes), then after the compute the next item's q8
-     * operands, biases and pair weights, then the slabs two items ahead.
+     * operands (unless kept) and biases, then the slabs two items ahead.
      * Loads complete in order, so no wait for an item's operands ever waits
-     * for a younger slab, and every slab has a whole item of lead. */
+     * for a younger slab, and every slab has a whole item of lead.  The
+     * slabs, q8 operands and biases are untracked loads; an item waits for
+     * them with the count of those issued after them: its slabs are
+     * followed by its q8 operands (XLOADS, if loaded), biases (2) and the
+     * next item's slabs (S, if there is a next item). */
+    constexpr int S = NM * CH;
     float acc[NM][MT][4];
     /* one pass: the partial sums of every wave to LDS, then 256 threads add
      * them in wave order and write one result each */
@@ -387,7 +449,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
         for (int m = 0; m < NM; m++)
 #pragma unroll
             for (int vv = 0; vv < 4; vv++) red[((w * NM + m) * 4 + vv) * 64 + lane] = acc[m][0][vv];
-        __syncthreads();
+        bar_lds();
         const int j = t0 + (el & 15);
         if (tid < 256 && j < cur.ne && er < rows) {
             float r2[NM];
@@ -423,25 +485,46 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
             nxt = expert(nx / nslab);
             fetch_pairs(nxt, nxrows, nwts);
         }
-        __syncthreads();   /* the previous item is done with LDS */
+        bar_lds();   /* the previous item is done with LDS */
+        if (xnew) {
+            if (has_nx) vm_wait<XLOADS + 2 + S>();
+            else vm_wait<XLOADS + 2>();
+        } else {
+            if (has_nx) vm_wait<2 + S>();
+            else vm_wait<2>();
+        }
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int c = 0; c < CH; c++)
+            for (int c = 0; c < CH; c++) {
+                pin(v[m][c]);
                 *(u32x4 *)((uint8_t *)lds + m * sstride + (uint32_t)(tid + NT * c) * 16u) = v[m][c];
-        __syncthreads();
+            }
+        bar_lds();
         /* first pass: its first batch of q8 operands is in registers */
+        if (has_nx) vm_wait<2 + S>();
+        else vm_wait<2>();
+#pragma unroll
+        for (int q = 0; q < NG; q++) {
+            pin(xb.hi[0][q]);
+            pin(xb.lo[0][q]);
+            pin(xb.d[0][q]);
+        }
         zero();
         mma_batch<NM, MT>(lds, sstride, rb, xb, b0w, min(b1w, b0w + XB), 1, lane, acc);
         for (int bb = b0w + XB; bb < b1w; bb += XB) {   /* rows wider than NWAVE * XB blocks */
             load_batch(xb, xs, bb, min(b1w, bb + XB), 1, xrow, g);
             mma_batch<NM, MT>(lds, sstride, rb, xb, bb, min(b1w, bb + XB), 1, lane, acc);
         }
+        if (has_nx) vm_wait<S>();
+        else vm_wait<0>();
+        pin(bias0);
+        pin(bias1);
         finish(0);
         /* further passes over the resident slab for an expert with more than
          * 16 pairs */
         for (int t0 = 16 * MT, k = 1; t0 < cur.ne; t0 += 16 * MT, k++) {
-            __syncthreads();   /* red is rewritten by this pass */
+            bar_lds();   /* red is rewritten by this pass */
             int r = 0;
             float wk = 0.f;
 #pragma unroll
@@ -450,7 +533,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
                     r = xrows[q];
                     wk = wts[q];
                 }
-            xrow[0] = k < NPRE ? r : pair_row(cur, t0 + c16);
+            xrow[0] = k < NPRE ? (t0 + c16 < cur.ne ? r : -1) : pair_row(cur, t0 + c16);
             if (DOWN) wt = k < NPRE ? wk : pair_w(cur, t0 + (el & 15));
             zero();
             for (int bb = b0w; bb < b1w; bb += XB) {
@@ -458,12 +541,19 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
                 mma_batch<NM, MT>(lds, sstride, rb, xb, bb, min(b1w, bb + XB), 1, lane, acc);
             }
             finish(t0);
+            /* a wait the compiler sees: the pass's own loads (issued after
+             * the next slabs, which they waited for already) are not left
+             * pending where the compiler merges paths */
+            wait_copies();
         }
         /* the next item's q8 operands (unless this item's first-pass ones
          * serve it: same expert, one pass, one batch), biases, pair weights */
         if (has_nx) {
             const bool keep = !new_ex && cur.ne <= 16 * MT && b1w - b0w <= XB;
             if (new_ex) {
+                /* the new expert's pair loads (issued after the next slabs,
+                 * so this waits for those too) */
+                wait_copies();
                 cur = nxt;
 #pragma unroll
                 for (int q = 0; q < NPRE; q++) {
@@ -471,11 +561,12 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
                     wts[q] = nwts[q];
                 }
             }
-            xrow[0] = xrows[0];
-            if (!keep) load_batch(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
+            xrow[0] = c16 < cur.ne ? xrows[0] : -1;
+            if (!keep) load_batch<MT, true>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
+            xnew = !keep;
             er = ep_row(nx);
-            bias0 = __uint_as_float(ld4(cur.bias[0], (uint32_t)er * 4u));
-            bias1 = __uint_as_float(ld4(cur.bias[1], (uint32_t)er * 4u));
+            bias0 = __uint_as_float(ldu4(cur.bias[0], (uint32_t)er * 4u));
+            bias1 = __uint_as_float(ldu4(cur.bias[1], (uint32_t)er * 4u));
             wt = wts[0];
         }
         /* then the slabs two items ahead, into the registers just stored */

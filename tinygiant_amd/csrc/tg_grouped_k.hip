@@ -104,9 +104,10 @@ __device__ inline Q4Hdr q4_hdr(u32x4 h) {
 __device__ inline int byte_of(uint32_t w, int i) { return (int)((w >> (8 * i)) & 0xFFu); }
 
 /* copy_lanes with the nontemporal hint: each slab byte is read once per
- * call (64- and 128-token Qwen3 prefills measured 5% faster with it) */
+ * call (64- and 128-token Qwen3 prefills measured 5% faster with it); the
+ * same 5 wait states before the load */
 __device__ inline void copy_lanes_nt(const u32x4 &desc, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 3\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
                  :
                  : "s"(lds), "v"(voff), "s"(desc)
                  : "memory");

@@ -86,23 +86,26 @@ __device__ inline uint32_t pick(const u32x4 &v, int c) { return c == 0 ? v.x : c
  * track: the kernels below wait for them themselves (s_waitcnt vmcnt(N) with
  * N = the loads issued after the ones waited for; the counter completes in
  * order).  Across register sets that take turns, the compiler's own wait
- * analysis lost count and waited for every prefetched load. */
+ * analysis lost count and waited for every prefetched load.  Each load
+ * carries s_nop 4: a vector memory instruction may read an SGPR (the
+ * descriptor) only 5 wait states after a VALU instruction wrote it, and the
+ * compiler pads its own loads for that but not inline assembly. */
 template <int OFF>
 __device__ inline u32x2 ldw8(const u32x4 &d, uint32_t v) {
     u32x2 r;
-    asm volatile("buffer_load_dwordx2 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx2 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
     return r;
 }
 template <int OFF>
 __device__ inline u32x4 ldw16(const u32x4 &d, uint32_t v) {
     u32x4 r;
-    asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
     return r;
 }
 template <int OFF>
 __device__ inline uint32_t ldw4(const u32x4 &d, uint32_t v) {
     uint32_t r;
-    asm volatile("buffer_load_dword %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
+    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
     return r;
 }
 /* one lane's half-block for k_head_q6k through those loads */

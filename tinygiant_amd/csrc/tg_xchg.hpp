@@ -126,9 +126,14 @@ __device__ inline uint32_t lds_addr(const void *p) {
 }
 /* M0 holds the copy's LDS address.  M0 is a reserved register the compiler
  * does not let inline assembly clobber; the kernels that use these copies
- * set M0 nowhere else (their generated code has no other M0 write). */
+ * set M0 nowhere else (their generated code has no other M0 write).
+ * The s_mov and s_nop 3 put 5 wait states before the load: a vector memory
+ * instruction may read an SGPR (the descriptor) only 5 wait states after a
+ * VALU instruction wrote it (v_readlane restoring a spilled SGPR, for one),
+ * and the compiler pads its own loads for that but not inline assembly
+ * (the M0 write needs 1). */
 __device__ inline void copy_lanes(const u32x4 &desc, uint32_t voff, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 3\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                  :
                  : "s"(lds), "v"(voff), "s"(desc)
                  : "memory");
