@@ -86,41 +86,30 @@ __device__ inline uint32_t pick(const u32x4 &v, int c) { return c == 0 ? v.x : c
  * track: the kernels below wait for them themselves (s_waitcnt vmcnt(N) with
  * N = the loads issued after the ones waited for; the counter completes in
  * order).  Across register sets that take turns, the compiler's own wait
- * analysis lost count and waited for every prefetched load.  Each load
- * carries s_nop 4: a vector memory instruction may read an SGPR (the
- * descriptor) only 5 wait states after a VALU instruction wrote it, and the
- * compiler pads its own loads for that but not inline assembly. */
-template <int OFF>
-__device__ inline u32x2 ldw8(const u32x4 &d, uint32_t v) {
-    u32x2 r;
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx2 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
-    return r;
-}
-template <int OFF>
-__device__ inline u32x4 ldw16(const u32x4 &d, uint32_t v) {
-    u32x4 r;
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
-    return r;
-}
-template <int OFF>
-__device__ inline uint32_t ldw4(const u32x4 &d, uint32_t v) {
-    uint32_t r;
-    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen offset:%3" : "=v"(r) : "v"(v), "s"(d), "n"(OFF));
-    return r;
-}
-/* one lane's half-block for k_head_q6k through those loads */
+ * analysis lost count and waited for every prefetched load.  A vector memory
+ * instruction may read an SGPR (the descriptor) only 5 wait states after a
+ * VALU instruction wrote it; the compiler pads its own loads for that but
+ * not inline assembly, so each item's loads form one statement that starts
+ * with s_nop 4 (nothing can be scheduled between them).  The outputs are
+ * early-clobber: no destination shares a register with an address that a
+ * later load of the statement reads. */
 constexpr int HLOADS = 8;
+/* one lane's half-block for k_head_q6k */
 __device__ inline HHalf load_hhalf_asm(const u32x4 &d, uint32_t blk, int h) {
     HHalf r;
-    const uint32_t ql = blk + 64u * (uint32_t)h, qh = blk + 32u * (uint32_t)h;
-    r.la0 = ldw16<0>(d, ql);
-    r.la1 = ldw16<16>(d, ql);
-    r.lb0 = ldw16<32>(d, ql);
-    r.lb1 = ldw16<48>(d, ql);
-    r.h0 = ldw16<128>(d, qh);
-    r.h1 = ldw16<144>(d, qh);
-    r.sc = ldw8<192>(d, blk + 8u * (uint32_t)h);
-    r.d = ldw4<206>(d, blk);
+    const uint32_t ql = blk + 64u * (uint32_t)h, qh = blk + 32u * (uint32_t)h, sc = blk + 8u * (uint32_t)h;
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %0, %8, %12, 0 offen offset:0\n\t"
+        "buffer_load_dwordx4 %1, %8, %12, 0 offen offset:16\n\t"
+        "buffer_load_dwordx4 %2, %8, %12, 0 offen offset:32\n\t"
+        "buffer_load_dwordx4 %3, %8, %12, 0 offen offset:48\n\t"
+        "buffer_load_dwordx4 %4, %9, %12, 0 offen offset:128\n\t"
+        "buffer_load_dwordx4 %5, %9, %12, 0 offen offset:144\n\t"
+        "buffer_load_dwordx2 %6, %10, %12, 0 offen offset:192\n\t"
+        "buffer_load_dword %7, %11, %12, 0 offen offset:206"
+        : "=&v"(r.la0), "=&v"(r.la1), "=&v"(r.lb0), "=&v"(r.lb1), "=&v"(r.h0), "=&v"(r.h1), "=&v"(r.sc), "=&v"(r.d)
+        : "v"(ql), "v"(qh), "v"(sc), "v"(blk), "s"(d));
     return r;
 }
 template <int N>
@@ -350,14 +339,19 @@ constexpr int MLOADS = 8;
 __device__ inline MItem load_mitem(const u32x4 &d, uint32_t r0, int w, int c16, int g) {
     MItem it;
     const uint32_t ba = (r0 + (uint32_t)c16) * HRB + 210u * (uint32_t)w, bq = ba + 8u * (uint32_t)g;
-    it.ql[0][0] = ldw8<0>(d, bq);
-    it.ql[0][1] = ldw8<32>(d, bq);
-    it.ql[1][0] = ldw8<64>(d, bq);
-    it.ql[1][1] = ldw8<96>(d, bq);
-    it.qh[0] = ldw8<128>(d, bq);
-    it.qh[1] = ldw8<160>(d, bq);
-    it.sc = ldw16<192>(d, ba);
-    it.dd = ldw4<206>(d, ba);
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx2 %0, %8, %10, 0 offen offset:0\n\t"
+        "buffer_load_dwordx2 %1, %8, %10, 0 offen offset:32\n\t"
+        "buffer_load_dwordx2 %2, %8, %10, 0 offen offset:64\n\t"
+        "buffer_load_dwordx2 %3, %8, %10, 0 offen offset:96\n\t"
+        "buffer_load_dwordx2 %4, %8, %10, 0 offen offset:128\n\t"
+        "buffer_load_dwordx2 %5, %8, %10, 0 offen offset:160\n\t"
+        "buffer_load_dwordx4 %6, %9, %10, 0 offen offset:192\n\t"
+        "buffer_load_dword %7, %9, %10, 0 offen offset:206"
+        : "=&v"(it.ql[0][0]), "=&v"(it.ql[0][1]), "=&v"(it.ql[1][0]), "=&v"(it.ql[1][1]), "=&v"(it.qh[0]),
+          "=&v"(it.qh[1]), "=&v"(it.sc), "=&v"(it.dd)
+        : "v"(bq), "v"(ba), "s"(d));
     return it;
 }
 /* the item's loads have completed once at most N later loads are in flight;
