@@ -85,21 +85,57 @@ __device__ inline u32x4 ld16_nt(Buf b, uint32_t off) {
  * A vector memory instruction may read an SGPR only 5 wait states after a
  * VALU instruction wrote it (v_readlane restoring a spilled descriptor, for
  * one).  The compiler pads its own loads but not inline assembly, so each
- * load here carries the padding itself (s_nop 4). */
-__device__ inline u32x4 ldu16(const u32x4 &d, uint32_t off) {
-    u32x4 r;
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(r) : "v"(off), "s"(d));
-    return r;
+ * group of loads is one statement that starts with the padding (s_nop 4);
+ * the outputs are early-clobber, so no destination shares a register with
+ * an address a later load of the statement reads. */
+/* one q8 group of a batch: hi and lo halves of two blocks, and the scale */
+__device__ inline void ldu_xgroup(u32x4 &h0, u32x4 &h1, u32x4 &l0, u32x4 &l1, uint32_t &dv, const u32x4 &sp,
+                                  const u32x4 &dd, uint32_t oa, uint32_t ob, uint32_t oa2, uint32_t ob2, uint32_t od) {
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %0, %5, %10, 0 offen\n\t"
+        "buffer_load_dwordx4 %1, %6, %10, 0 offen\n\t"
+        "buffer_load_dwordx4 %2, %7, %10, 0 offen\n\t"
+        "buffer_load_dwordx4 %3, %8, %10, 0 offen\n\t"
+        "buffer_load_dword %4, %9, %11, 0 offen"
+        : "=&v"(h0), "=&v"(h1), "=&v"(l0), "=&v"(l1), "=&v"(dv)
+        : "v"(oa), "v"(ob), "v"(oa2), "v"(ob2), "v"(od), "s"(sp), "s"(dd));
 }
-__device__ inline u32x4 ldu16_nt(const u32x4 &d, uint32_t off) {
-    u32x4 r;
-    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(r) : "v"(off), "s"(d));
-    return r;
+/* one matrix's slab chunks of an item (nontemporal: read once per call) */
+template <int CH>
+__device__ inline void ldu_slab(u32x4 (&v)[CH], const u32x4 &d, const uint32_t (&o)[CH]);
+template <>
+__device__ inline void ldu_slab<3>(u32x4 (&v)[3], const u32x4 &d, const uint32_t (&o)[3]) {
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %0, %3, %6, 0 offen nt\n\t"
+        "buffer_load_dwordx4 %1, %4, %6, 0 offen nt\n\t"
+        "buffer_load_dwordx4 %2, %5, %6, 0 offen nt"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2])
+        : "v"(o[0]), "v"(o[1]), "v"(o[2]), "s"(d));
 }
-__device__ inline uint32_t ldu4(const u32x4 &d, uint32_t off) {
-    uint32_t r;
-    asm volatile("s_nop 4\n\tbuffer_load_dword %0, %1, %2, 0 offen" : "=v"(r) : "v"(off), "s"(d));
-    return r;
+template <>
+__device__ inline void ldu_slab<4>(u32x4 (&v)[4], const u32x4 &d, const uint32_t (&o)[4]) {
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dwordx4 %0, %4, %8, 0 offen nt\n\t"
+        "buffer_load_dwordx4 %1, %5, %8, 0 offen nt\n\t"
+        "buffer_load_dwordx4 %2, %6, %8, 0 offen nt\n\t"
+        "buffer_load_dwordx4 %3, %7, %8, 0 offen nt"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+        : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]), "s"(d));
+}
+/* an item's two biases (gate and up, or down and a zero) */
+__device__ inline void ldu_bias(float &b0, float &b1, const u32x4 &d0, const u32x4 &d1, uint32_t off) {
+    uint32_t r0, r1;
+    asm volatile(
+        "s_nop 4\n\t"
+        "buffer_load_dword %0, %2, %3, 0 offen\n\t"
+        "buffer_load_dword %1, %2, %4, 0 offen"
+        : "=&v"(r0), "=&v"(r1)
+        : "v"(off), "s"(d0), "s"(d1));
+    b0 = __uint_as_float(r0);
+    b1 = __uint_as_float(r1);
 }
 template <int N>
 __device__ inline void vm_wait() {
@@ -196,13 +232,22 @@ __device__ inline void load_batch(XBatch<MT> &s, const XSrc &o, int b0, int b1, 
             const uint32_t oa = ok && ba < b1 ? rbase + (uint32_t)ba * 64u : OOB;
             const uint32_t ob = ok && bb < b1 ? rbase + (uint32_t)bb * 64u : OOB;
             const uint32_t oa2 = oa == OOB ? OOB : oa + 32u, ob2 = ob == OOB ? OOB : ob + 32u;
-            const u32x4 h0 = U ? ldu16(o.spd, oa) : ld16(o.sp, oa), h1 = U ? ldu16(o.spd, ob) : ld16(o.sp, ob);
-            const u32x4 l0 = U ? ldu16(o.spd, oa2) : ld16(o.sp, oa2), l1 = U ? ldu16(o.spd, ob2) : ld16(o.sp, ob2);
-            s.hi[t][q] = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
-            s.lo[t][q] = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
             const int bq = b0 + GB * q;
             const uint32_t od = ok && bq < b1 ? (row * o.nb8 + (uint32_t)(bq >> 3)) * 4u : OOB;
-            s.d[t][q] = __uint_as_float(U ? ldu4(o.dd, od) : ld4(o.d, od));
+            u32x4 h0, h1, l0, l1;
+            uint32_t dv;
+            if (U) {
+                ldu_xgroup(h0, h1, l0, l1, dv, o.spd, o.dd, oa, ob, oa2, ob2, od);
+            } else {
+                h0 = ld16(o.sp, oa);
+                h1 = ld16(o.sp, ob);
+                l0 = ld16(o.sp, oa2);
+                l1 = ld16(o.sp, ob2);
+                dv = ld4(o.d, od);
+            }
+            s.hi[t][q] = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
+            s.lo[t][q] = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
+            s.d[t][q] = __uint_as_float(dv);
         }
     }
 }
@@ -335,12 +380,15 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
         if (item / nslab != iss_ai) set_issuer(item / nslab);
         const uint32_t off = (uint32_t)(item % nslab) * 16u * rb;
 #pragma unroll
-        for (int m = 0; m < NM; m++)
+        for (int m = 0; m < NM; m++) {
+            uint32_t o[CH];
 #pragma unroll
             for (int c = 0; c < CH; c++) {
                 const uint32_t i = (uint32_t)(tid + NT * c) * 16u;
-                v[m][c] = ldu16_nt(iss_w[m], i < slab ? off + i : OOB);
+                o[c] = i < slab ? off + i : OOB;
             }
+            ldu_slab<CH>(v[m], iss_w[m], o);
+        }
     };
 
     XBatch<MT> xb;
@@ -425,8 +473,8 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     load_batch<MT, true>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
     bool xnew = true;   /* this item's first q8 batch was loaded for it (not kept) */
     int er = ep_row(it);
-    float bias0 = __uint_as_float(ldu4(cur.bias[0], (uint32_t)er * 4u));
-    float bias1 = __uint_as_float(ldu4(cur.bias[1], (uint32_t)er * 4u));
+    float bias0, bias1;
+    ldu_bias(bias0, bias1, cur.bias[0], cur.bias[1], (uint32_t)er * 4u);
     float wt = wts[0];
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < it_end) issue(vB, it + 1);
@@ -565,8 +613,7 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
             if (!keep) load_batch<MT, true>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
             xnew = !keep;
             er = ep_row(nx);
-            bias0 = __uint_as_float(ldu4(cur.bias[0], (uint32_t)er * 4u));
-            bias1 = __uint_as_float(ldu4(cur.bias[1], (uint32_t)er * 4u));
+            ldu_bias(bias0, bias1, cur.bias[0], cur.bias[1], (uint32_t)er * 4u);
             wt = wts[0];
         }
         /* then the slabs two items ahead, into the registers just stored */
