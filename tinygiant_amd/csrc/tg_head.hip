@@ -17,8 +17,8 @@
  *                   the best (logit, row) per input row, commits it with one
  *                   64-bit atomic max, and the last workgroup to finish
  *                   writes the argmax.
- *   k_head_q6k_mfma the same head on int8 MFMA for 14 or more rows: 16 vocab
- *                   rows an item, one 256-block per wave, logits formed and
+ *   k_head_q6k_mfma the same head on int8 MFMA for 10 or more rows: 16 vocab
+ *                   rows an item staged in LDS, one 256-block per wave, logits formed and
  *                   added block by block as the reference does (bit-equal
  *                   to it where its float block sums are exact).
  *   k_argmax_rows   argmax of materialized logits (any format, via k_gemv).
@@ -325,55 +325,43 @@ __device__ inline v4i mma_i8(long a, long b) {
 /* One lane's share of a 16-row item in block w: its A row's codes (both
  * halves), the row's 16 sub-scales and d (the other lanes' D rows take
  * theirs from the lanes that hold them) */
-struct MItem {
-    u32x2 ql[2][2];   /* [half h][run parity p]: 8 bytes at 64 h + 32 p + 8 g */
-    u32x2 qh[2];      /* [half h]: 8 bytes at 128 + 32 h + 8 g */
-    u32x4 sc;         /* the block's 16 sub-scales */
-    uint32_t dd;      /* bytes 206..209: d in the high half */
-};
-/* The item loads go through the untracked loads above; the loop waits
- * itself (wait_item): an item is MLOADS loads, items are issued in order,
- * so with PF later items issued vmcnt(PF * MLOADS) leaves exactly those in
- * flight. */
-constexpr int MLOADS = 8;
-__device__ inline MItem load_mitem(const u32x4 &d, uint32_t r0, int w, int c16, int g) {
-    MItem it;
-    const uint32_t ba = (r0 + (uint32_t)c16) * HRB + 210u * (uint32_t)w, bq = ba + 8u * (uint32_t)g;
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx2 %0, %8, %10, 0 offen offset:0\n\t"
-        "buffer_load_dwordx2 %1, %8, %10, 0 offen offset:32\n\t"
-        "buffer_load_dwordx2 %2, %8, %10, 0 offen offset:64\n\t"
-        "buffer_load_dwordx2 %3, %8, %10, 0 offen offset:96\n\t"
-        "buffer_load_dwordx2 %4, %8, %10, 0 offen offset:128\n\t"
-        "buffer_load_dwordx2 %5, %8, %10, 0 offen offset:160\n\t"
-        "buffer_load_dwordx4 %6, %9, %10, 0 offen offset:192\n\t"
-        "buffer_load_dword %7, %9, %10, 0 offen offset:206"
-        : "=&v"(it.ql[0][0]), "=&v"(it.ql[0][1]), "=&v"(it.ql[1][0]), "=&v"(it.ql[1][1]), "=&v"(it.qh[0]),
-          "=&v"(it.qh[1]), "=&v"(it.sc), "=&v"(it.dd)
-        : "v"(bq), "v"(ba), "s"(d));
-    return it;
+/* The MFMA kernel stages each item (16 vocab rows, 26,880 contiguous,
+ * 16-byte-aligned bytes) in LDS through direct-to-LDS copies, 1 KiB an
+ * instruction, in the rows' own layout.  Loads of 8 bytes a lane straight
+ * from the rows touch 16 rows x 32 bytes an instruction; a timing probe with
+ * the same compute and contiguous loads ran 1.4x faster.  A block starts at
+ * 210 w within its row, so the fields of the odd 256-blocks lie at 2 mod 4:
+ * lds8 / lds16 read the covering dwords and shift (the LDS copies read
+ * 16-byte-aligned sources only). */
+constexpr int HITEM = 27 * 1024;       /* 16 rows (26,880 B) and the rest of the last copy */
+constexpr int HCOP = HITEM / 1024;     /* 27 copies an item */
+constexpr int HNB = 3;                 /* LDS item buffers: an item computes while two are in flight */
+static_assert(16 * HRB <= HITEM && HITEM - 16 * HRB < 1024, "whole copies");
+/* 8 and 16 bytes at LDS offset a of base (a even): the covering dwords from
+ * a & ~3, shifted by sh = a & 3 bytes (no branch: the shift is 0 or 2) */
+__device__ inline u32x2 lds8(const uint8_t *base, uint32_t a, uint32_t sh) {
+    const uint32_t *p = (const uint32_t *)(base + (a & ~3u));
+    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+    return u32x2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
 }
-/* the item's loads have completed once at most N later loads are in flight;
- * the operands tie its registers to the wait */
-template <int N>
-__device__ inline void wait_item(MItem &it) {
-    asm volatile("s_waitcnt vmcnt(%8)"
-                 : "+v"(it.ql[0][0]), "+v"(it.ql[0][1]), "+v"(it.ql[1][0]), "+v"(it.ql[1][1]), "+v"(it.qh[0]),
-                   "+v"(it.qh[1]), "+v"(it.sc), "+v"(it.dd)
-                 : "n"(N));
+__device__ inline u32x4 lds16(const uint8_t *base, uint32_t a, uint32_t sh) {
+    const uint32_t *p = (const uint32_t *)(base + (a & ~3u));
+    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2], d3 = p[3], d4 = p[4];
+    return u32x4{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh),
+                 __builtin_amdgcn_alignbyte(d3, d2, sh), __builtin_amdgcn_alignbyte(d4, d3, sh)};
 }
-
 }  // namespace
 
 /* Q6_K head, 2048 columns, k <= 16 input rows: the contract of k_head_q6k. */
 __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
                                                      float *logits, unsigned long long *best, int32_t *idx,
                                                      float *val) {
-    __shared__ __attribute__((aligned(16))) float red[2][MW][4][64];
+    __shared__ __attribute__((aligned(16))) float red[MW][4][64];
     __shared__ unsigned long long wb_best[16][16];
     __shared__ int last_wg;
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+    extern __shared__ __attribute__((aligned(16))) uint8_t hl[];   /* [HNB][HITEM] */
+    const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, g = lane >> 4;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     /* input row c16's operands of block w, for the whole kernel: run m of
      * half h at K slice 8 g .. 8 g + 7, zeroed outside the sub-block each
@@ -410,37 +398,60 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
     /* epilogue thread (tid < 256): D register ev of lane el */
     const int ev = tid >> 6, el = tid & 63, ej = el & 15;
     uint64_t mybest = 0;
-    int q = blockIdx.x, it = 0;
-    /* one item: the loads of the item PF ahead go out first (PF + 1 register
-     * sets take turns, so no copy waits for them), then this item is
-     * computed */
-    constexpr int PF = 4;
-    auto item = [&](MItem &cur, MItem &nxt) {
-        nxt = load_mitem(wd, 16u * (uint32_t)(q + PF * (int)gridDim.x), w, c16, g);
-        wait_item<PF * MLOADS>(cur);
-        /* the sub-scales and d of D rows 4 g + v, from the lanes holding those rows */
+    int q = blockIdx.x;
+    /* copy j of this wave moves the item's KiB w + 8 j */
+    const int ncw = (HCOP - w + 7) / 8;   /* 4 or 3 copies an item */
+    uint32_t csrc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) csrc[j] = 1024u * (uint32_t)(w + 8 * j) + 16u * (uint32_t)lane;
+    auto issue_item = [&](int qi, int b) {
+        const uint32_t base = (uint32_t)qi * 16u * HRB;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (j < ncw) copy_lanes(wd, base + csrc[j], lds_addr(hl + b * HITEM + 1024 * (w + 8 * j)));
+    };
+    const int G = (int)gridDim.x;
+    issue_item(q, 0);
+    issue_item(q + G, 1);
+    for (int bi = 0; q < nq; bi = bi == HNB - 1 ? 0 : bi + 1) {
+        /* the item two ahead into the buffer the previous item used (every
+         * wave passed the barrier after its compute) */
+        issue_item(q + 2 * G, bi == 0 ? 2 : bi - 1);
+        /* this item's copies: the two later items' (ncw each) stay in flight */
+        if (ncw == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        bar_lds();
+        const uint8_t *ib = hl + bi * HITEM;
+        const uint32_t odd = 2u * (uint32_t)(w & 1);   /* byte shift of block w's fields */
+        const uint32_t mb = (uint32_t)c16 * HRB + 210u * (uint32_t)w;   /* this lane's row of block w */
+        u32x2 qlv[2][2], qhv[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            qlv[h][0] = lds8(ib, mb + 64u * h + 8u * g, odd);
+            qlv[h][1] = lds8(ib, mb + 64u * h + 32u + 8u * g, odd);
+            qhv[h] = lds8(ib, mb + 128u + 32u * h + 8u * g, odd);
+        }
+        const u32x4 sco = lds16(ib, mb + 192u, odd);
+        /* the sub-scales and d of D rows 4 g + v */
         u32x4 sc[4];
         float dv[4];
 #pragma unroll
         for (int v = 0; v < 4; v++) {
-            const int src = 4 * g + v;
-            sc[v].x = (uint32_t)__shfl((int)cur.sc.x, src, 64);
-            sc[v].y = (uint32_t)__shfl((int)cur.sc.y, src, 64);
-            sc[v].z = (uint32_t)__shfl((int)cur.sc.z, src, 64);
-            sc[v].w = (uint32_t)__shfl((int)cur.sc.w, src, 64);
-            dv[v] = ref_f16((uint32_t)__shfl((int)cur.dd, src, 64) >> 16);
+            const uint32_t rv = (uint32_t)(4 * g + v) * HRB + 210u * (uint32_t)w;
+            sc[v] = lds16(ib, rv + 192u, odd);
+            dv[v] = ref_f16(*(const uint16_t *)(ib + rv + 208u));
         }
         int isum[4] = {0, 0, 0, 0};
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint32_t sw0 = h ? cur.sc.z : cur.sc.x, sw1 = h ? cur.sc.w : cur.sc.y;
+            const uint32_t sw0 = h ? sco.z : sco.x, sw1 = h ? sco.w : sco.y;
             v4f cf = {0.f, 0.f, 0.f, 0.f};
             cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(sw0 >> (8 * g)), s16a[h], cf, 0, 0, 0);
             cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(sw1 >> (8 * g)), s16b[h], cf, 0, 0, 0);
             int ai[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int m = 0; m < 4; m++) {
-                const u32x2 ql = cur.ql[h][m & 1], qh = cur.qh[h];
+                const u32x2 ql = qlv[h][m & 1], qh = qhv[h];
                 const int sl = 4 * (m >> 1), sh = 2 * m;
                 u32x2 c;
                 c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
@@ -448,8 +459,8 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
                 const v4i d0 = mma_i8(as_long(c), x0[h][m]), d1 = mma_i8(as_long(c), x1[h][m]);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const u32x4 &s = sc[v];
-                    const uint32_t sw = (m >> 1) ? (h ? s.w : s.y) : (h ? s.z : s.x);
+                    const u32x4 &sv = sc[v];
+                    const uint32_t sw = (m >> 1) ? (h ? sv.w : sv.y) : (h ? sv.z : sv.x);
                     const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))), sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
                     ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 per term */
                 }
@@ -458,10 +469,10 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
             for (int v = 0; v < 4; v++) isum[v] += ai[v] - 32 * (int)cf[v];
         }
         /* the block's term d * d_x * sum, as the reference forms it */
-        float (&rb)[MW][4][64] = red[it & 1];
+        float (&rb)[MW][4][64] = red;   /* rewritten only after the next item's first barrier */
 #pragma unroll
         for (int v = 0; v < 4; v++) rb[w][v][lane] = __fmul_rn(__fmul_rn(dv[v], xd), (float)isum[v]);
-        bar_lds();   /* LDS only: the prefetched items stay in flight */
+        bar_lds();   /* LDS only: the items in flight stay in flight */
         if (tid < 256) {
             const uint32_t row = 16u * (uint32_t)q + 4u * (uint32_t)(el >> 4) + (uint32_t)ev;
             float s = 0.f;
@@ -473,29 +484,9 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
                 mybest = key > mybest ? key : mybest;
             }
         }
-        q += gridDim.x;
-        it++;
-    };
-    const int G = (int)gridDim.x;
-    MItem s0 = load_mitem(wd, 16u * (uint32_t)q, w, c16, g);
-    MItem s1 = load_mitem(wd, 16u * (uint32_t)(q + G), w, c16, g);
-    MItem s2 = load_mitem(wd, 16u * (uint32_t)(q + 2 * G), w, c16, g);
-    MItem s3 = load_mitem(wd, 16u * (uint32_t)(q + 3 * G), w, c16, g);
-    MItem s4;
-    static_assert(PF == 4, "five register sets below");
-    for (;;) {
-        if (q >= nq) break;
-        item(s0, s4);
-        if (q >= nq) break;
-        item(s1, s0);
-        if (q >= nq) break;
-        item(s2, s1);
-        if (q >= nq) break;
-        item(s3, s2);
-        if (q >= nq) break;
-        item(s4, s3);
+        q += G;
     }
-    /* the prefetched items past the end land before the wave ends */
+    /* the copies of the items past the end land before the wave ends */
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     /* workgroup best per input row (16 epilogue threads each), then one
      * atomic max each; the last workgroup writes the result */
@@ -548,10 +539,10 @@ __global__ void k_argmax_finish(const unsigned long long *best, int k, int32_t *
 bool head_fast_ok(int fmt, int ncols, int k) { return fmt == TG_FMT_Q6K && ncols == NBH * 256 && k >= 1 && k <= 16; }
 
 /* From this many input rows the int8 MFMA kernel reads the head: its work
- * does not grow with k (151936 x 2048: 92-96 us for every k), the v_dot4
- * kernel's does (73 us at k = 9, 99 at 14, 109 at 16). */
+ * does not grow with k (151936 x 2048: 83-85 us for every k), the v_dot4
+ * kernel's does (70 us at k = 9, 85-87 at 10, 91 at 12, 111 at 16). */
 #ifndef TG_HEAD_MFMA_MIN_K
-#define TG_HEAD_MFMA_MIN_K 14
+#define TG_HEAD_MFMA_MIN_K 10
 #endif
 static int g_head_mfma_min_k = TG_HEAD_MFMA_MIN_K;
 int set_head_mfma_min_k(int k) {
@@ -567,12 +558,13 @@ void launch_head_q6k(const uint8_t *W, int nrows, const Q8Rows &x, int k, float 
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (g_head_mfma_min_k > 0 && k >= g_head_mfma_min_k) {
         static int occ = -1;
-        if (occ < 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_head_q6k_mfma, MT, 0) != hipSuccess ||
+        const size_t lds = (size_t)HNB * HITEM;
+        if (occ < 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_head_q6k_mfma, MT, lds) != hipSuccess ||
                         occ < 1))
             occ = 1;
         const int nq = (nrows + 15) / 16;
         const int grid = std::max(1, std::min(std::max(cus, 1) * occ, nq));
-        hipLaunchKernelGGL(k_head_q6k_mfma, dim3(grid), dim3(MT), 0, st, W, nrows, x, k, logits, best, idx, val);
+        hipLaunchKernelGGL(k_head_q6k_mfma, dim3(grid), dim3(MT), lds, st, W, nrows, x, k, logits, best, idx, val);
         return;
     }
     const int nq = (nrows + RPW - 1) / RPW;
