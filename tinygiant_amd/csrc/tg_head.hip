@@ -335,7 +335,13 @@ __device__ inline v4i mma_i8(long a, long b) {
  * 16-byte-aligned sources only). */
 constexpr int HITEM = 27 * 1024;       /* 16 rows (26,880 B) and the rest of the last copy */
 constexpr int HCOP = HITEM / 1024;     /* 27 copies an item */
-constexpr int HNB = 3;                 /* LDS item buffers: an item computes while two are in flight */
+#ifndef TG_HEAD_NB
+#define TG_HEAD_NB 2
+#endif
+/* LDS item buffers: an item computes while HNB - 1 are in flight.  Two
+ * (55 KB with the static arrays' 10 KB: two workgroups a CU) ran 69-72 us,
+ * three (93 KB: one workgroup a CU) 84-86 us. */
+constexpr int HNB = TG_HEAD_NB;
 static_assert(16 * HRB <= HITEM && HITEM - 16 * HRB < 1024, "whole copies");
 /* 8 and 16 bytes at LDS offset a of base (a even): the covering dwords from
  * a & ~3, shifted by sh = a & 3 bytes (no branch: the shift is 0 or 2) */
@@ -411,15 +417,15 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
             if (j < ncw) copy_lanes(wd, base + csrc[j], lds_addr(hl + b * HITEM + 1024 * (w + 8 * j)));
     };
     const int G = (int)gridDim.x;
-    issue_item(q, 0);
-    issue_item(q + G, 1);
+#pragma unroll
+    for (int i = 0; i < HNB - 1; i++) issue_item(q + i * G, i);
     for (int bi = 0; q < nq; bi = bi == HNB - 1 ? 0 : bi + 1) {
-        /* the item two ahead into the buffer the previous item used (every
-         * wave passed the barrier after its compute) */
-        issue_item(q + 2 * G, bi == 0 ? 2 : bi - 1);
-        /* this item's copies: the two later items' (ncw each) stay in flight */
-        if (ncw == 4) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+        /* the item HNB - 1 ahead into the buffer the previous item used
+         * (every wave passed the barrier after its compute) */
+        issue_item(q + (HNB - 1) * G, bi == 0 ? HNB - 1 : bi - 1);
+        /* this item's copies: the later items' (ncw each) stay in flight */
+        if (ncw == 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (HNB - 1)) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (HNB - 1)) : "memory");
         bar_lds();
         const uint8_t *ib = hl + bi * HITEM;
         const uint32_t odd = 2u * (uint32_t)(w & 1);   /* byte shift of block w's fields */
@@ -539,7 +545,7 @@ __global__ void k_argmax_finish(const unsigned long long *best, int k, int32_t *
 bool head_fast_ok(int fmt, int ncols, int k) { return fmt == TG_FMT_Q6K && ncols == NBH * 256 && k >= 1 && k <= 16; }
 
 /* From this many input rows the int8 MFMA kernel reads the head: its work
- * does not grow with k (151936 x 2048: 83-85 us for every k), the v_dot4
+ * does not grow with k (151936 x 2048: 69-72 us for every k), the v_dot4
  * kernel's does (70 us at k = 9, 85-87 at 10, 91 at 12, 111 at 16). */
 #ifndef TG_HEAD_MFMA_MIN_K
 #define TG_HEAD_MFMA_MIN_K 10
