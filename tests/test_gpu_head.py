@@ -297,3 +297,26 @@ def test_head_q6k_mfma_ties_and_zero_rows(tg, orc):
             assert am[j] == 333
         else:
             assert logits[j][am[j]] == 0.0 and am[j] == 0
+
+
+@pytest.mark.parametrize("k", [3, 4, 5])
+@pytest.mark.parametrize("nrows", [1999, 40001])
+def test_head_q6k_argmax_at_loop_exit(tg, orc, k, nrows):
+    """Row counts where every wave leaves the row-group loop after one group
+    (1999 rows: 125 workgroups of four waves) or after two and three (40001
+    rows on the 1024-workgroup grid), with the next group's loads still in
+    flight at the exit: the argmax-only kernel (no logits buffer) and the
+    one that also writes logits, each against the oracle."""
+    import tinygiant_amd.synth as S
+    ncols = 2048
+    say(f"head q6k loop exit k={k} nrows={nrows}")
+    mat = S.matrix_host(Q6K, S.tensor_seed(21, 0, 0, 3), nrows, ncols)
+    x = np.random.default_rng(300 + k).standard_normal((k, ncols)).astype(np.float32)
+    ref = _oracle(orc, Q6K, mat, x, nrows, ncols)
+    _, am, mv = _head(tg, Q6K, mat, x, nrows, ncols, want_logits=False)
+    _check(ref, None, am, mv, 1e-5)
+    for j in range(k):
+        assert abs(mv[j] - ref[j][am[j]]) <= 1e-5 * np.abs(ref).max(), j
+    logits, am2, mv2 = _head(tg, Q6K, mat, x, nrows, ncols)
+    _check(ref, logits, am2, mv2, 1e-5)
+    assert np.array_equal(am, am2) and np.array_equal(mv, mv2)

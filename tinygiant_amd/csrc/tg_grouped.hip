@@ -73,81 +73,6 @@ __device__ inline u32x4 ld16_nt(Buf b, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, CPOL_NT);
 }
 
-/* Loads issued from inline assembly, which the compiler does not track.
- * Merging the paths of k_moe_mx's item loop (an item that keeps its q8
- * operands, the last items), its wait analysis took the slab just issued for
- * a later item as the newest load and waited for it before the current
- * item's compute: no slab was in flight while an item computed.  k_moe_mx
- * waits for these loads itself, s_waitcnt vmcnt(N) with N = the vector
- * memory operations issued after the ones waited for (the counter completes
- * in order; operations left out of N only make a wait stricter), and pins
- * the registers behind the wait.
- * A vector memory instruction may read an SGPR only 5 wait states after a
- * VALU instruction wrote it (v_readlane restoring a spilled descriptor, for
- * one).  The compiler pads its own loads but not inline assembly, so each
- * group of loads is one statement that starts with the padding (s_nop 4);
- * the outputs are early-clobber, so no destination shares a register with
- * an address a later load of the statement reads. */
-/* one q8 group of a batch: hi and lo halves of two blocks, and the scale */
-__device__ inline void ldu_xgroup(u32x4 &h0, u32x4 &h1, u32x4 &l0, u32x4 &l1, uint32_t &dv, const u32x4 &sp,
-                                  const u32x4 &dd, uint32_t oa, uint32_t ob, uint32_t oa2, uint32_t ob2, uint32_t od) {
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %5, %10, 0 offen\n\t"
-        "buffer_load_dwordx4 %1, %6, %10, 0 offen\n\t"
-        "buffer_load_dwordx4 %2, %7, %10, 0 offen\n\t"
-        "buffer_load_dwordx4 %3, %8, %10, 0 offen\n\t"
-        "buffer_load_dword %4, %9, %11, 0 offen"
-        : "=&v"(h0), "=&v"(h1), "=&v"(l0), "=&v"(l1), "=&v"(dv)
-        : "v"(oa), "v"(ob), "v"(oa2), "v"(ob2), "v"(od), "s"(sp), "s"(dd));
-}
-/* one matrix's slab chunks of an item (nontemporal: read once per call) */
-template <int CH>
-__device__ inline void ldu_slab(u32x4 (&v)[CH], const u32x4 &d, const uint32_t (&o)[CH]);
-template <>
-__device__ inline void ldu_slab<3>(u32x4 (&v)[3], const u32x4 &d, const uint32_t (&o)[3]) {
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %3, %6, 0 offen nt\n\t"
-        "buffer_load_dwordx4 %1, %4, %6, 0 offen nt\n\t"
-        "buffer_load_dwordx4 %2, %5, %6, 0 offen nt"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2])
-        : "v"(o[0]), "v"(o[1]), "v"(o[2]), "s"(d));
-}
-template <>
-__device__ inline void ldu_slab<4>(u32x4 (&v)[4], const u32x4 &d, const uint32_t (&o)[4]) {
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %4, %8, 0 offen nt\n\t"
-        "buffer_load_dwordx4 %1, %5, %8, 0 offen nt\n\t"
-        "buffer_load_dwordx4 %2, %6, %8, 0 offen nt\n\t"
-        "buffer_load_dwordx4 %3, %7, %8, 0 offen nt"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
-        : "v"(o[0]), "v"(o[1]), "v"(o[2]), "v"(o[3]), "s"(d));
-}
-/* an item's two biases (gate and up, or down and a zero) */
-__device__ inline void ldu_bias(float &b0, float &b1, const u32x4 &d0, const u32x4 &d1, uint32_t off) {
-    uint32_t r0, r1;
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dword %0, %2, %3, 0 offen\n\t"
-        "buffer_load_dword %1, %2, %4, 0 offen"
-        : "=&v"(r0), "=&v"(r1)
-        : "v"(off), "s"(d0), "s"(d1));
-    b0 = __uint_as_float(r0);
-    b1 = __uint_as_float(r1);
-}
-template <int N>
-__device__ inline void vm_wait() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
-}
-/* after a wait: the value may not be read before it (volatile statements
- * keep their order) */
-template <class T>
-__device__ inline void pin(T &v) {
-    asm volatile("" : "+v"(v));
-}
-
 /* Read-only tables through explicit address spaces: wave-uniform reads of
  * the constant space become scalar loads (counted apart from the vector
  * loads), per-lane reads of the global space in-order vector loads. */
@@ -210,15 +135,10 @@ struct XBatch {
 struct XSrc {
     Buf sp;           /* fp8 halves, [rows][nblk][2][32] */
     Buf d;            /* q8 scales */
-    u32x4 spd, dd;    /* the same as descriptors for the untracked loads */
     int nblk, nb8;
 };
 
-/* vector loads of one batch with one tile */
-constexpr int XLOADS = NG * 5;
-
-/* U: through the untracked loads */
-template <int MT, bool U = false>
+template <int MT>
 __device__ inline void load_batch(XBatch<MT> &s, const XSrc &o, int b0, int b1, int nt, const int *xrow, int g) {
 #pragma unroll
     for (int t = 0; t < MT; t++) {
@@ -234,17 +154,8 @@ __device__ inline void load_batch(XBatch<MT> &s, const XSrc &o, int b0, int b1, 
             const uint32_t oa2 = oa == OOB ? OOB : oa + 32u, ob2 = ob == OOB ? OOB : ob + 32u;
             const int bq = b0 + GB * q;
             const uint32_t od = ok && bq < b1 ? (row * o.nb8 + (uint32_t)(bq >> 3)) * 4u : OOB;
-            u32x4 h0, h1, l0, l1;
-            uint32_t dv;
-            if (U) {
-                ldu_xgroup(h0, h1, l0, l1, dv, o.spd, o.dd, oa, ob, oa2, ob2, od);
-            } else {
-                h0 = ld16(o.sp, oa);
-                h1 = ld16(o.sp, ob);
-                l0 = ld16(o.sp, oa2);
-                l1 = ld16(o.sp, ob2);
-                dv = ld4(o.d, od);
-            }
+            const u32x4 h0 = ld16(o.sp, oa), h1 = ld16(o.sp, ob), l0 = ld16(o.sp, oa2), l1 = ld16(o.sp, ob2);
+            const uint32_t dv = ld4(o.d, od);
             s.hi[t][q] = v8i{(int)h0.x, (int)h0.y, (int)h0.z, (int)h0.w, (int)h1.x, (int)h1.y, (int)h1.z, (int)h1.w};
             s.lo[t][q] = v8i{(int)l0.x, (int)l0.y, (int)l0.z, (int)l0.w, (int)l1.x, (int)l1.y, (int)l1.z, (int)l1.w};
             s.d[t][q] = __uint_as_float(dv);
@@ -344,7 +255,10 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     const int nact = DOWN ? a.n_act_b : a.n_act_a;
     const int nitems = nact * nslab;
     float *red = (float *)((uint8_t *)lds + NM * sstride);   /* [NWAVE][NM][4][64] */
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+    /* w is wave-uniform (readfirstlane), so every condition below that
+     * decides which loads a wave issues is a scalar branch */
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              c16 = lane & 15;
     const uint32_t mbytes = (uint32_t)rows * rb;              /* rows past the end read zero */
     /* epilogue thread (tid < 256): register ev of D lane el, i.e. weight row
      * 4 (el / 16) + ev of the slab and pair el % 16 of the tile */
@@ -360,12 +274,10 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     xs.nb8 = q.nb;
     xs.sp = make_buf(DOWN ? a.hp : a.xp, (uint32_t)((size_t)qrows * nblk * 64));
     xs.d = make_buf(q.d, (uint32_t)((size_t)qrows * q.nb * 4));
-    xs.spd = buf_desc(DOWN ? a.hp : a.xp, (uint32_t)((size_t)qrows * nblk * 64));
-    xs.dd = buf_desc(q.d, (uint32_t)((size_t)qrows * q.nb * 4));
 
     /* the expert of the item being issued, and its matrices */
     int iss_ai = -1;
-    u32x4 iss_w[NM];
+    Buf iss_w[NM];
     u32x4 vA[NM][CH], vB[NM][CH];   /* slabs of two items ahead, alternating */
     auto set_issuer = [&](int ai) {
         iss_ai = ai;
@@ -373,24 +285,9 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
 #pragma unroll
         for (int m = 0; m < NM; m++) {
             const uint64_t base = DOWN ? ldc(a.down, e) : (m ? ldc(a.up, e) : ldc(a.gate, e));
-            iss_w[m] = buf_desc((const void *)(uintptr_t)base, mbytes);
+            iss_w[m] = make_buf((const void *)(uintptr_t)base, mbytes);
         }
     };
-    auto issue = [&](u32x4 (&v)[NM][CH], int item) {
-        if (item / nslab != iss_ai) set_issuer(item / nslab);
-        const uint32_t off = (uint32_t)(item % nslab) * 16u * rb;
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-            uint32_t o[CH];
-#pragma unroll
-            for (int c = 0; c < CH; c++) {
-                const uint32_t i = (uint32_t)(tid + NT * c) * 16u;
-                o[c] = i < slab ? off + i : OOB;
-            }
-            ldu_slab<CH>(v[m], iss_w[m], o);
-        }
-    };
-
     XBatch<MT> xb;
     int xrow[MT];
     /* this workgroup's run of items: an equal share of the total cost */
@@ -410,12 +307,28 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     const int it_end = blockIdx.x + 1 == gridDim.x ? nitems : (nact ? item_at(total * (blockIdx.x + 1) / gridDim.x) : 0);
     if (it >= it_end) return;   /* uniform */
 
+    /* an item's slabs; an item past the run reads zeros (no memory access),
+     * so every item issues the same loads */
+    auto issue = [&](u32x4 (&v)[NM][CH], int item) {
+        const bool ok = item < it_end;
+        if (ok && item / nslab != iss_ai) set_issuer(item / nslab);
+        const uint32_t off = (uint32_t)(item % nslab) * 16u * rb;
+#pragma unroll
+        for (int m = 0; m < NM; m++) {
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const uint32_t i = (uint32_t)(tid + NT * c) * 16u;
+                v[m][c] = ld16_nt(iss_w[m], ok && i < slab ? off + i : OOB);
+            }
+        }
+    };
+
     /* per-expert state: the expert's pairs, biases (empty buffers read
      * zero) and the input rows of its first 16 pairs */
     struct Expert {
         int ai, p0, ne;
         bool has0, has1;
-        u32x4 bias[2];
+        Buf bias[2];
     };
     const Buf prow_buf = make_buf(a.p_row, (uint32_t)a.P * 4u), pw_buf = make_buf(a.p_w, (uint32_t)a.P * 4u);
     auto expert = [&](int ai) {
@@ -429,8 +342,8 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
         const float *b1p = DOWN ? nullptr : (a.ubias ? (const float *)(uintptr_t)ldc(a.ubias, e) : nullptr);
         x.has0 = b0p != nullptr;
         x.has1 = b1p != nullptr;
-        x.bias[0] = buf_desc(b0p, b0p ? (uint32_t)rows * 4u : 0u);
-        x.bias[1] = buf_desc(b1p, b1p ? (uint32_t)rows * 4u : 0u);
+        x.bias[0] = make_buf(b0p, b0p ? (uint32_t)rows * 4u : 0u);
+        x.bias[1] = make_buf(b1p, b1p ? (uint32_t)rows * 4u : 0u);
         return x;
     };
     /* input row of pair j of an expert (phase A: its q8 row, phase B: the
@@ -470,25 +383,20 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
     wait_copies();   /* a wait the compiler sees: the pair loads are not pending in the item loop */
     xrow[0] = c16 < cur.ne ? xrows[0] : -1;
     issue(vA, it);
-    load_batch<MT, true>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
-    bool xnew = true;   /* this item's first q8 batch was loaded for it (not kept) */
+    load_batch<MT>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
     int er = ep_row(it);
-    float bias0, bias1;
-    ldu_bias(bias0, bias1, cur.bias[0], cur.bias[1], (uint32_t)er * 4u);
+    float bias0 = __uint_as_float(ld4(cur.bias[0], (uint32_t)er * 4u));
+    float bias1 = __uint_as_float(ld4(cur.bias[1], (uint32_t)er * 4u));
     float wt = wts[0];
     __builtin_amdgcn_sched_barrier(0);
-    if (it + 1 < it_end) issue(vB, it + 1);
+    issue(vB, it + 1);
 
     /* Per item, loads are issued in one fixed order: the next expert's pair
      * rows (when it changes), then after the compute the next item's q8
-     * operands (unless kept) and biases, then the slabs two items ahead.
-     * Loads complete in order, so no wait for an item's operands ever waits
-     * for a younger slab, and every slab has a whole item of lead.  The
-     * slabs, q8 operands and biases are untracked loads; an item waits for
-     * them with the count of those issued after them: its slabs are
-     * followed by its q8 operands (XLOADS, if loaded), biases (2) and the
-     * next item's slabs (S, if there is a next item). */
-    constexpr int S = NM * CH;
+     * operands (unless kept) and biases, then the slabs two items ahead (past
+     * the run they read zeros).  Loads complete in order, so the compiler's
+     * wait for an item's slab leaves the next item's slab in flight, and
+     * every slab has a whole item of lead. */
     float acc[NM][MT][4];
     /* one pass: the partial sums of every wave to LDS, then 256 threads add
      * them in wave order and write one result each */
@@ -534,40 +442,18 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
             fetch_pairs(nxt, nxrows, nwts);
         }
         bar_lds();   /* the previous item is done with LDS */
-        if (xnew) {
-            if (has_nx) vm_wait<XLOADS + 2 + S>();
-            else vm_wait<XLOADS + 2>();
-        } else {
-            if (has_nx) vm_wait<2 + S>();
-            else vm_wait<2>();
-        }
 #pragma unroll
         for (int m = 0; m < NM; m++)
 #pragma unroll
-            for (int c = 0; c < CH; c++) {
-                pin(v[m][c]);
+            for (int c = 0; c < CH; c++)
                 *(u32x4 *)((uint8_t *)lds + m * sstride + (uint32_t)(tid + NT * c) * 16u) = v[m][c];
-            }
         bar_lds();
-        /* first pass: its first batch of q8 operands is in registers */
-        if (has_nx) vm_wait<2 + S>();
-        else vm_wait<2>();
-#pragma unroll
-        for (int q = 0; q < NG; q++) {
-            pin(xb.hi[0][q]);
-            pin(xb.lo[0][q]);
-            pin(xb.d[0][q]);
-        }
         zero();
         mma_batch<NM, MT>(lds, sstride, rb, xb, b0w, min(b1w, b0w + XB), 1, lane, acc);
         for (int bb = b0w + XB; bb < b1w; bb += XB) {   /* rows wider than NWAVE * XB blocks */
             load_batch(xb, xs, bb, min(b1w, bb + XB), 1, xrow, g);
             mma_batch<NM, MT>(lds, sstride, rb, xb, bb, min(b1w, bb + XB), 1, lane, acc);
         }
-        if (has_nx) vm_wait<S>();
-        else vm_wait<0>();
-        pin(bias0);
-        pin(bias1);
         finish(0);
         /* further passes over the resident slab for an expert with more than
          * 16 pairs */
@@ -610,15 +496,15 @@ __global__ __launch_bounds__(NT) void k_moe_mx(MoeArgs a) {
                 }
             }
             xrow[0] = c16 < cur.ne ? xrows[0] : -1;
-            if (!keep) load_batch<MT, true>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
-            xnew = !keep;
+            if (!keep) load_batch<MT>(xb, xs, b0w, min(b1w, b0w + XB), 1, xrow, g);
             er = ep_row(nx);
-            ldu_bias(bias0, bias1, cur.bias[0], cur.bias[1], (uint32_t)er * 4u);
+            bias0 = __uint_as_float(ld4(cur.bias[0], (uint32_t)er * 4u));
+            bias1 = __uint_as_float(ld4(cur.bias[1], (uint32_t)er * 4u));
             wt = wts[0];
         }
         /* then the slabs two items ahead, into the registers just stored */
         __builtin_amdgcn_sched_barrier(0);
-        if (it + 2 < it_end) issue(v, it + 2);
+        issue(v, it + 2);
         it = nx;
     };
     while (it < it_end) {

@@ -7,7 +7,7 @@
  * takes numpy.argmax of each row's logits (tinygiant/specdec.py:77,90,
  * engine.py:187).  Here the head is read once for all k rows:
  *
- *   k_head_q6k<K>   Q6_K head with 2048 columns: every lane owns one 128-value
+ *   k_head_q6k<K,L> Q6_K head with 2048 columns: every lane owns one 128-value
  *                   half-block of one vocab row, decodes its 6-bit codes once
  *                   and dots them with the k q8 rows staged in LDS; the 16
  *                   lanes of a row are summed by DPP; the next row group's
@@ -26,6 +26,15 @@
  * Argmax keys pack an order-preserving image of the f32 logit above the
  * complement of the row index, so the maximum key is the largest logit and,
  * among equal logits, the first row -- numpy.argmax's tie rule.
+ *
+ * The finish is ordered by the atomics themselves, all relaxed and all on the
+ * device-coherent words best[]: a workgroup's atomicMax returns (its result
+ * is stored before the workgroup barrier) before thread 0 takes the ticket,
+ * so every key is in best[] before the ticket that sees gridDim.x - 1, and
+ * the last workgroup reads best[] with device-scope atomic loads.  Release /
+ * acquire orderings on the ticket would add nothing the keys need and make
+ * every workgroup write back and invalidate its L2 (buffer_wbl2 / buffer_inv):
+ * measured 45.5 -> 70.4 us for the 1-row head.
  */
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -66,58 +75,34 @@ struct HHalf {
     u32x2 sc;
     uint32_t d;
 };
-__device__ inline HHalf load_hhalf(Buf b, uint32_t blk, int h) {
+/* Its loads, tracked by the compiler, from byte `off` of the matrix (the
+ * whole offset in the VGPR: a raw buffer's range check covers that offset
+ * and not the SGPR one, and loads past the matrix must read zero) */
+__device__ inline HHalf load_hhalf(Buf b, uint32_t off, int h) {
     HHalf r;
-    const uint32_t ql = blk + 64u * h, qh = blk + 128u + 32u * h;
-    r.la0 = ld16(b, ql);
-    r.la1 = ld16(b, ql + 16);
-    r.lb0 = ld16(b, ql + 32);
-    r.lb1 = ld16(b, ql + 48);
-    r.h0 = ld16(b, qh);
-    r.h1 = ld16(b, qh + 16);
-    r.sc = ld8(b, blk + 192u + 8u * h);
-    r.d = ld4(b, blk + 206u);
+    const int ql = (int)off + 64 * h, qh = (int)off + 128 + 32 * h;
+    r.la0 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql, 0, 0);
+    r.la1 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql + 16, 0, 0);
+    r.lb0 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql + 32, 0, 0);
+    r.lb1 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql + 48, 0, 0);
+    r.h0 = __builtin_amdgcn_raw_buffer_load_b128(b.r, qh, 0, 0);
+    r.h1 = __builtin_amdgcn_raw_buffer_load_b128(b.r, qh + 16, 0, 0);
+    r.sc = __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)off + 192 + 8 * h, 0, 0);
+    r.d = __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)off + 206, 0, 0);
     return r;
+}
+
+/* An empty statement that reads every register of a half-block: the
+ * compiler waits for its loads there, on every path (the decode below may
+ * otherwise be sunk into the branch of the first input row, and a path that
+ * skips it would leave the loads pending into the next turn of the loop,
+ * where their registers get reused and the compiler then waits for every
+ * load, the prefetch included). */
+__device__ inline void consume(const HHalf &r) {
+    asm volatile("" ::"v"(r.la0), "v"(r.la1), "v"(r.lb0), "v"(r.lb1), "v"(r.h0), "v"(r.h1), "v"(r.sc), "v"(r.d));
 }
 
 __device__ inline uint32_t pick(const u32x4 &v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
-
-/* Weight loads issued from inline assembly, which the compiler does not
- * track: the kernels below wait for them themselves (s_waitcnt vmcnt(N) with
- * N = the loads issued after the ones waited for; the counter completes in
- * order).  Across register sets that take turns, the compiler's own wait
- * analysis lost count and waited for every prefetched load.  A vector memory
- * instruction may read an SGPR (the descriptor) only 5 wait states after a
- * VALU instruction wrote it; the compiler pads its own loads for that but
- * not inline assembly, so each item's loads form one statement that starts
- * with s_nop 4 (nothing can be scheduled between them).  The outputs are
- * early-clobber: no destination shares a register with an address that a
- * later load of the statement reads. */
-constexpr int HLOADS = 8;
-/* one lane's half-block for k_head_q6k */
-__device__ inline HHalf load_hhalf_asm(const u32x4 &d, uint32_t blk, int h) {
-    HHalf r;
-    const uint32_t ql = blk + 64u * (uint32_t)h, qh = blk + 32u * (uint32_t)h, sc = blk + 8u * (uint32_t)h;
-    asm volatile(
-        "s_nop 4\n\t"
-        "buffer_load_dwordx4 %0, %8, %12, 0 offen offset:0\n\t"
-        "buffer_load_dwordx4 %1, %8, %12, 0 offen offset:16\n\t"
-        "buffer_load_dwordx4 %2, %8, %12, 0 offen offset:32\n\t"
-        "buffer_load_dwordx4 %3, %8, %12, 0 offen offset:48\n\t"
-        "buffer_load_dwordx4 %4, %9, %12, 0 offen offset:128\n\t"
-        "buffer_load_dwordx4 %5, %9, %12, 0 offen offset:144\n\t"
-        "buffer_load_dwordx2 %6, %10, %12, 0 offen offset:192\n\t"
-        "buffer_load_dword %7, %11, %12, 0 offen offset:206"
-        : "=&v"(r.la0), "=&v"(r.la1), "=&v"(r.lb0), "=&v"(r.lb1), "=&v"(r.h0), "=&v"(r.h1), "=&v"(r.sc), "=&v"(r.d)
-        : "v"(ql), "v"(qh), "v"(sc), "v"(blk), "s"(d));
-    return r;
-}
-template <int N>
-__device__ inline void wait_hhalf(HHalf &r) {
-    asm volatile("s_waitcnt vmcnt(%8)"
-                 : "+v"(r.la0), "+v"(r.la1), "+v"(r.lb0), "+v"(r.lb1), "+v"(r.h0), "+v"(r.h1), "+v"(r.sc), "+v"(r.d)
-                 : "n"(N));
-}
 
 }  // namespace
 
@@ -158,7 +143,7 @@ constexpr int log2_of(int n) { return n <= 1 ? 0 : n == 2 ? 1 : n == 4 ? 2 : n =
  * receive the argmax keys and best[16] counts finished workgroups; both
  * start at zero (cleared by the kernel that quantizes x).  The last
  * workgroup to finish writes idx[j] / val[j]. */
-template <int K>
+template <int K, bool LOGITS>
 __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
                                                  float *logits, unsigned long long *best, int32_t *idx, float *val) {
     constexpr int N = pow2_at_least(K);
@@ -184,25 +169,26 @@ __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(con
      * several lanes hold the same one and the first of them owns it */
     const int slot = hb >> (4 - log2_of(N));
     const bool owner = (hb & (16 / N - 1)) == 0 && slot < k;
-    const int gw = blockIdx.x * HW + (threadIdx.x >> 6), nw = gridDim.x * HW;
+    /* wave-uniform (readfirstlane): the loop branches on scalars */
+    const int gw = __builtin_amdgcn_readfirstlane(blockIdx.x * HW + (threadIdx.x >> 6)), nw = gridDim.x * HW;
     const int nq = (nrows + RPW - 1) / RPW;
     uint64_t mybest = 0;
 
-#ifndef TG_HEAD_PF
-#define TG_HEAD_PF 1
-#endif
-    /* row group q of this lane: its half-block; PF + 1 register sets take
-     * turns, the loads of the group PF ahead go out before each group is
-     * computed */
-    constexpr int PF = TG_HEAD_PF;
-    const u32x4 wd = buf_desc(W, (uint32_t)((size_t)nrows * HRB));
-    auto group_at = [&](int qq) {
-        return load_hhalf_asm(wd, (uint32_t)(RPW * qq + rsub) * HRB + (uint32_t)b * 210u, h);
-    };
+    /* Row group q of this lane: its half-block.  Two register sets take
+     * turns: the loads of the next group go out (the scheduling barrier
+     * keeps them first) before the current group is computed, and the
+     * compiler waits for the current one with the next one's 8 loads still
+     * in flight (the group past the last reads zero past the end).  The
+     * argmax-only kernel stores nothing in the loop: with stores pending
+     * beside the loads the compiler's waits become vmcnt(0). */
+    const Buf wbuf = make_buf(W, (uint32_t)((size_t)nrows * HRB));
+    const uint32_t lane_off = (uint32_t)(rsub * HRB + b * 210);
+    auto group_at = [&](int qq) { return load_hhalf(wbuf, lane_off + (uint32_t)(RPW * qq * HRB), h); };
     int q = gw;
     auto step = [&](HHalf &cur, HHalf &nxt) {
-        nxt = group_at(q + PF * nw);
-        wait_hhalf<PF * HLOADS>(cur);
+        nxt = group_at(q + nw);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(cur);
         const uint32_t row = (uint32_t)(RPW * q + rsub);
         /* 6-bit codes of the half (q = ql nibble | qh pair << 4), decoded once */
         const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
@@ -249,32 +235,24 @@ __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(con
         }
         const float v = rscatter16<N>(vv, hb);
         if (owner && row < (uint32_t)nrows) {
-            if (logits) logits[(size_t)slot * nrows + row] = v;
+            if (LOGITS) logits[(size_t)slot * nrows + row] = v;
             const uint64_t key = argmax_key(v, row);
             mybest = key > mybest ? key : mybest;
         }
         q += nw;
     };
-    HHalf s0 = group_at(q), s1, s2;
-    if (PF == 1) {
-        for (;;) {
-            if (q >= nq) break;
-            step(s0, s1);
-            if (q >= nq) break;
-            step(s1, s0);
-        }
-    } else {
-        s1 = group_at(q + nw);
-        for (;;) {
-            if (q >= nq) break;
-            step(s0, s2);
-            if (q >= nq) break;
-            step(s1, s0);
-            if (q >= nq) break;
-            step(s2, s1);
-        }
+    /* the wave's groups in pairs, one exit at the loop's top (an exit after
+     * the first step of a pair would join the loop's head with that step's
+     * loads pending, and the compiler would wait for them there), then the
+     * odd one */
+    const int nsteps = q < nq ? (nq - 1 - q) / nw + 1 : 0;
+    HHalf s0 = group_at(q), s1;
+    int i = 0;
+    for (; i + 2 <= nsteps; i += 2) {
+        step(s0, s1);
+        step(s1, s0);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   /* the prefetch past the last group */
+    if (i < nsteps) step(s0, s1);
     /* workgroup best per input row, then one atomic max each */
     if (owner && slot < K) wb_best[slot][(threadIdx.x >> 6) * RPW + rsub] = mybest;
     __syncthreads();
@@ -576,7 +554,13 @@ void launch_head_q6k(const uint8_t *W, int nrows, const Q8Rows &x, int k, float 
     const int nq = (nrows + RPW - 1) / RPW;
     const int grid = std::max(1, std::min(cus * 4, (nq + HW - 1) / HW));
 /* k is rounded up to an instantiated K; rows j >= k skip their dots */
-#define TG_HEAD(KK) hipLaunchKernelGGL(k_head_q6k<KK>, dim3(grid), dim3(HT), 0, st, W, nrows, x, k, logits, best, idx, val)
+#define TG_HEAD(KK)                                                                                         \
+    do {                                                                                                    \
+        if (logits)                                                                                         \
+            hipLaunchKernelGGL((k_head_q6k<KK, true>), dim3(grid), dim3(HT), 0, st, W, nrows, x, k, logits, best, idx, val);  \
+        else                                                                                                \
+            hipLaunchKernelGGL((k_head_q6k<KK, false>), dim3(grid), dim3(HT), 0, st, W, nrows, x, k, logits, best, idx, val); \
+    } while (0)
     if (k <= 1) TG_HEAD(1);
     else if (k <= 2) TG_HEAD(2);
     else if (k <= 4) TG_HEAD(4);
