@@ -341,48 +341,61 @@ def phase_breakdown(tg, step, layers):
     return out
 
 
-def boundary_probe(tg, routes, calls=50):
+def boundary_probe(tg, routes, calls=52, n_layers=13):
     """The reference's own entry point through ctypes: tg_moe_forward_rows_v2
-    on host input/output arrays for one layer (k = 1), its 24 weight matrices
-    made HBM-resident with tg_mlock as tinygiant/cache.py:153-162 does.  Each
+    on host input/output arrays for one layer (k = 1), the 24 weight matrices
+    of each of n_layers layers made HBM-resident with tg_mlock as
+    tinygiant/cache.py:153-162 does; the calls take the layers in turn (13
+    layers put 318 MB of weights between two reads of the same bytes).  Each
     call copies the 8 KB input in and the 8 KB output back over PCIe and
     synchronizes, so this is the per-layer latency an unchanged engine sees."""
     import tinygiant_amd.synth as S
     lib = tg.lib()
-    idx, w = routes[0]
-    mats = []
-    for e in idx:
-        for part, kind, nb in ((0, 0, I * (D // 256) * 144), (1, 0, I * (D // 256) * 144),
-                               (2, 2, D * (I // 256) * 210)):
-            m = tg.synth_host(kind, S.tensor_seed(SEED, 0, int(e), part), nb)
-            if lib.tg_mlock(m.ctypes.data, ctypes.c_size_t(m.nbytes)) != 0:
-                raise RuntimeError("tg_mlock failed")
-            mats.append(m)
-    n = len(idx)
-    gates, ups, downs = mats[0::3], mats[1::3], mats[2::3]
+    layers, keep = [], []
+    for li in range(n_layers):
+        idx, w = routes[li % len(routes)]
+        mats = []
+        for e in idx:
+            for part, kind, nb in ((0, 0, I * (D // 256) * 144), (1, 0, I * (D // 256) * 144),
+                                   (2, 2, D * (I // 256) * 210)):
+                m = tg.synth_host(kind, S.tensor_seed(SEED, li, int(e), part), nb)
+                if lib.tg_mlock(m.ctypes.data, ctypes.c_size_t(m.nbytes)) != 0:
+                    raise RuntimeError("tg_mlock failed")
+                mats.append(m)
+        keep += mats
+        layers.append((mats[0::3], mats[1::3], mats[2::3], w.reshape(-1, 1).astype(np.float32)))
     x = np.random.default_rng(SEED + 3).standard_normal((1, D)).astype(np.float32)
-    rw = w.reshape(-1, 1).astype(np.float32)
     out = np.zeros((1, D), np.float32)
-    for _ in range(5):
-        tg.moe_forward_rows_v2(gates, ups, downs, 0, [2] * n, None, None, None, 0, rw, x, out, I)
+
+    def call(i):
+        g, u, d, rw = layers[i % n_layers]
+        tg.moe_forward_rows_v2(g, u, d, 0, [2] * len(g), None, None, None, 0, rw, x, out, I)
+    for i in range(n_layers):
+        call(i)
     t0 = time.perf_counter()
-    for _ in range(calls):
-        tg.moe_forward_rows_v2(gates, ups, downs, 0, [2] * n, None, None, None, 0, rw, x, out, I)
+    for i in range(calls):
+        call(i)
     dt = (time.perf_counter() - t0) / calls
-    for m in mats:
+    for m in keep:
         lib.tg_hip_unregister(m.ctypes.data)
+    n = len(layers[0][0])
     return {"entry": "tg_moe_forward_rows_v2 via ctypes, host buffers, tg_mlock-resident weights, k=1",
+            "rotation": {"layers": n_layers, "distinct_bytes": n_layers * n * EXPERT_B},
             "us_per_layer_call": round(dt * 1e6, 1), "weight_gbps": round(n * EXPERT_B / dt / 1e9, 1),
             "tok_s_if_48_calls": round(1.0 / (dt * L), 1)}
 
 
-def verify_probe(tg, base, ks=(5, 9, 1), iters=20):
+def verify_probe(tg, bases, ks=(5, 9, 1), iters=20):
     """One layer of a self-speculative verify batch: k rows (the draft tokens
-    plus t0), each picking its own top-8 of the 128 resident experts of layer 0
-    (Zipf), through the planned multi-row MoE path (tg_hip_moe_plan_run: q8,
-    gate/up + SwiGLU, q8 of hidden, down, expert-order combine).  Weight
-    bytes = every expert of the union, read once.  k = 1 is one Qwen3 layer
-    for one token on the per-layer kernels."""
+    plus t0), each picking its own top-8 of the 128 resident experts (Zipf),
+    through the planned multi-row MoE path (tg_hip_moe_plan_run: q8, gate/up +
+    SwiGLU, q8 of hidden, down, expert-order combine).  The same routing is
+    planned on each of the layers in `bases` (their own 128 experts) and the
+    timed calls rotate over them, so a call reads weights the previous
+    len(bases) - 1 calls did not (the union of k = 5 is ~95 MB; six layers
+    put ~570 MB between two reads of the same bytes, over the 256 MB
+    Infinity Cache).  Weight bytes = every expert of the union, read once.
+    k = 1 is one Qwen3 layer for one token on the per-layer kernels."""
     import tinygiant_amd.synth as S
     lib = tg.lib()
     rng = np.random.default_rng(SEED + 19)
@@ -393,33 +406,93 @@ def verify_probe(tg, base, ks=(5, 9, 1), iters=20):
         kr = rng if k != 1 else np.random.default_rng(SEED + 18)
         experts, rw = S.routing_rows(kr, k, E, TOPK, 1.1, perm)
         n = len(experts)
-        gp = (ctypes.c_void_p * n)(*[base + int(e) * GATE_B for e in experts])
-        up = (ctypes.c_void_p * n)(*[base + E * GATE_B + int(e) * GATE_B for e in experts])
-        dp = (ctypes.c_void_p * n)(*[base + 2 * E * GATE_B + int(e) * DOWN_B for e in experts])
         fm = np.full(n, tg.FMT_Q6K, np.int32)
         rwc = np.ascontiguousarray(rw, np.float32)
-        plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
-                                          tg.FMT_Q4K, fm.ctypes.data, None, None, None, tg.ACT_SILU, n,
-                                          rwc.ctypes.data, k, D, I)
-        if not plan:
-            raise RuntimeError(tg.last_error())
+        plans = []
+        for base in bases:
+            gp = (ctypes.c_void_p * n)(*[base + int(e) * GATE_B for e in experts])
+            up = (ctypes.c_void_p * n)(*[base + E * GATE_B + int(e) * GATE_B for e in experts])
+            dp = (ctypes.c_void_p * n)(*[base + 2 * E * GATE_B + int(e) * DOWN_B for e in experts])
+            plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
+                                              tg.FMT_Q4K, fm.ctypes.data, None, None, None, tg.ACT_SILU, n,
+                                              rwc.ctypes.data, k, D, I)
+            if not plan:
+                raise RuntimeError(tg.last_error())
+            plans.append(plan)
         x = tg.DeviceArray(k * D * 4)
         x.upload(kr.standard_normal((k, D)).astype(np.float32))
         y = tg.DeviceArray(k * D * 4)
-        for _ in range(3):
-            lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None)
+        for p in plans:
+            lib.tg_hip_moe_plan_run(p, x.ptr, y.ptr, None)
         lib.tg_hip_mark(0)
-        for _ in range(iters):
-            lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None)
+        for i in range(iters):
+            lib.tg_hip_moe_plan_run(plans[i % len(plans)], x.ptr, y.ptr, None)
         lib.tg_hip_mark(1)
         us = lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
         nbytes = n * EXPERT_B
         out[k] = {"experts": n, "rows_per_expert_max": int((rw != 0).sum(axis=1).max()), "us": round(us, 2),
                   "weight_bytes": nbytes, "weight_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
-                  "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-        lib.tg_hip_moe_plan_destroy(plan)
+                  "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                  "rotation": {"layers": len(plans), "distinct_bytes": len(plans) * nbytes}}
+        for p in plans:
+            lib.tg_hip_moe_plan_destroy(p)
         x.free()
         y.free()
+    return out
+
+
+def spec_probe(tg, ks=(4, 8), rounds=6, iters=20):
+    """The self-speculative verify workload end to end (tinygiant_amd.specdec):
+    greedy rounds of K draft passes (routing restricted to the 64 most
+    popular experts) and one exact verify pass over [t0] + drafts, each pass
+    one Qwen3-30B-A3B MoE layer with all 128 experts resident plus the
+    151936 x 2048 q6_K head, the drafts accepted while the target's argmax
+    agrees (tinygiant/specdec.py:57-108).  Two models of distinct weights
+    (646 MB each) take turns, round by round and pass by pass, so no pass
+    finds its bytes in the Infinity Cache.  Reported: the rounds' accepted
+    drafts, the wall time of a round as the host drives it (routing read back
+    per pass, as the reference routes in Python), and the device time of a
+    verify pass and of a draft pass (RMSNorm, router, MoE over the union,
+    head with argmax) with their weight bytes."""
+    import tinygiant_amd.specdec as SD
+    models = [SD.SpecLayer(SEED + 101 + i) for i in range(2)]
+    out = {"layer": "qwen3-30b-a3b MoE layer, 128 resident experts (q4_K gate/up, q6_K down), router 128x2048 f32 "
+                    "with Zipf(1.1) bias, q6_K head 151936x2048", "resident_for_drafts": 64,
+           "rotation": {"models": 2, "distinct_bytes": 2 * models[0].weight_bytes()}, "k": {}}
+    try:
+        for K in ks:
+            rr = np.random.default_rng(SEED + 120 + K)
+            wall, acc, unions, first = [], [], [], None
+            for r in range(rounds):
+                t0 = int(rr.integers(SD.VOCAB))
+                t = time.perf_counter()
+                res = models[r % 2].verify_round(t0, K)
+                wall.append(time.perf_counter() - t)
+                acc.append(res["accepted"])
+                unions.append(len(res["union"]))
+                if first is None:
+                    first = (t0, res["drafts"])
+            t0, drafts = first
+            v_us, v_bytes, v_exp = SD.time_passes(models, [t0] + drafts, draft=False, iters=iters)
+            d_us, d_bytes, _ = SD.time_passes(models, [t0], draft=True, iters=iters)
+            dev_round = K * d_us + v_us
+            emitted = float(np.mean(acc)) + 1.0
+            out["k"][K] = {
+                "rounds": rounds, "accepted": acc, "union_experts": unions,
+                "round_wall_us": round(float(np.median(wall)) * 1e6, 1),
+                "verify_pass": {"rows": K + 1, "experts": v_exp, "us": round(v_us, 2), "weight_bytes": v_bytes,
+                                "weight_gbps": round(v_bytes / (v_us * 1e-6) / 1e9, 1),
+                                "hbm_frac": round(v_bytes / (v_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                "draft_pass": {"rows": 1, "us": round(d_us, 2), "weight_bytes": d_bytes,
+                               "weight_gbps": round(d_bytes / (d_us * 1e-6) / 1e9, 1),
+                               "hbm_frac": round(d_bytes / (d_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)},
+                "round_device_us": round(dev_round, 2),
+                "tokens_per_round": round(emitted, 2),
+                "tok_s_device": round(emitted / (dev_round * 1e-6), 1)}
+            log(f"  spec K={K}: accepted {acc}, verify pass {v_us:.1f} us, draft pass {d_us:.1f} us")
+    finally:
+        for m in models:
+            m.free()
     return out
 
 
@@ -667,43 +740,55 @@ def prefill_probe(tg, iters=20, tokens=64):
 def head_probe(tg, ks=(1, 5, 9, 16), iters=20):
     """The q6_K output head of Qwen3-30B-A3B (151936 x 2048, 255,252,480 B) over
     k verify rows with the argmax fused in (tg_hip_head_argmax_dev, RMSNorm
-    weight applied): time per call from HIP events, weight bytes read once."""
+    weight applied): time per call from HIP events, weight bytes read once.
+    Two heads of distinct bytes take turns, so a call never finds the head
+    it reads in the 256 MB Infinity Cache (510 MB between two reads)."""
     lib = tg.lib()
     nrows, ncols = 151936, 2048
     nbytes = nrows * (ncols // 256) * 210
-    head = tg.DeviceArray(nbytes)
-    lib.tg_hip_synth_fill(2, SEED + 17, head.ptr, nbytes, None)
+    heads = []
+    for i in range(2):
+        h = tg.DeviceArray(nbytes)
+        lib.tg_hip_synth_fill(2, SEED + 17 + 100 * i, h.ptr, nbytes, None)
+        heads.append(h)
     rng = np.random.default_rng(SEED + 18)
     norm = tg.DeviceArray(ncols * 4)
     norm.upload(rng.uniform(0.5, 1.5, ncols).astype(np.float32))
-    out = {"rows": nrows, "cols": ncols, "fmt": "q6_K", "weight_bytes": nbytes, "k": {}}
+    out = {"rows": nrows, "cols": ncols, "fmt": "q6_K", "weight_bytes": nbytes, "rotation": {"heads": 2}, "k": {}}
     for k in ks:
         x = tg.DeviceArray(k * ncols * 4)
         x.upload(rng.standard_normal((k, ncols)).astype(np.float32))
         am = tg.DeviceArray(k * 4)
         sc = tg.DeviceArray(lib.tg_hip_head_scratch_bytes(k, nrows, ncols))
-        args = (2, head.ptr, x.ptr, norm.ptr, ctypes.c_float(1e-6), k, nrows, ncols, None, am.ptr, None, sc.ptr, None)
-        for _ in range(3):
-            lib.tg_hip_head_argmax_dev(*args)
+
+        def call(i):
+            lib.tg_hip_head_argmax_dev(2, heads[i % 2].ptr, x.ptr, norm.ptr, ctypes.c_float(1e-6), k, nrows, ncols,
+                                       None, am.ptr, None, sc.ptr, None)
+        for i in range(4):
+            call(i)
         lib.tg_hip_mark(0)
-        for _ in range(iters):
-            lib.tg_hip_head_argmax_dev(*args)
+        for i in range(iters):
+            call(i)
         lib.tg_hip_mark(1)
         us = lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
         out["k"][k] = {"us": round(us, 2), "weight_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
                        "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
         for a in (x, am, sc):
             a.free()
-    head.free()
-    norm.free()
+    for a in heads + [norm]:
+        a.free()
     return out
 
 
-def attention_probe(tg, kv_lens=(512, 4096), iters=20):
-    """Decode attention of one Qwen3-30B-A3B layer on the device
+def attention_probe(tg, kv_lens=(512, 4096), iters=28, n_layers=28):
+    """Decode attention of a Qwen3-30B-A3B layer on the device
     (tg_hip_attention_dev): D 2048, 32 query heads, 4 KV heads of 128, q4_K
-    q/k/o, q6_K v, QK norm, f32 KV cache.  Algorithmic bytes: the four
-    projection matrices plus one read of the attended K and V rows."""
+    q/k/o, q6_K v, QK norm, f32 KV cache.  n_layers layers, each with its own
+    projection matrices and KV cache, take turns (10.9 MB of weights and up
+    to 16.8 MB of cache a layer; 28 layers hold over 300 MB of weights), so
+    a call reads bytes the Infinity Cache no longer holds, as in a 48-layer
+    step.  Algorithmic bytes: the four projection matrices plus one read of
+    the attended K and V rows."""
     lib = tg.lib()
     D, nh, nkv, hd = 2048, 32, 4, 128
     qd, kd = nh * hd, nkv * hd
@@ -711,13 +796,21 @@ def attention_probe(tg, kv_lens=(512, 4096), iters=20):
     fmts = (0, 0, 2, 0)
     shapes = ((qd, D), (kd, D), (kd, D), (D, qd))
     rng = np.random.default_rng(SEED + 31)
-    mats, wbytes = [], 0
-    for i, ((r, c), f) in enumerate(zip(shapes, fmts)):
-        nb = r * lib.tg_row_bytes(f, c)
-        m = tg.DeviceArray(nb)
-        lib.tg_hip_synth_fill(f, SEED + 32 + i, m.ptr, nb, None)
-        mats.append(m)
-        wbytes += nb
+    layers, wbytes = [], 0
+    kv0 = rng.standard_normal(nkv * kv_max * hd).astype(np.float32)
+    for li in range(n_layers):
+        mats, wb = [], 0
+        for i, ((r, c), f) in enumerate(zip(shapes, fmts)):
+            nb = r * lib.tg_row_bytes(f, c)
+            m = tg.DeviceArray(nb)
+            lib.tg_hip_synth_fill(f, SEED + 32 + i + 8 * li, m.ptr, nb, None)
+            mats.append(m)
+            wb += nb
+        wbytes = wb
+        cache = [tg.DeviceArray(nkv * kv_max * hd * 4) for _ in range(2)]
+        for a in cache:
+            a.upload(kv0)
+        layers.append((mats, cache))
     norms = []
     for _ in range(2):
         a = tg.DeviceArray(hd * 4)
@@ -728,29 +821,32 @@ def attention_probe(tg, kv_lens=(512, 4096), iters=20):
     rc, rs = tg.DeviceArray(kv_max * half * 4), tg.DeviceArray(kv_max * half * 4)
     rc.upload(np.cos(ang).astype(np.float32))
     rs.upload(np.sin(ang).astype(np.float32))
-    cache = [tg.DeviceArray(nkv * kv_max * hd * 4) for _ in range(2)]
-    for a in cache:
-        a.upload((rng.standard_normal(nkv * kv_max * hd)).astype(np.float32))
     x, y = tg.DeviceArray(D * 4), tg.DeviceArray(D * 4)
     x.upload(rng.standard_normal(D).astype(np.float32))
     sc = tg.DeviceArray(lib.tg_hip_attention_scratch_bytes(D, nh, nkv, hd, kv_max))
     out = {"embed_dim": D, "n_heads": nh, "n_kv_heads": nkv, "head_dim": hd, "formats": "q4_K q/k/o, q6_K v",
-           "weight_bytes": wbytes, "kv_len": {}}
+           "weight_bytes": wbytes, "rotation": {"layers": n_layers, "distinct_weight_bytes": n_layers * wbytes},
+           "kv_len": {}}
     for L in kv_lens:
-        args = (*fmts, *[m.ptr for m in mats], None, None, None, None, norms[0].ptr, norms[1].ptr, None,
-                cache[0].ptr, cache[1].ptr, L, kv_max, 0, rc.ptr, rs.ptr, x.ptr, y.ptr, D, nh, nkv, hd, L,
-                ctypes.c_float(1e-6), None, sc.ptr, None)
-        for _ in range(3):
-            lib.tg_hip_attention_dev(*args)
+        def call(i):
+            mats, cache = layers[i % n_layers]
+            lib.tg_hip_attention_dev(*fmts, *[m.ptr for m in mats], None, None, None, None, norms[0].ptr,
+                                     norms[1].ptr, None, cache[0].ptr, cache[1].ptr, L, kv_max, 0, rc.ptr, rs.ptr,
+                                     x.ptr, y.ptr, D, nh, nkv, hd, L, ctypes.c_float(1e-6), None, sc.ptr, None)
+        for i in range(n_layers):
+            call(i)
         lib.tg_hip_mark(0)
-        for _ in range(iters):
-            lib.tg_hip_attention_dev(*args)
+        for i in range(iters):
+            call(i)
         lib.tg_hip_mark(1)
         us = lib.tg_hip_marks_ms(0, 1) * 1e3 / iters
         nbytes = wbytes + 2 * nkv * (L + 1) * hd * 4
         out["kv_len"][L] = {"us": round(us, 2), "bytes": nbytes, "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
                             "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
-    for a in mats + norms + cache + [rc, rs, x, y, sc]:
+    for mats, cache in layers:
+        for a in mats + cache:
+            a.free()
+    for a in norms + [rc, rs, x, y, sc]:
         a.free()
     return out
 
@@ -854,6 +950,9 @@ def main():
                     help="only time a plain 1 GiB device copy (HBM reference / counter calibration)")
     ap.add_argument("--prefill-probe", action="store_true",
                     help="only the gpt-oss 64-token prefill layer on the MFMA expert phases (counter passes)")
+    ap.add_argument("--spec-probe", action="store_true",
+                    help="only the verify-batch probes: the q6_K head, the k-row verify layer and the speculative "
+                         "round (kernel traces and counter passes)")
     ap.add_argument("--qk-prefill-probe", action="store_true",
                     help="only the Qwen3 128-token prefill layer (int8 MFMA and v_dot4 expert phases; counter passes)")
     args = ap.parse_args()
@@ -866,6 +965,19 @@ def main():
     lib = tg.lib()
     if args.copy_probe or args.prefill_probe:
         out = copy_probe(tg) if args.copy_probe else prefill_probe(tg)
+        lib.tg_hip_shutdown()
+        print(json.dumps(out), flush=True)
+        return 0
+    if args.spec_probe:
+        routes6 = routing(6)
+        vbufs, vplans = setup_gpu(tg, 6, routes6)
+        for p in vplans:
+            lib.tg_hip_moe_plan_destroy(p)
+        out = {"verify_layer": verify_probe(tg, [b.ptr for b in vbufs])}
+        for b in vbufs:
+            b.free()
+        out["head_argmax"] = head_probe(tg)
+        out["spec_round"] = spec_probe(tg)
         lib.tg_hip_shutdown()
         print(json.dumps(out), flush=True)
         return 0
@@ -1006,9 +1118,11 @@ def main():
     lib.tg_hip_decode_destroy(step)
     if not args.no_verify:
         log("verify batch probe ...")
-        result["verify_layer"] = verify_probe(tg, bufs[0].ptr)
+        result["verify_layer"] = verify_probe(tg, [b.ptr for b in bufs[:6]])
         log("qwen3 prefill probe ...")
         result["qwen_prefill"] = qwen_prefill_probe(tg, bufs[0].ptr)
+        log("speculative round probe ...")
+        result["spec_round"] = spec_probe(tg)
     for p in plans:
         lib.tg_hip_moe_plan_destroy(p)
     for b in bufs + nbufs + [h]:

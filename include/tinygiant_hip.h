@@ -204,6 +204,16 @@ void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const floa
                       int n_experts, int dim, int top_k, int32_t *idx_dev, float *w_dev,
                       void *scratch_dev, void *stream);
 size_t tg_hip_route_scratch_bytes(int k, int n_experts);
+/* The same with the selection restricted to the resident experts
+ * (resident_dev: one byte per expert, nonzero = resident), as
+ * Router.select(restrict=True) does for a draft pass (tinygiant/router.py:
+ * 46-54, called from engine.py:287 with mode="draft"): the other experts'
+ * logits count as -inf for the top-k, the weights are the softmax of the
+ * selected experts' own logits, and when fewer than top_k experts are
+ * resident the selection is the unrestricted one. */
+void tg_hip_route_restricted_dev(const float *router_dev, const float *bias_dev, const float *x_dev, int k,
+                                 int n_experts, int dim, int top_k, const uint8_t *resident_dev,
+                                 int32_t *idx_dev, float *w_dev, void *scratch_dev, void *stream);
 
 /* Copies nbytes of the file at path, from file_offset on, into device
  * memory at dev_dst: pread into two pinned staging buffers of chunk_bytes

@@ -247,21 +247,30 @@ def expert_forward(q4_data, x, output, weight, D, I):
     return output
 
 
-def route(router, bias, x, top_k):
+def route(router, bias, x, top_k, resident=None):
     """Restates Router.logits, _topk and _weights (tinygiant/router.py:29-42)
     for one normalized row x: float32 logits = router @ x (+ bias), the top_k
     experts by descending logit, and float32 softmax weights over the selected
-    logits only.  Returns (logits, idx, weights).
+    logits only.  Returns (logits, idx, weights).  With a resident mask (bool
+    per expert) the selection is Router.select(restrict=True)
+    (router.py:46-54): the top_k of the logits with the non-resident ones at
+    -inf, weights from the unmasked logits of the selected experts; fewer than
+    top_k resident experts fall back to the unrestricted top_k.
 
     Pinned by: a full sort of the logits on small inputs (selection and
-    order), and closed forms of the softmax (weights sum to 1, are decreasing
-    with the logits, and equal for equal logits) in tests/test_oracle_pins.py."""
+    order), closed forms of the softmax (weights sum to 1, are decreasing
+    with the logits, and equal for equal logits), and the restricted
+    selection against a brute-force filter of the sorted logits, in
+    tests/test_oracle_pins.py."""
     router = np.asarray(router, np.float32)
     logits = router @ np.asarray(x, np.float32)
     if bias is not None:
         logits = logits + np.asarray(bias, np.float32)
-    idx = np.argpartition(logits, -top_k)[-top_k:]
-    idx = idx[np.argsort(logits[idx])[::-1]]
+    sel_from = logits
+    if resident is not None and int(np.count_nonzero(resident)) >= top_k:
+        sel_from = np.where(np.asarray(resident, bool), logits, np.float32(-np.inf))
+    idx = np.argpartition(sel_from, -top_k)[-top_k:]
+    idx = idx[np.argsort(sel_from[idx])[::-1]]
     sel = logits[idx]
     e = np.exp(sel - sel.max())
     return logits, idx, (e / e.sum()).astype(np.float32)

@@ -21,7 +21,7 @@ def say(*a):
     sys.stdout.flush()
 
 
-def _route(tg, router, bias, x, top_k):
+def _route(tg, router, bias, x, top_k, resident=None):
     lib = tg.lib()
     k, dim = x.shape
     n_exp = router.shape[0]
@@ -39,7 +39,13 @@ def _route(tg, router, bias, x, top_k):
     w = tg.DeviceArray(k * top_k * 4)
     sc = tg.DeviceArray(lib.tg_hip_route_scratch_bytes(k, n_exp))
     lib.tg_hip_clear_error()
-    lib.tg_hip_route_dev(rd.ptr, bd.ptr if bd else None, xd.ptr, k, n_exp, dim, top_k, idx.ptr, w.ptr, sc.ptr, None)
+    if resident is None:
+        lib.tg_hip_route_dev(rd.ptr, bd.ptr if bd else None, xd.ptr, k, n_exp, dim, top_k, idx.ptr, w.ptr, sc.ptr,
+                             None)
+    else:
+        md = dev(np.asarray(resident, np.uint8))
+        lib.tg_hip_route_restricted_dev(rd.ptr, bd.ptr if bd else None, xd.ptr, k, n_exp, dim, top_k, md.ptr, idx.ptr,
+                                        w.ptr, sc.ptr, None)
     lib.tg_hip_synchronize()
     assert tg.last_error() == "", tg.last_error()
     gi = idx.download(np.int32, k * top_k).reshape(k, top_k)
@@ -69,3 +75,32 @@ def test_route_matches_oracle(tg, orc, n_exp, dim, top_k, k, with_bias):
             continue
         assert np.abs(gw[j] - w).max() <= 2e-6, (j, gw[j], w)
         assert abs(float(gw[j].sum()) - 1.0) <= 1e-6
+
+
+@pytest.mark.parametrize("n_res", [64, 9, 8, 3])
+def test_route_restricted_matches_oracle(tg, orc, n_res):
+    """A draft pass's routing (Router.select(restrict=True),
+    tinygiant/router.py:46-54) over 128 experts of which n_res are resident:
+    the same bars as above, against the oracle's restricted selection (3
+    resident experts: fewer than top_k, the unrestricted selection)."""
+    n_exp, dim, top_k, k = 128, 2048, 8, 5
+    say(f"route restricted n_res={n_res}")
+    rng = np.random.default_rng(700 + n_res)
+    router = (rng.standard_normal((n_exp, dim)) * 0.05).astype(np.float32)
+    bias = (rng.standard_normal(n_exp) * 0.1).astype(np.float32)
+    resident = np.zeros(n_exp, bool)
+    resident[rng.choice(n_exp, n_res, replace=False)] = True
+    x = rng.standard_normal((k, dim)).astype(np.float32)
+    gi, gw = _route(tg, router, bias, x, top_k, resident=resident)
+    for j in range(k):
+        logits, idx, w = orc.route(router, bias, x[j], top_k, resident=resident)
+        if n_res >= top_k:
+            assert all(resident[e] for e in gi[j]), (j, list(gi[j]))
+        tol = 1e-5 * np.abs(logits).max()
+        if list(gi[j]) != list(idx):
+            pool = logits[resident] if n_res >= top_k else logits
+            order = np.sort(pool)[::-1]
+            gaps = np.abs(np.diff(order[:top_k + 1]))
+            assert gaps.min() <= tol, (j, list(gi[j]), list(idx))
+            continue
+        assert np.abs(gw[j] - w).max() <= 2e-6, (j, gw[j], w)

@@ -483,6 +483,36 @@ def test_route_oracle_selection_and_softmax(orc):
     assert np.allclose(w, 0.25)
 
 
+
+def test_route_oracle_restricted_selection(orc):
+    """Router.select(restrict=True) (tinygiant/router.py:46-54): the top_k of
+    the resident experts by a brute-force filter of the fully sorted logits,
+    weights equal to an unrestricted route over just those experts' rows
+    (the softmax of their own logits), and the unrestricted selection when
+    fewer than top_k experts are resident."""
+    rng = np.random.default_rng(11)
+    for n_exp, dim, top_k, n_res in ((128, 64, 8, 64), (32, 16, 4, 5), (16, 8, 2, 2)):
+        router = rng.standard_normal((n_exp, dim)).astype(np.float32)
+        bias = rng.standard_normal(n_exp).astype(np.float32)
+        x = rng.standard_normal(dim).astype(np.float32)
+        resident = np.zeros(n_exp, bool)
+        resident[rng.choice(n_exp, n_res, replace=False)] = True
+        logits, idx, w = orc.route(router, bias, x, top_k, resident=resident)
+        full = np.argsort(-logits.astype(np.float64), kind="stable")
+        assert list(idx) == [e for e in full if resident[e]][:top_k]
+        sub = np.flatnonzero(resident)
+        _, sidx, sw = orc.route(router[sub], bias[sub], x, top_k)
+        assert list(sub[sidx]) == list(idx)
+        assert np.array_equal(sw, w)
+    # fewer resident experts than top_k: unrestricted
+    router = rng.standard_normal((16, 8)).astype(np.float32)
+    x = rng.standard_normal(8).astype(np.float32)
+    resident = np.zeros(16, bool)
+    resident[:3] = True
+    a = orc.route(router, None, x, 4, resident=resident)
+    b = orc.route(router, None, x, 4)
+    assert list(a[1]) == list(b[1]) and np.array_equal(a[2], b[2])
+
 # ---- decode attention (tg_attention_v2, csrc/libtinygiant.c:939-983) ----
 
 def _attn_case(seed, D=256, nh=8, nkv=2, hd=32, kv_max=40, kv_len=17, zero_q=False, bias=True, norms=True):

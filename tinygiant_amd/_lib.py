@@ -99,6 +99,7 @@ def register_extensions(lib):
     _reg(lib.tg_hip_head_scratch_bytes, [CI, CI, CI], SZ)
     _reg(lib.tg_hip_route_dev, [VP, VP, VP, CI, CI, CI, CI, VP, VP, VP, VP])
     _reg(lib.tg_hip_route_scratch_bytes, [CI, CI], SZ)
+    _reg(lib.tg_hip_route_restricted_dev, [VP, VP, VP, CI, CI, CI, CI, VP, VP, VP, VP, VP])
     _reg(lib.tg_hip_attention_dev, [CI, CI, CI, CI, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, VP, CI, CI, CI,
                                     VP, VP, VP, VP, CI, CI, CI, CI, CI, CF, VP, VP, VP])
     _reg(lib.tg_hip_attention_scratch_bytes, [CI, CI, CI, CI, CI], SZ)

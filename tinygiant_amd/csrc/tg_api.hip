@@ -1383,18 +1383,36 @@ TG_API int64_t tg_hip_upload_file(const char *path, uint64_t file_offset, uint64
 /* ---- router ---- */
 TG_API size_t tg_hip_route_scratch_bytes(int k, int n_experts) { return (size_t)k * n_experts * 4; }
 
-TG_API void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const float *x_dev, int k, int n_experts,
-                             int dim, int top_k, int32_t *idx_dev, float *w_dev, void *scratch_dev, void *stream) {
+static void route_dev(const char *name, const float *router_dev, const float *bias_dev, const float *x_dev, int k,
+                      int n_experts, int dim, int top_k, const uint8_t *resident_dev, int32_t *idx_dev, float *w_dev,
+                      void *scratch_dev, void *stream) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     if (!router_dev || !x_dev || !idx_dev || !w_dev || !scratch_dev || k <= 0 || dim <= 0 || n_experts <= 0 ||
         n_experts > 256 || top_k <= 0 || top_k > 64 || top_k > n_experts) {
-        set_err("tg_hip_route_dev: bad arguments (n_experts <= 256, 1 <= top_k <= 64)");
+        set_err("%s: bad arguments (n_experts <= 256, 1 <= top_k <= 64)", name);
         return;
     }
     ensure_init();
-    launch_route(router_dev, bias_dev, x_dev, k, n_experts, dim, top_k, (float *)scratch_dev, idx_dev, w_dev,
-                 stream ? (hipStream_t)stream : g.st);
+    launch_route(router_dev, bias_dev, x_dev, k, n_experts, dim, top_k, resident_dev, (float *)scratch_dev, idx_dev,
+                 w_dev, stream ? (hipStream_t)stream : g.st);
     HIPCHECK(hipGetLastError());
+}
+
+TG_API void tg_hip_route_dev(const float *router_dev, const float *bias_dev, const float *x_dev, int k, int n_experts,
+                             int dim, int top_k, int32_t *idx_dev, float *w_dev, void *scratch_dev, void *stream) {
+    route_dev("tg_hip_route_dev", router_dev, bias_dev, x_dev, k, n_experts, dim, top_k, nullptr, idx_dev, w_dev,
+              scratch_dev, stream);
+}
+
+TG_API void tg_hip_route_restricted_dev(const float *router_dev, const float *bias_dev, const float *x_dev, int k,
+                                        int n_experts, int dim, int top_k, const uint8_t *resident_dev,
+                                        int32_t *idx_dev, float *w_dev, void *scratch_dev, void *stream) {
+    if (!resident_dev) {
+        set_err("tg_hip_route_restricted_dev: no resident mask");
+        return;
+    }
+    route_dev("tg_hip_route_restricted_dev", router_dev, bias_dev, x_dev, k, n_experts, dim, top_k, resident_dev,
+              idx_dev, w_dev, scratch_dev, stream);
 }
 
 /* ---- output head with fused argmax ----

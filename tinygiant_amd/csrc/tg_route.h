@@ -9,9 +9,10 @@
 namespace tg {
 
 /* logits [k][n_experts] (scratch), idx/w [k][k_top]; k_top <= 64,
- * n_experts <= 256 */
+ * n_experts <= 256; resident (may be NULL): one byte per expert, nonzero
+ * for the experts the selection is restricted to */
 void launch_route(const float *router, const float *bias, const float *x, int k, int n_experts, int dim, int k_top,
-                  float *logits, int32_t *idx, float *w, hipStream_t st);
+                  const uint8_t *resident, float *logits, int32_t *idx, float *w, hipStream_t st);
 
 }  // namespace tg
 #endif

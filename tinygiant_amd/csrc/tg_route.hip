@@ -10,7 +10,12 @@
  *   k_route_topk     one wave per input row: top-k by repeated wave argmax
  *                    (larger logit first, lower expert index on equal
  *                    logits), then exp(l - max) / sum with the sum grouped
- *                    as numpy's float32 pairwise sum groups 8 values
+ *                    as numpy's float32 pairwise sum groups 8 values;
+ *                    optionally restricted to a resident set of experts
+ *                    (Router.select(restrict=True), router.py:46-54: the
+ *                    others take -inf before the top-k, the weights come
+ *                    from the same logits, and with fewer than k resident
+ *                    experts the selection is unrestricted)
  */
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -41,17 +46,30 @@ __global__ __launch_bounds__(256) void k_route_logits(const float *__restrict__ 
 /* top-k + softmax over the selected, one wave per input row (k_top <= 64,
  * n_experts <= 256) */
 __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ logits, int n_experts, int k_top,
-                                                   int32_t *idx_out, float *w_out) {
+                                                   const uint8_t *__restrict__ resident, int32_t *idx_out,
+                                                   float *w_out) {
     const int lane = threadIdx.x;
     const int j = blockIdx.x;
     const float *lg = logits + (size_t)j * n_experts;
-    float v[4];
+    /* the mask applies only when at least k_top experts are resident */
+    bool masked = resident != nullptr;
+    if (masked) {
+        int cnt = 0;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int e = lane + 64 * t;
+            cnt += __popcll(__ballot(e < n_experts && resident[e] != 0));
+        }
+        masked = cnt >= k_top;
+    }
+    float v[4], lv[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int e = lane + 64 * t;
-        v[t] = e < n_experts ? lg[e] : -INFINITY;
+        lv[t] = e < n_experts ? lg[e] : -INFINITY;
+        v[t] = e < n_experts && (!masked || resident[e] != 0) ? lv[t] : -INFINITY;
     }
-    float sel_l = 0.f;   /* lane s keeps the s-th selected logit */
+    float sel_l = 0.f;   /* lane s keeps the s-th selected logit (unmasked) */
     int sel_e = 0;
     for (int s = 0; s < k_top; s++) {
         /* lane-local best: larger logit, then lower index */
@@ -72,8 +90,14 @@ __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ log
                 be = oe;
             }
         }
+        /* the selected expert's own logit (the mask only excludes) */
+        float own = lv[0];
+#pragma unroll
+        for (int t = 1; t < 4; t++)
+            if (t == (be >> 6)) own = lv[t];
+        own = __shfl(own, be & 63, 64);
         if (lane == s) {
-            sel_l = bv;
+            sel_l = own;
             sel_e = be;
         }
         if ((be & 63) == lane) {
@@ -110,10 +134,10 @@ __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ log
 }
 
 void launch_route(const float *router, const float *bias, const float *x, int k, int n_experts, int dim, int k_top,
-                  float *logits, int32_t *idx, float *w, hipStream_t st) {
+                  const uint8_t *resident, float *logits, int32_t *idx, float *w, hipStream_t st) {
     hipLaunchKernelGGL(k_route_logits, dim3((n_experts + 3) / 4), dim3(256), 0, st, router, bias, x, k, n_experts, dim,
                        logits);
-    hipLaunchKernelGGL(k_route_topk, dim3(k), dim3(64), 0, st, logits, n_experts, k_top, idx, w);
+    hipLaunchKernelGGL(k_route_topk, dim3(k), dim3(64), 0, st, logits, n_experts, k_top, resident, idx, w);
 }
 
 }  // namespace tg
