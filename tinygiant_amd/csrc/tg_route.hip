@@ -4,9 +4,9 @@
  * softmax over the selected logits only (Router.logits/_topk/_weights,
  * tinygiant/router.py:29-42; selection without cache bias, router.py:62-63).
  *
- *   k_route_logits   one wave per expert row: f32 router row . x_j (+ bias)
- *                    for every input row j, lanes accumulating in fixed
- *                    order and a fixed DPP tree
+ *   k_route_logits   one wave per (expert, input row): f32 router row . x_j
+ *                    (+ bias), lanes accumulating in fixed order and a
+ *                    fixed DPP tree
  *   k_route_topk     one wave per input row: top-k by repeated wave argmax
  *                    (larger logit first, lower expert index on equal
  *                    logits), then exp(l - max) / sum with the sum grouped
@@ -26,28 +26,48 @@
 
 namespace tg {
 
-/* logits[j][e] = router[e] . x_j (+ bias[e]); one wave per expert row */
+/* logits[j][e] = router[e] . x_j (+ bias[e]); one wave per (expert, input
+ * row) pair, so every row's logits are independent waves (k x n_experts of
+ * them); lanes read 16-byte pieces of the two rows when they are 16-byte
+ * aligned and dim a multiple of 256, and accumulate in a fixed order. */
 __global__ __launch_bounds__(256) void k_route_logits(const float *__restrict__ router, const float *__restrict__ bias,
                                                       const float *__restrict__ x, int k, int n_experts, int dim,
-                                                      float *logits) {
+                                                      int vec, float *logits) {
     const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (e >= n_experts) return;   /* uniform per wave */
+    const int p = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (p >= n_experts * k) return;   /* uniform per wave */
+    const int e = p % n_experts, j = p / n_experts;
     const float *w = router + (size_t)e * dim;
-    for (int j = 0; j < k; j++) {
-        const float *xr = x + (size_t)j * dim;
-        float acc = 0.f;
+    const float *xr = x + (size_t)j * dim;
+    float acc = 0.f;
+    if (vec) {
+#pragma unroll 4
+        for (int i = 4 * lane; i < dim; i += 256) {
+            const float4 a = *reinterpret_cast<const float4 *>(w + i);
+            const float4 b = *reinterpret_cast<const float4 *>(xr + i);
+            acc = fmaf(a.x, b.x, acc);
+            acc = fmaf(a.y, b.y, acc);
+            acc = fmaf(a.z, b.z, acc);
+            acc = fmaf(a.w, b.w, acc);
+        }
+    } else {
         for (int i = lane; i < dim; i += 64) acc = fmaf(w[i], xr[i], acc);
-        acc = wave_sum(acc);
-        if (lane == 0) logits[(size_t)j * n_experts + e] = bias ? acc + bias[e] : acc;
     }
+    acc = wave_sum(acc);
+    if (lane == 0) logits[(size_t)j * n_experts + e] = bias ? acc + bias[e] : acc;
 }
 
 /* top-k + softmax over the selected, one wave per input row (k_top <= 64,
- * n_experts <= 256) */
+ * n_experts <= 256).  Each expert's rank is the number of experts ahead of
+ * it (a larger logit, or an equal one at a lower index), counted against
+ * the row's logits staged in LDS; the experts of rank < k_top are the
+ * selection, in rank order. */
 __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ logits, int n_experts, int k_top,
                                                    const uint8_t *__restrict__ resident, int32_t *idx_out,
                                                    float *w_out) {
+    __shared__ float sv[256];
+    __shared__ float sel_v[64];
+    __shared__ int sel_i[64];
     const int lane = threadIdx.x;
     const int j = blockIdx.x;
     const float *lg = logits + (size_t)j * n_experts;
@@ -68,44 +88,29 @@ __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ log
         const int e = lane + 64 * t;
         lv[t] = e < n_experts ? lg[e] : -INFINITY;
         v[t] = e < n_experts && (!masked || resident[e] != 0) ? lv[t] : -INFINITY;
+        sv[e] = v[t];
     }
-    float sel_l = 0.f;   /* lane s keeps the s-th selected logit (unmasked) */
-    int sel_e = 0;
-    for (int s = 0; s < k_top; s++) {
-        /* lane-local best: larger logit, then lower index */
-        float bv = v[0];
-        int be = lane;
+    __syncthreads();
+    int rank[4] = {0, 0, 0, 0};
+    for (int o = 0; o < n_experts; o++) {
+        const float u = sv[o];   /* one broadcast read for the whole wave */
 #pragma unroll
-        for (int t = 1; t < 4; t++)
-            if (v[t] > bv) {
-                bv = v[t];
-                be = lane + 64 * t;
-            }
-        /* wave best by the same rule */
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oe = __shfl_xor(be, o, 64);
-            if (ov > bv || (ov == bv && oe < be)) {
-                bv = ov;
-                be = oe;
-            }
-        }
-        /* the selected expert's own logit (the mask only excludes) */
-        float own = lv[0];
-#pragma unroll
-        for (int t = 1; t < 4; t++)
-            if (t == (be >> 6)) own = lv[t];
-        own = __shfl(own, be & 63, 64);
-        if (lane == s) {
-            sel_l = own;
-            sel_e = be;
-        }
-        if ((be & 63) == lane) {
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-                if (t == (be >> 6)) v[t] = -INFINITY;
+        for (int t = 0; t < 4; t++) {
+            const int e = lane + 64 * t;
+            rank[t] += (u > v[t]) || (u == v[t] && o < e);
         }
     }
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int e = lane + 64 * t;
+        if (e < n_experts && rank[t] < k_top) {
+            sel_v[rank[t]] = lv[t];   /* the selected expert's own logit (the mask only excludes) */
+            sel_i[rank[t]] = e;
+        }
+    }
+    __syncthreads();
+    const float sel_l = lane < k_top ? sel_v[lane] : 0.f;
+    const int sel_e = lane < k_top ? sel_i[lane] : 0;
     /* softmax over the selected (descending order, so the max is the first) */
     const float mx = __shfl(sel_l, 0, 64);
     const float ex = lane < k_top ? expf(sel_l - mx) : 0.f;
@@ -135,8 +140,9 @@ __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ log
 
 void launch_route(const float *router, const float *bias, const float *x, int k, int n_experts, int dim, int k_top,
                   const uint8_t *resident, float *logits, int32_t *idx, float *w, hipStream_t st) {
-    hipLaunchKernelGGL(k_route_logits, dim3((n_experts + 3) / 4), dim3(256), 0, st, router, bias, x, k, n_experts, dim,
-                       logits);
+    const int vec = dim % 256 == 0 && ((uintptr_t)router & 15) == 0 && ((uintptr_t)x & 15) == 0;
+    hipLaunchKernelGGL(k_route_logits, dim3((n_experts * k + 3) / 4), dim3(256), 0, st, router, bias, x, k, n_experts,
+                       dim, vec, logits);
     hipLaunchKernelGGL(k_route_topk, dim3(k), dim3(64), 0, st, logits, n_experts, k_top, resident, idx, w);
 }
 
