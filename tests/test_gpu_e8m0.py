@@ -14,10 +14,13 @@ build rows by hand:
   * the MoE phases -- per-pair, expert-major and the block-scaled MFMA
     phases: one expert whose gate and up rows are all e in {0, 1}, so its
     hidden rows are of order 1e-34 and the per-row bars pin the branch;
-  * e = 255 on the MFMA phases: the OCP MX format reads that byte as NaN, and
-    the hardware does; the MoE call then returns NaN for the rows that
-    block feeds, where the reference computes with 2^127 (real MXFP4 weights
-    never hold 255).
+  * e = 255 where the block-scaled MFMA phases would run: the OCP MX format
+    reads that byte as NaN, and the hardware does, so a layer whose active
+    MXFP4 matrices hold one runs the v_dot4 phases instead (the library scans
+    the scale bytes: per call for staged weights, once per registered range
+    or plan); the results equal the oracle's 2^127 arithmetic on the host
+    call and on a plan, and the persistent gpt-oss step, which has no v_dot4
+    form, refuses such a layer.
 """
 
 import sys
@@ -139,39 +142,160 @@ def test_moe_e8m0_denormal_expert(tg, orc, path):
     assert ok, (path, "down+combine", rel)
 
 
-def test_moe_mfma_e8m0_255_is_nan(tg, orc):
-    """The MFMA phases read an e8m0 byte of 255 as NaN (OCP MX); the per-pair
-    path follows the reference's 2^127."""
-    rng = np.random.default_rng(2551)
-    n, D, I, k = 2, 1024, 1024, 8
+def _e255_case(rng, n=2, D=1024, I=1024):
     g, u, d = [], [], []
     for e in range(n):
         g.append(_mx_rows(rng, I, D, list(range(118, 131))).reshape(I, D // 32, RB))
         u.append(_mx_rows(rng, I, D, list(range(118, 131))).reshape(-1))
         d.append(_mx_rows(rng, D, I, list(range(118, 131))).reshape(-1))
     g[0][5, 3, 0] = 255          # gate row 5 of expert 0, block 3
-    g = [a.reshape(-1) for a in g]
+    return [a.reshape(-1) for a in g], u, d
+
+
+@pytest.mark.parametrize("registered", [False, True])
+def test_moe_e8m0_255_takes_the_exact_phases(tg, orc, registered):
+    """With the MFMA phases forced on (threshold 1 pair), a layer holding an
+    e = 255 block gives the oracle's 2^127 results, finite where the
+    reference's are, both with staged (host) weights and with weights made
+    resident by tg_mlock (scanned once, then remembered)."""
+    rng = np.random.default_rng(2551)
+    n, D, I, k = 2, 1024, 1024, 8
+    g, u, d = _e255_case(rng, n, D, I)
     rw = np.full((n, k), 0.5, np.float32)
     x = rng.uniform(-1e-3, 1e-3, (k, D)).astype(np.float32)
     fm = [O.FMT_MXFP4] * n
     lib = tg.lib()
-    outs = {}
-    for name, rows in (("mfma", 1), ("per-pair", 0)):
-        prev = lib.tg_hip_set_moe_grouped_min_rows(rows)
-        try:
+    if registered:
+        for m in g + u + d:
+            assert lib.tg_mlock(m.ctypes.data, m.nbytes) == 0
+    h_ref = np.zeros((n * k, I), np.float32)
+    ref = orc.moe_v2(g, u, d, O.FMT_MXFP4, fm, None, None, None, O.ACT_SILU, rw, x, np.zeros((k, D), np.float32), I,
+                     hidden_out=h_ref)
+    assert np.all(np.isfinite(h_ref[:k, 5])) and np.all(np.isfinite(ref))
+    prev = lib.tg_hip_set_moe_grouped_min_rows(1)
+    try:
+        for rep in range(2):   # the second call of a registered layer takes the remembered result
             h = np.zeros((n * k, I), np.float32)
-            tg.moe_forward_rows_v2(g, u, d, O.FMT_MXFP4, fm, None, None, None, O.ACT_SILU, rw, x,
-                                   np.zeros((k, D), np.float32), I, hidden_out=h)
-            outs[name] = h
+            got = tg.moe_forward_rows_v2(g, u, d, O.FMT_MXFP4, fm, None, None, None, O.ACT_SILU, rw, x,
+                                         np.zeros((k, D), np.float32), I, hidden_out=h)
+            assert np.all(np.isfinite(h)) and np.all(np.isfinite(got)), rep
+            for p in range(n * k):
+                ok, rel = close(h[p], h_ref[p], tol=1e-4)
+                assert ok, (rep, p, rel)
+            ref_b = orc.moe_v2(g, u, d, O.FMT_MXFP4, fm, None, None, None, O.ACT_SILU, rw, x,
+                               np.zeros((k, D), np.float32), I, hidden_in=h)
+            ok, rel = close(got, ref_b)
+            assert ok, (rep, rel)
+    finally:
+        lib.tg_hip_set_moe_grouped_min_rows(prev)
+        if registered:
+            for m in g + u + d:
+                lib.tg_hip_unregister(m.ctypes.data)
+
+
+def test_moe_e8m0_255_on_a_plan(tg, orc):
+    """A device-resident plan with an e = 255 block (scanned when the plan is
+    made), run with the MFMA phases forced on, equals the oracle."""
+    import ctypes
+    rng = np.random.default_rng(2552)
+    n, D, I, k = 2, 1024, 1024, 8
+    g, u, d = _e255_case(rng, n, D, I)
+    rw = np.full((n, k), 0.5, np.float32)
+    x = rng.uniform(-1e-3, 1e-3, (k, D)).astype(np.float32)
+    lib = tg.lib()
+    bufs = []
+
+    def put(a):
+        b = tg.DeviceArray(a.nbytes)
+        b.upload(a)
+        bufs.append(b)
+        return b.ptr
+    try:
+        gp = (ctypes.c_void_p * n)(*[put(a) for a in g])
+        up = (ctypes.c_void_p * n)(*[put(a) for a in u])
+        dp = (ctypes.c_void_p * n)(*[put(a) for a in d])
+        fm = np.full(n, O.FMT_MXFP4, np.int32)
+        plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
+                                          O.FMT_MXFP4, fm.ctypes.data, None, None, None, O.ACT_SILU, n,
+                                          rw.ctypes.data, k, D, I)
+        assert plan, tg.last_error()
+        xd = tg.DeviceArray(x.nbytes)
+        xd.upload(x)
+        yd = tg.DeviceArray(x.nbytes)
+        yd.upload(np.zeros_like(x))
+        bufs += [xd, yd]
+        prev = lib.tg_hip_set_moe_grouped_min_rows(1)
+        try:
+            lib.tg_hip_moe_plan_run(plan, xd.ptr, yd.ptr, None)
+            lib.tg_hip_synchronize()
         finally:
             lib.tg_hip_set_moe_grouped_min_rows(prev)
-    h_ref = np.zeros((n * k, I), np.float32)
-    orc.moe_v2(g, u, d, O.FMT_MXFP4, fm, None, None, None, O.ACT_SILU, rw, x, np.zeros((k, D), np.float32), I,
-               hidden_out=h_ref)
-    # pairs 0..k-1 are expert 0's: hidden column 5 of each comes from the e = 255 block
-    assert np.all(np.isnan(outs["mfma"][:k, 5]))
-    assert not np.isnan(outs["mfma"][:k, :5]).any() and not np.isnan(outs["mfma"][k:]).any()
-    assert np.all(np.isfinite(h_ref[:k, 5])) and np.all(np.isfinite(outs["per-pair"][:k, 5]))
-    for p in range(n * k):
-        ok, rel = close(outs["per-pair"][p], h_ref[p], tol=1e-4)
-        assert ok, ("per-pair", p, rel)
+            lib.tg_hip_moe_plan_destroy(plan)
+        got = yd.download(np.float32, k * D).reshape(k, D)
+        ref = orc.moe_v2(g, u, d, O.FMT_MXFP4, list(fm), None, None, None, O.ACT_SILU, rw, x,
+                         np.zeros((k, D), np.float32), I)
+        assert np.all(np.isfinite(got))
+        ok, rel = close(got, ref, tol=1e-4)
+        assert ok, rel
+    finally:
+        for b in bufs:
+            b.free()
+
+
+def test_decode_mx_step_refuses_e8m0_255(tg):
+    """The persistent gpt-oss step (block-scaled MFMA, no v_dot4 form) is not
+    created over a layer holding an e = 255 block: NULL and an error naming
+    the byte, while modes 0 and 1 (per-layer kernels) accept it."""
+    import ctypes
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    D = I = 2880
+    n = 4
+    rb = lib.tg_row_bytes(O.FMT_MXFP4, D)
+    bufs = []
+
+    def mat(seed, nrows, poke=False):
+        b = tg.DeviceArray(nrows * rb)
+        lib.tg_hip_synth_fill(3, seed, b.ptr, nrows * rb, None)
+        if poke:
+            b.upload(np.array([255], np.uint8), offset=7 * rb + 17 * 11)   # row 7, block 11: its scale byte
+        bufs.append(b)
+        return b.ptr
+    try:
+        gp = (ctypes.c_void_p * n)(*[mat(S.tensor_seed(91, 0, e, 0), I, poke=e == 2) for e in range(n)])
+        up = (ctypes.c_void_p * n)(*[mat(S.tensor_seed(91, 0, e, 1), I) for e in range(n)])
+        dp = (ctypes.c_void_p * n)(*[mat(S.tensor_seed(91, 0, e, 2), D) for e in range(n)])
+        biases = []
+        for nrows in (I, I, D):
+            arr = []
+            for e in range(n):
+                b = tg.DeviceArray(nrows * 4)
+                b.upload(np.zeros(nrows, np.float32))
+                bufs.append(b)
+                arr.append(b.ptr)
+            biases.append((ctypes.c_void_p * n)(*arr))
+        fm = np.full(n, O.FMT_MXFP4, np.int32)
+        rw = np.full((n, 1), 0.25, np.float32)
+        plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
+                                          O.FMT_MXFP4, fm.ctypes.data, *[ctypes.addressof(b) for b in biases],
+                                          O.ACT_GPTOSS, n, rw.ctypes.data, 1, D, I)
+        assert plan, tg.last_error()
+        h = tg.DeviceArray(D * 4)
+        h.upload(np.zeros(D, np.float32))
+        bufs.append(h)
+        arr = (ctypes.c_void_p * 1)(plan)
+        try:
+            for mode, ok in ((3, False), (2, False), (0, True), (1, True)):
+                lib.tg_hip_clear_error()
+                st = lib.tg_hip_decode_create(ctypes.addressof(arr), 1, None, ctypes.c_float(1e-5), h.ptr, mode)
+                if ok:
+                    assert st, (mode, tg.last_error())
+                    lib.tg_hip_decode_destroy(st)
+                else:
+                    assert not st, mode
+                    assert "255" in tg.last_error(), tg.last_error()
+        finally:
+            lib.tg_hip_moe_plan_destroy(plan)
+    finally:
+        for b in bufs:
+            b.free()

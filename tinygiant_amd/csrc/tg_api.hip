@@ -178,6 +178,10 @@ struct Bump {
     }
 };
 
+/* MXFP4 matrices of registered ranges already scanned for the scale byte
+ * 255 (mx_any_e255 below): (device address, bytes) -> found */
+static std::map<std::pair<uint64_t, uint64_t>, bool> g_e255_known;
+
 /* ---- HBM residency registry (tg_mlock) ---- */
 struct Region {
     size_t len;
@@ -206,6 +210,7 @@ int do_register(const void *addr, size_t len) {
         HIPCHECK(hipStreamSynchronize(g.st));
         HIPCHECK(hipFree(it->second.dev));
         g_regs.erase(it);
+        g_e255_known.clear();
     }
     uint8_t *dev = nullptr;
     hipError_t e = hipMalloc(&dev, len);
@@ -272,6 +277,71 @@ struct HostPlan {
     bool has_gb = false, has_ub = false, has_db = false;
     std::vector<int> fmts_present;
 };
+
+/* ---- MXFP4 scale byte 255 ----
+ * The reference reads the e8m0 byte 255 as 2^127; the block-scaled MFMA
+ * phases cannot (k_mx_scan_e255), so a layer whose active MXFP4 matrices hold
+ * such a block runs the v_dot4 phases.  Registered ranges are immutable
+ * device copies: their result is kept (until the range is unregistered). */
+static unsigned *g_e255_flags = nullptr;
+static size_t g_e255_cap = 0;
+
+/* the active experts' MXFP4 matrices of a host plan (device addresses) */
+static std::vector<std::pair<uint64_t, uint64_t>> mx_matrices(const HostPlan &h, std::vector<int> *which = nullptr) {
+    std::vector<std::pair<uint64_t, uint64_t>> m;
+    const uint64_t gb = (uint64_t)h.I * row_bytes(TG_FMT_MXFP4, h.D), db = (uint64_t)h.D * row_bytes(TG_FMT_MXFP4, h.I);
+    for (int e = 0; e < h.n; e++) {
+        if (h.p_off[e + 1] == h.p_off[e]) continue;
+        if (h.gate_fmt == TG_FMT_MXFP4) {
+            m.push_back({h.gate[e], gb});
+            m.push_back({h.up[e], gb});
+            if (which) which->insert(which->end(), {3 * e, 3 * e + 1});
+        }
+        if (h.down_fmt[e] == TG_FMT_MXFP4) {
+            m.push_back({h.down[e], db});
+            if (which) which->push_back(3 * e + 2);
+        }
+    }
+    return m;
+}
+
+static bool mx_any_e255(const std::vector<std::pair<uint64_t, uint64_t>> &mats, const std::vector<char> &keep) {
+    std::vector<size_t> todo;
+    for (size_t i = 0; i < mats.size(); i++) {
+        if (keep[i]) {
+            auto it = g_e255_known.find(mats[i]);
+            if (it != g_e255_known.end()) {
+                if (it->second) return true;
+                continue;
+            }
+        }
+        todo.push_back(i);
+    }
+    if (todo.empty()) return false;
+    if (todo.size() > g_e255_cap) {
+        if (g_e255_flags) {
+            HIPCHECK(hipStreamSynchronize(g.st));
+            HIPCHECK(hipFree(g_e255_flags));
+        }
+        g_e255_cap = std::max<size_t>(todo.size(), 64);
+        HIPCHECK(hipMalloc(&g_e255_flags, g_e255_cap * 4));
+    }
+    HIPCHECK(hipMemsetAsync(g_e255_flags, 0, todo.size() * 4, g.st));
+    for (size_t j = 0; j < todo.size(); j++)
+        launch_mx_scan_e255((const uint8_t *)(uintptr_t)mats[todo[j]].first, mats[todo[j]].second, g_e255_flags + j,
+                            g.st);
+    HIPCHECK(hipGetLastError());
+    std::vector<unsigned> f(todo.size());
+    HIPCHECK(hipMemcpyAsync(f.data(), g_e255_flags, f.size() * 4, hipMemcpyDeviceToHost, g.st));
+    HIPCHECK(hipStreamSynchronize(g.st));
+    bool any = false;
+    for (size_t j = 0; j < todo.size(); j++) {
+        if (keep[todo[j]]) g_e255_known[mats[todo[j]]] = f[j] != 0;
+        any = any || f[j] != 0;
+    }
+    return any;
+}
+
 
 bool validate_moe(int gate_fmt, const int *down_fmts, int n, int k, int D, int I, int act) {
     if (n < 0 || k < 0 || D <= 0 || I <= 0) {
@@ -581,6 +651,19 @@ void moe_host(const uint8_t *const *gate_ptrs, const uint8_t *const *up_ptrs, co
     a.ctr_n = a.ctr ? moe_ctr_words(D) : 0;
     HIPCHECK(hipMemcpyAsync(dev + L.tables, img, L.tables_len, hipMemcpyHostToDevice, g.st));
     for (auto &it : sg.items) HIPCHECK(hipMemcpyAsync(dev + it.off, it.host, it.n, hipMemcpyHostToDevice, g.st));
+    if (grouped_min_rows() > 0 && a.max_rows >= grouped_min_rows()) {
+        /* the MFMA phases are a candidate: no e8m0 byte of 255 may reach
+         * them (registered matrices are scanned once, staged ones per call) */
+        std::vector<int> which;
+        const auto mats = mx_matrices(h, &which);
+        std::vector<char> keep(mats.size(), 1);
+        for (auto &f : fixes) {
+            const int part = f.vec == &h.gate ? 0 : f.vec == &h.up ? 1 : f.vec == &h.down ? 2 : -1;
+            for (size_t i = 0; i < which.size(); i++)
+                if (part >= 0 && which[i] == 3 * f.idx + part) keep[i] = 0;
+        }
+        a.mx_e255 = mx_any_e255(mats, keep) ? 1 : 0;
+    }
     launch_moe(a, h.fmts_present.data(), (int)h.fmts_present.size(), g.st);
     HIPCHECK(hipGetLastError());
     HIPCHECK(hipStreamSynchronize(g.st));
@@ -780,6 +863,7 @@ TG_API int tg_hip_unregister(const void *addr) {
     HIPCHECK(hipStreamSynchronize(g.st));
     HIPCHECK(hipFree(it->second.dev));
     g_regs.erase(it);
+    g_e255_known.clear();
     return 0;
 }
 
@@ -965,6 +1049,10 @@ TG_API tg_hip_moe_plan *tg_hip_moe_plan_create(const void *const *gate_dev, cons
     HIPCHECK(hipMalloc(&p->dev, p->L.total));
     std::vector<uint8_t> img(p->L.tables_len);
     p->a = plan_args(h, p->L, p->dev, img.data());
+    /* the caller's device matrices, scanned once (the MFMA threshold may
+     * change after the plan is made) */
+    const auto mats = mx_matrices(h);
+    p->a.mx_e255 = mx_any_e255(mats, std::vector<char>(mats.size(), 0)) ? 1 : 0;
     HIPCHECK(hipMemcpy(p->dev + p->L.tables, img.data(), img.size(), hipMemcpyHostToDevice));
     HIPCHECK(hipMemset(p->dev + p->L.ctr, 0, (size_t)moe_ctr_words(h.D) * 4));
     return p;
@@ -1524,6 +1612,11 @@ struct tg_hip_decode {
 static bool persistent_mx_ok(tg_hip_decode *d, std::vector<DecodeLayerMx> &out) {
     for (int l = 0; l < d->L; l++) {
         const HostPlan &h = d->plans[l]->h;
+        if (d->plans[l]->a.mx_e255) {
+            set_err("persistent decode: layer %d has an MXFP4 scale byte of 255, which the step's block-scaled MFMA "
+                    "cannot apply as 2^127; use mode 0 or 1 (per-layer kernels)", l);
+            return false;
+        }
         if (h.k != 1 || h.D != DECODE_MX_D || h.I != DECODE_MX_D || h.gate_fmt != TG_FMT_MXFP4 ||
             h.act != TG_ACT_GPTOSS) {
             set_err("persistent decode: layer %d is not a 1-row gpt-oss MXFP4 step of %dx%d", l, DECODE_MX_D,

@@ -116,6 +116,24 @@ __global__ __launch_bounds__(256) void k_mx_split(Q8Rows q, int nrows, int nblk,
     *(uint32_t *)(dst + (size_t)r * nblk * 64 + (size_t)b * 64 + part * 32 + p0) = w;
 }
 
+/* The e8m0 scale byte 255 means 2^127 to the reference (e8m0_to_fp32_half,
+ * csrc/libtinygiant.c:516-519) and NaN to the block-scaled MFMA (OCP MX), and
+ * 2^127 times the products overflows the MFMA's f32 sums where the
+ * reference's integer block sum times its scales may stay finite: a layer
+ * with such a block takes the v_dot4 phases.  One thread per block. */
+__global__ __launch_bounds__(256) void k_mx_scan_e255(const uint8_t *__restrict__ p, uint64_t nblocks,
+                                                      unsigned *flag) {
+    const uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x;
+    const bool hit = i < nblocks && p[i * MXB] == 255;
+    if (__ballot(hit) && (threadIdx.x & 63) == __builtin_ctzll(__ballot(hit))) atomicOr(flag, 1u);
+}
+
+void launch_mx_scan_e255(const uint8_t *p, uint64_t nbytes, unsigned *flag_dev, hipStream_t st) {
+    const uint64_t nb = nbytes / MXB;
+    if (nb == 0) return;
+    hipLaunchKernelGGL(k_mx_scan_e255, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, st, p, nb, flag_dev);
+}
+
 void launch_mx_split(const Q8Rows &q, int nrows, int ncols, uint8_t *dst, hipStream_t st) {
     const size_t n = (size_t)nrows * (ncols / 32) * 16;
     if (n == 0) return;

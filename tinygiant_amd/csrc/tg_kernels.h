@@ -47,6 +47,7 @@ struct MoeArgs {
     uint32_t gate_rb;
     int max_rows;                           /* most pairs of any one expert */
     int mx_aligned;                         /* every MXFP4 matrix of an active expert starts 16-byte aligned */
+    int mx_e255;                            /* an active MXFP4 matrix holds an e8m0 scale byte of 255 */
     const int *mx_act;                      /* active experts, then active experts with an MXFP4 down matrix */
     const int *mx_cum;                      /* cost prefix of each list (n_act + 1 entries each) */
     uint8_t *xp, *hp;                       /* fp8 halves of xq / hq rows in MFMA order, or null */
@@ -104,6 +105,9 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
  * expert.  launch_mx_split prepares the fp8 halves of q8 rows. */
 bool grouped_lds_ok(int D, int I);
 void launch_mx_split(const Q8Rows &q, int nrows, int ncols, uint8_t *dst, hipStream_t st);
+/* sets *flag_dev (not cleared here) when a block of the MXFP4 bytes at p
+ * (nbytes, whole 17-byte blocks) has the scale byte 255 */
+void launch_mx_scan_e255(const uint8_t *p, uint64_t nbytes, unsigned *flag_dev, hipStream_t st);
 void launch_moe_a_mx(const MoeArgs &a, hipStream_t st);
 void launch_moe_b_mx(const MoeArgs &a, hipStream_t st);
 /* pairs per expert from which launch_moe takes the MFMA phases for MXFP4

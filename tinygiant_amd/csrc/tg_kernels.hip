@@ -948,7 +948,9 @@ void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts,
         if (mark) (*mark)(5);
         return;
     }
-    const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a);
+    /* (an e8m0 scale of 255 keeps the layer on the v_dot4 phases, which
+     * apply the reference's 2^127 exactly) */
+    const bool mx_grouped = g_grouped_min_rows > 0 && a.max_rows >= g_grouped_min_rows && grouped_fits(a) && !a.mx_e255;
     const bool mx_a = mx_grouped && a.gate_fmt == TG_FMT_MXFP4 && a.xp;
     int Ta;
     pick_S(items_per_row(a.gate_fmt, a.D), &Ta);
