@@ -953,6 +953,8 @@ def main():
     ap.add_argument("--spec-probe", action="store_true",
                     help="only the verify-batch probes: the q6_K head, the k-row verify layer and the speculative "
                          "round (kernel traces and counter passes)")
+    ap.add_argument("--attn-probe", action="store_true",
+                    help="only the decode-attention probe (kernel traces and counter passes)")
     ap.add_argument("--qk-prefill-probe", action="store_true",
                     help="only the Qwen3 128-token prefill layer (int8 MFMA and v_dot4 expert phases; counter passes)")
     args = ap.parse_args()
@@ -965,6 +967,11 @@ def main():
     lib = tg.lib()
     if args.copy_probe or args.prefill_probe:
         out = copy_probe(tg) if args.copy_probe else prefill_probe(tg)
+        lib.tg_hip_shutdown()
+        print(json.dumps(out), flush=True)
+        return 0
+    if args.attn_probe:
+        out = {"attention_layer": attention_probe(tg)}
         lib.tg_hip_shutdown()
         print(json.dumps(out), flush=True)
         return 0

@@ -58,59 +58,72 @@ __global__ __launch_bounds__(256) void k_route_logits(const float *__restrict__ 
 }
 
 /* top-k + softmax over the selected, one wave per input row (k_top <= 64,
- * n_experts <= 256).  Each expert's rank is the number of experts ahead of
- * it (a larger logit, or an equal one at a lower index), counted against
- * the row's logits staged in LDS; the experts of rank < k_top are the
- * selection, in rank order. */
+ * n_experts <= 256) */
 __global__ __launch_bounds__(64) void k_route_topk(const float *__restrict__ logits, int n_experts, int k_top,
                                                    const uint8_t *__restrict__ resident, int32_t *idx_out,
                                                    float *w_out) {
-    __shared__ float sv[256];
-    __shared__ float sel_v[64];
-    __shared__ int sel_i[64];
     const int lane = threadIdx.x;
     const int j = blockIdx.x;
     const float *lg = logits + (size_t)j * n_experts;
+    /* every load first (clamped indices, no branches), so the row costs one
+     * memory latency */
+    float lv[4];
+    uint32_t rv[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int ec = min(lane + 64 * t, n_experts - 1);
+        lv[t] = lg[ec];
+        rv[t] = resident ? resident[ec] : 1u;
+    }
     /* the mask applies only when at least k_top experts are resident */
-    bool masked = resident != nullptr;
-    if (masked) {
-        int cnt = 0;
+    int cnt = 0;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int e = lane + 64 * t;
-            cnt += __popcll(__ballot(e < n_experts && resident[e] != 0));
-        }
-        masked = cnt >= k_top;
-    }
-    float v[4], lv[4];
+    for (int t = 0; t < 4; t++) cnt += __popcll(__ballot(lane + 64 * t < n_experts && rv[t] != 0));
+    const bool masked = resident != nullptr && cnt >= k_top;
+    float v[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) {
         const int e = lane + 64 * t;
-        lv[t] = e < n_experts ? lg[e] : -INFINITY;
-        v[t] = e < n_experts && (!masked || resident[e] != 0) ? lv[t] : -INFINITY;
-        sv[e] = v[t];
+        if (e >= n_experts) lv[t] = -INFINITY;
+        v[t] = e < n_experts && (!masked || rv[t] != 0) ? lv[t] : -INFINITY;
     }
-    __syncthreads();
-    int rank[4] = {0, 0, 0, 0};
-    for (int o = 0; o < n_experts; o++) {
-        const float u = sv[o];   /* one broadcast read for the whole wave */
+    /* top-k by repeated wave argmax: larger logit first, lower expert index
+     * on equal logits; lane s keeps the s-th selected (its own, unmasked,
+     * logit) */
+    float sel_l = 0.f;
+    int sel_e = 0;
+    for (int s = 0; s < k_top; s++) {
+        float bv = v[0];
+        int be = lane;
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int e = lane + 64 * t;
-            rank[t] += (u > v[t]) || (u == v[t] && o < e);
+        for (int t = 1; t < 4; t++)
+            if (v[t] > bv) {
+                bv = v[t];
+                be = lane + 64 * t;
+            }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oe = __shfl_xor(be, o, 64);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+            }
+        }
+        float own = lv[0];
+#pragma unroll
+        for (int t = 1; t < 4; t++)
+            if (t == (be >> 6)) own = lv[t];
+        own = __shfl(own, be & 63, 64);
+        if (lane == s) {
+            sel_l = own;
+            sel_e = be;
+        }
+        if ((be & 63) == lane) {
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+                if (t == (be >> 6)) v[t] = -INFINITY;
         }
     }
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        const int e = lane + 64 * t;
-        if (e < n_experts && rank[t] < k_top) {
-            sel_v[rank[t]] = lv[t];   /* the selected expert's own logit (the mask only excludes) */
-            sel_i[rank[t]] = e;
-        }
-    }
-    __syncthreads();
-    const float sel_l = lane < k_top ? sel_v[lane] : 0.f;
-    const int sel_e = lane < k_top ? sel_i[lane] : 0;
     /* softmax over the selected (descending order, so the max is the first) */
     const float mx = __shfl(sel_l, 0, 64);
     const float ex = lane < k_top ? expf(sel_l - mx) : 0.f;
