@@ -441,6 +441,81 @@ def verify_probe(tg, bases, ks=(5, 9, 1), iters=20):
     return out
 
 
+def rows_pass_probe(tg, bases, ks=(5, 9, 8), iters=10):
+    """A k-row pass over all 48 layers: per layer every row picks its own
+    top-8 of that layer's 128 resident experts (Zipf), and the layers chain
+    as h <- h + MoE_l(RMSNorm_l(h)) on the k rows -- the verify pass of a
+    self-speculative round at K + 1 = 5 and 9 rows (tinygiant/specdec.py:66)
+    and an 8-row prefill chunk (engine.py:213-217), without attention.  The
+    pass runs as the persistent multi-row kernel (one cooperative launch) and,
+    for comparison, as the HIP graph of per-layer kernels; both read the
+    union's weights of every layer (~4.5-6 GB, far over the Infinity Cache).
+    Weight bytes = every expert of every layer's union, read once."""
+    import tinygiant_amd.synth as S
+    lib = tg.lib()
+    rng = np.random.default_rng(SEED + 31)
+    perms = [rng.permutation(E) for _ in bases]
+    nws = norm_weights(len(bases))
+    nbufs = []
+    for w in nws:
+        a = tg.DeviceArray(D * 4)
+        a.upload(w)
+        nbufs.append(a)
+    narr = (ctypes.c_void_p * len(bases))(*[a.ptr for a in nbufs])
+    out = {}
+    try:
+        for k in ks:
+            plans, nexp, pairs = [], 0, 0
+            for l, base in enumerate(bases):
+                experts, rw = S.routing_rows(rng, k, E, TOPK, 1.1, perms[l])
+                n = len(experts)
+                nexp += n
+                pairs += int((rw != 0).sum())
+                gp = (ctypes.c_void_p * n)(*[base + int(e) * GATE_B for e in experts])
+                up = (ctypes.c_void_p * n)(*[base + E * GATE_B + int(e) * GATE_B for e in experts])
+                dp = (ctypes.c_void_p * n)(*[base + 2 * E * GATE_B + int(e) * DOWN_B for e in experts])
+                fm = np.full(n, tg.FMT_Q6K, np.int32)
+                rwc = np.ascontiguousarray(rw, np.float32)
+                plan = lib.tg_hip_moe_plan_create(ctypes.addressof(gp), ctypes.addressof(up), ctypes.addressof(dp),
+                                                  tg.FMT_Q4K, fm.ctypes.data, None, None, None, tg.ACT_SILU, n,
+                                                  rwc.ctypes.data, k, D, I)
+                if not plan:
+                    raise RuntimeError(tg.last_error())
+                plans.append(plan)
+            h = tg.DeviceArray(k * D * 4)
+            h.upload(rng.standard_normal((k, D)).astype(np.float32))
+            parr = (ctypes.c_void_p * len(plans))(*plans)
+            res = {"rows": k, "layers": len(plans), "experts": nexp, "pairs": pairs,
+                   "weight_bytes": nexp * EXPERT_B}
+            for mode, key in ((2, "persistent"), (3, "persistent_plain"), (1, "graph")):
+                step = lib.tg_hip_decode_create(ctypes.addressof(parr), len(plans), ctypes.addressof(narr),
+                                                ctypes.c_float(1e-6), h.ptr, mode)
+                if not step:
+                    raise RuntimeError(tg.last_error())
+                for _ in range(2):
+                    lib.tg_hip_decode_run(step, None)
+                us = lib.tg_hip_decode_time(step, iters) * 1e3 / iters
+                if lib.tg_hip_decode_status(step) not in (0,):
+                    raise RuntimeError("multi-row step: a barrier wait timed out")
+                lib.tg_hip_decode_destroy(step)
+                res[key + "_us"] = round(us, 2)
+            us = res["persistent_us"]
+            res["weight_gbps"] = round(res["weight_bytes"] / (us * 1e-6) / 1e9, 1)
+            res["hbm_frac"] = round(res["weight_bytes"] / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+            res["per_layer_us"] = round(us / len(plans), 2)
+            res["graph_per_layer_us"] = round(res["graph_us"] / len(plans), 2)
+            out[k] = res
+            log(f"  {k}-row pass over {len(plans)} layers: persistent {us:.1f} us "
+                f"({res['hbm_frac'] * 100:.1f}% of HBM), graph {res['graph_us']:.1f} us")
+            for p_ in plans:
+                lib.tg_hip_moe_plan_destroy(p_)
+            h.free()
+    finally:
+        for a in nbufs:
+            a.free()
+    return out
+
+
 def spec_probe(tg, ks=(4, 8), rounds=6, iters=20):
     """The self-speculative verify workload end to end (tinygiant_amd.specdec):
     greedy rounds of K draft passes (routing restricted to the 64 most
@@ -955,6 +1030,8 @@ def main():
                          "round (kernel traces and counter passes)")
     ap.add_argument("--attn-probe", action="store_true",
                     help="only the decode-attention probe (kernel traces and counter passes)")
+    ap.add_argument("--rows-probe", action="store_true",
+                    help="only the 48-layer k-row passes on the persistent multi-row kernel (kernel traces)")
     ap.add_argument("--qk-prefill-probe", action="store_true",
                     help="only the Qwen3 128-token prefill layer (int8 MFMA and v_dot4 expert phases; counter passes)")
     args = ap.parse_args()
@@ -985,6 +1062,16 @@ def main():
             b.free()
         out["head_argmax"] = head_probe(tg)
         out["spec_round"] = spec_probe(tg)
+        lib.tg_hip_shutdown()
+        print(json.dumps(out), flush=True)
+        return 0
+    if args.rows_probe:
+        rbufs, rplans = setup_gpu(tg, L, routing(L))
+        for p in rplans:
+            lib.tg_hip_moe_plan_destroy(p)
+        out = {"rows_pass": rows_pass_probe(tg, [b.ptr for b in rbufs])}
+        for b in rbufs:
+            b.free()
         lib.tg_hip_shutdown()
         print(json.dumps(out), flush=True)
         return 0
@@ -1126,6 +1213,8 @@ def main():
     if not args.no_verify:
         log("verify batch probe ...")
         result["verify_layer"] = verify_probe(tg, [b.ptr for b in bufs[:6]])
+        log("multi-row pass probe ...")
+        result["rows_pass"] = rows_pass_probe(tg, [b.ptr for b in bufs])
         log("qwen3 prefill probe ...")
         result["qwen_prefill"] = qwen_prefill_probe(tg, bufs[0].ptr)
         log("speculative round probe ...")

@@ -267,7 +267,12 @@ size_t tg_hip_head_scratch_bytes(int k, int nrows, int ncols);
  * (tinygiant/engine.py:281-282,335-341).  norm_w_dev may be NULL (weight 1).
  * mode 0 queues the per-layer kernels, 1 replays them as one HIP graph,
  * 2 runs the whole step as one persistent cooperative kernel on 256
- * co-resident workgroups, <= 64 layers of k = 1, for two expert shapes:
+ * co-resident workgroups.  For k = 2..16 rows (a verify pass of K + 1 rows,
+ * tinygiant/specdec.py:66, or a prefill chunk, engine.py:213-217) that is
+ * the multi-row kernel: any number of layers of the Qwen3-30B-A3B expert
+ * shape (D = 2048, I = 768, Q4_K gate/up, Q6_K down, SiLU, no biases), up to
+ * 128 active experts and 256 pairs per layer, the bits of mode 0.  For
+ * k = 1, <= 64 layers of one of two expert shapes:
  *   Qwen3-30B-A3B: D = 2048, I = 768, Q4_K gate/up, Q6_K down, SiLU, no
  *     biases, exactly 8 active experts per layer;
  *   gpt-oss-120b: D = I = 2880, MXFP4 gate/up/down, the clamped SwiGLU,

@@ -24,7 +24,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
 ]
-HIP_SOURCES = ["tg_kernels.hip", "tg_grouped.hip", "tg_grouped_k.hip", "tg_decode.hip", "tg_decode_mx.hip", "tg_head.hip", "tg_route.hip", "tg_attn.hip", "tg_api.hip"]
+HIP_SOURCES = ["tg_kernels.hip", "tg_grouped.hip", "tg_grouped_k.hip", "tg_decode.hip", "tg_decode_mx.hip", "tg_decode_rows.hip", "tg_head.hip", "tg_route.hip", "tg_attn.hip", "tg_api.hip"]
 CXX_SOURCES = ["tg_host_ops.cpp"]
 
 

@@ -1605,6 +1605,8 @@ struct tg_hip_decode {
     unsigned *place = nullptr;   /* Qwen3 kernel: HW_REG_XCC_ID of each workgroup, last launch */
     int pol = 0;                 /* persistent kernels: 1 = every exchange slot stored device-coherently */
     int placement_bad = 0;       /* a launch ran with workgroup g off XCD g % 8 */
+    RowsLayer *layers_rows = nullptr;   /* kind 2, the multi-row kernel: its layers */
+    size_t rows_rec = 0;                /* ... and the bytes of its per-layer debug record */
 };
 
 /* the gpt-oss kernel covers k = 1 steps of 4 MXFP4 experts of 2880 x 2880
@@ -1687,6 +1689,104 @@ static bool persistent_ok(tg_hip_decode *d, std::vector<DecodeLayer> &out) {
     return true;
 }
 
+/* The multi-row kernel covers steps of k = 2..ROWS_MAXK rows of the Qwen
+ * expert shape (up to ROWS_MAXE active experts and ROWS_MAXP pairs per
+ * layer).  It builds the kernel's layer table and its buffers: barrier flags
+ * | q8 rows of x | hidden [Pmax][I] | partials [Pmax][D] | item ranges
+ * [L][2][ROWS_GRID + 1] | the layers' expert and pair tables. */
+static bool persistent_rows_create(tg_hip_decode *d) {
+    const DecodeShape sh = decode_qwen_shape();
+    if (d->k < 2 || d->k > ROWS_MAXK) {
+        set_err("persistent decode: the multi-row kernel runs 2 to %d rows, the plans hold %d", ROWS_MAXK, d->k);
+        return false;
+    }
+    int pmax = 1;
+    for (int l = 0; l < d->L; l++) {
+        const HostPlan &h = d->plans[l]->h;
+        if (h.D != sh.D || h.I != sh.I || h.gate_fmt != sh.gate_fmt || h.act != TG_ACT_SILU || h.has_gb || h.has_ub ||
+            h.has_db) {
+            set_err("persistent decode: layer %d is not a SiLU Q4_K gate/up step of %dx%d without biases", l, sh.D,
+                    sh.I);
+            return false;
+        }
+        int n_act = 0;
+        for (int e = 0; e < h.n; e++)
+            if (h.p_off[e + 1] > h.p_off[e]) {
+                n_act++;
+                if (h.down_fmt[e] != sh.down_fmt) {
+                    set_err("persistent decode: layer %d has an active expert whose down matrix is not Q6_K", l);
+                    return false;
+                }
+            }
+        if (n_act > ROWS_MAXE || h.P > ROWS_MAXP) {
+            set_err("persistent decode: layer %d has %d active experts and %d pairs; the multi-row kernel takes at "
+                    "most %d and %d", l, n_act, h.P, ROWS_MAXE, ROWS_MAXP);
+            return false;
+        }
+        pmax = std::max(pmax, h.P);
+    }
+    if (decode_rows_max_grid() < ROWS_GRID) {
+        set_err("persistent decode: the multi-row kernel needs %d co-resident workgroups (co-resident %d)", ROWS_GRID,
+                decode_rows_max_grid());
+        return false;
+    }
+    const size_t XS = q8_lds_stride(sh.D / 256), NS = 2 * (ROWS_GRID + 1);
+    const size_t o_xq = ROWS_GRID * 4, o_hid = o_xq + (size_t)ROWS_MAXK * XS,
+                 o_part = o_hid + (size_t)pmax * sh.I * 4, o_split = o_part + (size_t)pmax * sh.D * 4,
+                 o_tab = (o_split + (size_t)d->L * NS * 4 + 255) & ~(size_t)255,
+                 total = o_tab + (size_t)d->L * ROWS_TAB_BYTES;
+    HIPCHECK(hipMalloc(&d->hidden, total));
+    HIPCHECK(hipMemset(d->hidden, 0, total));
+    uint8_t *base = (uint8_t *)d->hidden;
+    std::vector<int> splits((size_t)d->L * NS);
+    std::vector<RowsLayer> ls(d->L);
+    for (int l = 0; l < d->L; l++) {
+        const tg_hip_moe_plan *p = d->plans[l];
+        const HostPlan &h = p->h;
+        std::vector<int> np;
+        std::vector<uint8_t> tab(ROWS_TAB_BYTES, 0);
+        for (int e = 0; e < h.n; e++) {
+            if (h.p_off[e + 1] == h.p_off[e]) continue;
+            RowsExp x = {h.gate[e], h.up[e], h.down[e], h.p_off[e], h.p_off[e + 1] - h.p_off[e]};
+            memcpy(tab.data() + np.size() * sizeof x, &x, sizeof x);
+            np.push_back(x.np);
+        }
+        const size_t n_act = np.size();
+        memcpy(tab.data() + n_act * 32, h.p_row.data(), (size_t)h.P * 4);
+        memcpy(tab.data() + n_act * 32 + (size_t)h.P * 4, h.p_w.data(), (size_t)h.P * 4);
+        memcpy(tab.data() + n_act * 32 + (size_t)h.P * 8, h.r_off.data(), (size_t)(h.k + 1) * 4);
+        memcpy(tab.data() + n_act * 32 + (size_t)h.P * 8 + (size_t)(h.k + 1) * 4, h.r_pair.data(), (size_t)h.P * 4);
+        const size_t tb = (n_act * 32 + (size_t)h.P * 12 + (size_t)(h.k + 1) * 4 + 15) & ~(size_t)15;
+        HIPCHECK(hipMemcpy(base + o_tab + (size_t)l * ROWS_TAB_BYTES, tab.data(), tb, hipMemcpyHostToDevice));
+        decode_rows_split(np.data(), (int)n_act, splits.data() + (size_t)l * NS);
+        RowsLayer &r = ls[l];
+        memset(&r, 0, sizeof r);
+        r.tab = base + o_tab + (size_t)l * ROWS_TAB_BYTES;
+        r.tab_bytes = (int)tb;
+        r.split = (const int *)(base + o_split) + (size_t)l * NS;
+        r.norm_w = d->norm_w.empty() ? nullptr : d->norm_w[l];
+        r.hidden = (float *)(base + o_hid);
+        r.part = (float *)(base + o_part);
+        r.xq = base + o_xq;
+        r.flags = (unsigned *)base;
+        r.n_act = (int)np.size();
+        r.P = h.P;
+        r.k = d->k;
+        r.rec_bytes = (int)(((size_t)2 * d->k * sh.D + (size_t)pmax * sh.I) * 4);
+    }
+    d->rows_rec = (size_t)ls[0].rec_bytes;
+    HIPCHECK(hipMemcpy(base + o_split, splits.data(), splits.size() * 4, hipMemcpyHostToDevice));
+    HIPCHECK(hipMalloc(&d->layers_rows, ls.size() * sizeof(RowsLayer)));
+    HIPCHECK(hipMemcpy(d->layers_rows, ls.data(), ls.size() * sizeof(RowsLayer), hipMemcpyHostToDevice));
+    HIPCHECK(hipMalloc(&d->sync, 256));
+    HIPCHECK(hipMemset(d->sync, 0, 256));
+    HIPCHECK(hipMalloc(&d->place, DECODE_GRID * sizeof(unsigned)));
+    HIPCHECK(hipMemset(d->place, 0xFF, DECODE_GRID * sizeof(unsigned)));
+    d->grid = ROWS_GRID;
+    d->pol = 1;   /* no intra-XCD exchange: nothing to check about placement */
+    return true;
+}
+
 /* Per layer: RMSNorm of h fused with q8 of the result (into the plan's q8
  * rows), then the MoE kernels, which add into h.  A layer without pairs
  * leaves h as it is. */
@@ -1719,7 +1819,9 @@ static void coop_graph_drop(tg_hip_decode *d) {
 static void coop_graph_build(tg_hip_decode *d) {
     coop_graph_drop(d);
     d->cstale = false;
-    const void *layers = d->kind == 1 ? (const void *)d->layers_mx : (const void *)d->layers;
+    const void *layers = d->kind == 2   ? (const void *)d->layers_rows
+                         : d->kind == 1 ? (const void *)d->layers_mx
+                                        : (const void *)d->layers;
     int L = d->L, pol = d->pol;
     float *h = d->h;
     void *slots = d->hidden;
@@ -1733,9 +1835,9 @@ static void coop_graph_build(tg_hip_decode *d) {
                     (void *)&eps,    (void *)&debug, (void *)&times, (void *)&place, (void *)&pol};
     hipKernelNodeParams kp;
     memset(&kp, 0, sizeof kp);
-    kp.func = (void *)(d->kind == 1 ? decode_mx_fn() : decode_qwen_fn());
+    kp.func = (void *)(d->kind == 2 ? decode_rows_fn() : d->kind == 1 ? decode_mx_fn() : decode_qwen_fn());
     kp.gridDim = dim3(d->grid);
-    kp.blockDim = dim3(d->kind == 1 ? decode_mx_threads() : decode_threads());
+    kp.blockDim = dim3(d->kind == 2 ? decode_rows_threads() : d->kind == 1 ? decode_mx_threads() : decode_threads());
     kp.sharedMemBytes = 0;
     kp.kernelParams = args;
     kp.extra = nullptr;
@@ -1753,6 +1855,8 @@ static void coop_graph_build(tg_hip_decode *d) {
         d->cgraph = nullptr;
     }
 }
+
+TG_API void tg_hip_decode_destroy(tg_hip_decode *d);
 
 TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_layers, const float *const *norm_w_dev,
                                            float eps, float *h_dev, int use_graph) {
@@ -1794,6 +1898,15 @@ TG_API tg_hip_decode *tg_hip_decode_create(tg_hip_moe_plan *const *plans, int n_
         std::vector<DecodeLayer> ls;
         std::vector<DecodeLayerMx> lm;
         const HostPlan &h0 = d->plans[0]->h;
+        if (d->k > 1) {   /* the multi-row kernel */
+            d->kind = 2;
+            if (!persistent_rows_create(d)) {
+                tg_hip_decode_destroy(d);
+                return nullptr;
+            }
+            if (d->mode == 2) coop_graph_build(d);
+            return d;
+        }
         d->kind = h0.gate_fmt == TG_FMT_MXFP4 && h0.D == DECODE_MX_D ? 1 : 0;
         if (d->kind == 1 ? !persistent_mx_ok(d, lm) : !persistent_ok(d, ls)) {
             HIPCHECK(hipFree(d->x));
@@ -1878,6 +1991,9 @@ TG_API void tg_hip_decode_run(tg_hip_decode *d, void *stream) {
     if (d->mode == 2 && d->cstale) coop_graph_build(d);
     if (d->mode == 2 && d->cexec) {
         HIPCHECK(hipGraphLaunch(d->cexec, st));
+    } else if (d->mode >= 2 && d->kind == 2) {
+        HIPCHECK(launch_decode_rows(d->layers_rows, d->L, d->h, d->sync, d->eps, d->debug, d->times, d->place,
+                                    d->mode == 2, st));
     } else if (d->mode >= 2 && d->kind == 1) {
         HIPCHECK(launch_decode_mx(d->layers_mx, d->L, d->h, d->hidden, d->sync, d->eps, d->debug, d->times, d->place,
                                   d->pol, d->mode == 2, st));
@@ -1908,6 +2024,7 @@ TG_API size_t tg_hip_decode_debug_bytes(void) { return (size_t)DecodeDebug::BYTE
  * f32 of width 2880); 0 for a step that is not persistent. */
 TG_API size_t tg_hip_decode_record_bytes(tg_hip_decode *d) {
     if (!d || d->mode < 2) return 0;
+    if (d->kind == 2) return d->rows_rec;
     return d->kind == 1 ? (size_t)DecodeDebugMx::BYTES : (size_t)DecodeDebug::BYTES;
 }
 
@@ -1990,6 +2107,7 @@ TG_API void tg_hip_decode_destroy(tg_hip_decode *d) {
     HIPCHECK(hipFree(d->x));
     if (d->layers) HIPCHECK(hipFree(d->layers));
     if (d->layers_mx) HIPCHECK(hipFree(d->layers_mx));
+    if (d->layers_rows) HIPCHECK(hipFree(d->layers_rows));
     if (d->hidden) HIPCHECK(hipFree(d->hidden));
     if (d->sync) HIPCHECK(hipFree(d->sync));
     if (d->qdown) HIPCHECK(hipFree(d->qdown));

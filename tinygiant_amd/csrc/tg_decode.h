@@ -97,5 +97,45 @@ int decode_qwen_max_grid();
  * per 8 rows {ql[8 nb][128] | qh[8 nb][64] | sc[8 nb][16] | d[8 nb]}. */
 hipError_t launch_q6k_row_groups(const void *src, void *dst, int nrows, int nb, hipStream_t st);
 
+/* The multi-row step (tg_decode_rows.hip): k = 2..ROWS_MAXK rows of the
+ * Qwen3 expert shape on ROWS_GRID co-resident workgroups.  One layer: its
+ * active experts and pairs (a compact table the kernel stages in LDS), the
+ * plan's per-row pair lists, the step's shared buffers, and the workgroups'
+ * item ranges: split[w] .. split[w + 1] of the gate/up items (expert-major,
+ * 16 rows each) and split[ROWS_GRID + 1 + w] .. of the down items (64 rows
+ * each). */
+constexpr int ROWS_MAXK = 16;
+constexpr int ROWS_GRID = 256;
+constexpr int ROWS_MAXE = 128;    /* active experts of a layer */
+constexpr int ROWS_MAXP = 256;    /* pairs of a layer */
+/* an active expert: its matrices and its pairs [p0, p0 + np) */
+struct RowsExp {
+    uint64_t gate, up, down;
+    int p0, np;
+};
+/* the layer's table: RowsExp [n_act] | pair rows int [P] | pair weights f32 [P]
+ * | first entry of each row's pair list int [k + 1] | the lists int [P] */
+constexpr int ROWS_TAB_BYTES = ROWS_MAXE * 32 + ROWS_MAXP * 12 + (ROWS_MAXK + 1) * 4 + 12;
+struct RowsLayer {
+    const uint8_t *tab;           /* the table above, tab_bytes (a multiple of 16) */
+    const int *split;
+    const float *norm_w;          /* RMSNorm weight before this layer, null = 1 */
+    float *hidden, *part;         /* [P][I], [P][D] */
+    uint8_t *xq;                  /* [k] q8 rows of x in the LDS image layout */
+    unsigned *flags;              /* [ROWS_GRID] barrier words */
+    int n_act, P, k, rec_bytes;   /* rec_bytes: debug record of a layer */
+    int tab_bytes, pad;
+};
+static_assert(sizeof(RowsExp) == 32, "table layout");
+/* Per-layer debug record: h_in f32[k][D] | x f32[k][D] | hidden f32[Pmax][I] */
+int decode_rows_max_grid();
+/* the item ranges of one layer from each active expert's pair count */
+void decode_rows_split(const int *np, int n_act, int *split /* [2 (ROWS_GRID + 1)] */);
+hipError_t launch_decode_rows(const RowsLayer *layers_dev, int L, float *h_dev, unsigned *sync_dev, float eps,
+                              uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, bool cooperative,
+                              hipStream_t st);
+const void *decode_rows_fn();
+int decode_rows_threads();
+
 }  // namespace tg
 #endif

@@ -1,0 +1,563 @@
+/*
+ * tg_decode_rows.hip -- the persistent multi-row decode step: L planned
+ * Qwen3-30B-A3B expert layers (D = 2048, I = 768, Q4_K gate/up, Q6_K down,
+ * SiLU, no biases) over k = 2..16 rows of h in one cooperative launch of 256
+ * workgroups.  Per layer it runs the chain tinygiant/engine.py:281-282,
+ * 335-341 applies to the rows of forward_rows -- a verify pass of K + 1 rows
+ * (tinygiant/specdec.py:66) or a prefill chunk (engine.py:213-217):
+ *
+ *   C  workgroup r < k, row r: h_r += the previous layer's partials of row r
+ *      in expert order (k_moe_combine); x_r = RMSNorm(h_r) * w_l; q8(x_r)
+ *   -- grid barrier --
+ *   A  gate/up items (active expert, 16 rows of I): both dots and the SiLU
+ *      product for every pair of the expert -> hidden[pair]
+ *   -- grid barrier --
+ *   B  down items (active expert, 64 rows of D): q8 of the expert's hidden
+ *      rows into LDS, then w_pair * dot for every pair -> part[pair]
+ *   -- grid barrier --
+ *
+ * Each workgroup takes a contiguous range of the layer's A items and one of
+ * its B items (split on the host by an estimate of each item's time) and
+ * streams them through registers: the next item's weight loads are in flight
+ * while the current item computes, and a phase's first item is loaded before
+ * the barrier that opens the phase, so the weights keep streaming across it.
+ * The per-row arithmetic is that of the per-layer kernels the plans run
+ * (k_rms_norm_q8, k_moe_ax<FQ4K, 32>, k_moe_bx<FQ6K, 16>, k_moe_combine):
+ * the step gives their bits.
+ *
+ * What one workgroup writes and another reads (q8 rows of x, hidden rows,
+ * partials, h) is stored with sc1, written through to memory, and loaded with
+ * sc1, which takes no stale line from the reader's L2: the workgroups sit on
+ * all 8 XCDs.  A barrier: each wave waits for its stores, then thread 0
+ * writes the barrier's tag into the workgroup's flag word; wave 0 of every
+ * workgroup polls the 256 words.  Tags grow by 3 L per launch from a device
+ * word, so the node of a graph replays unchanged, and every wait is bounded
+ * (a wait that runs out raises the abort word, which releases the rest).
+ */
+#include <algorithm>
+#include <vector>
+
+#include "tg_decode.h"
+#include "tg_kernels.h"
+#include "tg_xchg.hpp"
+
+namespace tg {
+namespace {
+
+constexpr int NT = 512, NWV = NT / 64;
+constexpr int D = 2048, I = 768, NBX = D / 256, NBH = I / 256;
+constexpr uint32_t GRB = 1152, DRB = 630;            /* Q4_K row of 2048 values, Q6_K row of 768 */
+constexpr uint32_t GMB = I * GRB, DMB = D * DRB;     /* bytes of a gate (up) and of a down matrix */
+constexpr int A_ROWS = 16, A_TILES = I / A_ROWS;     /* 8 waves x 2 rows of 32 lanes */
+constexpr int B_PASS = 2, B_ROWS = 32 * B_PASS;      /* 8 waves x 4 rows of 16 lanes, twice */
+constexpr int B_TILES = D / B_ROWS;
+constexpr int B_ITEMS = 12;                          /* Q6_K items of a 768-value row */
+constexpr uint32_t OOB = 0x80000000u;                /* past every buffer: reads zeros, touches nothing */
+constexpr uint32_t XS = q8_lds_stride(NBX), HS = q8_lds_stride(NBH);
+constexpr int NTS = 24;                              /* timing words per (workgroup, layer) */
+static_assert(XS == 2848 && HS == 1072, "q8 LDS image");
+static_assert(XS % 16 == 0, "the x image moves in 16-byte units");
+
+__device__ inline void st1(Buf b, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), b.r, (int)off, 0, CPOL_SC1);
+}
+__device__ inline void st1(Buf b, uint32_t off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, b.r, (int)off, 0, CPOL_SC1);
+}
+__device__ inline u32x4 ld1x4(Buf b, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, CPOL_SC1);
+}
+
+/* ---- grid barrier ---- */
+
+/* every wave's stores have completed, then the workgroup's flag takes tag */
+__device__ inline void bar_arrive(Buf flags, unsigned tag) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
+    bar_lds();
+    if (threadIdx.x == 0) st1(flags, blockIdx.x * 4u, tag);
+}
+/* wave 0 polls the gridDim.x flag words (four a lane) until each holds tag
+ * or a later one; false if the wait ran out or another workgroup aborted */
+__device__ inline bool bar_wait(Buf flags, unsigned tag, unsigned *abort_flag, int *s_ok) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        unsigned spins = 0;
+        int ok = 1;
+        while (true) {
+            const u32x4 v = ld1x4(flags, (uint32_t)lane * 16u);
+            const int n = (int)gridDim.x - 4 * lane;   /* words of this lane in the grid */
+            const bool in = ((int)(v.x - tag) >= 0 | n < 1) & ((int)(v.y - tag) >= 0 | n < 2) &
+                            ((int)(v.z - tag) >= 0 | n < 3) & ((int)(v.w - tag) >= 0 | n < 4);
+            if (__ballot(!in) == 0) break;
+            if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+                ok = 0;
+                break;
+            }
+            if (spins > SPIN_LIMIT) {
+                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ok = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) *s_ok = ok;
+    }
+    bar_lds();
+    return *s_ok != 0;
+}
+
+/* ---- the layer's tables, staged in LDS ----
+ * Values every lane of the workgroup reads alike come through LDS and
+ * readfirstlane: a vector load from global memory here would return behind
+ * the weight loads in flight (a CU returns its loads in order), and a
+ * descriptor built from a VGPR would wrap every load in a waterfall loop. */
+__device__ inline int ufl(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ inline const void *ufl_ptr(uint64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return (const void *)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+struct Tab {
+    const RowsExp *ex;
+    const int *prow;
+    const float *pw;
+    const int *roff, *rpair;
+};
+__device__ inline Tab tab_view(const uint8_t *t, int n_act, int P, int k) {
+    const int *pr = reinterpret_cast<const int *>(t + n_act * 32);
+    return Tab{reinterpret_cast<const RowsExp *>(t), pr, reinterpret_cast<const float *>(pr + P), pr + 2 * P,
+               pr + 2 * P + k + 1};
+}
+/* the layer's table (tab_bytes, 16-byte units) into LDS, one load a thread */
+__device__ inline void tab_load(const RowsLayer &ly, uint8_t *dst) {
+    const Buf b = make_buf(ly.tab, (uint32_t)ly.tab_bytes);
+    if (threadIdx.x * 16 < (unsigned)ly.tab_bytes)
+        *reinterpret_cast<u32x4 *>(dst + 16 * threadIdx.x) = ld16(b, threadIdx.x * 16u);
+}
+
+/* ---- items ---- */
+
+struct WA {
+    FQ4K::W g, u;
+};
+struct WB {
+    FQ6K::W w[B_PASS];
+};
+
+/* gate/up row of A item `item` this lane's segment works on */
+__device__ inline int a_row(int item, int wave, int lane) { return (item % A_TILES) * A_ROWS + 2 * wave + (lane >> 5); }
+__device__ inline int b_row(int item, int q, int wave, int lane) {
+    return (item % B_TILES) * B_ROWS + 32 * q + 4 * wave + (lane >> 4);
+}
+
+/* the weights of A item `item` (item < 0: out-of-range loads, zeros); tb
+ * may be read from global memory (nothing in flight then) or LDS */
+__device__ inline WA a_load(const Tab &tb, int item, int wave, int lane) {
+    item = ufl(item);
+    const int it = item < 0 ? 0 : item;
+    const RowsExp &e = tb.ex[it / A_TILES];
+    const uint32_t off = item < 0 ? OOB : (uint32_t)a_row(it, wave, lane) * GRB;
+    const Buf gb = make_buf(ufl_ptr(e.gate), GMB), ub = make_buf(ufl_ptr(e.up), GMB);
+    WA w;
+    w.g = FQ4K::load_w(gb, off, lane & 31);
+    w.u = FQ4K::load_w(ub, off, lane & 31);
+    return w;
+}
+__device__ inline WB b_load(const Tab &tb, int item, int wave, int lane) {
+    item = ufl(item);
+    const int it = item < 0 ? 0 : item;
+    const RowsExp &e = tb.ex[it / B_TILES];
+    const int sl = lane & 15;
+    const bool v = item >= 0 && sl < B_ITEMS;
+    const Buf db = make_buf(ufl_ptr(e.down), DMB);
+    WB w;
+#pragma unroll
+    for (int q = 0; q < B_PASS; q++)
+        w.w[q] = FQ6K::load_w(db, v ? (uint32_t)b_row(it, q, wave, lane) * DRB : OOB, v ? sl : 0);
+    return w;
+}
+
+/* gate/up + SiLU of every pair of the item's expert (k_moe_ax's sums) */
+__device__ inline void a_compute(const Tab &tb, int item, const WA &w, const uint8_t *xl, Buf hid, float *dbg_hid,
+                                 int wave, int lane) {
+    item = ufl(item);
+    const int s = item / A_TILES, p0 = ufl(tb.ex[s].p0), np = ufl(tb.ex[s].np);
+    const int r = a_row(item, wave, lane), sl = lane & 31;
+    const FQ4K::Wd g = FQ4K::decode(w.g, sl), u = FQ4K::decode(w.u, sl);
+    for (int j = 0; j < np; j++) {
+        const int p = p0 + j;
+        const Q8Lds xr = q8_lds_slot(xl, NBX, ufl(tb.prow[p]));
+        const FQ4K::X x = FQ4K::load_x(xr, sl);
+        float ag = 0.f, au = 0.f;
+        ag += FQ4K::value_d(g, x);
+        au += FQ4K::value_d(u, x);
+        const float vg = seg_sum_x<32>(ag), vu = seg_sum_x<32>(au);
+        if (sl == 0) {
+            const float hv = act_fn(TG_ACT_SILU, vg, vu);
+            st1(hid, (uint32_t)(p * I + r) * 4u, hv);
+            if (dbg_hid) dbg_hid[p * I + r] = hv;
+        }
+    }
+}
+
+/* q8 of the expert's hidden rows into LDS slots 0..np-1, one 256-block per
+ * wave (q8_quant_rows_lds's arithmetic) */
+__device__ inline void b_hidden_q8(int p0, int np, Buf hid, uint8_t *hl, int wave, int lane) {
+    constexpr int BATCH = 4;
+    const int nblk = np * NBH;
+    for (int u0 = wave; u0 < nblk; u0 += NWV * BATCH) {
+        u32x4 raw[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; i++) {
+            const int u = u0 + i * NWV;
+            const int s = u / NBH, b = u % NBH;
+            raw[i] = ld1x4(hid, u < nblk ? (uint32_t)((p0 + s) * I + b * 256 + 4 * lane) * 4u : OOB);
+        }
+#pragma unroll
+        for (int i = 0; i < BATCH; i++) {
+            const int u = u0 + i * NWV;
+            if (u >= nblk) continue;   /* uniform per wave */
+            const int s = u / NBH, b = u % NBH;
+            const Q8Quant q = q8_block_quant_dpp(__uint_as_float(raw[i].x), __uint_as_float(raw[i].y),
+                                                 __uint_as_float(raw[i].z), __uint_as_float(raw[i].w));
+            uint8_t *slot = hl + (size_t)s * HS;
+            reinterpret_cast<uint32_t *>(slot + b * 256)[lane] = q.packed;
+            if ((lane & 3) == 0) reinterpret_cast<int32_t *>(slot + NBH * 288)[b * 16 + (lane >> 2)] = q.s16;
+            if ((lane & 7) == 0) reinterpret_cast<int32_t *>(slot + NBH * 256)[b * 8 + (lane >> 3)] = q.s32;
+            if (lane == 0) reinterpret_cast<float *>(slot + NBH * 352)[b] = q.sc;
+        }
+    }
+}
+
+/* down rows of every pair of the item's expert, weighted (k_moe_bx's sums) */
+__device__ inline void b_compute(const Tab &tb, int item, const WB &w, const uint8_t *hl, Buf part, int wave,
+                                 int lane) {
+    item = ufl(item);
+    const int s = item / B_TILES, p0 = ufl(tb.ex[s].p0), np = ufl(tb.ex[s].np);
+    const int sl = lane & 15;
+    FQ6K::Wd wd[B_PASS];
+#pragma unroll
+    for (int q = 0; q < B_PASS; q++) wd[q] = FQ6K::decode(w.w[q], sl);
+    for (int j = 0; j < np; j++) {
+        const int p = p0 + j;
+        const Q8Lds xr = q8_lds_slot(hl, NBH, j);
+        const float pw = __int_as_float(ufl(__float_as_int(tb.pw[p])));
+        const FQ6K::X x = FQ6K::load_x(xr, sl < B_ITEMS ? sl : 0);
+#pragma unroll
+        for (int q = 0; q < B_PASS; q++) {
+            float acc = 0.f;
+            if (sl < B_ITEMS) acc += FQ6K::value_d(wd[q], x);
+            const float v = seg_sum_x<16>(acc);
+            if (sl == 0) st1(part, (uint32_t)(p * D + b_row(item, q, wave, lane)) * 4u, pw * (v + 0.f));
+        }
+    }
+}
+
+/* Items i0 .. i1-1 through two register sets: item i + 1's loads are issued
+ * before item i computes (pre(i, its registers) runs before that issue).
+ * s0 holds item i0's loads on entry.  The loop has one exit and no register
+ * copies, so the compiler's waits for the loads stay partial. */
+template <class W, class Load, class Pre, class Comp>
+__device__ inline void pipe(int i0, int i1, W s0, Load load, Pre pre, Comp comp) {
+    const int n = i1 - i0;
+    W s1;
+    int j = 0;
+    for (; j + 2 <= n; j += 2) {
+        pre(i0 + j, s0);
+        s1 = load(i0 + j + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        comp(i0 + j, s0);
+        pre(i0 + j + 1, s1);
+        s0 = load(i0 + j + 2 < i1 ? i0 + j + 2 : -1);
+        __builtin_amdgcn_sched_barrier(0);
+        comp(i0 + j + 1, s1);
+    }
+    if (j < n) {
+        pre(i0 + j, s0);
+        comp(i0 + j, s0);
+    }
+}
+
+/* Phase C for workgroup r < k: layer l's combine of row r (l >= 0), then the
+ * RMSNorm (weight norm_w) and q8 of the row for the next layer (when
+ * `next`), thread t owning values 4t .. 4t+3 as k_rms_norm_q8's lane t % 64
+ * of wave t / 64 does. */
+__device__ inline void phase_c(const RowsLayer *ly, const Tab *tb, const RowsLayer *nx, int r, float *h, float eps,
+                               float *red, uint8_t *rec_next, int wave, int lane) {
+    const int t = threadIdx.x;
+    const Buf hb = make_buf(h + (size_t)r * D, D * 4u);
+    const u32x4 hv = ld1x4(hb, (uint32_t)t * 16u);
+    float o[4] = {__uint_as_float(hv.x), __uint_as_float(hv.y), __uint_as_float(hv.z), __uint_as_float(hv.w)};
+    if (ly) {
+        const Buf pb = make_buf(ly->part, (uint32_t)ly->P * D * 4u);
+        const int q0 = ufl(tb->roff[r]), q1 = ufl(tb->roff[r + 1]);
+        for (int qb = q0; qb < q1; qb += 8) {
+            u32x4 v[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                v[i] = ld1x4(pb, qb + i < q1 ? (uint32_t)(ufl(tb->rpair[qb + i]) * D + 4 * t) * 4u : OOB);
+#pragma unroll
+            for (int i = 0; i < 8; i++)
+                if (qb + i < q1) {
+                    o[0] += __uint_as_float(v[i].x);
+                    o[1] += __uint_as_float(v[i].y);
+                    o[2] += __uint_as_float(v[i].z);
+                    o[3] += __uint_as_float(v[i].w);
+                }
+        }
+        u32x4 ov;
+        ov.x = __float_as_uint(o[0]);
+        ov.y = __float_as_uint(o[1]);
+        ov.z = __float_as_uint(o[2]);
+        ov.w = __float_as_uint(o[3]);
+        __builtin_amdgcn_raw_buffer_store_b128(ov, hb.r, (int)(t * 16u), 0, CPOL_SC1);
+    }
+    if (!nx) return;
+    if (rec_next) reinterpret_cast<float4 *>(rec_next + (size_t)r * D * 4)[t] = make_float4(o[0], o[1], o[2], o[3]);
+    /* RMSNorm: the lane's squares in order, the wave's butterfly, the waves' sum in order */
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; c++) ss += o[c] * o[c];
+    ss = wave_sum_x(ss);
+    if (lane == 0) red[wave] = ss;
+    bar_lds();
+    float tot = 0.f;
+    for (int i = 0; i < NWV; i++) tot += red[i];
+    const float scale = 1.f / sqrtf(tot / (float)D + eps);
+    float x[4];
+    const float *w = nx->norm_w;
+#pragma unroll
+    for (int c = 0; c < 4; c++) x[c] = (o[c] * scale) * (w ? w[4 * t + c] : 1.f);
+    if (rec_next)
+        reinterpret_cast<float4 *>(rec_next + (size_t)(nx->k + r) * D * 4)[t] = make_float4(x[0], x[1], x[2], x[3]);
+    /* q8 of block `wave` into row r's LDS image in global memory */
+    const Q8Quant q = q8_block_quant_dpp(x[0], x[1], x[2], x[3]);
+    const Buf xb = make_buf(nx->xq + (size_t)r * XS, XS);
+    const int b = wave;
+    st1(xb, (uint32_t)(b * 256 + 4 * lane), q.packed);
+    if ((lane & 3) == 0) st1(xb, (uint32_t)(NBX * 288 + (b * 16 + (lane >> 2)) * 4), (uint32_t)q.s16);
+    if ((lane & 7) == 0) st1(xb, (uint32_t)(NBX * 256 + (b * 8 + (lane >> 3)) * 4), (uint32_t)q.s32);
+    if (lane == 0) st1(xb, (uint32_t)(NBX * 352 + b * 4), q.sc);
+}
+
+__global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict__ layers, int L, float *h,
+                                                    void *slots, unsigned *sync, float eps, uint8_t *debug,
+                                                    uint64_t *times, unsigned *place, int pol) {
+    (void)slots;
+    (void)pol;
+    __shared__ __attribute__((aligned(16))) uint8_t xl[ROWS_MAXK * XS];   /* q8 rows of x */
+    __shared__ __attribute__((aligned(16))) uint8_t hl[ROWS_MAXK * HS];   /* q8 hidden rows of one expert */
+    __shared__ __attribute__((aligned(16))) uint8_t tabs[2][ROWS_TAB_BYTES];   /* layer tables, by parity */
+    __shared__ float red[NWV];
+    __shared__ unsigned s_base;
+    __shared__ int s_ok;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wg = blockIdx.x;
+    unsigned *abort_flag = sync;
+    if (threadIdx.x == 0) {
+        s_base = read_epoch(sync);
+        if (place) {
+            unsigned xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            place[wg] = xcc;
+        }
+    }
+    tab_load(layers[0], tabs[0]);
+    bar_lds();
+    const unsigned base = s_base;
+    const int k = layers[0].k;
+    const Buf flags = make_buf(layers[0].flags, gridDim.x * 4u);
+    unsigned tag = base;
+    bool ok = true;
+
+    /* C(-1): the first layer's RMSNorm and q8 */
+    if (wg < k) phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, wave, lane);
+    bar_arrive(flags, ++tag);
+    WA a0;
+    {
+        const RowsLayer &ly = layers[0];
+        const Tab tb = tab_view(tabs[0], ly.n_act, ly.P, ly.k);
+        const int i0 = ly.split[wg], i1 = ly.split[wg + 1];
+        a0 = a_load(tb, i0 < i1 ? i0 : -1, wave, lane);
+    }
+    ok = bar_wait(flags, tag, abort_flag, &s_ok);
+
+    for (int l = 0; l < L && ok; l++) {
+        const RowsLayer &ly = layers[l];
+        const Tab tb = tab_view(tabs[l & 1], ly.n_act, ly.P, ly.k);
+        const bool tw = times && threadIdx.x == 0;
+        uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
+        uint8_t *rec = debug ? debug + (size_t)l * ly.rec_bytes : nullptr;
+        const int ia0 = ly.split[wg], ia1 = ly.split[wg + 1];
+        const int ib0 = ly.split[ROWS_GRID + 1 + wg], ib1 = ly.split[ROWS_GRID + 2 + wg];
+        /* ---- A ---- */
+        {
+            /* the k q8 rows of x, every load in flight at once */
+            constexpr int XU = ROWS_MAXK * (XS / 16) / NT + 1;
+            const uint32_t nu = (uint32_t)k * (XS / 16);
+            const Buf xg = make_buf(ly.xq, nu * 16u);
+            u32x4 v[XU];
+#pragma unroll
+            for (int i = 0; i < XU; i++) v[i] = ld1x4(xg, (threadIdx.x + i * NT) * 16u);
+#pragma unroll
+            for (int i = 0; i < XU; i++)
+                if (threadIdx.x + i * NT < nu) *reinterpret_cast<u32x4 *>(xl + 16 * (threadIdx.x + i * NT)) = v[i];
+            bar_lds();
+            if (tw) tr[0] = wall_clock64();
+            const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 4u);
+            float *dh = rec ? reinterpret_cast<float *>(rec + (size_t)2 * k * D * 4) : nullptr;
+            pipe(
+                ia0, ia1, a0, [&](int i) { return a_load(tb, i, wave, lane); }, [](int, const WA &) {},
+                [&](int i, const WA &w) { a_compute(tb, i, w, xl, hid, dh, wave, lane); });
+        }
+        if (tw) tr[1] = wall_clock64();
+        bar_arrive(flags, ++tag);
+        WB b0 = b_load(tb, ib0 < ib1 ? ib0 : -1, wave, lane);
+        if (!bar_wait(flags, tag, abort_flag, &s_ok)) {
+            ok = false;
+            break;
+        }
+        if (tw) tr[2] = wall_clock64();
+        /* ---- B ---- */
+        {
+            const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 4u);
+            const Buf part = make_buf(ly.part, (uint32_t)ly.P * D * 4u);
+            int cur = -1;   /* expert whose q8 hidden rows hl holds */
+            pipe(
+                ib0, ib1, b0, [&](int i) { return b_load(tb, i, wave, lane); },
+                [&](int i, const WB &) {
+                    const int s = ufl(i) / B_TILES;
+                    if (s != cur) {
+                        bar_lds();   /* every wave is done with the previous rows */
+                        b_hidden_q8(ufl(tb.ex[s].p0), ufl(tb.ex[s].np), hid, hl, wave, lane);
+                        bar_lds();
+                        cur = s;
+                    }
+                },
+                [&](int i, const WB &w) { b_compute(tb, i, w, hl, part, wave, lane); });
+        }
+        if (tw) tr[3] = wall_clock64();
+        bar_arrive(flags, ++tag);
+        if (!bar_wait(flags, tag, abort_flag, &s_ok)) {
+            ok = false;
+            break;
+        }
+        if (tw) tr[4] = wall_clock64();
+        /* ---- C ---- */
+        const bool more = l + 1 < L;
+        if (wg < k)
+            phase_c(&ly, &tb, more ? &layers[l + 1] : nullptr, wg, h, eps, red,
+                    debug && more ? debug + (size_t)(l + 1) * ly.rec_bytes : nullptr, wave, lane);
+        if (tw) tr[5] = wall_clock64();
+        if (!more) break;
+        bar_arrive(flags, ++tag);
+        {
+            /* the next layer's table, then its first gate/up item in flight
+             * across the barrier */
+            const RowsLayer &nl = layers[l + 1];
+            tab_load(nl, tabs[(l + 1) & 1]);
+            bar_lds();
+            const Tab nt = tab_view(tabs[(l + 1) & 1], nl.n_act, nl.P, nl.k);
+            const int i0 = nl.split[wg], i1 = nl.split[wg + 1];
+            a0 = a_load(nt, i0 < i1 ? i0 : -1, wave, lane);
+        }
+        if (!bar_wait(flags, tag, abort_flag, &s_ok)) {
+            ok = false;
+            break;
+        }
+        if (tw) tr[6] = wall_clock64();
+    }
+    wait_copies();
+    if (wg == 0 && threadIdx.x == 0)
+        __hip_atomic_store(sync + 1, base + 3u * (unsigned)L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+int decode_rows_max_grid() {
+    int dev = 0, per_cu = 0;
+    hipDeviceProp_t pr;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&pr, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void *)k_decode_rows, NT, 0) != hipSuccess)
+        return 0;
+    return per_cu * pr.multiProcessorCount;
+}
+
+hipError_t launch_decode_rows(const RowsLayer *layers_dev, int L, float *h_dev, unsigned *sync_dev, float eps,
+                              uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, bool cooperative,
+                              hipStream_t st) {
+    void *slots = nullptr;
+    int pol = 1;
+    void *args[] = {(void *)&layers_dev, (void *)&L,         (void *)&h_dev,     (void *)&slots,
+                    (void *)&sync_dev,   (void *)&eps,       (void *)&debug_dev, (void *)&times_dev,
+                    (void *)&place_dev,  (void *)&pol};
+    if (cooperative)
+        return hipLaunchCooperativeKernel((const void *)k_decode_rows, dim3(ROWS_GRID), dim3(NT), args, 0, st);
+    return hipLaunchKernel((const void *)k_decode_rows, dim3(ROWS_GRID), dim3(NT), args, 0, st);
+}
+
+const void *decode_rows_fn() { return (const void *)k_decode_rows; }
+int decode_rows_threads() { return NT; }
+
+/* Item ranges of one layer.  Each active expert gets a share of the
+ * workgroups in proportion to its cost (largest remainders, at least one,
+ * at most one per item) and its items are split evenly over them, so a
+ * workgroup works on one expert per phase: a down item that starts another
+ * expert would first wait a memory round trip for that expert's hidden rows.
+ * Cost of an item, relative, from per-workgroup phase times of 48-layer
+ * steps: its weight bytes (36,864 B an A item, 40,320 B a B item) count 1,
+ * each pair of its expert 0.33. */
+void decode_rows_split(const int *np, int n_act, int *split) {
+    for (int ph = 0; ph < 2; ph++) {
+        const int tiles = ph == 0 ? A_TILES : B_TILES;
+        int *s = split + ph * (ROWS_GRID + 1);
+        std::vector<int> wgs(n_act, 0);
+        if (n_act > 0) {
+            double total = 0;
+            for (int e = 0; e < n_act; e++) total += 1.0 + 0.33 * np[e];
+            std::vector<std::pair<double, int>> rem;
+            int used = 0;
+            for (int e = 0; e < n_act; e++) {
+                const double share = ROWS_GRID * (1.0 + 0.33 * np[e]) / total;
+                wgs[e] = std::min(tiles, std::max(1, (int)share));
+                used += wgs[e];
+                rem.push_back({share - (int)share, e});
+            }
+            std::sort(rem.begin(), rem.end(), [](const std::pair<double, int> &a, const std::pair<double, int> &b) {
+                return a.first > b.first || (a.first == b.first && a.second < b.second);
+            });
+            /* hand out what is left by remainder, then round robin while
+             * some expert can still take a workgroup */
+            for (size_t i = 0; used < ROWS_GRID && i < rem.size(); i++)
+                if (wgs[rem[i].second] < tiles) {
+                    wgs[rem[i].second]++;
+                    used++;
+                }
+            for (bool more = true; used < ROWS_GRID && more;) {
+                more = false;
+                for (int e = 0; e < n_act && used < ROWS_GRID; e++)
+                    if (wgs[e] < tiles) {
+                        wgs[e]++;
+                        used++;
+                        more = true;
+                    }
+            }
+            while (used > ROWS_GRID) {   /* more experts than workgroups would need this; take from the largest */
+                int e = (int)(std::max_element(wgs.begin(), wgs.end()) - wgs.begin());
+                if (wgs[e] <= 1) break;
+                wgs[e]--;
+                used--;
+            }
+        }
+        int w = 0;
+        s[0] = 0;
+        for (int e = 0; e < n_act; e++)
+            for (int j = 0; j < wgs[e] && w < ROWS_GRID; j++) s[++w] = e * tiles + (int)((int64_t)tiles * (j + 1) / wgs[e]);
+        while (w < ROWS_GRID) {
+            s[w + 1] = s[w];
+            w++;
+        }
+        s[ROWS_GRID] = n_act * tiles;
+    }
+}
+
+}  // namespace tg

@@ -162,6 +162,25 @@ __device__ inline float seg_sum_rt(float v, int S) {
     return v;
 }
 
+/* The bits of seg_sum<S> (S = 16 or 32) without its chain of LDS round
+ * trips.  After the butterfly's stages of strides above s, all lanes of a
+ * class i mod 2s hold the same bits (a + b and b + a round alike), so any
+ * lane of class (i mod 2s) ^ s is a partner as good as i ^ s: a rotation of
+ * the 16-lane row by s is one, once the stride-2s stage is done
+ * ((x - s) mod 2s = x ^ s).  Stride 16, which crosses rows, is one
+ * ds_swizzle (xor 16 within 32 lanes); stride 8 is row_ror:8, an exact xor
+ * inside a row; 4 is row_ror:4; 2 and 1 are exact quad permutations. */
+template <int S>
+__device__ inline float seg_sum_x(float v) {
+    static_assert(S == 16 || S == 32, "segment");
+    if (S == 32) v += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+    v += dpp_f<0x128>(v, v);   /* row_ror:8 */
+    v += dpp_f<0x124>(v, v);   /* row_ror:4 */
+    v += dpp_f<0x4E>(v, v);    /* quad_perm [2,3,0,1] */
+    v += dpp_f<0xB1>(v, v);    /* quad_perm [1,0,3,2] */
+    return v;
+}
+
 /* ---- q8 activation rows on the device ----
  * Row r of an activation matrix with nb 256-blocks:
  *   qs  int8[nb*256] (zero padded), d f32[nb] (block scale),
@@ -218,6 +237,44 @@ __device__ inline Q8Quant q8_block_quant(float v0, float v1, float v2, float v3)
     tot += __shfl_xor(tot, 32, 64);
     r.tot = tot;
     return r;
+}
+
+/* LDS bytes of one staged q8 row of nb blocks: qs [nb*256], s32 [nb*8],
+ * s16 [nb*16], d [nb] */
+__host__ __device__ constexpr uint32_t q8_lds_stride(int nb) { return ((uint32_t)nb * 356u + 15u) & ~15u; }
+
+__device__ inline Q8Lds q8_lds_slot(const uint8_t *base, int nb, int s) {
+    const uint8_t *b = base + (size_t)s * q8_lds_stride(nb);
+    return Q8Lds{b, b + nb * 352, b + nb * 256, b + nb * 288};
+}
+
+/* q8_block_quant's quants, 16- and 32-element sums and scale (not the block
+ * total) without LDS round trips: the maximum and the integer sums are exact
+ * in any order, so DPP partners of the right lane class stand in for the
+ * xor partners (row_half_mirror pairs the two quads of 8 lanes). */
+__device__ inline Q8Quant q8_block_quant_dpp(float v0, float v1, float v2, float v3) {
+    const float amax = wave_max(fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3))));
+    Q8Quant r;
+    r.sc = amax / 127.f;                  /* correctly rounded */
+    const float inv = amax > 0.f ? 127.f / amax : 0.f;
+    int q0 = (int)__builtin_rintf(v0 * inv), q1 = (int)__builtin_rintf(v1 * inv);
+    int q2 = (int)__builtin_rintf(v2 * inv), q3 = (int)__builtin_rintf(v3 * inv);
+    r.packed = (uint32_t)(q0 & 0xFF) | ((uint32_t)(q1 & 0xFF) << 8) | ((uint32_t)(q2 & 0xFF) << 16) |
+               ((uint32_t)(q3 & 0xFF) << 24);
+    int s = q0 + q1 + q2 + q3;
+    s += dpp_i<0xB1>(s, s);
+    s += dpp_i<0x4E>(s, s);               /* 16-element sum */
+    r.s16 = s;
+    r.s32 = s + dpp_i<0x141>(s, s);       /* 32-element sum */
+    r.tot = 0;
+    return r;
+}
+
+/* The bits of the 64-lane shfl_xor butterfly (strides 32 .. 1) of v: one
+ * LDS permute for stride 32, then seg_sum_x<32>. */
+__device__ inline float wave_sum_x(float v) {
+    v += __shfl_xor(v, 32, 64);
+    return seg_sum_x<32>(v);
 }
 
 /* q8_block_quant of the wave's block, written to block b of row r */
@@ -309,18 +366,43 @@ struct FQ4K {
             m_hi = ((s2 >> (8 * jh + 4)) & 0xF) | (((s1 >> (8 * jh + 6)) & 3) << 4);
         }
     }
+    /* the item decoded once for several input rows: its nibbles, scales,
+     * mins and the two f16 factors */
+    struct Wd {
+        uint32_t lo[8], hi[8];
+        int sc_lo, m_lo, sc_hi, m_hi;
+        float d, dmin;
+    };
+    __device__ static inline Wd decode(const W &w, int item) {
+        const uint32_t m = 0x0F0F0F0Fu;
+        const uint32_t q[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
+        Wd r;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            r.lo[i] = q[i] & m;
+            r.hi[i] = (q[i] >> 4) & m;
+        }
+        scales(w, item & 3, r.sc_lo, r.m_lo, r.sc_hi, r.m_hi);
+        r.d = ref_f16(w.hdr.x);
+        r.dmin = ref_f16(w.hdr.x >> 16);
+        return r;
+    }
     /* x.d * (d*(sc_lo*lo + sc_hi*hi) - dmin*(m_lo*bs_lo + m_hi*bs_hi)):
      * both integer brackets are below 2^24, so they convert exactly. */
-    __device__ static inline float value(const W &w, const X &x, int item) {
-        int s[2];
-        isums(w, x, s);
-        int sc_lo, m_lo, sc_hi, m_hi;
-        scales(w, item & 3, sc_lo, m_lo, sc_hi, m_hi);
-        float d = ref_f16(w.hdr.x), dmin = ref_f16(w.hdr.x >> 16);
-        int A = sc_lo * s[0] + sc_hi * s[1];
-        int B = m_lo * x.s_lo + m_hi * x.s_hi;
-        return x.d * (d * (float)A - dmin * (float)B);
+    __device__ static inline float value_d(const Wd &w, const X &x) {
+        const uint32_t a[8] = {x.a0.x, x.a0.y, x.a0.z, x.a0.w, x.a1.x, x.a1.y, x.a1.z, x.a1.w};
+        const uint32_t b[8] = {x.b0.x, x.b0.y, x.b0.z, x.b0.w, x.b1.x, x.b1.y, x.b1.z, x.b1.w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            lo = dot4(w.lo[i], a[i], lo);
+            hi = dot4(w.hi[i], b[i], hi);
+        }
+        int A = w.sc_lo * lo + w.sc_hi * hi;
+        int B = w.m_lo * x.s_lo + w.m_hi * x.s_hi;
+        return x.d * (w.d * (float)A - w.dmin * (float)B);
     }
+    __device__ static inline float value(const W &w, const X &x, int item) { return value_d(decode(w, item), x); }
     /* where this item's integer sums go in the per-row isum vector
      * (8 sub-blocks per 256-block) */
     __device__ static inline int isum_index(int item, int i) { return (item >> 2) * 8 + 2 * (item & 3) + i; }
@@ -387,17 +469,49 @@ struct FQ6K {
         out[2] = a2 - 32 * x.s2;
         out[3] = a3 - 32 * x.s3;
     }
-    __device__ static inline float value(const W &w, const X &x, int item) {
-        int s[4];
-        isums(w, x, s);
-        int odd = item & 1;   /* sub-scale byte (u&1) + 2q of sc[8h..8h+7] */
-        int sc0 = (int)(int8_t)(w.sc.x >> (8 * odd));
-        int sc1 = (int)(int8_t)(w.sc.x >> (8 * odd + 16));
-        int sc2 = (int)(int8_t)(w.sc.y >> (8 * odd));
-        int sc3 = (int)(int8_t)(w.sc.y >> (8 * odd + 16));
-        int A = sc0 * s[0] + sc1 * s[1] + sc2 * s[2] + sc3 * s[3];
-        return ref_f16(w.d >> 16) * x.d * (float)A;
+    /* the item decoded once for several input rows: the 6-bit codes of its
+     * four 16-element groups (q[group][column]), their sub-scales, d */
+    struct Wd {
+        uint32_t q[4][4];
+        int sc[4];
+        float d;
+    };
+    __device__ static inline Wd decode(const W &w, int item) {
+        const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
+        const uint32_t la[4] = {w.qla.x, w.qla.y, w.qla.z, w.qla.w};
+        const uint32_t lb[4] = {w.qlb.x, w.qlb.y, w.qlb.z, w.qlb.w};
+        const uint32_t hh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+        Wd r;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            r.q[0][c] = (la[c] & m4) | ((hh[c] << 4) & m2);
+            r.q[1][c] = (lb[c] & m4) | ((hh[c] << 2) & m2);
+            r.q[2][c] = ((la[c] >> 4) & m4) | (hh[c] & m2);
+            r.q[3][c] = ((lb[c] >> 4) & m4) | ((hh[c] >> 2) & m2);
+        }
+        const int odd = item & 1;   /* sub-scale byte (u&1) + 2q of sc[8h..8h+7] */
+        r.sc[0] = (int)(int8_t)(w.sc.x >> (8 * odd));
+        r.sc[1] = (int)(int8_t)(w.sc.x >> (8 * odd + 16));
+        r.sc[2] = (int)(int8_t)(w.sc.y >> (8 * odd));
+        r.sc[3] = (int)(int8_t)(w.sc.y >> (8 * odd + 16));
+        r.d = ref_f16(w.d >> 16);
+        return r;
     }
+    __device__ static inline float value_d(const Wd &w, const X &x) {
+        const uint32_t xs[4][4] = {{x.x0.x, x.x0.y, x.x0.z, x.x0.w},
+                                   {x.x1.x, x.x1.y, x.x1.z, x.x1.w},
+                                   {x.x2.x, x.x2.y, x.x2.z, x.x2.w},
+                                   {x.x3.x, x.x3.y, x.x3.z, x.x3.w}};
+        int a[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) a[g] = dot4(w.q[g][c], xs[g][c], a[g]);
+        const int s0 = a[0] - 32 * x.s0, s1 = a[1] - 32 * x.s1, s2 = a[2] - 32 * x.s2, s3 = a[3] - 32 * x.s3;
+        int A = w.sc[0] * s0 + w.sc[1] * s1 + w.sc[2] * s2 + w.sc[3] * s3;
+        return w.d * x.d * (float)A;
+    }
+    __device__ static inline float value(const W &w, const X &x, int item) { return value_d(decode(w, item), x); }
     __device__ static inline int isum_index(int item, int i) {
         int u = item & 3;
         return (item >> 2) * 16 + 8 * (u >> 1) + (u & 1) + 2 * i;

@@ -359,15 +359,6 @@ __global__ __launch_bounds__(256) void k_moe_b(MoeArgs a, int fmt, uint32_t rb, 
 constexpr int MOE_X_MAXP = 8;
 static_assert(MOE_X_MAXP == EXP_ROWS, "the first chunk's rows come from the expert descriptor");
 
-/* LDS bytes of one staged q8 row of nb blocks: qs [nb*256], s32 [nb*8],
- * s16 [nb*16], d [nb] */
-__host__ __device__ constexpr uint32_t q8_lds_stride(int nb) { return ((uint32_t)nb * 356u + 15u) & ~15u; }
-
-__device__ inline Q8Lds q8_lds_slot(const uint8_t *base, int nb, int s) {
-    const uint8_t *b = base + (size_t)s * q8_lds_stride(nb);
-    return Q8Lds{b, b + nb * 352, b + nb * 256, b + nb * 288};
-}
-
 /* q8 rows rows[0..n) of q into LDS slots 0..n-1 by the whole workgroup */
 __device__ inline void q8_rows_to_lds(const Q8Rows &q, const int *rows, int n, uint8_t *lds) {
     const int nb = q.nb, per = nb * 22;   /* 16-byte units of qs, s32 and s16 */
