@@ -1691,9 +1691,10 @@ static bool persistent_ok(tg_hip_decode *d, std::vector<DecodeLayer> &out) {
 
 /* The multi-row kernel covers steps of k = 2..ROWS_MAXK rows of the Qwen
  * expert shape (up to ROWS_MAXE active experts and ROWS_MAXP pairs per
- * layer).  It builds the kernel's layer table and its buffers: barrier flags
- * | q8 rows of x | hidden [Pmax][I] | partials [Pmax][D] | item ranges
- * [L][2][ROWS_GRID + 1] | the layers' expert and pair tables. */
+ * layer).  It builds the kernel's layer table and its buffers, each layer's
+ * its own: row flags [L][ROWS_MAXK] | q8 rows of x [L][ROWS_MAXK] | item
+ * ranges [L][2][ROWS_GRID + 1] | the layers' expert and pair tables | tagged
+ * hidden words [P_l][I] | tagged partials [P_l][D]. */
 static bool persistent_rows_create(tg_hip_decode *d) {
     const DecodeShape sh = decode_qwen_shape();
     if (d->k < 2 || d->k > ROWS_MAXK) {
@@ -1731,15 +1732,18 @@ static bool persistent_rows_create(tg_hip_decode *d) {
         return false;
     }
     const size_t XS = q8_lds_stride(sh.D / 256), NS = 2 * (ROWS_GRID + 1);
-    const size_t o_xq = ROWS_GRID * 4, o_hid = o_xq + (size_t)ROWS_MAXK * XS,
-                 o_part = o_hid + (size_t)pmax * sh.I * 4, o_split = o_part + (size_t)pmax * sh.D * 4,
+    size_t words = 0;   /* tagged hidden and partial words of all layers */
+    for (int l = 0; l < d->L; l++) words += (size_t)d->plans[l]->h.P * (sh.I + sh.D);
+    const size_t o_xq = ((size_t)d->L * ROWS_MAXK * 4 + 255) & ~(size_t)255,
+                 o_split = o_xq + (size_t)d->L * ROWS_MAXK * XS,
                  o_tab = (o_split + (size_t)d->L * NS * 4 + 255) & ~(size_t)255,
-                 total = o_tab + (size_t)d->L * ROWS_TAB_BYTES;
+                 o_words = o_tab + (size_t)d->L * ROWS_TAB_BYTES, total = o_words + words * 8;
     HIPCHECK(hipMalloc(&d->hidden, total));
     HIPCHECK(hipMemset(d->hidden, 0, total));
     uint8_t *base = (uint8_t *)d->hidden;
     std::vector<int> splits((size_t)d->L * NS);
     std::vector<RowsLayer> ls(d->L);
+    uint64_t *wp = (uint64_t *)(base + o_words);
     for (int l = 0; l < d->L; l++) {
         const tg_hip_moe_plan *p = d->plans[l];
         const HostPlan &h = p->h;
@@ -1765,10 +1769,11 @@ static bool persistent_rows_create(tg_hip_decode *d) {
         r.tab_bytes = (int)tb;
         r.split = (const int *)(base + o_split) + (size_t)l * NS;
         r.norm_w = d->norm_w.empty() ? nullptr : d->norm_w[l];
-        r.hidden = (float *)(base + o_hid);
-        r.part = (float *)(base + o_part);
-        r.xq = base + o_xq;
-        r.flags = (unsigned *)base;
+        r.hidden = wp;
+        r.part = wp + (size_t)h.P * sh.I;
+        wp += (size_t)h.P * (sh.I + sh.D);
+        r.xq = base + o_xq + (size_t)l * ROWS_MAXK * XS;
+        r.xflag = (unsigned *)base + (size_t)l * ROWS_MAXK;
         r.n_act = (int)np.size();
         r.P = h.P;
         r.k = d->k;

@@ -100,10 +100,11 @@ hipError_t launch_q6k_row_groups(const void *src, void *dst, int nrows, int nb, 
 /* The multi-row step (tg_decode_rows.hip): k = 2..ROWS_MAXK rows of the
  * Qwen3 expert shape on ROWS_GRID co-resident workgroups.  One layer: its
  * active experts and pairs (a compact table the kernel stages in LDS), the
- * plan's per-row pair lists, the step's shared buffers, and the workgroups'
- * item ranges: split[w] .. split[w + 1] of the gate/up items (expert-major,
- * 16 rows each) and split[ROWS_GRID + 1 + w] .. of the down items (64 rows
- * each). */
+ * plan's per-row pair lists, the layer's own exchange buffers, and the
+ * workgroups' item ranges: split[w] .. split[w + 1] of the gate/up items
+ * (expert-major, 16 rows each) and split[ROWS_GRID + 1 + w] .. of the down
+ * items (64 rows each).  Hidden values and partials are 8-byte words {tag,
+ * f32 value}; the tag of layer l in a launch is epoch + l + 1. */
 constexpr int ROWS_MAXK = 16;
 constexpr int ROWS_GRID = 256;
 constexpr int ROWS_MAXE = 128;    /* active experts of a layer */
@@ -120,9 +121,9 @@ struct RowsLayer {
     const uint8_t *tab;           /* the table above, tab_bytes (a multiple of 16) */
     const int *split;
     const float *norm_w;          /* RMSNorm weight before this layer, null = 1 */
-    float *hidden, *part;         /* [P][I], [P][D] */
+    uint64_t *hidden, *part;      /* [P][I], [P][D] tagged words */
     uint8_t *xq;                  /* [k] q8 rows of x in the LDS image layout */
-    unsigned *flags;              /* [ROWS_GRID] barrier words */
+    unsigned *xflag;              /* [ROWS_MAXK] row r of xq is complete when word r holds the tag */
     int n_act, P, k, rec_bytes;   /* rec_bytes: debug record of a layer */
     int tab_bytes, pad;
 };

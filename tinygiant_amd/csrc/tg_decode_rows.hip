@@ -6,33 +6,37 @@
  * 335-341 applies to the rows of forward_rows -- a verify pass of K + 1 rows
  * (tinygiant/specdec.py:66) or a prefill chunk (engine.py:213-217):
  *
- *   C  workgroup r < k, row r: h_r += the previous layer's partials of row r
- *      in expert order (k_moe_combine); x_r = RMSNorm(h_r) * w_l; q8(x_r)
- *   -- grid barrier --
- *   A  gate/up items (active expert, 16 rows of I): both dots and the SiLU
- *      product for every pair of the expert -> hidden[pair]
- *   -- grid barrier --
- *   B  down items (active expert, 64 rows of D): q8 of the expert's hidden
- *      rows into LDS, then w_pair * dot for every pair -> part[pair]
- *   -- grid barrier --
+ *   A  gate/up items (active expert, 16 rows of I), once the k rows of x are
+ *      flagged: both dots and the SiLU product for every pair of the expert
+ *      -> hidden[pair]
+ *   B  down items (active expert, 64 rows of D), once the expert's hidden
+ *      rows are there: their q8 into LDS, then w_pair * dot for every pair
+ *      -> part[pair]
+ *   C  workgroup r < k, row r, once its partials are there: h_r += them in
+ *      expert order (k_moe_combine); x_r = RMSNorm(h_r) * w_{l+1}; q8(x_r);
+ *      then row r's flag for layer l + 1
+ *
+ * No barrier separates the phases: every value one workgroup writes and
+ * another reads sits in a buffer of its layer as an 8-byte word {tag, value}
+ * (the q8 rows of x: behind a per-row flag word), the tag being the layer's
+ * in this launch, and the reader polls the words it needs until their tags
+ * match.  A workgroup thus waits only for what it reads: a down item for its
+ * expert's hidden rows, a row's combine for the row's partials.
  *
  * Each workgroup takes a contiguous range of the layer's A items and one of
  * its B items (split on the host by an estimate of each item's time) and
  * streams them through registers: the next item's weight loads are in flight
  * while the current item computes, and a phase's first item is loaded before
- * the barrier that opens the phase, so the weights keep streaming across it.
- * The per-row arithmetic is that of the per-layer kernels the plans run
- * (k_rms_norm_q8, k_moe_ax<FQ4K, 32>, k_moe_bx<FQ6K, 16>, k_moe_combine):
- * the step gives their bits.
+ * the wait that opens the phase.  The per-row arithmetic is that of the
+ * per-layer kernels the plans run (k_rms_norm_q8, k_moe_ax<FQ4K, 32>,
+ * k_moe_bx<FQ6K, 16>, k_moe_combine): the step gives their bits.
  *
- * What one workgroup writes and another reads (q8 rows of x, hidden rows,
- * partials, h) is stored with sc1, written through to memory, and loaded with
- * sc1, which takes no stale line from the reader's L2: the workgroups sit on
- * all 8 XCDs.  A barrier: each wave waits for its stores, then thread 0
- * writes the barrier's tag into the workgroup's flag word; wave 0 of every
- * workgroup polls the 256 words.  Tags grow by 3 L per launch from a device
- * word, so the node of a graph replays unchanged, and every wait is bounded
- * (a wait that runs out raises the abort word, which releases the rest).
+ * Exchanged data is stored with sc1, written through to memory, and loaded
+ * with sc1, which takes no stale line from the reader's L2: the workgroups
+ * sit on all 8 XCDs.  Tags grow by L per launch from a device word (the last
+ * workgroup to leave advances it), so the node of a graph replays unchanged,
+ * and every wait is bounded (a wait that runs out raises the abort word,
+ * which releases the rest).
  */
 #include <algorithm>
 #include <vector>
@@ -68,42 +72,28 @@ __device__ inline u32x4 ld1x4(Buf b, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(b.r, (int)off, 0, CPOL_SC1);
 }
 
-/* ---- grid barrier ---- */
-
-/* every wave's stores have completed, then the workgroup's flag takes tag */
-__device__ inline void bar_arrive(Buf flags, unsigned tag) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
-    bar_lds();
-    if (threadIdx.x == 0) st1(flags, blockIdx.x * 4u, tag);
+/* ---- tagged words ----
+ * A value another workgroup reads is stored as one 8-byte word {tag, value}
+ * (the tag of its layer in this launch); the reader polls the words it
+ * needs until every tag matches, so no store waits for its completion and
+ * no barrier separates the phases. */
+__device__ inline void st_tag(Buf b, uint32_t idx, unsigned tag, float v) {
+    u32x2 w;
+    w.x = tag;
+    w.y = __float_as_uint(v);
+    __builtin_amdgcn_raw_buffer_store_b64(w, b.r, (int)(idx * 8u), 0, CPOL_SC1);
 }
-/* wave 0 polls the gridDim.x flag words (four a lane) until each holds tag
- * or a later one; false if the wait ran out or another workgroup aborted */
-__device__ inline bool bar_wait(Buf flags, unsigned tag, unsigned *abort_flag, int *s_ok) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        unsigned spins = 0;
-        int ok = 1;
-        while (true) {
-            const u32x4 v = ld1x4(flags, (uint32_t)lane * 16u);
-            const int n = (int)gridDim.x - 4 * lane;   /* words of this lane in the grid */
-            const bool in = ((int)(v.x - tag) >= 0 | n < 1) & ((int)(v.y - tag) >= 0 | n < 2) &
-                            ((int)(v.z - tag) >= 0 | n < 3) & ((int)(v.w - tag) >= 0 | n < 4);
-            if (__ballot(!in) == 0) break;
-            if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                ok = 0;
-                break;
-            }
-            if (spins > SPIN_LIMIT) {
-                __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ok = 0;
-                break;
-            }
-            __builtin_amdgcn_s_sleep(1);
-        }
-        if (lane == 0) *s_ok = ok;
+
+/* a bounded poll round: false once the wait has run out or another
+ * workgroup aborted (then the abort word is set) */
+__device__ inline bool poll_more(unsigned &spins, unsigned *abort_flag) {
+    if ((++spins & 63) == 0 && __hip_atomic_load(abort_flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return false;
+    if (spins > SPIN_LIMIT) {
+        __hip_atomic_store(abort_flag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return false;
     }
-    bar_lds();
-    return *s_ok != 0;
+    __builtin_amdgcn_s_sleep(1);
+    return true;
 }
 
 /* ---- the layer's tables, staged in LDS ----
@@ -178,8 +168,8 @@ __device__ inline WB b_load(const Tab &tb, int item, int wave, int lane) {
 }
 
 /* gate/up + SiLU of every pair of the item's expert (k_moe_ax's sums) */
-__device__ inline void a_compute(const Tab &tb, int item, const WA &w, const uint8_t *xl, Buf hid, float *dbg_hid,
-                                 int wave, int lane) {
+__device__ inline void a_compute(const Tab &tb, int item, const WA &w, const uint8_t *xl, Buf hid, unsigned tag,
+                                 float *dbg_hid, int wave, int lane) {
     item = ufl(item);
     const int s = item / A_TILES, p0 = ufl(tb.ex[s].p0), np = ufl(tb.ex[s].np);
     const int r = a_row(item, wave, lane), sl = lane & 31;
@@ -194,32 +184,43 @@ __device__ inline void a_compute(const Tab &tb, int item, const WA &w, const uin
         const float vg = seg_sum_x<32>(ag), vu = seg_sum_x<32>(au);
         if (sl == 0) {
             const float hv = act_fn(TG_ACT_SILU, vg, vu);
-            st1(hid, (uint32_t)(p * I + r) * 4u, hv);
+            st_tag(hid, (uint32_t)(p * I + r), tag, hv);
             if (dbg_hid) dbg_hid[p * I + r] = hv;
         }
     }
 }
 
 /* q8 of the expert's hidden rows into LDS slots 0..np-1, one 256-block per
- * wave (q8_quant_rows_lds's arithmetic) */
-__device__ inline void b_hidden_q8(int p0, int np, Buf hid, uint8_t *hl, int wave, int lane) {
+ * wave (q8_quant_rows_lds's arithmetic), once every value carries the
+ * layer's tag; false if the wait ran out */
+__device__ inline bool b_hidden_q8(int p0, int np, Buf hid, unsigned tag, unsigned *abort_flag, uint8_t *hl, int wave,
+                                   int lane) {
     constexpr int BATCH = 4;
     const int nblk = np * NBH;
     for (int u0 = wave; u0 < nblk; u0 += NWV * BATCH) {
-        u32x4 raw[BATCH];
+        u32x4 raw[BATCH][2];
+        unsigned spins = 0;
+        while (true) {
+            bool in = true;
 #pragma unroll
-        for (int i = 0; i < BATCH; i++) {
-            const int u = u0 + i * NWV;
-            const int s = u / NBH, b = u % NBH;
-            raw[i] = ld1x4(hid, u < nblk ? (uint32_t)((p0 + s) * I + b * 256 + 4 * lane) * 4u : OOB);
+            for (int i = 0; i < BATCH; i++) {
+                const int u = u0 + i * NWV;
+                const int s = u / NBH, b = u % NBH;
+                const uint32_t w0 = u < nblk ? (uint32_t)((p0 + s) * I + b * 256 + 4 * lane) * 8u : OOB;
+                raw[i][0] = ld1x4(hid, w0);
+                raw[i][1] = ld1x4(hid, w0 == OOB ? OOB : w0 + 16u);
+                in &= u >= nblk || (raw[i][0].x == tag && raw[i][0].z == tag && raw[i][1].x == tag && raw[i][1].z == tag);
+            }
+            if (__ballot(!in) == 0) break;
+            if (!poll_more(spins, abort_flag)) return false;
         }
 #pragma unroll
         for (int i = 0; i < BATCH; i++) {
             const int u = u0 + i * NWV;
             if (u >= nblk) continue;   /* uniform per wave */
             const int s = u / NBH, b = u % NBH;
-            const Q8Quant q = q8_block_quant_dpp(__uint_as_float(raw[i].x), __uint_as_float(raw[i].y),
-                                                 __uint_as_float(raw[i].z), __uint_as_float(raw[i].w));
+            const Q8Quant q = q8_block_quant_dpp(__uint_as_float(raw[i][0].y), __uint_as_float(raw[i][0].w),
+                                                 __uint_as_float(raw[i][1].y), __uint_as_float(raw[i][1].w));
             uint8_t *slot = hl + (size_t)s * HS;
             reinterpret_cast<uint32_t *>(slot + b * 256)[lane] = q.packed;
             if ((lane & 3) == 0) reinterpret_cast<int32_t *>(slot + NBH * 288)[b * 16 + (lane >> 2)] = q.s16;
@@ -227,11 +228,12 @@ __device__ inline void b_hidden_q8(int p0, int np, Buf hid, uint8_t *hl, int wav
             if (lane == 0) reinterpret_cast<float *>(slot + NBH * 352)[b] = q.sc;
         }
     }
+    return true;
 }
 
 /* down rows of every pair of the item's expert, weighted (k_moe_bx's sums) */
-__device__ inline void b_compute(const Tab &tb, int item, const WB &w, const uint8_t *hl, Buf part, int wave,
-                                 int lane) {
+__device__ inline void b_compute(const Tab &tb, int item, const WB &w, const uint8_t *hl, Buf part, unsigned tag,
+                                 int wave, int lane) {
     item = ufl(item);
     const int s = item / B_TILES, p0 = ufl(tb.ex[s].p0), np = ufl(tb.ex[s].np);
     const int sl = lane & 15;
@@ -248,7 +250,7 @@ __device__ inline void b_compute(const Tab &tb, int item, const WB &w, const uin
             float acc = 0.f;
             if (sl < B_ITEMS) acc += FQ6K::value_d(wd[q], x);
             const float v = seg_sum_x<16>(acc);
-            if (sl == 0) st1(part, (uint32_t)(p * D + b_row(item, q, wave, lane)) * 4u, pw * (v + 0.f));
+            if (sl == 0) st_tag(part, (uint32_t)(p * D + b_row(item, q, wave, lane)), tag, pw * (v + 0.f));
         }
     }
 }
@@ -278,31 +280,44 @@ __device__ inline void pipe(int i0, int i1, W s0, Load load, Pre pre, Comp comp)
     }
 }
 
-/* Phase C for workgroup r < k: layer l's combine of row r (l >= 0), then the
- * RMSNorm (weight norm_w) and q8 of the row for the next layer (when
- * `next`), thread t owning values 4t .. 4t+3 as k_rms_norm_q8's lane t % 64
- * of wave t / 64 does. */
-__device__ inline void phase_c(const RowsLayer *ly, const Tab *tb, const RowsLayer *nx, int r, float *h, float eps,
-                               float *red, uint8_t *rec_next, int wave, int lane) {
+/* Phase C for workgroup r < k: layer ly's combine of row r (ly non-null),
+ * then the RMSNorm (weight nx->norm_w) and q8 of the row for layer nx (when
+ * non-null), thread t owning values 4t .. 4t+3 as k_rms_norm_q8's lane t % 64
+ * of wave t / 64 does.  False if a wait for a partial ran out. */
+__device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLayer *nx, int r, float *h, float eps,
+                               float *red, uint8_t *rec_next, unsigned tag, unsigned *abort_flag, int wave, int lane) {
     const int t = threadIdx.x;
     const Buf hb = make_buf(h + (size_t)r * D, D * 4u);
     const u32x4 hv = ld1x4(hb, (uint32_t)t * 16u);
     float o[4] = {__uint_as_float(hv.x), __uint_as_float(hv.y), __uint_as_float(hv.z), __uint_as_float(hv.w)};
+    bool good = true;   /* a wave whose wait ran out goes on (the barriers below count every wave) */
     if (ly) {
-        const Buf pb = make_buf(ly->part, (uint32_t)ly->P * D * 4u);
+        /* row r's partials, eight pairs at a time, each word polled until
+         * it carries the layer's tag; added in expert order */
+        const Buf pb = make_buf(ly->part, (uint32_t)ly->P * D * 8u);
         const int q0 = ufl(tb->roff[r]), q1 = ufl(tb->roff[r + 1]);
         for (int qb = q0; qb < q1; qb += 8) {
-            u32x4 v[8];
+            u32x4 v[8][2];
+            unsigned spins = 0;
+            while (good) {
+                bool in = true;
 #pragma unroll
-            for (int i = 0; i < 8; i++)
-                v[i] = ld1x4(pb, qb + i < q1 ? (uint32_t)(ufl(tb->rpair[qb + i]) * D + 4 * t) * 4u : OOB);
+                for (int i = 0; i < 8; i++) {
+                    const uint32_t w0 = qb + i < q1 ? (uint32_t)(ufl(tb->rpair[qb + i]) * D + 4 * t) * 8u : OOB;
+                    v[i][0] = ld1x4(pb, w0);
+                    v[i][1] = ld1x4(pb, w0 == OOB ? OOB : w0 + 16u);
+                    in &= qb + i >= q1 || (v[i][0].x == tag && v[i][0].z == tag && v[i][1].x == tag && v[i][1].z == tag);
+                }
+                if (__ballot(!in) == 0) break;
+                good = poll_more(spins, abort_flag);
+            }
 #pragma unroll
             for (int i = 0; i < 8; i++)
                 if (qb + i < q1) {
-                    o[0] += __uint_as_float(v[i].x);
-                    o[1] += __uint_as_float(v[i].y);
-                    o[2] += __uint_as_float(v[i].z);
-                    o[3] += __uint_as_float(v[i].w);
+                    o[0] += __uint_as_float(v[i][0].y);
+                    o[1] += __uint_as_float(v[i][0].w);
+                    o[2] += __uint_as_float(v[i][1].y);
+                    o[3] += __uint_as_float(v[i][1].w);
                 }
         }
         u32x4 ov;
@@ -312,7 +327,7 @@ __device__ inline void phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
         ov.w = __float_as_uint(o[3]);
         __builtin_amdgcn_raw_buffer_store_b128(ov, hb.r, (int)(t * 16u), 0, CPOL_SC1);
     }
-    if (!nx) return;
+    if (!nx) return good;
     if (rec_next) reinterpret_cast<float4 *>(rec_next + (size_t)r * D * 4)[t] = make_float4(o[0], o[1], o[2], o[3]);
     /* RMSNorm: the lane's squares in order, the wave's butterfly, the waves' sum in order */
     float ss = 0.f;
@@ -338,6 +353,35 @@ __device__ inline void phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
     if ((lane & 3) == 0) st1(xb, (uint32_t)(NBX * 288 + (b * 16 + (lane >> 2)) * 4), (uint32_t)q.s16);
     if ((lane & 7) == 0) st1(xb, (uint32_t)(NBX * 256 + (b * 8 + (lane >> 3)) * 4), (uint32_t)q.s32);
     if (lane == 0) st1(xb, (uint32_t)(NBX * 352 + b * 4), q.sc);
+    return good;
+}
+
+/* row r of layer ly's x is complete: every wave's stores have completed,
+ * then its flag takes the layer's tag */
+__device__ inline void x_publish(const RowsLayer &ly, int r, unsigned tag) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
+    bar_lds();
+    if (threadIdx.x == 0) st1(make_buf(ly.xflag, ROWS_MAXK * 4u), (uint32_t)r * 4u, tag);
+}
+/* wave 0 polls the k row flags of layer ly; false if the wait ran out */
+__device__ inline bool x_wait(const RowsLayer &ly, int k, unsigned tag, unsigned *abort_flag, int *s_ok) {
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        const Buf fb = make_buf(ly.xflag, ROWS_MAXK * 4u);
+        unsigned spins = 0;
+        int ok = 1;
+        while (true) {
+            const uint32_t f = lane < k ? __builtin_amdgcn_raw_buffer_load_b32(fb.r, lane * 4, 0, CPOL_SC1) : tag;
+            if (__ballot(f != tag) == 0) break;
+            if (!poll_more(spins, abort_flag)) {
+                ok = 0;
+                break;
+            }
+        }
+        if (lane == 0) *s_ok = ok;
+    }
+    bar_lds();
+    return *s_ok != 0;
 }
 
 __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict__ layers, int L, float *h,
@@ -350,7 +394,7 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     __shared__ __attribute__((aligned(16))) uint8_t tabs[2][ROWS_TAB_BYTES];   /* layer tables, by parity */
     __shared__ float red[NWV];
     __shared__ unsigned s_base;
-    __shared__ int s_ok;
+    __shared__ int s_ok, s_okc;   /* a wait ran out: x and B waits; C waits */
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wg = blockIdx.x;
     unsigned *abort_flag = sync;
     if (threadIdx.x == 0) {
@@ -365,13 +409,13 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     bar_lds();
     const unsigned base = s_base;
     const int k = layers[0].k;
-    const Buf flags = make_buf(layers[0].flags, gridDim.x * 4u);
-    unsigned tag = base;
     bool ok = true;
 
     /* C(-1): the first layer's RMSNorm and q8 */
-    if (wg < k) phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, wave, lane);
-    bar_arrive(flags, ++tag);
+    if (wg < k) {
+        phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, 0u, abort_flag, wave, lane);
+        x_publish(layers[0], wg, base + 1u);
+    }
     WA a0;
     {
         const RowsLayer &ly = layers[0];
@@ -379,18 +423,23 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
         const int i0 = ly.split[wg], i1 = ly.split[wg + 1];
         a0 = a_load(tb, i0 < i1 ? i0 : -1, wave, lane);
     }
-    ok = bar_wait(flags, tag, abort_flag, &s_ok);
 
     for (int l = 0; l < L && ok; l++) {
         const RowsLayer &ly = layers[l];
+        const unsigned tag = base + 1u + (unsigned)l;   /* this layer's tag in this launch */
         const Tab tb = tab_view(tabs[l & 1], ly.n_act, ly.P, ly.k);
         const bool tw = times && threadIdx.x == 0;
         uint64_t *tr = times ? times + ((size_t)wg * L + l) * NTS : nullptr;
         uint8_t *rec = debug ? debug + (size_t)l * ly.rec_bytes : nullptr;
         const int ia0 = ly.split[wg], ia1 = ly.split[wg + 1];
         const int ib0 = ly.split[ROWS_GRID + 1 + wg], ib1 = ly.split[ROWS_GRID + 2 + wg];
+        const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 8u);
         /* ---- A ---- */
         {
+            if (!x_wait(ly, k, tag, abort_flag, &s_ok)) {
+                ok = false;
+                break;
+            }
             /* the k q8 rows of x, every load in flight at once */
             constexpr int XU = ROWS_MAXK * (XS / 16) / NT + 1;
             const uint32_t nu = (uint32_t)k * (XS / 16);
@@ -403,56 +452,60 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
                 if (threadIdx.x + i * NT < nu) *reinterpret_cast<u32x4 *>(xl + 16 * (threadIdx.x + i * NT)) = v[i];
             bar_lds();
             if (tw) tr[0] = wall_clock64();
-            const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 4u);
             float *dh = rec ? reinterpret_cast<float *>(rec + (size_t)2 * k * D * 4) : nullptr;
             pipe(
                 ia0, ia1, a0, [&](int i) { return a_load(tb, i, wave, lane); }, [](int, const WA &) {},
-                [&](int i, const WA &w) { a_compute(tb, i, w, xl, hid, dh, wave, lane); });
+                [&](int i, const WA &w) { a_compute(tb, i, w, xl, hid, tag, dh, wave, lane); });
         }
         if (tw) tr[1] = wall_clock64();
-        bar_arrive(flags, ++tag);
-        WB b0 = b_load(tb, ib0 < ib1 ? ib0 : -1, wave, lane);
-        if (!bar_wait(flags, tag, abort_flag, &s_ok)) {
-            ok = false;
-            break;
-        }
-        if (tw) tr[2] = wall_clock64();
-        /* ---- B ---- */
+        /* ---- B: each expert's hidden rows are polled when its first item starts ---- */
         {
-            const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 4u);
-            const Buf part = make_buf(ly.part, (uint32_t)ly.P * D * 4u);
+            WB b0 = b_load(tb, ib0 < ib1 ? ib0 : -1, wave, lane);
+            const Buf part = make_buf(ly.part, (uint32_t)ly.P * D * 8u);
             int cur = -1;   /* expert whose q8 hidden rows hl holds */
+            bool bok = true;
             pipe(
                 ib0, ib1, b0, [&](int i) { return b_load(tb, i, wave, lane); },
                 [&](int i, const WB &) {
                     const int s = ufl(i) / B_TILES;
                     if (s != cur) {
                         bar_lds();   /* every wave is done with the previous rows */
-                        b_hidden_q8(ufl(tb.ex[s].p0), ufl(tb.ex[s].np), hid, hl, wave, lane);
+                        const bool got =
+                            b_hidden_q8(ufl(tb.ex[s].p0), ufl(tb.ex[s].np), hid, tag, abort_flag, hl, wave, lane);
+                        if (!got) s_ok = 0;   /* every wave that gave up says so */
                         bar_lds();
+                        bok &= s_ok != 0;
                         cur = s;
                     }
                 },
-                [&](int i, const WB &w) { b_compute(tb, i, w, hl, part, wave, lane); });
+                [&](int i, const WB &w) { b_compute(tb, i, w, hl, part, tag, wave, lane); });
+            if (!bok) {
+                ok = false;
+                break;
+            }
         }
         if (tw) tr[3] = wall_clock64();
-        bar_arrive(flags, ++tag);
-        if (!bar_wait(flags, tag, abort_flag, &s_ok)) {
-            ok = false;
-            break;
-        }
-        if (tw) tr[4] = wall_clock64();
         /* ---- C ---- */
         const bool more = l + 1 < L;
-        if (wg < k)
-            phase_c(&ly, &tb, more ? &layers[l + 1] : nullptr, wg, h, eps, red,
-                    debug && more ? debug + (size_t)(l + 1) * ly.rec_bytes : nullptr, wave, lane);
+        if (wg < k) {
+            if (threadIdx.x == 0) s_okc = 1;
+            bar_lds();
+            const bool got = phase_c(&ly, &tb, more ? &layers[l + 1] : nullptr, wg, h, eps, red,
+                                     debug && more ? debug + (size_t)(l + 1) * ly.rec_bytes : nullptr, tag,
+                                     abort_flag, wave, lane);
+            if (!got) s_okc = 0;
+            bar_lds();
+            if (s_okc == 0) {
+                ok = false;
+                break;
+            }
+            if (more) x_publish(layers[l + 1], wg, tag + 1u);
+        }
         if (tw) tr[5] = wall_clock64();
         if (!more) break;
-        bar_arrive(flags, ++tag);
         {
             /* the next layer's table, then its first gate/up item in flight
-             * across the barrier */
+             * while the rows of x are awaited */
             const RowsLayer &nl = layers[l + 1];
             tab_load(nl, tabs[(l + 1) & 1]);
             bar_lds();
@@ -460,15 +513,15 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
             const int i0 = nl.split[wg], i1 = nl.split[wg + 1];
             a0 = a_load(nt, i0 < i1 ? i0 : -1, wave, lane);
         }
-        if (!bar_wait(flags, tag, abort_flag, &s_ok)) {
-            ok = false;
-            break;
-        }
-        if (tw) tr[6] = wall_clock64();
     }
     wait_copies();
-    if (wg == 0 && threadIdx.x == 0)
-        __hip_atomic_store(sync + 1, base + 3u * (unsigned)L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    /* the last workgroup to finish advances the launch epoch by L (every
+     * workgroup read it before taking its ticket) and clears the ticket word */
+    if (threadIdx.x == 0 &&
+        __hip_atomic_fetch_add(sync + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1) {
+        __hip_atomic_store(sync + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sync + 1, base + (unsigned)L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 }  // namespace
