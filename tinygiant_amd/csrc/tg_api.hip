@@ -1692,9 +1692,9 @@ static bool persistent_ok(tg_hip_decode *d, std::vector<DecodeLayer> &out) {
 /* The multi-row kernel covers steps of k = 2..ROWS_MAXK rows of the Qwen
  * expert shape (up to ROWS_MAXE active experts and ROWS_MAXP pairs per
  * layer).  It builds the kernel's layer table and its buffers, each layer's
- * its own: row flags [L][ROWS_MAXK] | q8 rows of x [L][ROWS_MAXK] | item
- * ranges [L][2][ROWS_GRID + 1] | the layers' expert and pair tables | tagged
- * hidden words [P_l][I] | tagged partials [P_l][D]. */
+ * its own: tagged q8 rows of x [L][ROWS_MAXK][2 XS] | item ranges
+ * [L][2][ROWS_GRID + 1] | the layers' expert and pair tables | tagged hidden
+ * words [P_l][I] | tagged partials [P_l][D]. */
 static bool persistent_rows_create(tg_hip_decode *d) {
     const DecodeShape sh = decode_qwen_shape();
     if (d->k < 2 || d->k > ROWS_MAXK) {
@@ -1734,8 +1734,7 @@ static bool persistent_rows_create(tg_hip_decode *d) {
     const size_t XS = q8_lds_stride(sh.D / 256), NS = 2 * (ROWS_GRID + 1);
     size_t words = 0;   /* tagged hidden and partial words of all layers */
     for (int l = 0; l < d->L; l++) words += (size_t)d->plans[l]->h.P * (sh.I + sh.D);
-    const size_t o_xq = ((size_t)d->L * ROWS_MAXK * 4 + 255) & ~(size_t)255,
-                 o_split = o_xq + (size_t)d->L * ROWS_MAXK * XS,
+    const size_t o_xq = 0, o_split = o_xq + (size_t)d->L * ROWS_MAXK * 2 * XS,
                  o_tab = (o_split + (size_t)d->L * NS * 4 + 255) & ~(size_t)255,
                  o_words = o_tab + (size_t)d->L * ROWS_TAB_BYTES, total = o_words + words * 8;
     HIPCHECK(hipMalloc(&d->hidden, total));
@@ -1762,7 +1761,7 @@ static bool persistent_rows_create(tg_hip_decode *d) {
         memcpy(tab.data() + n_act * 32 + (size_t)h.P * 8 + (size_t)(h.k + 1) * 4, h.r_pair.data(), (size_t)h.P * 4);
         const size_t tb = (n_act * 32 + (size_t)h.P * 12 + (size_t)(h.k + 1) * 4 + 15) & ~(size_t)15;
         HIPCHECK(hipMemcpy(base + o_tab + (size_t)l * ROWS_TAB_BYTES, tab.data(), tb, hipMemcpyHostToDevice));
-        decode_rows_split(np.data(), (int)n_act, splits.data() + (size_t)l * NS);
+        decode_rows_split(np.data(), (int)n_act, d->k, splits.data() + (size_t)l * NS);
         RowsLayer &r = ls[l];
         memset(&r, 0, sizeof r);
         r.tab = base + o_tab + (size_t)l * ROWS_TAB_BYTES;
@@ -1772,8 +1771,7 @@ static bool persistent_rows_create(tg_hip_decode *d) {
         r.hidden = wp;
         r.part = wp + (size_t)h.P * sh.I;
         wp += (size_t)h.P * (sh.I + sh.D);
-        r.xq = base + o_xq + (size_t)l * ROWS_MAXK * XS;
-        r.xflag = (unsigned *)base + (size_t)l * ROWS_MAXK;
+        r.xq = base + o_xq + (size_t)l * ROWS_MAXK * 2 * XS;
         r.n_act = (int)np.size();
         r.P = h.P;
         r.k = d->k;

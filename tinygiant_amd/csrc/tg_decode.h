@@ -103,8 +103,9 @@ hipError_t launch_q6k_row_groups(const void *src, void *dst, int nrows, int nb, 
  * plan's per-row pair lists, the layer's own exchange buffers, and the
  * workgroups' item ranges: split[w] .. split[w + 1] of the gate/up items
  * (expert-major, 16 rows each) and split[ROWS_GRID + 1 + w] .. of the down
- * items (64 rows each).  Hidden values and partials are 8-byte words {tag,
- * f32 value}; the tag of layer l in a launch is epoch + l + 1. */
+ * items (64 rows each).  Hidden values, partials and the 4-byte units of x
+ * are 8-byte words {tag, value}; the tag of layer l in a launch is epoch +
+ * l + 1. */
 constexpr int ROWS_MAXK = 16;
 constexpr int ROWS_GRID = 256;
 constexpr int ROWS_MAXE = 128;    /* active experts of a layer */
@@ -122,16 +123,16 @@ struct RowsLayer {
     const int *split;
     const float *norm_w;          /* RMSNorm weight before this layer, null = 1 */
     uint64_t *hidden, *part;      /* [P][I], [P][D] tagged words */
-    uint8_t *xq;                  /* [k] q8 rows of x in the LDS image layout */
-    unsigned *xflag;              /* [ROWS_MAXK] row r of xq is complete when word r holds the tag */
+    uint8_t *xq;                  /* [k] q8 rows of x, the LDS image as tagged 4-byte units (2 XS bytes a row) */
     int n_act, P, k, rec_bytes;   /* rec_bytes: debug record of a layer */
     int tab_bytes, pad;
 };
 static_assert(sizeof(RowsExp) == 32, "table layout");
 /* Per-layer debug record: h_in f32[k][D] | x f32[k][D] | hidden f32[Pmax][I] */
 int decode_rows_max_grid();
-/* the item ranges of one layer from each active expert's pair count */
-void decode_rows_split(const int *np, int n_act, int *split /* [2 (ROWS_GRID + 1)] */);
+/* the item ranges of one layer from each active expert's pair count; the
+ * down items go to workgroups c .. ROWS_GRID - 1 (c: the rows combined) */
+void decode_rows_split(const int *np, int n_act, int c, int *split /* [2 (ROWS_GRID + 1)] */);
 hipError_t launch_decode_rows(const RowsLayer *layers_dev, int L, float *h_dev, unsigned *sync_dev, float eps,
                               uint8_t *debug_dev, uint64_t *times_dev, unsigned *place_dev, bool cooperative,
                               hipStream_t st);

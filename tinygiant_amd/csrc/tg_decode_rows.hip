@@ -13,15 +13,15 @@
  *      rows are there: their q8 into LDS, then w_pair * dot for every pair
  *      -> part[pair]
  *   C  workgroup r < k, row r, once its partials are there: h_r += them in
- *      expert order (k_moe_combine); x_r = RMSNorm(h_r) * w_{l+1}; q8(x_r);
- *      then row r's flag for layer l + 1
+ *      expert order (k_moe_combine); x_r = RMSNorm(h_r) * w_{l+1}; q8(x_r)
  *
  * No barrier separates the phases: every value one workgroup writes and
  * another reads sits in a buffer of its layer as an 8-byte word {tag, value}
- * (the q8 rows of x: behind a per-row flag word), the tag being the layer's
- * in this launch, and the reader polls the words it needs until their tags
- * match.  A workgroup thus waits only for what it reads: a down item for its
- * expert's hidden rows, a row's combine for the row's partials.
+ * (hidden values, partials, the 4-byte units of the q8 rows of x), the tag
+ * being the layer's in this launch, and the reader polls the words it needs until their tags
+ * match (a lane reloads only the words whose tags did not).  A workgroup
+ * thus waits only for what it reads: a down item for its expert's hidden
+ * rows, a row's combine for the row's partials.
  *
  * Each workgroup takes a contiguous range of the layer's A items and one of
  * its B items (split on the host by an estimate of each item's time) and
@@ -190,29 +190,46 @@ __device__ inline void a_compute(const Tab &tb, int item, const WA &w, const uin
     }
 }
 
+/* tags of a loaded 16-byte unit: two tagged words */
+__device__ inline bool tagged(const u32x4 &v, unsigned tag) { return v.x == tag && v.z == tag; }
+
 /* q8 of the expert's hidden rows into LDS slots 0..np-1, one 256-block per
  * wave (q8_quant_rows_lds's arithmetic), once every value carries the
- * layer's tag; false if the wait ran out */
+ * layer's tag: a lane reloads only the units whose tags did not match; false
+ * if the wait ran out */
 __device__ inline bool b_hidden_q8(int p0, int np, Buf hid, unsigned tag, unsigned *abort_flag, uint8_t *hl, int wave,
                                    int lane) {
     constexpr int BATCH = 4;
     const int nblk = np * NBH;
     for (int u0 = wave; u0 < nblk; u0 += NWV * BATCH) {
         u32x4 raw[BATCH][2];
+        uint32_t off[BATCH];
+        bool got[BATCH];
+#pragma unroll
+        for (int i = 0; i < BATCH; i++) {
+            const int u = u0 + i * NWV;
+            const int s = u / NBH, b = u % NBH;
+            off[i] = u < nblk ? (uint32_t)((p0 + s) * I + b * 256 + 4 * lane) * 8u : OOB;
+            raw[i][0] = ld1x4(hid, off[i]);
+            raw[i][1] = ld1x4(hid, off[i] == OOB ? OOB : off[i] + 16u);
+            got[i] = u >= nblk;
+        }
         unsigned spins = 0;
         while (true) {
             bool in = true;
 #pragma unroll
             for (int i = 0; i < BATCH; i++) {
-                const int u = u0 + i * NWV;
-                const int s = u / NBH, b = u % NBH;
-                const uint32_t w0 = u < nblk ? (uint32_t)((p0 + s) * I + b * 256 + 4 * lane) * 8u : OOB;
-                raw[i][0] = ld1x4(hid, w0);
-                raw[i][1] = ld1x4(hid, w0 == OOB ? OOB : w0 + 16u);
-                in &= u >= nblk || (raw[i][0].x == tag && raw[i][0].z == tag && raw[i][1].x == tag && raw[i][1].z == tag);
+                got[i] = got[i] || (tagged(raw[i][0], tag) && tagged(raw[i][1], tag));
+                in &= got[i];
             }
             if (__ballot(!in) == 0) break;
             if (!poll_more(spins, abort_flag)) return false;
+#pragma unroll
+            for (int i = 0; i < BATCH; i++)
+                if (!got[i]) {
+                    raw[i][0] = ld1x4(hid, off[i]);
+                    raw[i][1] = ld1x4(hid, off[i] + 16u);
+                }
         }
 #pragma unroll
         for (int i = 0; i < BATCH; i++) {
@@ -283,33 +300,56 @@ __device__ inline void pipe(int i0, int i1, W s0, Load load, Pre pre, Comp comp)
 /* Phase C for workgroup r < k: layer ly's combine of row r (ly non-null),
  * then the RMSNorm (weight nx->norm_w) and q8 of the row for layer nx (when
  * non-null), thread t owning values 4t .. 4t+3 as k_rms_norm_q8's lane t % 64
- * of wave t / 64 does.  False if a wait for a partial ran out. */
+ * of wave t / 64 does.  The q8 row goes out as tagged words: byte o of row
+ * r's LDS image is the value half of the word at byte 2 o of row r's 2 XS
+ * bytes.  False if a wait for a partial ran out. */
+__device__ inline void st_x(Buf xb, uint32_t o, unsigned tag, uint32_t v) {
+    u32x2 w;
+    w.x = tag;
+    w.y = v;
+    __builtin_amdgcn_raw_buffer_store_b64(w, xb.r, (int)(2u * o), 0, CPOL_SC1);
+}
 __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLayer *nx, int r, float *h, float eps,
-                               float *red, uint8_t *rec_next, unsigned tag, unsigned *abort_flag, int wave, int lane) {
+                               float *red, uint8_t *rec_next, unsigned tag, unsigned next_tag, unsigned *abort_flag,
+                               int wave, int lane) {
     const int t = threadIdx.x;
     const Buf hb = make_buf(h + (size_t)r * D, D * 4u);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0): the previous layer's store of these values is done */
     const u32x4 hv = ld1x4(hb, (uint32_t)t * 16u);
     float o[4] = {__uint_as_float(hv.x), __uint_as_float(hv.y), __uint_as_float(hv.z), __uint_as_float(hv.w)};
     bool good = true;   /* a wave whose wait ran out goes on (the barriers below count every wave) */
     if (ly) {
-        /* row r's partials, eight pairs at a time, each word polled until
-         * it carries the layer's tag; added in expert order */
+        /* row r's partials, up to eight pairs at a time; a lane reloads only
+         * the units whose tags did not match; added in expert order */
         const Buf pb = make_buf(ly->part, (uint32_t)ly->P * D * 8u);
         const int q0 = ufl(tb->roff[r]), q1 = ufl(tb->roff[r + 1]);
         for (int qb = q0; qb < q1; qb += 8) {
             u32x4 v[8][2];
+            uint32_t off[8];
+            bool got[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                off[i] = qb + i < q1 ? (uint32_t)(ufl(tb->rpair[qb + i]) * D + 4 * t) * 8u : OOB;
+                v[i][0] = ld1x4(pb, off[i]);
+                v[i][1] = ld1x4(pb, off[i] == OOB ? OOB : off[i] + 16u);
+                got[i] = qb + i >= q1;
+            }
             unsigned spins = 0;
             while (good) {
                 bool in = true;
 #pragma unroll
                 for (int i = 0; i < 8; i++) {
-                    const uint32_t w0 = qb + i < q1 ? (uint32_t)(ufl(tb->rpair[qb + i]) * D + 4 * t) * 8u : OOB;
-                    v[i][0] = ld1x4(pb, w0);
-                    v[i][1] = ld1x4(pb, w0 == OOB ? OOB : w0 + 16u);
-                    in &= qb + i >= q1 || (v[i][0].x == tag && v[i][0].z == tag && v[i][1].x == tag && v[i][1].z == tag);
+                    got[i] = got[i] || (tagged(v[i][0], tag) && tagged(v[i][1], tag));
+                    in &= got[i];
                 }
                 if (__ballot(!in) == 0) break;
                 good = poll_more(spins, abort_flag);
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    if (!got[i]) {
+                        v[i][0] = ld1x4(pb, off[i]);
+                        v[i][1] = ld1x4(pb, off[i] + 16u);
+                    }
             }
 #pragma unroll
             for (int i = 0; i < 8; i++)
@@ -345,43 +385,57 @@ __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
     for (int c = 0; c < 4; c++) x[c] = (o[c] * scale) * (w ? w[4 * t + c] : 1.f);
     if (rec_next)
         reinterpret_cast<float4 *>(rec_next + (size_t)(nx->k + r) * D * 4)[t] = make_float4(x[0], x[1], x[2], x[3]);
-    /* q8 of block `wave` into row r's LDS image in global memory */
+    /* q8 of block `wave` into row r's tagged image */
     const Q8Quant q = q8_block_quant_dpp(x[0], x[1], x[2], x[3]);
-    const Buf xb = make_buf(nx->xq + (size_t)r * XS, XS);
+    const Buf xb = make_buf(nx->xq + (size_t)r * 2 * XS, 2 * XS);
     const int b = wave;
-    st1(xb, (uint32_t)(b * 256 + 4 * lane), q.packed);
-    if ((lane & 3) == 0) st1(xb, (uint32_t)(NBX * 288 + (b * 16 + (lane >> 2)) * 4), (uint32_t)q.s16);
-    if ((lane & 7) == 0) st1(xb, (uint32_t)(NBX * 256 + (b * 8 + (lane >> 3)) * 4), (uint32_t)q.s32);
-    if (lane == 0) st1(xb, (uint32_t)(NBX * 352 + b * 4), q.sc);
+    st_x(xb, (uint32_t)(b * 256 + 4 * lane), next_tag, q.packed);
+    if ((lane & 3) == 0) st_x(xb, (uint32_t)(NBX * 288 + (b * 16 + (lane >> 2)) * 4), next_tag, (uint32_t)q.s16);
+    if ((lane & 7) == 0) st_x(xb, (uint32_t)(NBX * 256 + (b * 8 + (lane >> 3)) * 4), next_tag, (uint32_t)q.s32);
+    if (lane == 0) st_x(xb, (uint32_t)(NBX * 352 + b * 4), next_tag, __float_as_uint(q.sc));
     return good;
 }
 
-/* row r of layer ly's x is complete: every wave's stores have completed,
- * then its flag takes the layer's tag */
-__device__ inline void x_publish(const RowsLayer &ly, int r, unsigned tag) {
-    __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0) */
-    bar_lds();
-    if (threadIdx.x == 0) st1(make_buf(ly.xflag, ROWS_MAXK * 4u), (uint32_t)r * 4u, tag);
-}
-/* wave 0 polls the k row flags of layer ly; false if the wait ran out */
-__device__ inline bool x_wait(const RowsLayer &ly, int k, unsigned tag, unsigned *abort_flag, int *s_ok) {
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        const Buf fb = make_buf(ly.xflag, ROWS_MAXK * 4u);
-        unsigned spins = 0;
-        int ok = 1;
-        while (true) {
-            const uint32_t f = lane < k ? __builtin_amdgcn_raw_buffer_load_b32(fb.r, lane * 4, 0, CPOL_SC1) : tag;
-            if (__ballot(f != tag) == 0) break;
-            if (!poll_more(spins, abort_flag)) {
-                ok = 0;
-                break;
-            }
-        }
-        if (lane == 0) *s_ok = ok;
+/* the k tagged q8 rows of layer ly's x into LDS, each wave polling its own
+ * units (a lane reloads only those whose tags did not match); false in the
+ * waves whose wait ran out */
+__device__ inline bool x_load(const RowsLayer &ly, int k, unsigned tag, unsigned *abort_flag, uint8_t *xl) {
+    constexpr int XU = (ROWS_MAXK * (XS / 8) + NT - 1) / NT;   /* 16-byte units (2 tagged words) a thread */
+    const uint32_t nu = (uint32_t)k * (XS / 8);
+    const Buf xg = make_buf(ly.xq, nu * 16u);
+    u32x4 v[XU];
+    bool got[XU];
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+        const uint32_t m = threadIdx.x + i * NT;
+        v[i] = ld1x4(xg, m < nu ? m * 16u : OOB);
+        got[i] = m >= nu;
     }
-    bar_lds();
-    return *s_ok != 0;
+    unsigned spins = 0;
+    while (true) {
+        bool in = true;
+#pragma unroll
+        for (int i = 0; i < XU; i++) {
+            got[i] = got[i] || tagged(v[i], tag);
+            in &= got[i];
+        }
+        if (__ballot(!in) == 0) break;
+        if (!poll_more(spins, abort_flag)) return false;
+#pragma unroll
+        for (int i = 0; i < XU; i++)
+            if (!got[i]) v[i] = ld1x4(xg, (threadIdx.x + i * NT) * 16u);
+    }
+#pragma unroll
+    for (int i = 0; i < XU; i++) {
+        const uint32_t m = threadIdx.x + i * NT;
+        if (m < nu) {
+            u32x2 w;
+            w.x = v[i].y;
+            w.y = v[i].w;
+            *reinterpret_cast<u32x2 *>(xl + 8 * m) = w;
+        }
+    }
+    return true;
 }
 
 __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict__ layers, int L, float *h,
@@ -394,10 +448,13 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     __shared__ __attribute__((aligned(16))) uint8_t tabs[2][ROWS_TAB_BYTES];   /* layer tables, by parity */
     __shared__ float red[NWV];
     __shared__ unsigned s_base;
-    __shared__ int s_ok, s_okc;   /* a wait ran out: x and B waits; C waits */
+    /* a wait ran out, one word per kind of wait (x, B, C): each only goes
+     * from 1 to 0, and is read after the barrier that follows its writes */
+    __shared__ int s_okx, s_okb, s_okc;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, wg = blockIdx.x;
     unsigned *abort_flag = sync;
     if (threadIdx.x == 0) {
+        s_okx = s_okb = s_okc = 1;
         s_base = read_epoch(sync);
         if (place) {
             unsigned xcc;
@@ -412,10 +469,7 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     bool ok = true;
 
     /* C(-1): the first layer's RMSNorm and q8 */
-    if (wg < k) {
-        phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, 0u, abort_flag, wave, lane);
-        x_publish(layers[0], wg, base + 1u);
-    }
+    if (wg < k) phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, 0u, base + 1u, abort_flag, wave, lane);
     WA a0;
     {
         const RowsLayer &ly = layers[0];
@@ -436,21 +490,12 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
         const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 8u);
         /* ---- A ---- */
         {
-            if (!x_wait(ly, k, tag, abort_flag, &s_ok)) {
+            if (!x_load(ly, k, tag, abort_flag, xl)) s_okx = 0;
+            bar_lds();
+            if (s_okx == 0) {
                 ok = false;
                 break;
             }
-            /* the k q8 rows of x, every load in flight at once */
-            constexpr int XU = ROWS_MAXK * (XS / 16) / NT + 1;
-            const uint32_t nu = (uint32_t)k * (XS / 16);
-            const Buf xg = make_buf(ly.xq, nu * 16u);
-            u32x4 v[XU];
-#pragma unroll
-            for (int i = 0; i < XU; i++) v[i] = ld1x4(xg, (threadIdx.x + i * NT) * 16u);
-#pragma unroll
-            for (int i = 0; i < XU; i++)
-                if (threadIdx.x + i * NT < nu) *reinterpret_cast<u32x4 *>(xl + 16 * (threadIdx.x + i * NT)) = v[i];
-            bar_lds();
             if (tw) tr[0] = wall_clock64();
             float *dh = rec ? reinterpret_cast<float *>(rec + (size_t)2 * k * D * 4) : nullptr;
             pipe(
@@ -472,9 +517,10 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
                         bar_lds();   /* every wave is done with the previous rows */
                         const bool got =
                             b_hidden_q8(ufl(tb.ex[s].p0), ufl(tb.ex[s].np), hid, tag, abort_flag, hl, wave, lane);
-                        if (!got) s_ok = 0;   /* every wave that gave up says so */
+                        if (!got) s_okb = 0;   /* every wave that gave up says so */
                         bar_lds();
-                        bok &= s_ok != 0;
+                        bok &= s_okb != 0;
+                        if (tw && cur < 0) tr[2] = wall_clock64();
                         cur = s;
                     }
                 },
@@ -488,18 +534,16 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
         /* ---- C ---- */
         const bool more = l + 1 < L;
         if (wg < k) {
-            if (threadIdx.x == 0) s_okc = 1;
-            bar_lds();
             const bool got = phase_c(&ly, &tb, more ? &layers[l + 1] : nullptr, wg, h, eps, red,
-                                     debug && more ? debug + (size_t)(l + 1) * ly.rec_bytes : nullptr, tag,
+                                     debug && more ? debug + (size_t)(l + 1) * ly.rec_bytes : nullptr, tag, tag + 1u,
                                      abort_flag, wave, lane);
             if (!got) s_okc = 0;
+            if (tw) tr[4] = wall_clock64();
             bar_lds();
             if (s_okc == 0) {
                 ok = false;
                 break;
             }
-            if (more) x_publish(layers[l + 1], wg, tag + 1u);
         }
         if (tw) tr[5] = wall_clock64();
         if (!more) break;
@@ -558,59 +602,63 @@ int decode_rows_threads() { return NT; }
  * expert would first wait a memory round trip for that expert's hidden rows.
  * Cost of an item, relative, from per-workgroup phase times of 48-layer
  * steps: its weight bytes (36,864 B an A item, 40,320 B a B item) count 1,
- * each pair of its expert 0.33. */
-void decode_rows_split(const int *np, int n_act, int *split) {
-    for (int ph = 0; ph < 2; ph++) {
-        const int tiles = ph == 0 ? A_TILES : B_TILES;
-        int *s = split + ph * (ROWS_GRID + 1);
-        std::vector<int> wgs(n_act, 0);
-        if (n_act > 0) {
-            double total = 0;
-            for (int e = 0; e < n_act; e++) total += 1.0 + 0.33 * np[e];
-            std::vector<std::pair<double, int>> rem;
-            int used = 0;
-            for (int e = 0; e < n_act; e++) {
-                const double share = ROWS_GRID * (1.0 + 0.33 * np[e]) / total;
-                wgs[e] = std::min(tiles, std::max(1, (int)share));
-                used += wgs[e];
-                rem.push_back({share - (int)share, e});
+ * each pair of its expert 0.33.  The down items skip workgroups 0 .. c - 1,
+ * which combine the rows: they start a row's combine as soon as its last
+ * partial lands. */
+static void split_phase(const int *np, int n_act, int tiles, int w0, int *s) {
+    const int G = ROWS_GRID - w0;
+    std::vector<int> wgs(n_act, 0);
+    if (n_act > 0) {
+        double total = 0;
+        for (int e = 0; e < n_act; e++) total += 1.0 + 0.33 * np[e];
+        std::vector<std::pair<double, int>> rem;
+        int used = 0;
+        for (int e = 0; e < n_act; e++) {
+            const double share = G * (1.0 + 0.33 * np[e]) / total;
+            wgs[e] = std::min(tiles, std::max(1, (int)share));
+            used += wgs[e];
+            rem.push_back({share - (int)share, e});
+        }
+        std::sort(rem.begin(), rem.end(), [](const std::pair<double, int> &a, const std::pair<double, int> &b) {
+            return a.first > b.first || (a.first == b.first && a.second < b.second);
+        });
+        /* hand out what is left by remainder, then round robin while some
+         * expert can still take a workgroup */
+        for (size_t i = 0; used < G && i < rem.size(); i++)
+            if (wgs[rem[i].second] < tiles) {
+                wgs[rem[i].second]++;
+                used++;
             }
-            std::sort(rem.begin(), rem.end(), [](const std::pair<double, int> &a, const std::pair<double, int> &b) {
-                return a.first > b.first || (a.first == b.first && a.second < b.second);
-            });
-            /* hand out what is left by remainder, then round robin while
-             * some expert can still take a workgroup */
-            for (size_t i = 0; used < ROWS_GRID && i < rem.size(); i++)
-                if (wgs[rem[i].second] < tiles) {
-                    wgs[rem[i].second]++;
+        for (bool more = true; used < G && more;) {
+            more = false;
+            for (int e = 0; e < n_act && used < G; e++)
+                if (wgs[e] < tiles) {
+                    wgs[e]++;
                     used++;
+                    more = true;
                 }
-            for (bool more = true; used < ROWS_GRID && more;) {
-                more = false;
-                for (int e = 0; e < n_act && used < ROWS_GRID; e++)
-                    if (wgs[e] < tiles) {
-                        wgs[e]++;
-                        used++;
-                        more = true;
-                    }
-            }
-            while (used > ROWS_GRID) {   /* more experts than workgroups would need this; take from the largest */
-                int e = (int)(std::max_element(wgs.begin(), wgs.end()) - wgs.begin());
-                if (wgs[e] <= 1) break;
-                wgs[e]--;
-                used--;
-            }
         }
-        int w = 0;
-        s[0] = 0;
-        for (int e = 0; e < n_act; e++)
-            for (int j = 0; j < wgs[e] && w < ROWS_GRID; j++) s[++w] = e * tiles + (int)((int64_t)tiles * (j + 1) / wgs[e]);
-        while (w < ROWS_GRID) {
-            s[w + 1] = s[w];
-            w++;
+        while (used > G) {   /* more experts than workgroups would need this; take from the largest */
+            int e = (int)(std::max_element(wgs.begin(), wgs.end()) - wgs.begin());
+            if (wgs[e] <= 1) break;
+            wgs[e]--;
+            used--;
         }
-        s[ROWS_GRID] = n_act * tiles;
     }
+    int w = w0;
+    for (int i = 0; i <= w0; i++) s[i] = 0;
+    for (int e = 0; e < n_act; e++)
+        for (int j = 0; j < wgs[e] && w < ROWS_GRID; j++) s[++w] = e * tiles + (int)((int64_t)tiles * (j + 1) / wgs[e]);
+    while (w < ROWS_GRID) {
+        s[w + 1] = s[w];
+        w++;
+    }
+    s[ROWS_GRID] = n_act * tiles;
+}
+
+void decode_rows_split(const int *np, int n_act, int c, int *split) {
+    split_phase(np, n_act, A_TILES, 0, split);
+    split_phase(np, n_act, B_TILES, c, split + ROWS_GRID + 1);
 }
 
 }  // namespace tg
