@@ -534,6 +534,9 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
         d.down_fmt = h.down_fmt[e];
         for (int s = 0; s < std::min(d.np, EXP_ROWS); s++) d.row[s] = h.p_row[d.p0 + s];
     }
+    /* the busiest experts first: their workgroups (the most passes) start
+     * first instead of trailing the launch */
+    std::stable_sort(ed.begin(), ed.end(), [](const ExpDesc &x, const ExpDesc &y) { return x.np > y.np; });
     a.ed = (const ExpDesc *)put(ed.data(), ed.size() * sizeof(ExpDesc));
     act_a.insert(act_a.end(), act_b.begin(), act_b.end());
     a.mx_act = (const int *)put(act_a.data(), act_a.size() * 4);

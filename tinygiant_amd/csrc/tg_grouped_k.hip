@@ -61,6 +61,11 @@ constexpr int NT = 64 * NW;
 constexpr uint32_t OOB = 0x80000000u;    /* past every buffer: the load reads zero */
 constexpr uint32_t Q4B = 144, Q6B = 210; /* bytes per 256-value block */
 constexpr uint32_t Q6S = 224;            /* LDS stride of a staged Q6_K block */
+/* A wave's q8 operands of a pass are loaded at once: QA_WB Q4_K blocks of a
+ * gate/up row (D <= 256 NW QA_WB), QB_WH Q6_K half-blocks of a down row
+ * (I <= 128 NW QB_WH).  Each kernel comes in a form for Qwen3's 8 blocks of D
+ * and 6 half-blocks of I (fewer registers) and one for longer rows. */
+constexpr int QA_WB_MAX = 3, QB_WH_MAX = 5;
 
 __device__ inline long as_long(u32x2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
 
@@ -120,6 +125,7 @@ __device__ inline void copy_lanes_nt(const u32x4 &desc, uint32_t voff, uint32_t 
  * a.ed[blockIdx.y]; Q4_K gate and up matrices of D = 256 nb columns.  The
  * slabs arrive by direct-to-LDS copies, while the first pass's q8 operands
  * load into registers. */
+template <int QA_WB>
 __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const ExpDesc &ex = a.ed[blockIdx.y];
@@ -152,31 +158,39 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     const float *gbias = a.gbias ? (const float *)(uintptr_t)a.gbias[e] : nullptr;
     const float *ubias = a.ubias ? (const float *)(uintptr_t)a.ubias[e] : nullptr;
 
-    /* pair c16's q8 operands of block b: sub-block s = 2 jg + half covers
-     * x[64 jg + 32 half ...], this lane's K slice 8 g .. 8 g + 7 */
-    long xb[8];
-    float bsg0, bsg1;   /* the pair's 32-value sums of sub-blocks g and 4 + g */
-    float xd;
-    auto load_x = [&](uint32_t prow, bool pv, int b) {
-        const uint32_t qb = prow * (uint32_t)nb + (uint32_t)b;
+    /* pair c16's q8 operands of the wave's blocks b = w + NW i of a pass,
+     * all loaded at once: sub-block s = 2 jg + half covers x[64 jg + 32 half
+     * ...], this lane's K slice 8 g .. 8 g + 7 */
+    long xb[QA_WB][8];
+    float bsg0[QA_WB], bsg1[QA_WB];   /* the pair's 32-value sums of sub-blocks g and 4 + g */
+    float xd[QA_WB];
+    auto load_x = [&](uint32_t prow, bool pv) {
 #pragma unroll
-        for (int s = 0; s < 8; s++)
-            xb[s] = as_long(ld8(qs_b, pv ? qb * 256u + 64u * (s >> 1) + 32u * (s & 1) + 8u * g : OOB));
-        bsg0 = (float)(int)ld4(s32_b, pv ? qb * 32u + 4u * g : OOB);
-        bsg1 = (float)(int)ld4(s32_b, pv ? qb * 32u + 16u + 4u * g : OOB);
-        xd = __uint_as_float(ld4(d_b, pv ? qb * 4u : OOB));
+        for (int i = 0; i < QA_WB; i++) {
+            const int b = w + NW * i;
+            const bool v = pv && b < nb;
+            const uint32_t qb = prow * (uint32_t)nb + (uint32_t)b;
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                xb[i][s] = as_long(ld8(qs_b, v ? qb * 256u + 64u * (s >> 1) + 32u * (s & 1) + 8u * g : OOB));
+            bsg0[i] = (float)(int)ld4(s32_b, v ? qb * 32u + 4u * g : OOB);
+            bsg1[i] = (float)(int)ld4(s32_b, v ? qb * 32u + 16u + 4u * g : OOB);
+            xd[i] = __uint_as_float(ld4(d_b, v ? qb * 4u : OOB));
+        }
     };
     int t0 = 0;
     bool pv = c16 < np;
     uint32_t prow = pv ? ld4(prow_b, (uint32_t)(p0 + c16) * 4u) : 0u;
-    if (w < nb) load_x(prow, pv, w);
+    load_x(prow, pv);
     wait_copies();
     __syncthreads();
 
     for (;;) {
         float acc[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        for (int b = w; b < nb; b += NW) {
-            if (b != w) load_x(prow, pv, b);
+#pragma unroll
+        for (int i = 0; i < QA_WB; i++) {
+            const int b = w + NW * i;
+            if (b >= nb) break;   /* uniform per wave */
 #pragma unroll 1
             for (int m = 0; m < 2; m++) {
                 const uint8_t *sb = lds + m * sreg;
@@ -188,8 +202,8 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
                  * lane group; products and sums are integers below 2^24, exact) */
                 const Q4Hdr hr = q4_hdr(*(const u32x4 *)(sb + c16 * rs + b * Q4B));
                 v4f im = {0.f, 0.f, 0.f, 0.f};
-                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnl, g), bsg0, im, 0, 0, 0);
-                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnh, g), bsg1, im, 0, 0, 0);
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnl, g), bsg0[i], im, 0, 0, 0);
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnh, g), bsg1[i], im, 0, 0, 0);
                 /* the scale terms sum_s sc[row][s] idot[row][pair][s]: one int8
                  * MFMA per sub-block, summed exactly in int32 */
                 const uint8_t *ab = sb + c16 * rs + b * Q4B + 16 + 8 * g;   /* row c16's codes */
@@ -202,8 +216,8 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
                     lo.y = qq.y & 0x0F0F0F0Fu;
                     hi.x = (qq.x >> 4) & 0x0F0F0F0Fu;
                     hi.y = (qq.y >> 4) & 0x0F0F0F0Fu;
-                    const v4i dl = mma(as_long(lo), xb[2 * jg]);
-                    const v4i dh = mma(as_long(hi), xb[2 * jg + 1]);
+                    const v4i dl = mma(as_long(lo), xb[i][2 * jg]);
+                    const v4i dh = mma(as_long(hi), xb[i][2 * jg + 1]);
 #pragma unroll
                     for (int v = 0; v < 4; v++) {
                         const uint32_t scw = jg < 2 ? hd[v].scl : hd[v].sch;
@@ -214,7 +228,7 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     /* acc indexed with constants only (m is a loop variable) */
-                    const float t = xd * (hd[v].d * (float)isc[v] - hd[v].dmin * im[v]);
+                    const float t = xd[i] * (hd[v].d * (float)isc[v] - hd[v].dmin * im[v]);
                     if (m == 0) acc[0][v] += t;
                     else acc[1][v] += t;
                 }
@@ -230,7 +244,7 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
         if (t1 < np) {
             pv = t1 + c16 < np;
             prow = pv ? ld4(prow_b, (uint32_t)(p0 + t1 + c16) * 4u) : 0u;
-            if (w < nb) load_x(prow, pv, w);
+            load_x(prow, pv);
         }
         __syncthreads();
         if (tid < 256) {
@@ -260,6 +274,7 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
  * first pass's q8 operands, then the slab is stored to LDS. */
 constexpr int QB_PIECES = 13;   /* 16-byte pieces of a block's bytes 0-207 */
 constexpr int QB_NPC = 2;       /* pieces per thread loaded ahead of the q8 operands */
+template <int QB_WH>
 __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const ExpDesc &ex = a.ed[blockIdx.y];
@@ -297,24 +312,30 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     /* pair c16's q8 operands of half h of block bi: chunk m covers
      * x[128 h + 32 m ...], this lane's K slice 8 g .. 8 g + 7; the 16-value
      * sums of sub-blocks 8 h .. 8 h + 7 */
-    long xb[4];
-    int s16[8];
-    float xd;
-    auto load_x = [&](uint32_t prow, bool pv, int hb) {
-        const int bi = hb >> 1, h = hb & 1;
-        const uint32_t qb = prow * (uint32_t)nbi + (uint32_t)bi;
+    long xb[QB_WH][4];
+    int s16g[QB_WH][2];   /* the pair's 16-value sums of sub-blocks 8 h + g and 8 h + 4 + g */
+    float xd[QB_WH];
+    auto load_x = [&](uint32_t prow, bool pv) {
 #pragma unroll
-        for (int m = 0; m < 4; m++) xb[m] = as_long(ld8(qs_b, pv ? qb * 256u + 128u * h + 32u * m + 8u * g : OOB));
-        const u32x4 s0 = ld16(s16_b, pv ? qb * 64u + 32u * h : OOB);
-        const u32x4 s1 = ld16(s16_b, pv ? qb * 64u + 32u * h + 16u : OOB);
-        s16[0] = (int)s0.x, s16[1] = (int)s0.y, s16[2] = (int)s0.z, s16[3] = (int)s0.w;
-        s16[4] = (int)s1.x, s16[5] = (int)s1.y, s16[6] = (int)s1.z, s16[7] = (int)s1.w;
-        xd = __uint_as_float(ld4(d_b, pv ? qb * 4u : OOB));
+        for (int i = 0; i < QB_WH; i++) {
+            const int hb = w + NW * i;
+            const bool v = pv && hb < 2 * nbi;
+            const int bi = hb >> 1, h = hb & 1;
+            const uint32_t qb = prow * (uint32_t)nbi + (uint32_t)bi;
+#pragma unroll
+            for (int m = 0; m < 4; m++)
+                xb[i][m] = as_long(ld8(qs_b, v ? qb * 256u + 128u * h + 32u * m + 8u * g : OOB));
+            const u32x4 s0 = ld16(s16_b, v ? qb * 64u + 32u * h : OOB);
+            const u32x4 s1 = ld16(s16_b, v ? qb * 64u + 32u * h + 16u : OOB);
+            s16g[i][0] = (int)(g == 0 ? s0.x : g == 1 ? s0.y : g == 2 ? s0.z : s0.w);
+            s16g[i][1] = (int)(g == 0 ? s1.x : g == 1 ? s1.y : g == 2 ? s1.z : s1.w);
+            xd[i] = __uint_as_float(ld4(d_b, v ? qb * 4u : OOB));
+        }
     };
     int t0 = 0;
     bool pv = c16 < np;
     uint32_t prow = (uint32_t)(pv ? p0 + c16 : 0);
-    if (w < 2 * nbi) load_x(prow, pv, w);
+    load_x(prow, pv);
 #pragma unroll
     for (int i = 0; i < QB_NPC; i++) {
         const int c = tid + NT * i;
@@ -330,8 +351,10 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
 
     for (;;) {
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int hb = w; hb < 2 * nbi; hb += NW) {
-            if (hb != w) load_x(prow, pv, hb);
+#pragma unroll
+        for (int i = 0; i < QB_WH; i++) {
+            const int hb = w + NW * i;
+            if (hb >= 2 * nbi) break;   /* uniform per wave */
             const int bi = hb >> 1, h = hb & 1;
             /* row c16's codes: ql bytes 64 h + 32 (m & 1) + 8 g, qh bytes 32 h + 8 g */
             const uint8_t *ab = lds + blk_at(c16, bi);
@@ -352,8 +375,8 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
              * 4 + g; integers below 2^24, exact) */
             const u32x2 scr = *(const u32x2 *)(lds + blk_at(c16, bi) + 192 + 8 * h);   /* row c16 */
             v4f cf = {0.f, 0.f, 0.f, 0.f};
-            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.x >> (8 * g)), (float)s16[g], cf, 0, 0, 0);
-            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.y >> (8 * g)), (float)s16[4 + g], cf, 0, 0, 0);
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.x >> (8 * g)), (float)s16g[i][0], cf, 0, 0, 0);
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.y >> (8 * g)), (float)s16g[i][1], cf, 0, 0, 0);
             int ai[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int m = 0; m < 4; m++) {
@@ -363,7 +386,7 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
                 c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
                 c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
                 /* K slots 0-15 (lane groups 0, 1) are sub-block 2 m, 16-31 sub-block 2 m + 1 */
-                const long x0 = g < 2 ? xb[m] : 0l, x1 = g < 2 ? 0l : xb[m];
+                const long x0 = g < 2 ? xb[i][m] : 0l, x1 = g < 2 ? 0l : xb[i][m];
                 const v4i d0 = mma(as_long(c), x0), d1 = mma(as_long(c), x1);
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
@@ -374,7 +397,7 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
             }
             /* sum (c - 32) x sc, exact in int32 */
 #pragma unroll
-            for (int v = 0; v < 4; v++) acc[v] += dv[v] * xd * (float)(ai[v] - 32 * (int)cf[v]);
+            for (int v = 0; v < 4; v++) acc[v] += dv[v] * xd[i] * (float)(ai[v] - 32 * (int)cf[v]);
         }
 #pragma unroll
         for (int v = 0; v < 4; v++) red[(w * 4 + v) * 64 + lane] = acc[v];
@@ -382,7 +405,7 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
         if (t1 < np) {
             pv = t1 + c16 < np;
             prow = (uint32_t)(pv ? p0 + t1 + c16 : 0);
-            if (w < 2 * nbi) load_x(prow, pv, w);
+            load_x(prow, pv);
         }
         __syncthreads();
         if (tid < 256) {
@@ -415,6 +438,7 @@ bool qk_grouped_fits(const MoeArgs &a) {
             max_lds = 0;
     }
     if (a.gate_fmt != TG_FMT_Q4K || a.D % 256 || a.I % 256 || a.n_act_a <= 0) return false;
+    if (a.D > 256 * NW * QA_WB_MAX || a.I > 128 * NW * QB_WH_MAX) return false;   /* a pass's operands in registers */
     const uint64_t lim = 1ull << 31;
     return qa_lds_bytes(a.D) <= (size_t)max_lds && qb_lds_bytes(a.I) <= (size_t)max_lds &&
            (uint64_t)a.I * (a.D / 256) * Q4B < lim && (uint64_t)a.D * (a.I / 256) * Q6B < lim &&
@@ -422,11 +446,15 @@ bool qk_grouped_fits(const MoeArgs &a) {
 }
 
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_moe_qa, dim3((a.I + 15) / 16, a.n_act_a), dim3(NT), qa_lds_bytes(a.D), st, a);
+    const dim3 grid((a.I + 15) / 16, a.n_act_a);
+    if (a.D <= 256 * NW * 2) hipLaunchKernelGGL(k_moe_qa<2>, grid, dim3(NT), qa_lds_bytes(a.D), st, a);
+    else hipLaunchKernelGGL(k_moe_qa<QA_WB_MAX>, grid, dim3(NT), qa_lds_bytes(a.D), st, a);
 }
 
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_moe_qb, dim3((a.D + 15) / 16, a.n_act_a), dim3(NT), qb_lds_bytes(a.I), st, a);
+    const dim3 grid((a.D + 15) / 16, a.n_act_a);
+    if (a.I <= 128 * NW * 2) hipLaunchKernelGGL(k_moe_qb<2>, grid, dim3(NT), qb_lds_bytes(a.I), st, a);
+    else hipLaunchKernelGGL(k_moe_qb<QB_WH_MAX>, grid, dim3(NT), qb_lds_bytes(a.I), st, a);
 }
 
 }  // namespace tg

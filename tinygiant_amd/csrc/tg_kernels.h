@@ -52,7 +52,7 @@ struct MoeArgs {
     const int *mx_cum;                      /* cost prefix of each list (n_act + 1 entries each) */
     uint8_t *xp, *hp;                       /* fp8 halves of xq / hq rows in MFMA order, or null */
     int n_act_a, n_act_b;
-    const ExpDesc *ed;                      /* [n_act_a] active experts, the order of mx_act */
+    const ExpDesc *ed;                      /* [n_act_a] active experts, the most pairs first */
     unsigned *ctr;                          /* [ctr_n] row-tile tickets of the fused combine, zero between calls, or null */
     int ctr_n;
     int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */
