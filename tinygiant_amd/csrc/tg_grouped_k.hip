@@ -61,11 +61,10 @@ constexpr int NT = 64 * NW;
 constexpr uint32_t OOB = 0x80000000u;    /* past every buffer: the load reads zero */
 constexpr uint32_t Q4B = 144, Q6B = 210; /* bytes per 256-value block */
 constexpr uint32_t Q6S = 224;            /* LDS stride of a staged Q6_K block */
-/* A wave's q8 operands of a pass are loaded at once: QA_WB Q4_K blocks of a
- * gate/up row (D <= 256 NW QA_WB), QB_WH Q6_K half-blocks of a down row
- * (I <= 128 NW QB_WH).  Each kernel comes in a form for Qwen3's 8 blocks of D
- * and 6 half-blocks of I (fewer registers) and one for longer rows. */
-constexpr int QA_WB_MAX = 3, QB_WH_MAX = 5;
+/* A gate/up wave's q8 operands of a pass are loaded at once: QA_WB Q4_K
+ * blocks of a row (D <= 256 NW QA_WB), in a form for Qwen3's 8 blocks of D
+ * (fewer registers) and one for longer rows. */
+constexpr int QA_WB_MAX = 3;
 
 __device__ inline long as_long(u32x2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
 
@@ -84,9 +83,7 @@ __host__ __device__ inline uint32_t qb_row_stride(int I) { return (uint32_t)(I /
 __host__ __device__ inline size_t qa_lds_bytes(int D) {
     return 2u * (size_t)qa_slab_region(D) + (size_t)NW * 2 * 4 * 64 * 4;
 }
-__host__ __device__ inline size_t qb_lds_bytes(int I) {
-    return 16u * (size_t)qb_row_stride(I) + (size_t)NW * 4 * 64 * 4;
-}
+__host__ __device__ inline size_t qb_lds_bytes(int I) { return 64u * (size_t)qb_row_stride(I); }
 
 /* 6-bit scales and mins of a Q4_K block header (get_scale_min_k4,
  * csrc/libtinygiant.c:146-155), four bytes at a time: sc of sub-blocks 0-3,
@@ -268,39 +265,50 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     }
 }
 
-/* Phase B: part[p][r] = w_p * (down_r . hq_p + bd[r]) for rows r of slab
- * blockIdx.x and every pair p of active expert a.ed[blockIdx.y]; Q6_K down
- * matrix of I = 256 nbi columns.  The slab's loads go out first, then the
- * first pass's q8 operands, then the slab is stored to LDS. */
-constexpr int QB_PIECES = 13;   /* 16-byte pieces of a block's bytes 0-207 */
-constexpr int QB_NPC = 2;       /* pieces per thread loaded ahead of the q8 operands */
-template <int QB_WH>
+/* Phase B: part[p][r] = w_p * (down_r . hq_p + bd[r]) for the 64 rows r of
+ * slab blockIdx.x and every pair p of active expert a.ed[blockIdx.y]; Q6_K
+ * down matrix of I = 256 nbi columns.  Wave w owns rows 16 w .. 16 w + 15 of
+ * the slab over the whole row, so its MFMA sums are the rows' results and no
+ * partial sums cross waves.  The slab's loads go out first, then the first
+ * pass's q8 operands, then the slab is stored to LDS. */
+constexpr int QB_ROWS = 64;                 /* rows of a down slab: one 16-row tile a wave */
+constexpr int QB_PIECES = 13;               /* 16-byte pieces of a block's bytes 0-207 */
+constexpr int QB_NPC = 10;                  /* pieces per thread in flight while the slab is staged */
+constexpr int QB_CH = 6;                    /* half-blocks whose q8 operands a wave holds at once */
+template <int>
 __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const ExpDesc &ex = a.ed[blockIdx.y];
     const int e = ex.e, p0 = ex.p0, np = ex.np;
-    const int nbi = a.I / 256;
+    const int nbi = a.I / 256, nhb = 2 * nbi;
     const uint32_t rb = (uint32_t)nbi * Q6B, rs = qb_row_stride(a.I);
-    float *red = (float *)(lds + 16 * rs);   /* [NW][4][64] */
     /* LDS offset of block blk of slab row row */
     auto blk_at = [&](int row, int blk) { return (uint32_t)row * rs + (uint32_t)blk * Q6S; };
-    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
-    const int r0 = blockIdx.x * 16;
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              c16 = lane & 15;
+    const int r0 = blockIdx.x * QB_ROWS;
 
     /* the slab, each block at a 224-byte stride: bytes 0-207 as 13 pieces,
      * then d at 208 (a load that ran past byte 209 would read zero in the
      * matrix's last block; rows past D read zero) */
     const Buf dw = make_buf_uniform((const void *)(uintptr_t)ex.down, (uint32_t)a.D * rb);
-    const int nch = 16 * nbi * QB_PIECES;
+    const int nch = QB_ROWS * nbi * QB_PIECES;
     auto piece_src = [&](int c) {
         const int piece = c % QB_PIECES, rbk = c / QB_PIECES, row = rbk / nbi, blk = rbk % nbi;
         return (uint32_t)(r0 + row) * rb + (uint32_t)blk * Q6B + 16u * piece;
     };
+    auto piece_dst = [&](int c) { return blk_at(c / QB_PIECES / nbi, c / QB_PIECES % nbi) + 16 * (c % QB_PIECES); };
     u32x4 pc[QB_NPC];
 #pragma unroll
     for (int i = 0; i < QB_NPC; i++) {
         const int c = tid + NT * i;
         pc[i] = ld16(dw, c < nch ? piece_src(c) : OOB);
+    }
+    uint32_t dd[(QB_ROWS * 12 + NT - 1) / NT];   /* d of the slab's blocks (I <= 3072) */
+#pragma unroll
+    for (int i = 0; i < (QB_ROWS * 12 + NT - 1) / NT; i++) {
+        const int rbk = tid + NT * i;
+        dd[i] = rbk < QB_ROWS * nbi ? ld2(dw, (uint32_t)(r0 + rbk / nbi) * rb + (uint32_t)(rbk % nbi) * Q6B + 208u) : 0u;
     }
 
     const Q8Rows &q = a.hq;
@@ -309,17 +317,17 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     const Buf d_b = make_buf(q.d, (uint32_t)((size_t)a.P * nbi * 4));
     const Buf pw_b = make_buf(a.p_w, (uint32_t)a.P * 4u);
     const float *dbias = a.dbias ? (const float *)(uintptr_t)a.dbias[e] : nullptr;
-    /* pair c16's q8 operands of half h of block bi: chunk m covers
-     * x[128 h + 32 m ...], this lane's K slice 8 g .. 8 g + 7; the 16-value
-     * sums of sub-blocks 8 h .. 8 h + 7 */
-    long xb[QB_WH][4];
-    int s16g[QB_WH][2];   /* the pair's 16-value sums of sub-blocks 8 h + g and 8 h + 4 + g */
-    float xd[QB_WH];
-    auto load_x = [&](uint32_t prow, bool pv) {
+    /* pair c16's q8 operands of half-blocks c0 .. c0 + QB_CH - 1: chunk m of
+     * half h of block bi covers x[128 h + 32 m ...], this lane's K slice
+     * 8 g .. 8 g + 7; the 16-value sums of sub-blocks 8 h + g and 8 h + 4 + g */
+    long xb[QB_CH][4];
+    int s16g[QB_CH][2];
+    float xd[QB_CH];
+    auto load_x = [&](uint32_t prow, bool pv, int c0) {
 #pragma unroll
-        for (int i = 0; i < QB_WH; i++) {
-            const int hb = w + NW * i;
-            const bool v = pv && hb < 2 * nbi;
+        for (int i = 0; i < QB_CH; i++) {
+            const int hb = c0 + i;
+            const bool v = pv && hb < nhb;
             const int bi = hb >> 1, h = hb & 1;
             const uint32_t qb = prow * (uint32_t)nbi + (uint32_t)bi;
 #pragma unroll
@@ -335,94 +343,95 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     int t0 = 0;
     bool pv = c16 < np;
     uint32_t prow = (uint32_t)(pv ? p0 + c16 : 0);
-    load_x(prow, pv);
+    load_x(prow, pv, 0);
 #pragma unroll
     for (int i = 0; i < QB_NPC; i++) {
         const int c = tid + NT * i;
-        if (c < nch) *(u32x4 *)(lds + blk_at(c / QB_PIECES / nbi, c / QB_PIECES % nbi) + 16 * (c % QB_PIECES)) = pc[i];
+        if (c < nch) *(u32x4 *)(lds + piece_dst(c)) = pc[i];
     }
-    for (int c = tid + NT * QB_NPC; c < nch; c += NT)   /* rows of more than 2 blocks */
-        *(u32x4 *)(lds + blk_at(c / QB_PIECES / nbi, c / QB_PIECES % nbi) + 16 * (c % QB_PIECES)) =
-            ld16(dw, piece_src(c));
-    for (int rbk = tid; rbk < 16 * nbi; rbk += NT)
-        *(uint32_t *)(lds + blk_at(rbk / nbi, rbk % nbi) + 208) =
-            ld2(dw, (uint32_t)(r0 + rbk / nbi) * rb + (uint32_t)(rbk % nbi) * Q6B + 208u);
+    for (int c = tid + NT * QB_NPC; c < nch; c += NT)   /* rows of more than 3 blocks */
+        *(u32x4 *)(lds + piece_dst(c)) = ld16(dw, piece_src(c));
+#pragma unroll
+    for (int i = 0; i < (QB_ROWS * 12 + NT - 1) / NT; i++) {
+        const int rbk = tid + NT * i;
+        if (rbk < QB_ROWS * nbi) *(uint32_t *)(lds + blk_at(rbk / nbi, rbk % nbi) + 208) = dd[i];
+    }
     __syncthreads();
 
+    const int tr = 16 * w;   /* the wave's first slab row */
     for (;;) {
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int c0 = 0; c0 < nhb; c0 += QB_CH) {
+            if (c0 > 0) load_x(prow, pv, c0);   /* rows of more than 3 blocks */
 #pragma unroll
-        for (int i = 0; i < QB_WH; i++) {
-            const int hb = w + NW * i;
-            if (hb >= 2 * nbi) break;   /* uniform per wave */
-            const int bi = hb >> 1, h = hb & 1;
-            /* row c16's codes: ql bytes 64 h + 32 (m & 1) + 8 g, qh bytes 32 h + 8 g */
-            const uint8_t *ab = lds + blk_at(c16, bi);
-            const u32x2 ql0 = *(const u32x2 *)(ab + 64 * h + 8 * g);
-            const u32x2 ql1 = *(const u32x2 *)(ab + 64 * h + 32 + 8 * g);
-            const u32x2 qh = *(const u32x2 *)(ab + 128 + 32 * h + 8 * g);
-            /* rows 4 g + v: sub-block scales 8 h .. 8 h + 7 and d */
-            u32x2 sc[4];
-            float dv[4];
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const uint8_t *rbk = lds + blk_at(4 * g + v, bi);
-                sc[v] = *(const u32x2 *)(rbk + 192 + 8 * h);
-                dv[v] = ref_f16(*(const uint32_t *)(rbk + 208) & 0xFFFFu);
-            }
-            /* the -32 offset terms sum_s sc[row][s] s16[pair][s] over the
-             * half's 8 sub-blocks: two f32 MFMAs of K = 4 (sub-blocks g and
-             * 4 + g; integers below 2^24, exact) */
-            const u32x2 scr = *(const u32x2 *)(lds + blk_at(c16, bi) + 192 + 8 * h);   /* row c16 */
-            v4f cf = {0.f, 0.f, 0.f, 0.f};
-            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.x >> (8 * g)), (float)s16g[i][0], cf, 0, 0, 0);
-            cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.y >> (8 * g)), (float)s16g[i][1], cf, 0, 0, 0);
-            int ai[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int m = 0; m < 4; m++) {
-                const u32x2 ql = (m & 1) ? ql1 : ql0;
-                const int sl = 4 * (m >> 1), sh = 2 * m;
-                u32x2 c;
-                c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
-                c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
-                /* K slots 0-15 (lane groups 0, 1) are sub-block 2 m, 16-31 sub-block 2 m + 1 */
-                const long x0 = g < 2 ? xb[i][m] : 0l, x1 = g < 2 ? 0l : xb[i][m];
-                const v4i d0 = mma(as_long(c), x0), d1 = mma(as_long(c), x1);
+            for (int i = 0; i < QB_CH; i++) {
+                const int hb = c0 + i;
+                if (hb >= nhb) break;   /* uniform */
+                const int bi = hb >> 1, h = hb & 1;
+                /* row c16's codes: ql bytes 64 h + 32 (m & 1) + 8 g, qh bytes 32 h + 8 g */
+                const uint8_t *ab = lds + blk_at(tr + c16, bi);
+                const u32x2 ql0 = *(const u32x2 *)(ab + 64 * h + 8 * g);
+                const u32x2 ql1 = *(const u32x2 *)(ab + 64 * h + 32 + 8 * g);
+                const u32x2 qh = *(const u32x2 *)(ab + 128 + 32 * h + 8 * g);
+                /* rows 4 g + v: sub-block scales 8 h .. 8 h + 7 and d */
+                u32x2 sc[4];
+                float dv[4];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
-                    const uint32_t sw = (m < 2 ? sc[v].x : sc[v].y);
-                    const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))), sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
-                    ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 per term */
+                    const uint8_t *rbk = lds + blk_at(tr + 4 * g + v, bi);
+                    sc[v] = *(const u32x2 *)(rbk + 192 + 8 * h);
+                    dv[v] = ref_f16(*(const uint32_t *)(rbk + 208) & 0xFFFFu);
                 }
+                /* the -32 offset terms sum_s sc[row][s] s16[pair][s] over the
+                 * half's 8 sub-blocks: two f32 MFMAs of K = 4 (sub-blocks g
+                 * and 4 + g; integers below 2^24, exact) */
+                const u32x2 scr = *(const u32x2 *)(ab + 192 + 8 * h);   /* row c16 */
+                v4f cf = {0.f, 0.f, 0.f, 0.f};
+                cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.x >> (8 * g)), (float)s16g[i][0], cf, 0,
+                                                          0, 0);
+                cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.y >> (8 * g)), (float)s16g[i][1], cf, 0,
+                                                          0, 0);
+                int ai[4] = {0, 0, 0, 0};
+#pragma unroll
+                for (int m = 0; m < 4; m++) {
+                    const u32x2 ql = (m & 1) ? ql1 : ql0;
+                    const int sl = 4 * (m >> 1), sh = 2 * m;
+                    u32x2 c;
+                    c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
+                    c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
+                    /* K slots 0-15 (lane groups 0, 1) are sub-block 2 m, 16-31 sub-block 2 m + 1 */
+                    const long x0 = g < 2 ? xb[i][m] : 0l, x1 = g < 2 ? 0l : xb[i][m];
+                    const v4i d0 = mma(as_long(c), x0), d1 = mma(as_long(c), x1);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const uint32_t sw = (m < 2 ? sc[v].x : sc[v].y);
+                        const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))),
+                                  sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
+                        ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 per term */
+                    }
+                }
+                /* sum (c - 32) x sc, exact in int32 */
+#pragma unroll
+                for (int v = 0; v < 4; v++) acc[v] += dv[v] * xd[i] * (float)(ai[v] - 32 * (int)cf[v]);
             }
-            /* sum (c - 32) x sc, exact in int32 */
-#pragma unroll
-            for (int v = 0; v < 4; v++) acc[v] += dv[v] * xd[i] * (float)(ai[v] - 32 * (int)cf[v]);
         }
-#pragma unroll
-        for (int v = 0; v < 4; v++) red[(w * 4 + v) * 64 + lane] = acc[v];
-        const int t1 = t0 + 16;
-        if (t1 < np) {
-            pv = t1 + c16 < np;
-            prow = (uint32_t)(pv ? p0 + t1 + c16 : 0);
-            load_x(prow, pv);
+        /* rows r0 + tr + 4 g + v of pair t0 + c16, in the half-blocks' order */
+        const int jj = t0 + c16, r = r0 + tr + 4 * g;
+        if (jj < np && r < a.D) {
+            const int p = p0 + jj;
+            const float pw = __uint_as_float(ld4(pw_b, (uint32_t)p * 4u));
+            float4 o;
+            o.x = pw * (acc[0] + (dbias ? dbias[r] : 0.f));
+            o.y = pw * (acc[1] + (dbias ? dbias[r + 1] : 0.f));
+            o.z = pw * (acc[2] + (dbias ? dbias[r + 2] : 0.f));
+            o.w = pw * (acc[3] + (dbias ? dbias[r + 3] : 0.f));
+            *reinterpret_cast<float4 *>(a.part + (size_t)p * a.D + r) = o;
         }
-        __syncthreads();
-        if (tid < 256) {
-            const int ev = tid >> 6, el = tid & 63;
-            const int jj = t0 + (el & 15), r = r0 + 4 * (el >> 4) + ev;
-            if (jj < np && r < a.D) {
-                float s = 0.f;
-#pragma unroll
-                for (int ww = 0; ww < NW; ww++) s += red[(ww * 4 + ev) * 64 + el];
-                if (dbias) s += dbias[r];
-                const int p = p0 + jj;
-                a.part[(size_t)p * a.D + r] = __uint_as_float(ld4(pw_b, (uint32_t)p * 4u)) * s;
-            }
-        }
-        if (t1 >= np) break;
-        t0 = t1;
-        __syncthreads();
+        t0 += 16;
+        if (t0 >= np) break;
+        pv = t0 + c16 < np;
+        prow = (uint32_t)(pv ? p0 + t0 + c16 : 0);
+        load_x(prow, pv, 0);
     }
 }
 
@@ -438,7 +447,7 @@ bool qk_grouped_fits(const MoeArgs &a) {
             max_lds = 0;
     }
     if (a.gate_fmt != TG_FMT_Q4K || a.D % 256 || a.I % 256 || a.n_act_a <= 0) return false;
-    if (a.D > 256 * NW * QA_WB_MAX || a.I > 128 * NW * QB_WH_MAX) return false;   /* a pass's operands in registers */
+    if (a.D > 256 * NW * QA_WB_MAX || a.I > 3072) return false;   /* a pass's operands and the slab's d in registers */
     const uint64_t lim = 1ull << 31;
     return qa_lds_bytes(a.D) <= (size_t)max_lds && qb_lds_bytes(a.I) <= (size_t)max_lds &&
            (uint64_t)a.I * (a.D / 256) * Q4B < lim && (uint64_t)a.D * (a.I / 256) * Q6B < lim &&
@@ -452,9 +461,7 @@ void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {
 }
 
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st) {
-    const dim3 grid((a.D + 15) / 16, a.n_act_a);
-    if (a.I <= 128 * NW * 2) hipLaunchKernelGGL(k_moe_qb<2>, grid, dim3(NT), qb_lds_bytes(a.I), st, a);
-    else hipLaunchKernelGGL(k_moe_qb<QB_WH_MAX>, grid, dim3(NT), qb_lds_bytes(a.I), st, a);
+    hipLaunchKernelGGL(k_moe_qb<0>, dim3((a.D + QB_ROWS - 1) / QB_ROWS, a.n_act_a), dim3(NT), qb_lds_bytes(a.I), st, a);
 }
 
 }  // namespace tg
