@@ -391,7 +391,8 @@ def device_asm(tmp_path_factory):
 
     def one(src):
         out = tmp / (src + ".s")
-        cmd = [B.HIPCC, *flags, "--cuda-device-only", "-S", "-I", str(B.CSRC), str(B.CSRC / src), "-o", str(out)]
+        cmd = [B.HIPCC, *flags, *B.HIP_EXTRA.get(src, []), "--cuda-device-only", "-S", "-I", str(B.CSRC),
+               str(B.CSRC / src), "-o", str(out)]
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stderr[-2000:]
         return src, out.read_text()

@@ -24,6 +24,9 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fvisibility=hidden", "-Wall", "-Wno-unused-function",
 ]
+# per-source flags: the int8 MFMA expert phases take their MFMA results in
+# VGPRs (no accumulator-register reads before the scale arithmetic)
+HIP_EXTRA = {"tg_grouped_k.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 HIP_SOURCES = ["tg_kernels.hip", "tg_grouped.hip", "tg_grouped_k.hip", "tg_decode.hip", "tg_decode_mx.hip", "tg_decode_rows.hip", "tg_head.hip", "tg_route.hip", "tg_attn.hip", "tg_api.hip"]
 CXX_SOURCES = ["tg_host_ops.cpp"]
 
@@ -45,7 +48,7 @@ def build(verbose=True):
     for s in HIP_SOURCES:
         o = BUILD / (s + ".o")
         objs.append(o)
-        jobs.append([HIPCC, *HIP_FLAGS, "-I", str(CSRC), "-c", str(CSRC / s), "-o", str(o)])
+        jobs.append([HIPCC, *HIP_FLAGS, *HIP_EXTRA.get(s, []), "-I", str(CSRC), "-c", str(CSRC / s), "-o", str(o)])
     for s in CXX_SOURCES:
         o = BUILD / (s + ".o")
         objs.append(o)

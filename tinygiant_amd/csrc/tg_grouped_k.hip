@@ -24,8 +24,10 @@
  * sub-block-by-sub-block sum.
  *
  * Operand layout of v_mfma_i32_16x16x32_i8 (measured on gfx950): A lane l =
- * weight row l % 16, K = 8 (l / 16) + byte; B lane l = pair l % 16, the same
- * K; D lane l, register v = weight row 4 (l / 16) + v, pair l % 16.
+ * row l % 16 of A, K = 8 (l / 16) + byte; B lane l = column l % 16, the same
+ * K; D lane l, register v = A row 4 (l / 16) + v, B column l % 16.  The pairs'
+ * q8 operands go in as A and the weight rows as B, so the four sums of a lane
+ * share one weight row (lane % 16) and its scales.
  *
  * Work: one workgroup per (16-row slab, active expert).  The slab is staged
  * in LDS (Q6_K blocks re-spaced to 224 bytes so every field is aligned, each
@@ -67,6 +69,13 @@ constexpr uint32_t Q6S = 224;            /* LDS stride of a staged Q6_K block */
 constexpr int QA_WB_MAX = 3;
 
 __device__ inline long as_long(u32x2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
+
+/* a wave-uniform read of a read-only table through the constant address
+ * space: a scalar load, counted apart from the vector loads */
+template <class T>
+__device__ inline T ldc(const T *p, size_t i) {
+    return ((const __attribute__((address_space(4))) T *)(uintptr_t)p)[i];
+}
 
 __device__ inline v4i mma(long a, long b) {
     const v4i z = {0, 0, 0, 0};
@@ -151,7 +160,18 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     const Buf qs_b = make_buf(q.qs, (uint32_t)((size_t)a.k * nb * 256));
     const Buf s32_b = make_buf(q.s32, (uint32_t)((size_t)a.k * nb * 32));
     const Buf d_b = make_buf(q.d, (uint32_t)((size_t)a.k * nb * 4));
-    const Buf prow_b = make_buf(a.p_row, (uint32_t)a.P * 4u);
+    /* the input row of pair t + c16 (0 past the expert's pairs): the 16 rows
+     * come through the scalar path, so waiting for them does not wait for
+     * the slab copies queued on the vector path */
+    auto pair_row = [&](int t) {
+        uint32_t rj[16];
+#pragma unroll
+        for (int j = 0; j < 16; j++) rj[j] = (uint32_t)ldc(a.p_row, (size_t)min(p0 + t + j, a.P - 1));
+        uint32_t r = 0u;
+#pragma unroll
+        for (int j = 0; j < 16; j++) r = c16 == j && t + j < np ? rj[j] : r;
+        return r;
+    };
     const float *gbias = a.gbias ? (const float *)(uintptr_t)a.gbias[e] : nullptr;
     const float *ubias = a.ubias ? (const float *)(uintptr_t)a.ubias[e] : nullptr;
 
@@ -177,7 +197,7 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     };
     int t0 = 0;
     bool pv = c16 < np;
-    uint32_t prow = pv ? ld4(prow_b, (uint32_t)(p0 + c16) * 4u) : 0u;
+    uint32_t prow = pair_row(0);
     load_x(prow, pv);
     wait_copies();
     __syncthreads();
@@ -191,17 +211,20 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
 #pragma unroll 1
             for (int m = 0; m < 2; m++) {
                 const uint8_t *sb = lds + m * sreg;
-                Q4Hdr hd[4];
-#pragma unroll
-                for (int v = 0; v < 4; v++) hd[v] = q4_hdr(*(const u32x4 *)(sb + (4 * g + v) * rs + b * Q4B));
-                /* the min terms sum_s m[row][s] bs[pair][s] of the 16 rows x 16
-                 * pairs: two f32 MFMAs of K = 4 (sub-blocks g and 4 + g of this
-                 * lane group; products and sums are integers below 2^24, exact) */
+                /* the pairs' q8 operands are the MFMA's A side and the weight
+                 * rows its B side, so a lane's four sums belong to one row
+                 * (c16) and four pairs (4 g + v): one header a lane */
                 const Q4Hdr hr = q4_hdr(*(const u32x4 *)(sb + c16 * rs + b * Q4B));
+                float xdv[4];
+#pragma unroll
+                for (int v = 0; v < 4; v++) xdv[v] = __shfl(xd[i], 4 * g + v, 64);
+                /* the min terms sum_s bs[pair][s] m[row][s] of the 16 pairs x 16
+                 * rows: two f32 MFMAs of K = 4 (sub-blocks g and 4 + g of this
+                 * lane group; products and sums are integers below 2^24, exact) */
                 v4f im = {0.f, 0.f, 0.f, 0.f};
-                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnl, g), bsg0[i], im, 0, 0, 0);
-                im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)byte_of(hr.mnh, g), bsg1[i], im, 0, 0, 0);
-                /* the scale terms sum_s sc[row][s] idot[row][pair][s]: one int8
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32(bsg0[i], (float)byte_of(hr.mnl, g), im, 0, 0, 0);
+                im = __builtin_amdgcn_mfma_f32_16x16x4f32(bsg1[i], (float)byte_of(hr.mnh, g), im, 0, 0, 0);
+                /* the scale terms sum_s sc[row][s] idot[pair][row][s]: one int8
                  * MFMA per sub-block, summed exactly in int32 */
                 const uint8_t *ab = sb + c16 * rs + b * Q4B + 16 + 8 * g;   /* row c16's codes */
                 int isc[4] = {0, 0, 0, 0};
@@ -213,19 +236,17 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
                     lo.y = qq.y & 0x0F0F0F0Fu;
                     hi.x = (qq.x >> 4) & 0x0F0F0F0Fu;
                     hi.y = (qq.y >> 4) & 0x0F0F0F0Fu;
-                    const v4i dl = mma(as_long(lo), xb[i][2 * jg]);
-                    const v4i dh = mma(as_long(hi), xb[i][2 * jg + 1]);
+                    const v4i dl = mma(xb[i][2 * jg], as_long(lo));
+                    const v4i dh = mma(xb[i][2 * jg + 1], as_long(hi));
+                    const uint32_t scw = jg < 2 ? hr.scl : hr.sch;
+                    const int s0 = byte_of(scw, 2 * (jg & 1)), s1 = byte_of(scw, 2 * (jg & 1) + 1);
 #pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        const uint32_t scw = jg < 2 ? hd[v].scl : hd[v].sch;
-                        const int i0 = 2 * (jg & 1);
-                        isc[v] += __mul24(byte_of(scw, i0), dl[v]) + __mul24(byte_of(scw, i0 + 1), dh[v]);
-                    }
+                    for (int v = 0; v < 4; v++) isc[v] += __mul24(s0, dl[v]) + __mul24(s1, dh[v]);
                 }
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
                     /* acc indexed with constants only (m is a loop variable) */
-                    const float t = xd[i] * (hd[v].d * (float)isc[v] - hd[v].dmin * im[v]);
+                    const float t = xdv[v] * (hr.d * (float)isc[v] - hr.dmin * im[v]);
                     if (m == 0) acc[0][v] += t;
                     else acc[1][v] += t;
                 }
@@ -240,13 +261,14 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
         const int t1 = t0 + 16;
         if (t1 < np) {
             pv = t1 + c16 < np;
-            prow = pv ? ld4(prow_b, (uint32_t)(p0 + t1 + c16) * 4u) : 0u;
+            prow = pair_row(t1);
             load_x(prow, pv);
         }
         __syncthreads();
         if (tid < 256) {
+            /* register ev of D lane el: pair 4 (el / 16) + ev, slab row el % 16 */
             const int ev = tid >> 6, el = tid & 63;
-            const int jj = t0 + (el & 15), r = r0 + 4 * (el >> 4) + ev;
+            const int jj = t0 + 4 * (el >> 4) + ev, r = r0 + (el & 15);
             if (jj < np && r < a.I) {
                 float gv = 0.f, uv = 0.f;
 #pragma unroll
@@ -333,10 +355,9 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
 #pragma unroll
             for (int m = 0; m < 4; m++)
                 xb[i][m] = as_long(ld8(qs_b, v ? qb * 256u + 128u * h + 32u * m + 8u * g : OOB));
-            const u32x4 s0 = ld16(s16_b, v ? qb * 64u + 32u * h : OOB);
-            const u32x4 s1 = ld16(s16_b, v ? qb * 64u + 32u * h + 16u : OOB);
-            s16g[i][0] = (int)(g == 0 ? s0.x : g == 1 ? s0.y : g == 2 ? s0.z : s0.w);
-            s16g[i][1] = (int)(g == 0 ? s1.x : g == 1 ? s1.y : g == 2 ? s1.z : s1.w);
+            /* each its own load: a select among loaded words would wait for the load */
+            s16g[i][0] = (int)ld4(s16_b, v ? qb * 64u + 32u * h + 4u * g : OOB);
+            s16g[i][1] = (int)ld4(s16_b, v ? qb * 64u + 32u * h + 16u + 4u * g : OOB);
             xd[i] = __uint_as_float(ld4(d_b, v ? qb * 4u : OOB));
         }
     };
@@ -373,23 +394,21 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
                 const u32x2 ql0 = *(const u32x2 *)(ab + 64 * h + 8 * g);
                 const u32x2 ql1 = *(const u32x2 *)(ab + 64 * h + 32 + 8 * g);
                 const u32x2 qh = *(const u32x2 *)(ab + 128 + 32 * h + 8 * g);
-                /* rows 4 g + v: sub-block scales 8 h .. 8 h + 7 and d */
-                u32x2 sc[4];
-                float dv[4];
+                /* the pairs' q8 operands are the MFMA's A side and the weight
+                 * rows its B side, so a lane's four sums belong to row c16
+                 * and pairs 4 g + v: its scales are row c16's */
+                const u32x2 scr = *(const u32x2 *)(ab + 192 + 8 * h);   /* sub-block scales 8 h .. 8 h + 7 */
+                const float dv = ref_f16(*(const uint32_t *)(ab + 208) & 0xFFFFu);
+                float xdv[4];
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const uint8_t *rbk = lds + blk_at(tr + 4 * g + v, bi);
-                    sc[v] = *(const u32x2 *)(rbk + 192 + 8 * h);
-                    dv[v] = ref_f16(*(const uint32_t *)(rbk + 208) & 0xFFFFu);
-                }
-                /* the -32 offset terms sum_s sc[row][s] s16[pair][s] over the
+                for (int v = 0; v < 4; v++) xdv[v] = __shfl(xd[i], 4 * g + v, 64);
+                /* the -32 offset terms sum_s s16[pair][s] sc[row][s] over the
                  * half's 8 sub-blocks: two f32 MFMAs of K = 4 (sub-blocks g
                  * and 4 + g; integers below 2^24, exact) */
-                const u32x2 scr = *(const u32x2 *)(ab + 192 + 8 * h);   /* row c16 */
                 v4f cf = {0.f, 0.f, 0.f, 0.f};
-                cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.x >> (8 * g)), (float)s16g[i][0], cf, 0,
+                cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s16g[i][0], (float)(int8_t)(scr.x >> (8 * g)), cf, 0,
                                                           0, 0);
-                cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int8_t)(scr.y >> (8 * g)), (float)s16g[i][1], cf, 0,
+                cf = __builtin_amdgcn_mfma_f32_16x16x4f32((float)s16g[i][1], (float)(int8_t)(scr.y >> (8 * g)), cf, 0,
                                                           0, 0);
                 int ai[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -401,31 +420,29 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
                     c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
                     /* K slots 0-15 (lane groups 0, 1) are sub-block 2 m, 16-31 sub-block 2 m + 1 */
                     const long x0 = g < 2 ? xb[i][m] : 0l, x1 = g < 2 ? 0l : xb[i][m];
-                    const v4i d0 = mma(as_long(c), x0), d1 = mma(as_long(c), x1);
+                    const v4i d0 = mma(x0, as_long(c)), d1 = mma(x1, as_long(c));
+                    const uint32_t sw = m < 2 ? scr.x : scr.y;
+                    const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))), sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
 #pragma unroll
-                    for (int v = 0; v < 4; v++) {
-                        const uint32_t sw = (m < 2 ? sc[v].x : sc[v].y);
-                        const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))),
-                                  sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
-                        ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 per term */
-                    }
+                    for (int v = 0; v < 4; v++) ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 */
                 }
                 /* sum (c - 32) x sc, exact in int32 */
 #pragma unroll
-                for (int v = 0; v < 4; v++) acc[v] += dv[v] * xd[i] * (float)(ai[v] - 32 * (int)cf[v]);
+                for (int v = 0; v < 4; v++) acc[v] += dv * xdv[v] * (float)(ai[v] - 32 * (int)cf[v]);
             }
         }
-        /* rows r0 + tr + 4 g + v of pair t0 + c16, in the half-blocks' order */
-        const int jj = t0 + c16, r = r0 + tr + 4 * g;
-        if (jj < np && r < a.D) {
-            const int p = p0 + jj;
-            const float pw = __uint_as_float(ld4(pw_b, (uint32_t)p * 4u));
-            float4 o;
-            o.x = pw * (acc[0] + (dbias ? dbias[r] : 0.f));
-            o.y = pw * (acc[1] + (dbias ? dbias[r + 1] : 0.f));
-            o.z = pw * (acc[2] + (dbias ? dbias[r + 2] : 0.f));
-            o.w = pw * (acc[3] + (dbias ? dbias[r + 3] : 0.f));
-            *reinterpret_cast<float4 *>(a.part + (size_t)p * a.D + r) = o;
+        /* row r0 + tr + c16 of pairs t0 + 4 g + v, in the half-blocks' order */
+        const int r = r0 + tr + c16;
+        if (r < a.D) {
+            const float bias = dbias ? dbias[r] : 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int jj = t0 + 4 * g + v;
+                if (jj < np) {
+                    const int p = p0 + jj;
+                    a.part[(size_t)p * a.D + r] = __uint_as_float(ld4(pw_b, (uint32_t)p * 4u)) * (acc[v] + bias);
+                }
+            }
         }
         t0 += 16;
         if (t0 >= np) break;
