@@ -303,6 +303,11 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     const ExpDesc &ex = a.ed[blockIdx.y];
     const int e = ex.e, p0 = ex.p0, np = ex.np;
     const int nbi = a.I / 256, nhb = 2 * nbi;
+    /* n / nbi for the slab's block indices n < 64 * 12 as (n * inv) >> 16:
+     * inv exceeds 2^16 / nbi by less than 1, so the product's error stays
+     * below 768 / 2^16 < 1 / nbi */
+    const uint32_t inv = (65536u + (uint32_t)nbi - 1u) / (uint32_t)nbi;
+    auto div_nbi = [&](int n) { return (int)(((uint32_t)n * inv) >> 16); };
     const uint32_t rb = (uint32_t)nbi * Q6B, rs = qb_row_stride(a.I);
     /* LDS offset of block blk of slab row row */
     auto blk_at = [&](int row, int blk) { return (uint32_t)row * rs + (uint32_t)blk * Q6S; };
@@ -316,10 +321,13 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     const Buf dw = make_buf_uniform((const void *)(uintptr_t)ex.down, (uint32_t)a.D * rb);
     const int nch = QB_ROWS * nbi * QB_PIECES;
     auto piece_src = [&](int c) {
-        const int piece = c % QB_PIECES, rbk = c / QB_PIECES, row = rbk / nbi, blk = rbk % nbi;
+        const int piece = c % QB_PIECES, rbk = c / QB_PIECES, row = div_nbi(rbk), blk = rbk - row * nbi;
         return (uint32_t)(r0 + row) * rb + (uint32_t)blk * Q6B + 16u * piece;
     };
-    auto piece_dst = [&](int c) { return blk_at(c / QB_PIECES / nbi, c / QB_PIECES % nbi) + 16 * (c % QB_PIECES); };
+    auto piece_dst = [&](int c) {
+        const int rbk = c / QB_PIECES, row = div_nbi(rbk);
+        return blk_at(row, rbk - row * nbi) + 16 * (c % QB_PIECES);
+    };
     u32x4 pc[QB_NPC];
 #pragma unroll
     for (int i = 0; i < QB_NPC; i++) {
@@ -330,7 +338,8 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
 #pragma unroll
     for (int i = 0; i < (QB_ROWS * 12 + NT - 1) / NT; i++) {
         const int rbk = tid + NT * i;
-        dd[i] = rbk < QB_ROWS * nbi ? ld2(dw, (uint32_t)(r0 + rbk / nbi) * rb + (uint32_t)(rbk % nbi) * Q6B + 208u) : 0u;
+        const int row = div_nbi(rbk);
+        dd[i] = rbk < QB_ROWS * nbi ? ld2(dw, (uint32_t)(r0 + row) * rb + (uint32_t)(rbk - row * nbi) * Q6B + 208u) : 0u;
     }
 
     const Q8Rows &q = a.hq;
@@ -375,12 +384,18 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
 #pragma unroll
     for (int i = 0; i < (QB_ROWS * 12 + NT - 1) / NT; i++) {
         const int rbk = tid + NT * i;
-        if (rbk < QB_ROWS * nbi) *(uint32_t *)(lds + blk_at(rbk / nbi, rbk % nbi) + 208) = dd[i];
+        const int row = div_nbi(rbk);
+        if (rbk < QB_ROWS * nbi) *(uint32_t *)(lds + blk_at(row, rbk - row * nbi) + 208) = dd[i];
     }
     __syncthreads();
 
     const int tr = 16 * w;   /* the wave's first slab row */
     for (;;) {
+        /* the weights of the lane's four pairs, waited for only at the end */
+        float pwv[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++)
+            pwv[v] = __uint_as_float(ld4(pw_b, t0 + 4 * g + v < np ? (uint32_t)(p0 + t0 + 4 * g + v) * 4u : OOB));
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
         for (int c0 = 0; c0 < nhb; c0 += QB_CH) {
             if (c0 > 0) load_x(prow, pv, c0);   /* rows of more than 3 blocks */
@@ -438,10 +453,7 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int jj = t0 + 4 * g + v;
-                if (jj < np) {
-                    const int p = p0 + jj;
-                    a.part[(size_t)p * a.D + r] = __uint_as_float(ld4(pw_b, (uint32_t)p * 4u)) * (acc[v] + bias);
-                }
+                if (jj < np) a.part[(size_t)(p0 + jj) * a.D + r] = pwv[v] * (acc[v] + bias);
             }
         }
         t0 += 16;
@@ -478,7 +490,8 @@ void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {
 }
 
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st) {
-    hipLaunchKernelGGL(k_moe_qb<0>, dim3((a.D + QB_ROWS - 1) / QB_ROWS, a.n_act_a), dim3(NT), qb_lds_bytes(a.I), st, a);
+    hipLaunchKernelGGL(k_moe_qb<0>, dim3((a.D + QB_ROWS - 1) / QB_ROWS, a.n_act_a), dim3(NT), qb_lds_bytes(a.I), st,
+                       a);
 }
 
 }  // namespace tg
