@@ -412,6 +412,20 @@ struct Layout {
     size_t tables, tables_len, xin, xq, hidden, hq, part, out, xp, hp, ctr, total;
 };
 
+/* compute units of the current device (workgroups of the persistent phases) */
+static int cu_count() {
+    static int n = 0;
+    if (n == 0) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            n = std::min(v, QA_RING_MAX_G);
+        else
+            n = 256;
+    }
+    return n;
+}
+
 /* row-tile tickets of the fused combine: at most one per 4 rows of D */
 static int moe_ctr_words(int D) { return D / 4 + 16; }
 
@@ -426,6 +440,8 @@ Layout plan_layout(const HostPlan &h) {
     t += (size_t)(n + 1) * 4 + (size_t)P * 4 * 4 + (size_t)(k + 1) * 4 + 8;   /* p_off, p_row, p_exp, p_w, r_off, r_pair */
     t += (size_t)4 * (n + 1) * 4 + 16;      /* active expert lists and their cost prefixes */
     t += (size_t)n * sizeof(ExpDesc) + 16;  /* active expert descriptors */
+    if (qa_ring_shape(h.gate_fmt, h.D, h.I))  /* the persistent gate/up phase's items and ranges */
+        t += (size_t)(h.I / 16) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 16;
     L.tables_len = t + 64;
     b.take(L.tables_len);
     L.xin = b.take((size_t)k * h.D * 4);
@@ -538,6 +554,13 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
      * first instead of trailing the launch */
     std::stable_sort(ed.begin(), ed.end(), [](const ExpDesc &x, const ExpDesc &y) { return x.np > y.np; });
     a.ed = (const ExpDesc *)put(ed.data(), ed.size() * sizeof(ExpDesc));
+    if (qa_ring_shape(h.gate_fmt, h.D, h.I) && a.n_act_a > 0) {
+        std::vector<int> items, off;
+        qa_ring_items(ed.data(), a.n_act_a, h.I, cu_count(), items, off);
+        a.rg_items = (const int *)put(items.data(), items.size() * 4);
+        a.rg_off = (const int *)put(off.data(), off.size() * 4);
+        a.rg_n = (int)off.size() - 1;
+    }
     act_a.insert(act_a.end(), act_b.begin(), act_b.end());
     a.mx_act = (const int *)put(act_a.data(), act_a.size() * 4);
     a.mx_cum = (const int *)put(cum.data(), cum.size() * 4);

@@ -287,6 +287,251 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
     }
 }
 
+/* Phase A, persistent, for Q4_K gate/up rows of D = 2048 (8 blocks): one
+ * workgroup a compute unit walks its list of items (active expert, 16-row
+ * slab, pass of 16 pairs), the slabs streaming through a ring of four LDS
+ * slots three items ahead of the item computed, so a compute unit always
+ * has weight bytes in flight.
+ *
+ * Eight compute waves: wave c takes matrix c / 4 (gate, up) and blocks
+ * c % 4 and c % 4 + 4 of it, so the partial sums of a block pair meet in
+ * LDS in the order of the expert-major kernel (wave order).  They hold the
+ * q8 operands of a run of items with the same expert and pass, loaded once
+ * a run (a compute unit returns its loads in issue order, so operands loaded
+ * per item would wait behind the slabs in flight each time); a workgroup's
+ * list is a contiguous stretch of the layer's items ordered expert, pass,
+ * slab, so it holds a few runs.  Four loader waves issue the slab copies
+ * (direct-to-LDS, half a matrix each), each waiting for its own with exact
+ * counts, and finish the previous item (its
+ * partial sums, double-buffered in LDS, the activation, the hidden values)
+ * while the compute waves work on the current one, one barrier an item.
+ *
+ * A slab's LDS image swizzles each row's 16-byte units within aligned
+ * groups of eight (unit u of row r at 72 r + (u ^ ((r >> 1) & 7))): the 16
+ * rows a lane group reads at one column then fall on distinct banks. */
+constexpr int RG_NB = 8;                              /* Q4_K blocks of a row */
+constexpr int RG_UNITS = RG_NB * 9;                   /* 16-byte units of a 1152-byte row */
+constexpr int RG_SLAB = 16 * RG_UNITS * 16;           /* 18,432 bytes: one matrix's 16 rows */
+constexpr int RG_COPIES = RG_SLAB / 1024;             /* 18 copies of 1 KiB */
+constexpr int RG_SLOTS = 4;
+constexpr int RG_CW = 8, RG_LW = 4;                   /* compute and loader waves */
+constexpr int RG_LC = RG_COPIES / 2;                  /* copies a loader wave issues per item */
+constexpr int RG_NT = 64 * (RG_CW + RG_LW);
+static_assert(RG_SLAB % 1024 == 0, "whole copies");
+static_assert(RG_UNITS % 8 == 0, "the swizzle stays inside a row");
+
+__device__ inline uint32_t rg_unit(int r, int u) { return (uint32_t)(RG_UNITS * r + (u ^ ((r >> 1) & 7))); }
+
+struct RgX {   /* a compute lane's q8 operands of one run, blocks c % 4 and c % 4 + 4 */
+    long xb[2][8];
+    uint32_t bs0[2], bs1[2], xd[2];
+};
+
+__global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[RG_SLOTS][2][RG_SLAB];
+    __shared__ __attribute__((aligned(16))) float red[2][RG_CW][4][64];   /* by item parity */
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              c16 = lane & 15;
+    const bool loader = w >= RG_CW;
+    const int i0 = ldc(a.rg_off, blockIdx.x), n = ldc(a.rg_off, blockIdx.x + 1) - i0;
+    if (n <= 0) return;   /* uniform */
+    const uint32_t mbytes = (uint32_t)a.I * (RG_NB * Q4B);
+    const Q8Rows &q = a.xq;
+    const Buf qs_b = make_buf(q.qs, (uint32_t)((size_t)a.k * RG_NB * 256));
+    const Buf s32_b = make_buf(q.s32, (uint32_t)((size_t)a.k * RG_NB * 32));
+    const Buf d_b = make_buf(q.d, (uint32_t)((size_t)a.k * RG_NB * 4));
+    const int mw = (w >> 2) & 1, bw = w & 3;   /* a compute wave's matrix and first block */
+
+    /* item j of the list (j < n): expert index, slab, pass */
+    auto item = [&](int j) { return ldc(a.rg_items, (size_t)(i0 + j)); };
+    /* what a loader wave needs of item j, read through the scalar path a
+     * step ahead of its use: its matrix (half (w - RG_CW) % 2 of matrix
+     * (w - RG_CW) / 2 is the wave's to copy), slab, pairs, biases */
+    struct Info {
+        uint64_t base;
+        int s, tp, p0, np;
+        const float *gb, *ub;
+    };
+    auto info_of = [&](int j) __attribute__((always_inline)) {
+        Info f;
+        const int it = item(min(j, n - 1)), ei = it >> 16, e = ldc(&a.ed[ei].e, 0);
+        f.base = (w - RG_CW) >> 1 ? ldc(&a.ed[ei].up, 0) : ldc(&a.ed[ei].gate, 0);
+        f.s = (it >> 8) & 255;
+        f.tp = 16 * (it & 255);
+        f.p0 = ldc(&a.ed[ei].p0, 0);
+        f.np = ldc(&a.ed[ei].np, 0);
+        f.gb = a.gbias ? (const float *)(uintptr_t)ldc(a.gbias, e) : nullptr;
+        f.ub = a.ubias ? (const float *)(uintptr_t)ldc(a.ubias, e) : nullptr;
+        return f;
+    };
+    /* the loader wave's share of item j's copies, 9 KiB */
+    auto issue_copies = [&](int j, const Info &f) __attribute__((always_inline)) {
+        const int s = f.s, m = (w - RG_CW) >> 1, k0 = RG_LC * ((w - RG_CW) & 1);
+        const u32x4 desc = buf_desc((const void *)(uintptr_t)f.base, mbytes);
+        uint8_t *dst = &ring[j % RG_SLOTS][m][0];
+#pragma unroll
+        for (int kk = 0; kk < RG_LC; kk++) {
+            const int k = k0 + kk, P = 64 * k + lane, r = P / RG_UNITS, u = (P % RG_UNITS) ^ ((r >> 1) & 7);
+            copy_lanes_nt(desc, (uint32_t)(s * 16 + r) * (RG_NB * Q4B) + 16u * (uint32_t)u, lds_addr(dst + 1024 * k));
+        }
+    };
+    /* the loader wave waits for item j's copies, k items' copies issued after them */
+    auto wait_copies_behind = [&](int k) __attribute__((always_inline)) {
+        if (k >= 2) wait_copies_but<2 * RG_LC>();
+        else if (k == 1) wait_copies_but<RG_LC>();
+        else wait_copies_but<0>();
+    };
+    /* the compute lane's operands of item j's run: pair t + c16 of the expert */
+    auto load_x = [&](int j, RgX &x) __attribute__((always_inline)) {
+        const int it = item(j), ei = it >> 16, tp = 16 * (it & 255);
+        const int p0 = ldc(&a.ed[ei].p0, 0), np = ldc(&a.ed[ei].np, 0);
+        uint32_t rj[16];
+#pragma unroll
+        for (int jj = 0; jj < 16; jj++) rj[jj] = (uint32_t)ldc(a.p_row, (size_t)min(p0 + tp + jj, a.P - 1));
+        uint32_t prow = 0u;
+#pragma unroll
+        for (int jj = 0; jj < 16; jj++) prow = c16 == jj ? rj[jj] : prow;
+        const bool pv = tp + c16 < np;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t qb = prow * RG_NB + (uint32_t)(bw + 4 * h);
+#pragma unroll
+            for (int s = 0; s < 8; s++)
+                x.xb[h][s] = as_long(ld8(qs_b, pv ? qb * 256u + 64u * (s >> 1) + 32u * (s & 1) + 8u * g : OOB));
+            x.bs0[h] = ld4(s32_b, pv ? qb * 32u + 4u * g : OOB);
+            x.bs1[h] = ld4(s32_b, pv ? qb * 32u + 16u + 4u * g : OOB);
+            x.xd[h] = ld4(d_b, pv ? qb * 4u : OOB);
+        }
+    };
+    /* compute item j from its slot with operands x: the wave's two blocks of
+     * its matrix, their sums to red */
+    auto compute = [&](int j, const RgX &x) __attribute__((always_inline)) {
+        const uint8_t *sb = &ring[j % RG_SLOTS][mw][0];
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int b = bw + 4 * h;
+            float xdv[4];
+#pragma unroll
+            for (int v = 0; v < 4; v++) xdv[v] = __uint_as_float(__shfl(x.xd[h], 4 * g + v, 64));
+            const Q4Hdr hr = q4_hdr(*(const u32x4 *)(sb + 16 * rg_unit(c16, 9 * b)));
+            v4f im = {0.f, 0.f, 0.f, 0.f};
+            im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int)x.bs0[h], (float)byte_of(hr.mnl, g), im, 0, 0, 0);
+            im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int)x.bs1[h], (float)byte_of(hr.mnh, g), im, 0, 0, 0);
+            int isc[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int jg = 0; jg < 4; jg++) {
+                const u32x2 qq = *(const u32x2 *)(sb + 16 * rg_unit(c16, 9 * b + 1 + 2 * jg + (g >> 1)) + 8 * (g & 1));
+                u32x2 lo, hi;
+                lo.x = qq.x & 0x0F0F0F0Fu;
+                lo.y = qq.y & 0x0F0F0F0Fu;
+                hi.x = (qq.x >> 4) & 0x0F0F0F0Fu;
+                hi.y = (qq.y >> 4) & 0x0F0F0F0Fu;
+                const v4i dl = mma(x.xb[h][2 * jg], as_long(lo));
+                const v4i dh = mma(x.xb[h][2 * jg + 1], as_long(hi));
+                const uint32_t scw = jg < 2 ? hr.scl : hr.sch;
+                const int s0 = byte_of(scw, 2 * (jg & 1)), s1 = byte_of(scw, 2 * (jg & 1) + 1);
+#pragma unroll
+                for (int v = 0; v < 4; v++) isc[v] += __mul24(s0, dl[v]) + __mul24(s1, dh[v]);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) acc[v] += xdv[v] * (hr.d * (float)isc[v] - hr.dmin * im[v]);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; v++) red[j & 1][w][v][lane] = acc[v];
+    };
+    /* the loader threads, one (pair, row) each: the gate and up waves' sums
+     * in wave order, the activation, the hidden values of item j; the sums
+     * of pair 4 g + v and row c16 sit in lane 16 g + c16, register v */
+    auto finish = [&](int j, const Info &fi) __attribute__((always_inline)) {
+        const int s = fi.s, tp = fi.tp, p0 = fi.p0, np = fi.np;
+        const float *gb = fi.gb, *ub = fi.ub;
+        {
+            const int f = tid - 64 * RG_CW, jj = f >> 4, rr = f & 15, ln = 16 * (jj >> 2) + rr, v = jj & 3;
+            float gv = 0.f, uv = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < 4; ww++) {
+                gv += red[j & 1][ww][v][ln];
+                uv += red[j & 1][4 + ww][v][ln];
+            }
+            const int r = 16 * s + rr;
+            if (gb) gv += gb[r];
+            if (ub) uv += ub[r];
+            if (tp + jj < np) a.hidden[(size_t)(p0 + tp + jj) * a.I + r] = act_fn(a.act, gv, uv);
+        }
+    };
+    /* a run: items of one expert and pass */
+    auto run_end = [&](int s) {
+        const int key = item(s) & ~0xFF00;   /* expert and pass */
+        int e = s + 1;
+        while (e < n && (item(e) & ~0xFF00) == key) e++;
+        return e;
+    };
+
+    /* The loader waves and the compute waves run loops of their own (so the
+     * compiler's waits for the compute waves' operand loads never land in
+     * the loaders' code), meeting at one barrier an item.  Between the
+     * barriers of items i and i + 1 the compute waves compute item i
+     * (reading slot i % 4, writing red[i % 2]) while the loaders copy item
+     * i + 3 into item i - 1's slot and finish item i - 1 (reading
+     * red[(i - 1) % 2]): each wave reaches the next barrier only after its
+     * part. */
+    if (loader) {
+        Info fc, ff;   /* the info of the next copies and of the next item to finish */
+        for (int j = 0; j < 3 && j < n; j++) issue_copies(j, info_of(j));
+        fc = info_of(3);
+        ff = info_of(0);
+        for (int i = 0; i < n; i++) {
+            wait_copies_behind(min(2, n - 1 - i));
+            /* a loader writes no LDS itself: its barrier leaves the scalar
+             * reads of the next items' info in flight */
+            asm volatile("s_barrier" ::: "memory");
+            if (i + 3 < n) issue_copies(i + 3, fc);
+            if (i > 0) {
+                finish(i - 1, ff);
+                ff = info_of(i);
+            }
+            fc = info_of(i + 4);
+        }
+        asm volatile("s_barrier" ::: "memory");   /* item n - 1's sums are in LDS */
+        finish(n - 1, ff);
+        wait_copies();   /* no copy outlives the workgroup */
+        return;
+    }
+    /* A run's operands are loaded into a staging set while the run before is
+     * computed, three items before its end (ahead of the copies of the next
+     * run's first items, which they would otherwise wait behind), and taken
+     * as the values of an empty asm statement when the run starts: the
+     * compiler waits for the loads there and not at their uses, and the set
+     * in use never has loads in flight. */
+    auto settle = [&](RgX &x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+            asm volatile(""
+                         : "+v"(x.xb[h][0]), "+v"(x.xb[h][1]), "+v"(x.xb[h][2]), "+v"(x.xb[h][3]), "+v"(x.xb[h][4]),
+                           "+v"(x.xb[h][5]), "+v"(x.xb[h][6]), "+v"(x.xb[h][7]), "+v"(x.bs0[h]), "+v"(x.bs1[h]),
+                           "+v"(x.xd[h]));
+    };
+    RgX cur, stage;
+    load_x(0, cur);
+    settle(cur);
+    int re = run_end(0);
+    for (int i = 0; i < n;) {
+        const int pf = max(i, re - 3);
+        for (; i < re; i++) {
+            if (i == pf && re < n) load_x(re, stage);
+            bar_lds();   /* item i's slab has landed, item i - 1's sums are read */
+            compute(i, cur);
+        }
+        if (i < n) {
+            re = run_end(i);
+            settle(stage);
+            cur = stage;
+        }
+    }
+    bar_lds();   /* item n - 1's sums are in LDS */
+}
+
 /* Phase B: part[p][r] = w_p * (down_r . hq_p + bd[r]) for the 64 rows r of
  * slab blockIdx.x and every pair p of active expert a.ed[blockIdx.y]; Q6_K
  * down matrix of I = 256 nbi columns.  Wave w owns rows 16 w .. 16 w + 15 of
@@ -483,7 +728,27 @@ bool qk_grouped_fits(const MoeArgs &a) {
            (uint64_t)a.P * a.I < lim && (uint64_t)a.k * a.D < lim && (uint64_t)a.P * (a.I / 256) * 64 < lim;
 }
 
+bool qa_ring_shape(int gate_fmt, int D, int I) { return gate_fmt == TG_FMT_Q4K && D == 256 * RG_NB && I % 16 == 0 && I <= 4096; }
+
+/* Items in the order expert (busiest first), pass, slab, cut into G
+ * contiguous stretches of equal length: each workgroup's stretch is a few
+ * runs of one (expert, pass), and the passes of an expert run at about the
+ * same time on neighbouring workgroups, so their slabs' second reads come
+ * from the caches. */
+void qa_ring_items(const ExpDesc *ed, int n_act, int I, int G, std::vector<int> &items, std::vector<int> &off) {
+    items.clear();
+    for (int ei = 0; ei < n_act; ei++)
+        for (int t = 0; t < std::max(1, (ed[ei].np + 15) / 16); t++)
+            for (int s = 0; s < I / 16; s++) items.push_back(ei << 16 | s << 8 | t);
+    off.resize(G + 1);
+    for (int w = 0; w <= G; w++) off[w] = (int)((int64_t)items.size() * w / G);
+}
+
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {
+    if (a.rg_items && qa_ring_shape(a.gate_fmt, a.D, a.I)) {
+        hipLaunchKernelGGL(k_moe_qa_ring, dim3(a.rg_n), dim3(RG_NT), 0, st, a);
+        return;
+    }
     const dim3 grid((a.I + 15) / 16, a.n_act_a);
     if (a.D <= 256 * NW * 2) hipLaunchKernelGGL(k_moe_qa<2>, grid, dim3(NT), qa_lds_bytes(a.D), st, a);
     else hipLaunchKernelGGL(k_moe_qa<QA_WB_MAX>, grid, dim3(NT), qa_lds_bytes(a.D), st, a);

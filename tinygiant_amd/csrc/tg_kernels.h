@@ -8,6 +8,7 @@
 #include <stdint.h>
 
 #include <functional>
+#include <vector>
 
 #include "tg_common.h"
 #include "tg_device.hpp"
@@ -56,6 +57,8 @@ struct MoeArgs {
     unsigned *ctr;                          /* [ctr_n] row-tile tickets of the fused combine, zero between calls, or null */
     int ctr_n;
     int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */
+    const int *rg_items, *rg_off;           /* the persistent gate/up phase's items and each workgroup's range, or null */
+    int rg_n;                               /* its workgroups */
 };
 
 int items_per_row(int fmt, int ncols);
@@ -118,6 +121,13 @@ int grouped_min_rows();
  * slabs (tg_grouped_k.hip), taken by launch_moe for layers whose experts
  * hold at least qk_min_rows() pairs (0: never) */
 bool qk_grouped_fits(const MoeArgs &a);
+/* The persistent int8 MFMA gate/up phase (Q4_K, D = 2048): its items, (index
+ * ei into the busiest-first active experts, 16-row slab s, pass t of 16
+ * pairs) as ei << 16 | s << 8 | t, and off[0 .. G] the range of each of G
+ * workgroups.  False when the shape is not the phase's. */
+bool qa_ring_shape(int gate_fmt, int D, int I);
+void qa_ring_items(const ExpDesc *ed, int n_act, int I, int G, std::vector<int> &items, std::vector<int> &off);
+constexpr int QA_RING_MAX_G = 1024;
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st);
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st);
 void set_qk_min_rows(int rows);
