@@ -149,12 +149,13 @@ def _check(orc, c, window, got, ref):
 Q4K, Q6K, Q80, F16 = O.FMT_Q4K, O.FMT_Q6K, O.FMT_Q80, O.FMT_F16
 
 
-@pytest.mark.parametrize("kv_len", [0, 31, 300, 1500])
+@pytest.mark.parametrize("kv_len", [0, 31, 300, 1023, 1500])
 def test_attention_qwen3_shape(tg, orc, kv_len):
     """Qwen3-30B-A3B attention: D 2048, 32 query heads, 4 KV heads of 128,
     q4_K q/k/o, q6_K v, QK norm, no biases, full attention.  Spans up to 32
-    chunks of 32 positions combine inside the partial kernel; 1501 positions
-    (47 chunks) take the separate combine kernel."""
+    chunks of 32 positions (1024 positions, kv_len 1023) combine inside the
+    partial kernel; 1501 positions (47 chunks) take the separate combine
+    kernel."""
     say("attention qwen3", kv_len)
     c = _case(10 + kv_len, 2048, 32, 4, 128, (Q4K, Q4K, Q6K, Q4K), max(512, kv_len + 1), kv_len, norms=True)
     got = _gpu(tg, c, 0)
