@@ -1560,7 +1560,7 @@ TG_API void tg_hip_head_argmax_dev(int fmt, const void *mat_dev, const float *in
     Q8Rows q = q8_view(q8p, k, ncols, xin);
     /* the fused kernel's keys and finish counter start at zero: the q8
      * kernel before it clears them */
-    const bool fast = head_fast_ok(fmt, ncols, k);
+    const bool fast = head_fast_ok(fmt, ncols, nrows, k);
     unsigned long long *clr = fast ? keys : nullptr;
     if (norm_w_dev) {
         /* RMSNorm fused with q8 of the normed rows */

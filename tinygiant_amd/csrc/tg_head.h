@@ -10,8 +10,9 @@
 
 namespace tg {
 
-/* The fused kernel covers Q6_K heads of 2048 columns and 1..16 rows. */
-bool head_fast_ok(int fmt, int ncols, int k);
+/* The fused kernel covers Q6_K heads of 2048 columns, up to 2^20 vocab rows
+ * and 1..16 input rows. */
+bool head_fast_ok(int fmt, int ncols, int nrows, int k);
 /* best[0..k) receive packed argmax keys and best[16] counts finished
  * workgroups: all 17 words must be zero at launch (launch_rms_norm_q8 and
  * launch_quantize clear them); the last workgroup writes idx[k] and val[k]

@@ -12,6 +12,9 @@
  *                   and dots them with the k q8 rows staged in LDS; the 16
  *                   lanes of a row are summed by DPP; the next row group's
  *                   weights are loaded while the current one is computed.
+ *                   A wave's group (4 rows, contiguous) is loaded as aligned
+ *                   16-byte pieces, 1 KiB an instruction, and regrouped into
+ *                   half-blocks through the wave's own LDS region.
  *                   Each lane ends with one input row's sum (a DPP
  *                   reduce-scatter over the 16 lanes); each workgroup keeps
  *                   the best (logit, row) per input row, commits it with one
@@ -55,8 +58,11 @@ constexpr int HPR = 2 * NBH;    /* half-blocks (lanes) per row */
 constexpr int RPW = 64 / HPR;   /* rows per wave */
 constexpr int HRB = NBH * 210;  /* Q6_K head row bytes */
 constexpr int XST = 144;        /* LDS stride of a staged 128-value half (bank spread) */
-constexpr int HT = 256;         /* threads per head workgroup */
+constexpr int HT = 512;         /* threads per head workgroup */
 constexpr int HW = HT / 64;
+constexpr int HGB = RPW * HRB;  /* a wave's row group: 6,720 contiguous bytes */
+constexpr int HGP = HGB / 1024; /* its whole KiB (6), then 36 lanes of 16 bytes */
+static_assert(HGB % 16 == 0 && HGB - 1024 * HGP <= 1024, "group pieces");
 
 __device__ inline uint64_t argmax_key(float v, uint32_t row) {
     uint32_t u = v == 0.f ? 0u : __float_as_uint(v);   /* -0 ties with +0, as in numpy */
@@ -73,33 +79,69 @@ __device__ inline float key_value(uint64_t key) {
 struct HHalf {
     u32x4 la0, la1, lb0, lb1, h0, h1;
     u32x2 sc;
-    uint32_t d;
+    uint32_t d;   /* the f16 bits */
 };
-/* Its loads, tracked by the compiler, from byte `off` of the matrix (the
+/* A wave's row group as lane pieces: lane l holds bytes 16 l + 1024 j of
+ * it (j < HGP), and lanes l < 36 also bytes 1024 HGP + 16 l.  Each load
+ * instruction reads 1 KiB of contiguous, aligned bytes; loads of the lanes'
+ * own half-blocks (16-byte pieces 105 bytes apart, half of them at 2 mod 4)
+ * touched eight times as many cache lines and ran ~1.25x slower. */
+struct HGroup {
+    u32x4 p[HGP + 1];
+};
+/* Its loads, tracked by the compiler, from byte `base` of the matrix (the
  * whole offset in the VGPR: a raw buffer's range check covers that offset
- * and not the SGPR one, and loads past the matrix must read zero) */
-__device__ inline HHalf load_hhalf(Buf b, uint32_t off, int h) {
-    HHalf r;
-    const int ql = (int)off + 64 * h, qh = (int)off + 128 + 32 * h;
-    r.la0 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql, 0, 0);
-    r.la1 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql + 16, 0, 0);
-    r.lb0 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql + 32, 0, 0);
-    r.lb1 = __builtin_amdgcn_raw_buffer_load_b128(b.r, ql + 48, 0, 0);
-    r.h0 = __builtin_amdgcn_raw_buffer_load_b128(b.r, qh, 0, 0);
-    r.h1 = __builtin_amdgcn_raw_buffer_load_b128(b.r, qh + 16, 0, 0);
-    r.sc = __builtin_amdgcn_raw_buffer_load_b64(b.r, (int)off + 192 + 8 * h, 0, 0);
-    r.d = __builtin_amdgcn_raw_buffer_load_b32(b.r, (int)off + 206, 0, 0);
-    return r;
+ * and not the SGPR one, and loads past the matrix read zero; the lanes past
+ * the group's last piece take an offset beyond any head and read nothing) */
+__device__ inline HGroup load_group(Buf b, uint32_t base, int lane) {
+    HGroup g;
+    const int o = (int)(base + 16u * (uint32_t)lane);
+#pragma unroll
+    for (int j = 0; j < HGP; j++) g.p[j] = __builtin_amdgcn_raw_buffer_load_b128(b.r, o + 1024 * j, 0, 0);
+    const bool tail = 16 * lane < HGB - 1024 * HGP;
+    g.p[HGP] = __builtin_amdgcn_raw_buffer_load_b128(b.r, tail ? o + 1024 * HGP : (int)0x80000000u, 0, 0);
+    return g;
 }
-
-/* An empty statement that reads every register of a half-block: the
- * compiler waits for its loads there, on every path (the decode below may
- * otherwise be sunk into the branch of the first input row, and a path that
- * skips it would leave the loads pending into the next turn of the loop,
- * where their registers get reused and the compiler then waits for every
- * load, the prefetch included). */
-__device__ inline void consume(const HHalf &r) {
-    asm volatile("" ::"v"(r.la0), "v"(r.la1), "v"(r.lb0), "v"(r.lb1), "v"(r.h0), "v"(r.h1), "v"(r.sc), "v"(r.d));
+/* An empty statement that reads every register of a group: the compiler
+ * waits for its loads there, on every path (a path that skipped a piece
+ * would leave its load pending into the next turn of the loop, where its
+ * registers get reused and the compiler then waits for every load, the
+ * prefetch included). */
+__device__ inline void consume(const HGroup &g) {
+    asm volatile("" ::"v"(g.p[0]), "v"(g.p[1]), "v"(g.p[2]), "v"(g.p[3]), "v"(g.p[4]), "v"(g.p[5]), "v"(g.p[6]));
+}
+static_assert(HGP == 6, "consume() names every piece");
+/* The group into the wave's LDS region, as the matrix lays it out */
+__device__ inline void stage_group(uint8_t *wl, const HGroup &g, int lane) {
+#pragma unroll
+    for (int j = 0; j < HGP; j++) *reinterpret_cast<u32x4 *>(wl + 1024 * j + 16 * lane) = g.p[j];
+    if (16 * lane < HGB - 1024 * HGP) *reinterpret_cast<u32x4 *>(wl + 1024 * HGP + 16 * lane) = g.p[HGP];
+}
+/* The half-block h of the block that starts at byte a of the region.  A
+ * block starts at 210 b of its row, so the fields of odd blocks lie at
+ * 2 mod 4: the covering dwords are read from a & ~3 and shifted by a & 3
+ * (0 or 2) bytes. */
+__device__ inline HHalf read_half(const uint8_t *wl, uint32_t a, int h) {
+    const uint32_t sh = a & 3u;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(wl + (a & ~3u));
+    auto al = [&](const uint32_t *q, int i) { return __builtin_amdgcn_alignbyte(q[i + 1], q[i], sh); };
+    uint32_t l[17], t[9], c[3];
+#pragma unroll
+    for (int i = 0; i < 17; i++) l[i] = p[16 * h + i];
+#pragma unroll
+    for (int i = 0; i < 9; i++) t[i] = p[32 + 8 * h + i];
+#pragma unroll
+    for (int i = 0; i < 3; i++) c[i] = p[48 + 2 * h + i];
+    HHalf r;
+    r.la0 = u32x4{al(l, 0), al(l, 1), al(l, 2), al(l, 3)};
+    r.la1 = u32x4{al(l, 4), al(l, 5), al(l, 6), al(l, 7)};
+    r.lb0 = u32x4{al(l, 8), al(l, 9), al(l, 10), al(l, 11)};
+    r.lb1 = u32x4{al(l, 12), al(l, 13), al(l, 14), al(l, 15)};
+    r.h0 = u32x4{al(t, 0), al(t, 1), al(t, 2), al(t, 3)};
+    r.h1 = u32x4{al(t, 4), al(t, 5), al(t, 6), al(t, 7)};
+    r.sc = u32x2{al(c, 0), al(c, 1)};
+    r.d = (p[52] >> (8u * sh)) & 0xFFFFu;
+    return r;
 }
 
 __device__ inline uint32_t pick(const u32x4 &v, int c) { return c == 0 ? v.x : c == 1 ? v.y : c == 2 ? v.z : v.w; }
@@ -144,7 +186,7 @@ constexpr int log2_of(int n) { return n <= 1 ? 0 : n == 2 ? 1 : n == 4 ? 2 : n =
  * start at zero (cleared by the kernel that quantizes x).  The last
  * workgroup to finish writes idx[j] / val[j]. */
 template <int K, bool LOGITS>
-__global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
+__global__ __launch_bounds__(HT, K <= 9 ? 4 : 2) void k_head_q6k(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
                                                  float *logits, unsigned long long *best, int32_t *idx, float *val) {
     constexpr int N = pow2_at_least(K);
     __shared__ __attribute__((aligned(16))) int8_t xq[K][HPR * XST];
@@ -152,6 +194,7 @@ __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(con
     __shared__ float xd[K][NBH];
     __shared__ unsigned long long wb_best[K][HW * RPW];
     __shared__ int last_wg;
+    __shared__ __attribute__((aligned(16))) uint8_t wgrp[HW][HGB];   /* each wave's staged group */
 
     /* stage the k q8 rows: 128-value halves at XST strides */
     for (int t = threadIdx.x; t < k * NBH * 64; t += HT) {
@@ -182,13 +225,21 @@ __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(con
      * argmax-only kernel stores nothing in the loop: with stores pending
      * beside the loads the compiler's waits become vmcnt(0). */
     const Buf wbuf = make_buf(W, (uint32_t)((size_t)nrows * HRB));
-    const uint32_t lane_off = (uint32_t)(rsub * HRB + b * 210);
-    auto group_at = [&](int qq) { return load_hhalf(wbuf, lane_off + (uint32_t)(RPW * qq * HRB), h); };
+    uint8_t *wl = wgrp[threadIdx.x >> 6];
+    const uint32_t lane_off = (uint32_t)(rsub * HRB + b * 210);   /* the lane's block in the group */
+    auto group_at = [&](int qq) { return load_group(wbuf, (uint32_t)(HGB * qq), lane); };
     int q = gw;
-    auto step = [&](HHalf &cur, HHalf &nxt) {
+    auto step = [&](HGroup &grp, HGroup &nxt) {
         nxt = group_at(q + nw);
         __builtin_amdgcn_sched_barrier(0);
-        consume(cur);
+        consume(grp);
+        /* the previous group's reads of the region are issued before these
+         * writes (the LDS runs a wave's instructions in order), and the
+         * reads below after them */
+        asm volatile("" ::: "memory");
+        stage_group(wl, grp, lane);
+        asm volatile("" ::: "memory");
+        const HHalf cur = read_half(wl, lane_off, h);
         const uint32_t row = (uint32_t)(RPW * q + rsub);
         /* 6-bit codes of the half (q = ql nibble | qh pair << 4), decoded once */
         const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x30303030u;
@@ -206,7 +257,7 @@ __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(con
         int sc[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) sc[i] = (int)(int8_t)((i < 4 ? cur.sc.x : cur.sc.y) >> (8 * (i & 3)));
-        const float dw = ref_f16(cur.d >> 16);
+        const float dw = ref_f16(cur.d);
         float vv[N];
 #pragma unroll
         for (int j = 0; j < N; j++) vv[j] = 0.f;
@@ -246,7 +297,7 @@ __global__ __launch_bounds__(HT, (K == 4 || K == 5) ? 4 : 1) void k_head_q6k(con
      * loads pending, and the compiler would wait for them there), then the
      * odd one */
     const int nsteps = q < nq ? (nq - 1 - q) / nw + 1 : 0;
-    HHalf s0 = group_at(q), s1;
+    HGroup s0 = group_at(q), s1;
     int i = 0;
     for (; i + 2 <= nsteps; i += 2) {
         step(s0, s1);
@@ -520,7 +571,11 @@ __global__ void k_argmax_finish(const unsigned long long *best, int k, int32_t *
     if (val) val[j] = key_value(key);
 }
 
-bool head_fast_ok(int fmt, int ncols, int k) { return fmt == TG_FMT_Q6K && ncols == NBH * 256 && k >= 1 && k <= 16; }
+/* At most 2^20 rows: a head (1.76 GB) and the groups read past its end stay
+ * below 2^31 bytes, where the tail lanes' offset points. */
+bool head_fast_ok(int fmt, int ncols, int nrows, int k) {
+    return fmt == TG_FMT_Q6K && ncols == NBH * 256 && nrows >= 1 && nrows <= (1 << 20) && k >= 1 && k <= 16;
+}
 
 /* From this many input rows the int8 MFMA kernel reads the head: its work
  * does not grow with k (151936 x 2048: 69-72 us for every k), the v_dot4
@@ -552,14 +607,21 @@ void launch_head_q6k(const uint8_t *W, int nrows, const Q8Rows &x, int k, float 
         return;
     }
     const int nq = (nrows + RPW - 1) / RPW;
-    const int grid = std::max(1, std::min(cus * 4, (nq + HW - 1) / HW));
+    /* one round of workgroups: each walks its groups with a fixed stride, so
+     * a second round would double the time */
+    auto launch = [&](const void *fn, int &occ) {
+        if (occ < 0 && (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, fn, HT, 0) != hipSuccess || occ < 1)) occ = 1;
+        const int grid = std::max(1, std::min(std::max(cus, 1) * occ, (nq + HW - 1) / HW));
+        void *args[] = {(void *)&W, (void *)&nrows, (void *)&x, (void *)&k, (void *)&logits, (void *)&best, (void *)&idx,
+                        (void *)&val};
+        (void)hipLaunchKernel(fn, dim3(grid), dim3(HT), args, 0, st);
+    };
 /* k is rounded up to an instantiated K; rows j >= k skip their dots */
-#define TG_HEAD(KK)                                                                                         \
-    do {                                                                                                    \
-        if (logits)                                                                                         \
-            hipLaunchKernelGGL((k_head_q6k<KK, true>), dim3(grid), dim3(HT), 0, st, W, nrows, x, k, logits, best, idx, val);  \
-        else                                                                                                \
-            hipLaunchKernelGGL((k_head_q6k<KK, false>), dim3(grid), dim3(HT), 0, st, W, nrows, x, k, logits, best, idx, val); \
+#define TG_HEAD(KK)                                                                  \
+    do {                                                                             \
+        static int occ_l = -1, occ_n = -1;                                           \
+        if (logits) launch(reinterpret_cast<const void *>(&k_head_q6k<KK, true>), occ_l);  \
+        else launch(reinterpret_cast<const void *>(&k_head_q6k<KK, false>), occ_n);        \
     } while (0)
     if (k <= 1) TG_HEAD(1);
     else if (k <= 2) TG_HEAD(2);
