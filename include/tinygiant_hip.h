@@ -339,7 +339,7 @@ int tg_hip_set_moe_qk_min_rows(int rows);
  * d * d_x * sum is added in block order, as dot_q6k_q8 does
  * (csrc/libtinygiant.c:403-443); below `k` the v_dot4 kernel runs (its work
  * grows with the row count); 0 keeps every call on the v_dot4 kernel.
- * Default 9.  Returns the previous setting.  No counterpart in the
+ * Default 8.  Returns the previous setting.  No counterpart in the
  * reference. */
 int tg_hip_set_head_mfma_min_k(int k);
 /* Q4_K / Q6_K expert layers, and MXFP4 ones below the MFMA threshold, run

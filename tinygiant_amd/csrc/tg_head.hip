@@ -20,7 +20,7 @@
  *                   the best (logit, row) per input row, commits it with one
  *                   64-bit atomic max, and the last workgroup to finish
  *                   writes the argmax.
- *   k_head_q6k_mfma the same head on int8 MFMA for 9 or more rows: 16 vocab
+ *   k_head_q6k_mfma the same head on int8 MFMA for 8 or more rows: 16 vocab
  *                   rows an item staged in LDS, one 256-block per wave, logits formed and
  *                   added block by block as the reference does (bit-equal
  *                   to it where its float block sums are exact).
@@ -578,10 +578,11 @@ bool head_fast_ok(int fmt, int ncols, int nrows, int k) {
 }
 
 /* From this many input rows the int8 MFMA kernel reads the head: its work
- * does not grow with k (151936 x 2048: 69-72 us for every k), the v_dot4
- * kernel's does (70-75 us at k = 9, 85-87 at 10, 91 at 12, 111 at 16). */
+ * does not grow with k (151936 x 2048: 68-70 us for every k), the v_dot4
+ * kernel's does (61-62 us at k = 5, 72-78 at 8, 76-79 at 9, 102-104 at 12,
+ * 121-123 at 16). */
 #ifndef TG_HEAD_MFMA_MIN_K
-#define TG_HEAD_MFMA_MIN_K 9
+#define TG_HEAD_MFMA_MIN_K 8
 #endif
 static int g_head_mfma_min_k = TG_HEAD_MFMA_MIN_K;
 int set_head_mfma_min_k(int k) {
