@@ -167,6 +167,67 @@ __device__ inline WB b_load(const Tab &tb, int item, int wave, int lane) {
     return w;
 }
 
+/* ---- down items staged in LDS ----
+ * A workgroup's first B_STAGE down items of a layer are copied into LDS
+ * (direct-to-LDS copies, 1 KiB an instruction) at the end of the layer
+ * before, while it waits for that layer's rows of x; the rest stream through
+ * registers, one item ahead.  An item is 64 rows of 630 bytes, contiguous and
+ * 16-byte aligned in the down matrix. */
+constexpr int B_STAGE = 2;
+constexpr int B_SLOT = B_ROWS * (int)DRB;            /* 40,320 bytes */
+constexpr int B_COP = (B_SLOT + 1023) / 1024;        /* 40 copies, the last of 24 lanes */
+constexpr int B_LAST = (B_SLOT - 1024 * (B_COP - 1)) / 16;
+static_assert(B_SLOT % 16 == 0 && B_LAST > 0 && B_LAST <= 64, "whole 16-byte pieces");
+/* copies of items i0 .. i0 + B_STAGE - 1 (those below i1) into the slots;
+ * their count */
+__device__ inline int b_stage(const Tab &tb, int i0, int i1, uint8_t *slots, int wave, int lane) {
+    const int ns = ufl(i1 - i0 < B_STAGE ? i1 - i0 : B_STAGE);
+    for (int t = 0; t < ns; t++) {
+        const int item = i0 + t;
+        const RowsExp &e = tb.ex[item / B_TILES];
+        const u32x4 dd = buf_desc(ufl_ptr(e.down), DMB);
+        const uint32_t src = (uint32_t)(item % B_TILES) * (uint32_t)B_SLOT + 16u * (uint32_t)lane;
+        for (int c = wave; c < B_COP; c += NWV)
+            if (c < B_COP - 1 || lane < B_LAST) copy_lanes(dd, src + 1024u * (uint32_t)c, lds_addr(slots + t * B_SLOT + 1024 * c));
+    }
+    return ns > 0 ? ns : 0;
+}
+/* 16, 8 and 4 bytes at LDS offset a (a even): the covering dwords from
+ * a & ~3, shifted by a & 3 bytes (rows of 630 bytes and blocks of 210 put the
+ * fields of odd rows and odd blocks at 2 mod 4) */
+__device__ inline u32x4 lds_u16(const uint8_t *base, uint32_t a) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(base + (a & ~3u));
+    const uint32_t sh = a & 3u;
+    return u32x4{__builtin_amdgcn_alignbyte(p[1], p[0], sh), __builtin_amdgcn_alignbyte(p[2], p[1], sh),
+                 __builtin_amdgcn_alignbyte(p[3], p[2], sh), __builtin_amdgcn_alignbyte(p[4], p[3], sh)};
+}
+__device__ inline u32x2 lds_u8(const uint8_t *base, uint32_t a) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(base + (a & ~3u));
+    const uint32_t sh = a & 3u;
+    return u32x2{__builtin_amdgcn_alignbyte(p[1], p[0], sh), __builtin_amdgcn_alignbyte(p[2], p[1], sh)};
+}
+/* the f16 at LDS offset a (a even) in the high half, as load_w's d word */
+__device__ inline uint32_t lds_f16_hi(const uint8_t *base, uint32_t a) {
+    const uint32_t v = *reinterpret_cast<const uint32_t *>(base + (a & ~3u));
+    return (a & 2u) ? (v & 0xFFFF0000u) : (v << 16);
+}
+/* the lane's weights of a staged item: FQ6K::load_w's bytes, from LDS */
+__device__ inline WB b_lds(const uint8_t *slot, int wave, int lane) {
+    const int sl = lane & 15, it = sl < B_ITEMS ? sl : 0;
+    const uint32_t u = (uint32_t)it & 3u, h = u >> 1, l0 = (u & 1u) * 16u;
+    WB w;
+#pragma unroll
+    for (int q = 0; q < B_PASS; q++) {
+        const uint32_t pr = (uint32_t)(32 * q + 4 * wave + (lane >> 4)) * DRB + (uint32_t)(it >> 2) * 210u;
+        w.w[q].qla = lds_u16(slot, pr + 64u * h + l0);
+        w.w[q].qlb = lds_u16(slot, pr + 64u * h + 32u + l0);
+        w.w[q].qh = lds_u16(slot, pr + 128u + 32u * h + l0);
+        w.w[q].sc = lds_u8(slot, pr + 192u + 8u * h);
+        w.w[q].d = lds_f16_hi(slot, pr + 208u);
+    }
+    return w;
+}
+
 /* gate/up + SiLU of every pair of the item's expert (k_moe_ax's sums) */
 __device__ inline void a_compute(const Tab &tb, int item, const WA &w, const uint8_t *xl, Buf hid, unsigned tag,
                                  float *dbg_hid, int wave, int lane) {
@@ -446,6 +507,7 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     __shared__ __attribute__((aligned(16))) uint8_t xl[ROWS_MAXK * XS];   /* q8 rows of x */
     __shared__ __attribute__((aligned(16))) uint8_t hl[ROWS_MAXK * HS];   /* q8 hidden rows of one expert */
     __shared__ __attribute__((aligned(16))) uint8_t tabs[2][ROWS_TAB_BYTES];   /* layer tables, by parity */
+    __shared__ __attribute__((aligned(16))) uint8_t bst[B_STAGE * B_SLOT];     /* staged down items */
     __shared__ float red[NWV];
     __shared__ unsigned s_base;
     /* a wait ran out, one word per kind of wait (x, B, C): each only goes
@@ -471,11 +533,13 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     /* C(-1): the first layer's RMSNorm and q8 */
     if (wg < k) phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, 0u, base + 1u, abort_flag, wave, lane);
     WA a0;
+    int nsb;   /* down items of the layer staged in bst */
     {
         const RowsLayer &ly = layers[0];
         const Tab tb = tab_view(tabs[0], ly.n_act, ly.P, ly.k);
         const int i0 = ly.split[wg], i1 = ly.split[wg + 1];
         a0 = a_load(tb, i0 < i1 ? i0 : -1, wave, lane);
+        nsb = b_stage(tb, ly.split[ROWS_GRID + 1 + wg], ly.split[ROWS_GRID + 2 + wg], bst, wave, lane);
     }
 
     for (int l = 0; l < L && ok; l++) {
@@ -503,27 +567,36 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
                 [&](int i, const WA &w) { a_compute(tb, i, w, xl, hid, tag, dh, wave, lane); });
         }
         if (tw) tr[1] = wall_clock64();
-        /* ---- B: each expert's hidden rows are polled when its first item starts ---- */
+        /* ---- B: each expert's hidden rows are polled when its first item
+         * starts; the first nsb items are in bst (every wave's copies have
+         * landed once it has waited for them and passed the barrier in pre) ---- */
         {
-            WB b0 = b_load(tb, ib0 < ib1 ? ib0 : -1, wave, lane);
+            wait_copies();
+            const int ibr = ib0 + nsb;   /* the first item through registers */
+            WB b0 = b_load(tb, ibr < ib1 ? ibr : -1, wave, lane);
             const Buf part = make_buf(ly.part, (uint32_t)ly.P * D * 8u);
             int cur = -1;   /* expert whose q8 hidden rows hl holds */
             bool bok = true;
+            auto pre = [&](int i, const WB &) {
+                const int s = ufl(i) / B_TILES;
+                if (s != cur) {
+                    bar_lds();   /* every wave is done with the previous rows */
+                    const bool got =
+                        b_hidden_q8(ufl(tb.ex[s].p0), ufl(tb.ex[s].np), hid, tag, abort_flag, hl, wave, lane);
+                    if (!got) s_okb = 0;   /* every wave that gave up says so */
+                    bar_lds();
+                    bok &= s_okb != 0;
+                    if (tw && cur < 0) tr[2] = wall_clock64();
+                    cur = s;
+                }
+            };
+            for (int t = 0; t < nsb; t++) {
+                pre(ib0 + t, b0);   /* the first turn passes a barrier */
+                const WB w = b_lds(bst + t * B_SLOT, wave, lane);
+                b_compute(tb, ib0 + t, w, hl, part, tag, wave, lane);
+            }
             pipe(
-                ib0, ib1, b0, [&](int i) { return b_load(tb, i, wave, lane); },
-                [&](int i, const WB &) {
-                    const int s = ufl(i) / B_TILES;
-                    if (s != cur) {
-                        bar_lds();   /* every wave is done with the previous rows */
-                        const bool got =
-                            b_hidden_q8(ufl(tb.ex[s].p0), ufl(tb.ex[s].np), hid, tag, abort_flag, hl, wave, lane);
-                        if (!got) s_okb = 0;   /* every wave that gave up says so */
-                        bar_lds();
-                        bok &= s_okb != 0;
-                        if (tw && cur < 0) tr[2] = wall_clock64();
-                        cur = s;
-                    }
-                },
+                ibr, ib1, b0, [&](int i) { return b_load(tb, i, wave, lane); }, pre,
                 [&](int i, const WB &w) { b_compute(tb, i, w, hl, part, tag, wave, lane); });
             if (!bok) {
                 ok = false;
@@ -556,6 +629,8 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
             const Tab nt = tab_view(tabs[(l + 1) & 1], nl.n_act, nl.P, nl.k);
             const int i0 = nl.split[wg], i1 = nl.split[wg + 1];
             a0 = a_load(nt, i0 < i1 ? i0 : -1, wave, lane);
+            /* the slots were last read before the barrier above */
+            nsb = b_stage(nt, nl.split[ROWS_GRID + 1 + wg], nl.split[ROWS_GRID + 2 + wg], bst, wave, lane);
         }
     }
     wait_copies();
@@ -595,54 +670,67 @@ hipError_t launch_decode_rows(const RowsLayer *layers_dev, int L, float *h_dev, 
 const void *decode_rows_fn() { return (const void *)k_decode_rows; }
 int decode_rows_threads() { return NT; }
 
-/* Item ranges of one layer.  Each active expert gets a share of the
- * workgroups in proportion to its cost (largest remainders, at least one,
- * at most one per item) and its items are split evenly over them, so a
- * workgroup works on one expert per phase: a down item that starts another
- * expert would first wait a memory round trip for that expert's hidden rows.
- * Cost of an item, relative, from per-workgroup phase times of 48-layer
- * steps: its weight bytes (36,864 B an A item, 40,320 B a B item) count 1,
- * each pair of its expert 0.33.  The down items skip workgroups 0 .. c - 1,
- * which combine the rows: they start a row's combine as soon as its last
- * partial lands. */
-static void split_phase(const int *np, int n_act, int tiles, int w0, int *s) {
+/* Item ranges of one layer.  Each active expert gets workgroups and its
+ * items are split evenly over them, so a workgroup works on one expert per
+ * phase: a down item that starts another expert would first wait a memory
+ * round trip for that expert's hidden rows.  A workgroup's time in a phase is
+ * about its items x an item's cost, fitted on per-workgroup phase times of
+ * 48-layer steps: an A item 0.91 us + 0.34 us a pair of its expert, a B item
+ * 0.90 us + 0.38 us a pair after the expert's hidden rows are in.  The split
+ * takes the smallest such time every expert can meet within the workgroups
+ * (items a workgroup = floor(T / cost), at least one), then hands the
+ * workgroups left over, one at a time, to the expert whose workgroups take
+ * longest.  Proportional shares rounded to whole workgroups had left some
+ * workgroups of the busiest experts one item over the rest (k = 5, 9 rows:
+ * 1,373-1,376 and 1,990-1,994 us a 48-layer pass against 1,283-1,295 and
+ * 1,812-1,820); a floor under the cost of an item (a CU's share of the
+ * weight stream, 1.5 us) moved workgroups off the busiest experts and was
+ * slower (1,342-1,357 and 1,908-1,916).  The down items
+ * skip workgroups 0 .. c - 1, which combine the rows: they start a row's
+ * combine as soon as its last partial lands. */
+static void split_phase(const int *np, int n_act, int tiles, int w0, double c1, int *s) {
     const int G = ROWS_GRID - w0;
-    std::vector<int> wgs(n_act, 0);
-    if (n_act > 0) {
-        double total = 0;
-        for (int e = 0; e < n_act; e++) total += 1.0 + 0.33 * np[e];
-        std::vector<std::pair<double, int>> rem;
-        int used = 0;
-        for (int e = 0; e < n_act; e++) {
-            const double share = G * (1.0 + 0.33 * np[e]) / total;
-            wgs[e] = std::min(tiles, std::max(1, (int)share));
-            used += wgs[e];
-            rem.push_back({share - (int)share, e});
-        }
-        std::sort(rem.begin(), rem.end(), [](const std::pair<double, int> &a, const std::pair<double, int> &b) {
-            return a.first > b.first || (a.first == b.first && a.second < b.second);
-        });
-        /* hand out what is left by remainder, then round robin while some
-         * expert can still take a workgroup */
-        for (size_t i = 0; used < G && i < rem.size(); i++)
-            if (wgs[rem[i].second] < tiles) {
-                wgs[rem[i].second]++;
-                used++;
+    std::vector<int> wgs(n_act, 1);
+    if (n_act > 0 && n_act <= G) {
+        std::vector<double> c(n_act);
+        for (int e = 0; e < n_act; e++) c[e] = 1.0 + c1 * np[e];   /* in units of an item without pairs */
+        /* workgroups each expert needs so that none takes longer than T */
+        auto need = [&](double T, std::vector<int> &w) {
+            long tot = 0;
+            for (int e = 0; e < n_act; e++) {
+                const int m = std::min(tiles, (int)(T / c[e] + 1e-9));
+                if (m < 1) return false;
+                w[e] = (tiles + m - 1) / m;
+                tot += w[e];
             }
-        for (bool more = true; used < G && more;) {
-            more = false;
-            for (int e = 0; e < n_act && used < G; e++)
-                if (wgs[e] < tiles) {
-                    wgs[e]++;
-                    used++;
-                    more = true;
-                }
+            return tot <= G;
+        };
+        std::vector<double> cand;
+        for (int e = 0; e < n_act; e++)
+            for (int m = 1; m <= tiles; m++) cand.push_back(m * c[e]);
+        std::sort(cand.begin(), cand.end());
+        size_t lo = 0, hi = cand.size() - 1;   /* the largest candidate needs one workgroup an expert */
+        std::vector<int> w(n_act);
+        while (lo < hi) {
+            const size_t mid = (lo + hi) / 2;
+            if (need(cand[mid], w)) hi = mid;
+            else lo = mid + 1;
         }
-        while (used > G) {   /* more experts than workgroups would need this; take from the largest */
-            int e = (int)(std::max_element(wgs.begin(), wgs.end()) - wgs.begin());
-            if (wgs[e] <= 1) break;
-            wgs[e]--;
-            used--;
+        need(cand[lo], wgs);
+        int used = 0;
+        for (int e = 0; e < n_act; e++) used += wgs[e];
+        for (; used < G; used++) {
+            int best = -1;
+            double bt = -1.0;
+            for (int e = 0; e < n_act; e++) {
+                const double t = ((tiles + wgs[e] - 1) / wgs[e]) * c[e];
+                if (wgs[e] < tiles && t > bt) {
+                    bt = t;
+                    best = e;
+                }
+            }
+            if (best < 0) break;
+            wgs[best]++;
         }
     }
     int w = w0;
@@ -657,8 +745,8 @@ static void split_phase(const int *np, int n_act, int tiles, int w0, int *s) {
 }
 
 void decode_rows_split(const int *np, int n_act, int c, int *split) {
-    split_phase(np, n_act, A_TILES, 0, split);
-    split_phase(np, n_act, B_TILES, c, split + ROWS_GRID + 1);
+    split_phase(np, n_act, A_TILES, 0, 0.34 / 0.91, split);
+    split_phase(np, n_act, B_TILES, c, 0.38 / 0.90, split + ROWS_GRID + 1);
 }
 
 }  // namespace tg
