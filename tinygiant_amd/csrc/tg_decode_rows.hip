@@ -378,6 +378,16 @@ __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
     __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0): the previous layer's store of these values is done */
     const u32x4 hv = ld1x4(hb, (uint32_t)t * 16u);
     float o[4] = {__uint_as_float(hv.x), __uint_as_float(hv.y), __uint_as_float(hv.z), __uint_as_float(hv.w)};
+    /* the next layer's RMSNorm weights, loaded now: after the partials they
+     * would add a memory round trip to every layer */
+    float nw[4] = {1.f, 1.f, 1.f, 1.f};
+    if (nx && nx->norm_w) {
+        const u32x4 wv = ld16(make_buf(nx->norm_w, D * 4u), (uint32_t)t * 16u);
+        nw[0] = __uint_as_float(wv.x);
+        nw[1] = __uint_as_float(wv.y);
+        nw[2] = __uint_as_float(wv.z);
+        nw[3] = __uint_as_float(wv.w);
+    }
     bool good = true;   /* a wave whose wait ran out goes on (the barriers below count every wave) */
     if (ly) {
         /* row r's partials, up to eight pairs at a time; a lane reloads only
@@ -441,9 +451,8 @@ __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
     for (int i = 0; i < NWV; i++) tot += red[i];
     const float scale = 1.f / sqrtf(tot / (float)D + eps);
     float x[4];
-    const float *w = nx->norm_w;
 #pragma unroll
-    for (int c = 0; c < 4; c++) x[c] = (o[c] * scale) * (w ? w[4 * t + c] : 1.f);
+    for (int c = 0; c < 4; c++) x[c] = (o[c] * scale) * nw[c];
     if (rec_next)
         reinterpret_cast<float4 *>(rec_next + (size_t)(nx->k + r) * D * 4)[t] = make_float4(x[0], x[1], x[2], x[3]);
     /* q8 of block `wave` into row r's tagged image */
