@@ -372,7 +372,7 @@ __device__ inline void st_x(Buf xb, uint32_t o, unsigned tag, uint32_t v) {
 }
 __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLayer *nx, int r, float *h, float eps,
                                float *red, uint8_t *rec_next, unsigned tag, unsigned next_tag, unsigned *abort_flag,
-                               int wave, int lane) {
+                               int wave, int lane, uint64_t *ts) {
     const int t = threadIdx.x;
     const Buf hb = make_buf(h + (size_t)r * D, D * 4u);
     __builtin_amdgcn_s_waitcnt(0x0F70);   /* vmcnt(0): the previous layer's store of these values is done */
@@ -431,6 +431,7 @@ __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
                     o[3] += __uint_as_float(v[i][1].w);
                 }
         }
+        if (ts) ts[6] = wall_clock64();   /* the partials are in (wave 0) */
         u32x4 ov;
         ov.x = __float_as_uint(o[0]);
         ov.y = __float_as_uint(o[1]);
@@ -447,6 +448,7 @@ __device__ inline bool phase_c(const RowsLayer *ly, const Tab *tb, const RowsLay
     ss = wave_sum_x(ss);
     if (lane == 0) red[wave] = ss;
     bar_lds();
+    if (ts) ts[7] = wall_clock64();   /* every wave's squares are in */
     float tot = 0.f;
     for (int i = 0; i < NWV; i++) tot += red[i];
     const float scale = 1.f / sqrtf(tot / (float)D + eps);
@@ -540,7 +542,8 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
     bool ok = true;
 
     /* C(-1): the first layer's RMSNorm and q8 */
-    if (wg < k) phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, 0u, base + 1u, abort_flag, wave, lane);
+    if (wg < k)
+        phase_c(nullptr, nullptr, &layers[0], wg, h, eps, red, debug, 0u, base + 1u, abort_flag, wave, lane, nullptr);
     WA a0;
     int nsb;   /* down items of the layer staged in bst */
     {
@@ -563,6 +566,7 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
         const Buf hid = make_buf(ly.hidden, (uint32_t)ly.P * I * 8u);
         /* ---- A ---- */
         {
+            if (tw) tr[8] = wall_clock64();   /* the wait for x starts */
             if (!x_load(ly, k, tag, abort_flag, xl)) s_okx = 0;
             bar_lds();
             if (s_okx == 0) {
@@ -618,7 +622,7 @@ __global__ __launch_bounds__(NT) void k_decode_rows(const RowsLayer *__restrict_
         if (wg < k) {
             const bool got = phase_c(&ly, &tb, more ? &layers[l + 1] : nullptr, wg, h, eps, red,
                                      debug && more ? debug + (size_t)(l + 1) * ly.rec_bytes : nullptr, tag, tag + 1u,
-                                     abort_flag, wave, lane);
+                                     abort_flag, wave, lane, tw ? tr : nullptr);
             if (!got) s_okc = 0;
             if (tw) tr[4] = wall_clock64();
             bar_lds();
