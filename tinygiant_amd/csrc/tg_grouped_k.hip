@@ -709,6 +709,268 @@ __global__ __launch_bounds__(NT) void k_moe_qb(MoeArgs a) {
     }
 }
 
+/* Phase B, persistent, for Q6_K down rows of I = 768 (3 blocks, 630 bytes
+ * a row) without a down bias: one workgroup a compute unit walks its list
+ * of items (active expert, 32-row slab, pass of 16 pairs), the slabs
+ * (20,160 contiguous bytes) streaming through a ring of six LDS slots five
+ * items ahead, as the gate/up ring does.  Twelve compute waves take one
+ * 128-value half-block of one 16-row tile each (wave c: half-block c % 6,
+ * block c % 6 / 2, tile c / 6; three a SIMD), with k_moe_qb's arithmetic,
+ * and leave each
+ * half-block's term d x d_x x (sum - 32 x offsets) in LDS.  Two copy waves
+ * issue the slab copies and wait for them with exact counts (they issue no
+ * other memory operation, which would enter the counts); two finishing
+ * waves finish the previous item: the six terms added in half-block order
+ * (k_moe_qb's order), times the pair's weight.  The slab
+ * keeps the matrix's layout in LDS (the copies read 16-byte-aligned sources
+ * only), so fields of odd rows and odd blocks lie at 2 mod 4 and are read
+ * as covering dwords, shifted. */
+constexpr int DR_NB = 3;                                  /* Q6_K blocks of a 768-value row */
+constexpr int DR_RB = DR_NB * (int)Q6B;                   /* 630 bytes a row */
+constexpr int DR_ROWS = 32;
+constexpr int DR_SLAB = DR_ROWS * DR_RB;                  /* 20,160 bytes */
+constexpr int DR_COPIES = (DR_SLAB + 1023) / 1024;        /* 20 copies, the last of DR_LAST lanes */
+constexpr int DR_LAST = (DR_SLAB - 1024 * (DR_COPIES - 1)) / 16;
+constexpr int DR_SLOTS = 6;
+constexpr int DR_HB = 2 * DR_NB;                        /* half-blocks of a row */
+constexpr int DR_CW = 2 * DR_HB, DR_YW = 2, DR_FW = 2;  /* compute, copy and finishing waves */
+constexpr int DR_LC = DR_COPIES / DR_YW;                  /* copies a copy wave issues per item */
+constexpr int DR_NT = 64 * (DR_CW + DR_YW + DR_FW);
+constexpr int DR_FO = 2 * 16 * 16 / (64 * DR_FW);         /* (pair, row) results a finishing thread writes */
+static_assert(DR_SLAB % 16 == 0 && DR_LAST > 0 && DR_LAST <= 64, "whole 16-byte pieces");
+static_assert(DR_COPIES % DR_YW == 0, "equal copy counts per copy wave");
+static_assert((DR_SLOTS - 2) * DR_LC <= 63, "a vmcnt count");
+
+/* 8 bytes at LDS offset o (o even) of base: the covering dwords, shifted */
+__device__ inline u32x2 dr_ld8(const uint8_t *base, uint32_t o) {
+    const uint32_t *p = (const uint32_t *)(base + (o & ~3u));
+    const uint32_t sh = o & 3u;
+    const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+    return u32x2{__builtin_amdgcn_alignbyte(d1, d0, sh), __builtin_amdgcn_alignbyte(d2, d1, sh)};
+}
+
+struct DrX {   /* a compute lane's q8 operands of one run: pair c16, its wave's half-block */
+    long x0[4], x1[4];   /* K slice 8 g of chunk m, zero in the half of K the other sub-block takes */
+    float s16a, s16b, xd;
+};
+
+__global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[DR_SLOTS][DR_SLAB];
+    __shared__ __attribute__((aligned(16))) float red[2][DR_HB][2][4][64];   /* by item parity */
+    __shared__ float pwl[DR_FW][16];                                          /* a finishing wave's pair weights */
+    const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
+              c16 = lane & 15;
+    const bool loader = w >= DR_CW, copier = loader && w < DR_CW + DR_YW;
+    const int i0 = ldc(a.rb_off, blockIdx.x), n = ldc(a.rb_off, blockIdx.x + 1) - i0;
+    if (n <= 0) return;   /* uniform */
+    const uint32_t mbytes = (uint32_t)a.D * DR_RB;
+    const Q8Rows &q = a.hq;
+    const Buf qs_b = make_buf(q.qs, (uint32_t)((size_t)a.P * DR_NB * 256));
+    const Buf s16_b = make_buf(q.s16, (uint32_t)((size_t)a.P * DR_NB * 64));
+    const Buf d_b = make_buf(q.d, (uint32_t)((size_t)a.P * DR_NB * 4));
+    const int hbw = w % DR_HB, bi = hbw >> 1, h = hbw & 1, tw = w / DR_HB;   /* a compute wave's half-block, tile */
+
+    auto item = [&](int j) { return ldc(a.rb_items, (size_t)(i0 + j)); };
+    /* What the copy and finishing waves need of an item comes through the
+     * scalar path in stages, each from loads issued an item earlier: an item
+     * code, then its expert's table entries, then the pair weights.  A chain
+     * of dependent scalar loads in one item's step would stall the wave for
+     * each load's round trip (about a microsecond under the weight stream)
+     * and the barrier with it. */
+    struct Info {   /* a copy wave's: the matrix and slab */
+        uint64_t base;
+        int s;
+    };
+    auto info_code = [&](int it) __attribute__((always_inline)) {
+        Info f;
+        f.base = ldc(&a.ed[it >> 16].down, 0);
+        f.s = (it >> 8) & 255;
+        return f;
+    };
+    struct Fin {   /* a finishing wave's: slab, pairs and their weights */
+        int s, tp, p0, np;
+        float pw[16];
+    };
+    auto fin_head = [&](int it) __attribute__((always_inline)) {
+        Fin f;
+        f.s = (it >> 8) & 255;
+        f.tp = 16 * (it & 255);
+        f.p0 = ldc(&a.ed[it >> 16].p0, 0);
+        f.np = ldc(&a.ed[it >> 16].np, 0);
+        return f;
+    };
+    auto fin_pw = [&](Fin &f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) f.pw[v] = ldc(a.p_w, (size_t)min(f.p0 + f.tp + v, a.P - 1));
+    };
+    /* the copy wave's share of item j's copies */
+    auto issue_copies = [&](int j, const Info &f) __attribute__((always_inline)) {
+        const u32x4 desc = buf_desc((const void *)(uintptr_t)f.base, mbytes);
+        uint8_t *dst = &ring[j % DR_SLOTS][0];
+        const uint32_t src = (uint32_t)f.s * DR_SLAB + 16u * (uint32_t)lane;
+#pragma unroll
+        for (int kk = 0; kk < DR_LC; kk++) {
+            const int k = DR_LC * (w - DR_CW) + kk;
+            if (k < DR_COPIES - 1 || lane < DR_LAST) copy_lanes_nt(desc, src + 1024u * k, lds_addr(dst + 1024 * k));
+        }
+    };
+    auto wait_copies_behind = [&](int k) __attribute__((always_inline)) {
+        if (k >= 4) wait_copies_but<4 * DR_LC>();
+        else if (k == 3) wait_copies_but<3 * DR_LC>();
+        else if (k == 2) wait_copies_but<2 * DR_LC>();
+        else if (k == 1) wait_copies_but<DR_LC>();
+        else wait_copies_but<0>();
+    };
+    static_assert(DR_SLOTS - 2 == 4, "wait_copies_behind covers the items in flight");
+    /* the compute lane's operands of item j's run: pair tp + c16 of the expert */
+    auto load_x = [&](int j, DrX &x) __attribute__((always_inline)) {
+        const int it = item(j), ei = it >> 16, tp = 16 * (it & 255);
+        const int p0 = ldc(&a.ed[ei].p0, 0), np = ldc(&a.ed[ei].np, 0);
+        const bool pv = tp + c16 < np;
+        const uint32_t qb = (uint32_t)(p0 + tp + c16) * DR_NB + (uint32_t)bi;
+#pragma unroll
+        for (int m = 0; m < 4; m++) {
+            const long xb = as_long(ld8(qs_b, pv ? qb * 256u + 128u * h + 32u * m + 8u * g : OOB));
+            x.x0[m] = g < 2 ? xb : 0l;
+            x.x1[m] = g < 2 ? 0l : xb;
+        }
+        x.s16a = (float)(int)ld4(s16_b, pv ? qb * 64u + 32u * h + 4u * g : OOB);
+        x.s16b = (float)(int)ld4(s16_b, pv ? qb * 64u + 32u * h + 16u + 4u * g : OOB);
+        x.xd = __uint_as_float(ld4(d_b, pv ? qb * 4u : OOB));
+    };
+    /* compute item j from its slot: the wave's half-block of its tile */
+    auto compute = [&](int j, const DrX &x) __attribute__((always_inline)) {
+        const uint8_t *sb = &ring[j % DR_SLOTS][0];
+        float xdv[4];
+#pragma unroll
+        for (int v = 0; v < 4; v++) xdv[v] = __shfl(x.xd, 4 * g + v, 64);
+        {
+            const int tq = tw;
+            const uint32_t rb = (uint32_t)(16 * tq + c16) * DR_RB + (uint32_t)bi * Q6B;   /* row c16's block */
+            const u32x2 ql0 = dr_ld8(sb, rb + 64u * h + 8u * g);
+            const u32x2 ql1 = dr_ld8(sb, rb + 64u * h + 32u + 8u * g);
+            const u32x2 qh = dr_ld8(sb, rb + 128u + 32u * h + 8u * g);
+            const u32x2 scr = dr_ld8(sb, rb + 192u + 8u * h);
+            const uint32_t dw = *(const uint32_t *)(sb + ((rb + 208u) & ~3u));
+            const float dv = ref_f16((rb & 2u) ? (dw >> 16) : (dw & 0xFFFFu));
+            v4f cf = {0.f, 0.f, 0.f, 0.f};
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32(x.s16a, (float)(int8_t)(scr.x >> (8 * g)), cf, 0, 0, 0);
+            cf = __builtin_amdgcn_mfma_f32_16x16x4f32(x.s16b, (float)(int8_t)(scr.y >> (8 * g)), cf, 0, 0, 0);
+            int ai[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int m = 0; m < 4; m++) {
+                const u32x2 ql = (m & 1) ? ql1 : ql0;
+                const int sl = 4 * (m >> 1), sh = 2 * m;
+                u32x2 c;
+                c.x = ((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> sh) & 0x03030303u) << 4);
+                c.y = ((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> sh) & 0x03030303u) << 4);
+                const v4i d0 = mma(x.x0[m], as_long(c)), d1 = mma(x.x1[m], as_long(c));
+                const uint32_t sw = m < 2 ? scr.x : scr.y;
+                const int sc0 = (int)(int8_t)(sw >> (16 * (m & 1))), sc1 = (int)(int8_t)(sw >> (16 * (m & 1) + 8));
+#pragma unroll
+                for (int v = 0; v < 4; v++) ai[v] += __mul24(sc0, d0[v]) + __mul24(sc1, d1[v]);   /* |.| < 2^24 */
+            }
+#pragma unroll
+            for (int v = 0; v < 4; v++) red[j & 1][hbw][tq][v][lane] = dv * xdv[v] * (float)(ai[v] - 32 * (int)cf[v]);
+        }
+    };
+    /* the finishing threads, DR_FO (pair, row) results each: the six
+     * half-block terms in order, times the pair's weight; the term of pair
+     * 4 g + v and row c16 of tile tq sits in lane 16 g + c16, register v */
+    auto finish = [&](int j, const Fin &fi) __attribute__((always_inline)) {
+        /* the weights (scalars) through the wave's own LDS words: a per-lane
+         * select among them became a lookup through scratch memory */
+        float *pl = pwl[w - DR_CW - DR_YW];
+        if (lane == 0) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) pl[v] = fi.pw[v];
+        }
+        const int f = tid - 64 * (DR_CW + DR_YW);
+#pragma unroll
+        for (int u = 0; u < DR_FO; u++) {
+            const int o = f + 64 * DR_FW * u, tq = o >> 8, jj = (o >> 4) & 15, rr = o & 15;
+            const int ln = 16 * (jj >> 2) + rr, v = jj & 3;
+            if (fi.tp + jj < fi.np) {
+                float acc = 0.f;
+#pragma unroll
+                for (int c = 0; c < DR_HB; c++) acc += red[j & 1][c][tq][v][ln];
+                const int r = DR_ROWS * fi.s + 16 * tq + rr;
+                a.part[(size_t)(fi.p0 + fi.tp + jj) * a.D + r] = pl[jj] * (acc + 0.f);
+            }
+        }
+    };
+    auto run_end = [&](int s0) {
+        const int key = item(s0) & ~0xFF00;   /* expert and pass */
+        int e = s0 + 1;
+        while (e < n && (item(e) & ~0xFF00) == key) e++;
+        return e;
+    };
+
+    /* as in the gate/up ring: between the barriers of items i and i + 1 the
+     * compute waves compute item i (slot i % DR_SLOTS, red[i % 2]) while the
+     * copy waves copy item i + DR_SLOTS - 1 into item i - 1's slot and the
+     * finishing waves finish item i - 1 (red[(i - 1) % 2]) */
+    if (copier) {
+        for (int j = 0; j < DR_SLOTS - 1 && j < n; j++) issue_copies(j, info_code(item(j)));
+        Info fc = info_code(item(min(DR_SLOTS - 1, n - 1)));   /* item i + DR_SLOTS - 1 */
+        int code = item(min(DR_SLOTS, n - 1));                  /* item i + DR_SLOTS */
+        for (int i = 0; i < n; i++) {
+            wait_copies_behind(min(DR_SLOTS - 2, n - 1 - i));
+            asm volatile("s_barrier" ::: "memory");   /* a copy wave writes no LDS itself */
+            if (i + DR_SLOTS - 1 < n) issue_copies(i + DR_SLOTS - 1, fc);
+            fc = info_code(code);
+            code = item(min(i + DR_SLOTS + 1, n - 1));
+        }
+        asm volatile("s_barrier" ::: "memory");
+        wait_copies();   /* no copy outlives the workgroup */
+        return;
+    }
+    if (loader) {
+        Fin ff = fin_head(item(0));                /* item i - 1, weights too */
+        fin_pw(ff);
+        Fin fh = fin_head(item(min(1, n - 1)));    /* item i */
+        int code = item(min(2, n - 1));            /* item i + 1 */
+        for (int i = 0; i < n; i++) {
+            bar_lds();   /* its own weight words are written and read in order */
+            if (i > 0) {
+                finish(i - 1, ff);
+                ff = fh;
+                fin_pw(ff);
+                fh = fin_head(code);
+                code = item(min(i + 2, n - 1));
+            }
+        }
+        bar_lds();   /* item n - 1's terms are in LDS */
+        finish(n - 1, ff);
+        return;
+    }
+    auto settle = [&](DrX &x) __attribute__((always_inline)) {
+        asm volatile(""
+                     : "+v"(x.x0[0]), "+v"(x.x0[1]), "+v"(x.x0[2]), "+v"(x.x0[3]), "+v"(x.x1[0]), "+v"(x.x1[1]),
+                       "+v"(x.x1[2]), "+v"(x.x1[3]), "+v"(x.s16a), "+v"(x.s16b), "+v"(x.xd));
+    };
+    DrX cur, stage;
+    load_x(0, cur);
+    settle(cur);
+    int re = run_end(0);
+    for (int i = 0; i < n;) {
+        const int pf = max(i, re - (DR_SLOTS - 1));
+        for (; i < re; i++) {
+            if (i == pf && re < n) load_x(re, stage);
+            bar_lds();   /* item i's slab has landed, item i - 1's terms are read */
+            compute(i, cur);
+        }
+        if (i < n) {
+            re = run_end(i);
+            settle(stage);
+            cur = stage;
+        }
+    }
+    bar_lds();   /* item n - 1's terms are in LDS */
+}
+
+bool qb_ring_shape(int I, int D) { return I == DR_NB * 256 && D % DR_ROWS == 0 && D / DR_ROWS <= 256; }
+
 /* The MFMA phases need Q4_K gate/up and Q6_K down matrices of whole blocks,
  * slabs within the device's LDS, and 31-bit buffer ranges. */
 bool qk_grouped_fits(const MoeArgs &a) {
@@ -735,11 +997,11 @@ bool qa_ring_shape(int gate_fmt, int D, int I) { return gate_fmt == TG_FMT_Q4K &
  * runs of one (expert, pass), and the passes of an expert run at about the
  * same time on neighbouring workgroups, so their slabs' second reads come
  * from the caches. */
-void qa_ring_items(const ExpDesc *ed, int n_act, int I, int G, std::vector<int> &items, std::vector<int> &off) {
+void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off) {
     items.clear();
     for (int ei = 0; ei < n_act; ei++)
         for (int t = 0; t < std::max(1, (ed[ei].np + 15) / 16); t++)
-            for (int s = 0; s < I / 16; s++) items.push_back(ei << 16 | s << 8 | t);
+            for (int s = 0; s < slabs; s++) items.push_back(ei << 16 | s << 8 | t);
     off.resize(G + 1);
     for (int w = 0; w <= G; w++) off[w] = (int)((int64_t)items.size() * w / G);
 }
@@ -755,6 +1017,10 @@ void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {
 }
 
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st) {
+    if (a.rb_items && !a.dbias && qb_ring_shape(a.I, a.D)) {
+        hipLaunchKernelGGL(k_moe_qb_ring, dim3(a.rb_n), dim3(DR_NT), 0, st, a);
+        return;
+    }
     hipLaunchKernelGGL(k_moe_qb<0>, dim3((a.D + QB_ROWS - 1) / QB_ROWS, a.n_act_a), dim3(NT), qb_lds_bytes(a.I), st,
                        a);
 }

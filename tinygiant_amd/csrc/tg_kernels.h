@@ -59,6 +59,8 @@ struct MoeArgs {
     int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */
     const int *rg_items, *rg_off;           /* the persistent gate/up phase's items and each workgroup's range, or null */
     int rg_n;                               /* its workgroups */
+    const int *rb_items, *rb_off;           /* the persistent down phase's, or null */
+    int rb_n;
 };
 
 int items_per_row(int fmt, int ncols);
@@ -126,7 +128,10 @@ bool qk_grouped_fits(const MoeArgs &a);
  * pairs) as ei << 16 | s << 8 | t, and off[0 .. G] the range of each of G
  * workgroups.  False when the shape is not the phase's. */
 bool qa_ring_shape(int gate_fmt, int D, int I);
-void qa_ring_items(const ExpDesc *ed, int n_act, int I, int G, std::vector<int> &items, std::vector<int> &off);
+bool qb_ring_shape(int I, int D);
+/* the persistent phases' items (expert, pass, slab of `slabs`) cut into G
+ * workgroup ranges */
+void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off);
 constexpr int QA_RING_MAX_G = 1024;
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st);
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st);
