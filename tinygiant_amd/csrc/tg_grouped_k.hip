@@ -300,9 +300,9 @@ __global__ __launch_bounds__(NT) void k_moe_qa(MoeArgs a) {
  * a run (a compute unit returns its loads in issue order, so operands loaded
  * per item would wait behind the slabs in flight each time); a workgroup's
  * list is a contiguous stretch of the layer's items ordered expert, pass,
- * slab, so it holds a few runs.  Four loader waves issue the slab copies
- * (direct-to-LDS, half a matrix each), each waiting for its own with exact
- * counts, and finish the previous item (its
+ * slab, so it holds a few runs.  Two copy waves issue the slab copies
+ * (direct-to-LDS, one matrix each) and nothing else, so each waits for its
+ * own with exact counts; two finishing waves finish the previous item (its
  * partial sums, double-buffered in LDS, the activation, the hidden values)
  * while the compute waves work on the current one, one barrier an item.
  *
@@ -314,9 +314,11 @@ constexpr int RG_UNITS = RG_NB * 9;                   /* 16-byte units of a 1152
 constexpr int RG_SLAB = 16 * RG_UNITS * 16;           /* 18,432 bytes: one matrix's 16 rows */
 constexpr int RG_COPIES = RG_SLAB / 1024;             /* 18 copies of 1 KiB */
 constexpr int RG_SLOTS = 4;
-constexpr int RG_CW = 8, RG_LW = 4;                   /* compute and loader waves */
-constexpr int RG_LC = RG_COPIES / 2;                  /* copies a loader wave issues per item */
-constexpr int RG_NT = 64 * (RG_CW + RG_LW);
+constexpr int RG_CW = 8, RG_YW = 2, RG_FW = 2;        /* compute, copy and finishing waves */
+constexpr int RG_LC = RG_COPIES;                      /* copies a copy wave issues per item (its matrix's slab) */
+constexpr int RG_NT = 64 * (RG_CW + RG_YW + RG_FW);
+constexpr int RG_FO = 16 * 16 / (64 * RG_FW);         /* (pair, row) results a finishing thread writes */
+static_assert(2 * RG_LC <= 63, "a vmcnt count");
 static_assert(RG_SLAB % 1024 == 0, "whole copies");
 static_assert(RG_UNITS % 8 == 0, "the swizzle stays inside a row");
 
@@ -332,7 +334,7 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
     __shared__ __attribute__((aligned(16))) float red[2][RG_CW][4][64];   /* by item parity */
     const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4,
               c16 = lane & 15;
-    const bool loader = w >= RG_CW;
+    const bool loader = w >= RG_CW, copier = loader && w < RG_CW + RG_YW;
     const int i0 = ldc(a.rg_off, blockIdx.x), n = ldc(a.rg_off, blockIdx.x + 1) - i0;
     if (n <= 0) return;   /* uniform */
     const uint32_t mbytes = (uint32_t)a.I * (RG_NB * Q4B);
@@ -344,34 +346,46 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
 
     /* item j of the list (j < n): expert index, slab, pass */
     auto item = [&](int j) { return ldc(a.rg_items, (size_t)(i0 + j)); };
-    /* what a loader wave needs of item j, read through the scalar path a
-     * step ahead of its use: its matrix (half (w - RG_CW) % 2 of matrix
-     * (w - RG_CW) / 2 is the wave's to copy), slab, pairs, biases */
-    struct Info {
+    /* What the copy and finishing waves need of an item comes through the
+     * scalar path in stages, each from loads issued an item earlier (an item
+     * code, then its expert's entries, then the biases): a chain of dependent
+     * scalar loads in one item's step would stall the wave for each round
+     * trip, and the barrier with it. */
+    struct Info {   /* a copy wave's: its matrix (gate for wave RG_CW, up for the next) and slab */
         uint64_t base;
-        int s, tp, p0, np;
-        const float *gb, *ub;
+        int s;
     };
-    auto info_of = [&](int j) __attribute__((always_inline)) {
+    auto info_code = [&](int it) __attribute__((always_inline)) {
         Info f;
-        const int it = item(min(j, n - 1)), ei = it >> 16, e = ldc(&a.ed[ei].e, 0);
-        f.base = (w - RG_CW) >> 1 ? ldc(&a.ed[ei].up, 0) : ldc(&a.ed[ei].gate, 0);
+        f.base = w - RG_CW ? ldc(&a.ed[it >> 16].up, 0) : ldc(&a.ed[it >> 16].gate, 0);
         f.s = (it >> 8) & 255;
-        f.tp = 16 * (it & 255);
-        f.p0 = ldc(&a.ed[ei].p0, 0);
-        f.np = ldc(&a.ed[ei].np, 0);
-        f.gb = a.gbias ? (const float *)(uintptr_t)ldc(a.gbias, e) : nullptr;
-        f.ub = a.ubias ? (const float *)(uintptr_t)ldc(a.ubias, e) : nullptr;
         return f;
     };
-    /* the loader wave's share of item j's copies, 9 KiB */
+    struct Fin {   /* a finishing wave's: slab, pairs, biases */
+        int s, tp, p0, np, e;
+        const float *gb, *ub;
+    };
+    auto fin_head = [&](int it) __attribute__((always_inline)) {
+        Fin f;
+        f.s = (it >> 8) & 255;
+        f.tp = 16 * (it & 255);
+        f.p0 = ldc(&a.ed[it >> 16].p0, 0);
+        f.np = ldc(&a.ed[it >> 16].np, 0);
+        f.e = ldc(&a.ed[it >> 16].e, 0);
+        return f;
+    };
+    auto fin_bias = [&](Fin &f) __attribute__((always_inline)) {
+        f.gb = a.gbias ? (const float *)(uintptr_t)ldc(a.gbias, f.e) : nullptr;
+        f.ub = a.ubias ? (const float *)(uintptr_t)ldc(a.ubias, f.e) : nullptr;
+    };
+    /* the copy wave's matrix slab of item j, 18 KiB */
     auto issue_copies = [&](int j, const Info &f) __attribute__((always_inline)) {
-        const int s = f.s, m = (w - RG_CW) >> 1, k0 = RG_LC * ((w - RG_CW) & 1);
+        const int s = f.s, m = w - RG_CW;
         const u32x4 desc = buf_desc((const void *)(uintptr_t)f.base, mbytes);
         uint8_t *dst = &ring[j % RG_SLOTS][m][0];
 #pragma unroll
-        for (int kk = 0; kk < RG_LC; kk++) {
-            const int k = k0 + kk, P = 64 * k + lane, r = P / RG_UNITS, u = (P % RG_UNITS) ^ ((r >> 1) & 7);
+        for (int k = 0; k < RG_LC; k++) {
+            const int P = 64 * k + lane, r = P / RG_UNITS, u = (P % RG_UNITS) ^ ((r >> 1) & 7);
             copy_lanes_nt(desc, (uint32_t)(s * 16 + r) * (RG_NB * Q4B) + 16u * (uint32_t)u, lds_addr(dst + 1024 * k));
         }
     };
@@ -381,6 +395,7 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
         else if (k == 1) wait_copies_but<RG_LC>();
         else wait_copies_but<0>();
     };
+    static_assert(RG_SLOTS - 2 == 2, "wait_copies_behind covers the items in flight");
     /* the compute lane's operands of item j's run: pair t + c16 of the expert */
     auto load_x = [&](int j, RgX &x) __attribute__((always_inline)) {
         const int it = item(j), ei = it >> 16, tp = 16 * (it & 255);
@@ -440,14 +455,16 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
 #pragma unroll
         for (int v = 0; v < 4; v++) red[j & 1][w][v][lane] = acc[v];
     };
-    /* the loader threads, one (pair, row) each: the gate and up waves' sums
-     * in wave order, the activation, the hidden values of item j; the sums
-     * of pair 4 g + v and row c16 sit in lane 16 g + c16, register v */
-    auto finish = [&](int j, const Info &fi) __attribute__((always_inline)) {
+    /* the finishing threads, RG_FO (pair, row) results each: the gate and
+     * up waves' sums in wave order, the activation, the hidden values of item
+     * j; the sums of pair 4 g + v and row c16 sit in lane 16 g + c16,
+     * register v */
+    auto finish = [&](int j, const Fin &fi) __attribute__((always_inline)) {
         const int s = fi.s, tp = fi.tp, p0 = fi.p0, np = fi.np;
         const float *gb = fi.gb, *ub = fi.ub;
-        {
-            const int f = tid - 64 * RG_CW, jj = f >> 4, rr = f & 15, ln = 16 * (jj >> 2) + rr, v = jj & 3;
+#pragma unroll
+        for (int o = tid - 64 * (RG_CW + RG_YW), u = 0; u < RG_FO; u++, o += 64 * RG_FW) {
+            const int jj = o >> 4, rr = o & 15, ln = 16 * (jj >> 2) + rr, v = jj & 3;
             float gv = 0.f, uv = 0.f;
 #pragma unroll
             for (int ww = 0; ww < 4; ww++) {
@@ -468,34 +485,47 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
         return e;
     };
 
-    /* The loader waves and the compute waves run loops of their own (so the
-     * compiler's waits for the compute waves' operand loads never land in
-     * the loaders' code), meeting at one barrier an item.  Between the
-     * barriers of items i and i + 1 the compute waves compute item i
-     * (reading slot i % 4, writing red[i % 2]) while the loaders copy item
-     * i + 3 into item i - 1's slot and finish item i - 1 (reading
-     * red[(i - 1) % 2]): each wave reaches the next barrier only after its
-     * part. */
-    if (loader) {
-        Info fc, ff;   /* the info of the next copies and of the next item to finish */
-        for (int j = 0; j < 3 && j < n; j++) issue_copies(j, info_of(j));
-        fc = info_of(3);
-        ff = info_of(0);
+    /* The three roles run loops of their own (so the compiler's waits for
+     * the compute waves' operand loads never land in the others' code),
+     * meeting at one barrier an item.  Between the barriers of items i and
+     * i + 1 the compute waves compute item i (reading slot i % 4, writing
+     * red[i % 2]) while the copy waves copy item i + 3 into item i - 1's slot
+     * and the finishing waves finish item i - 1 (reading red[(i - 1) % 2]):
+     * each wave reaches the next barrier only after its part. */
+    if (copier) {
+        for (int j = 0; j < RG_SLOTS - 1 && j < n; j++) issue_copies(j, info_code(item(j)));
+        Info fc = info_code(item(min(RG_SLOTS - 1, n - 1)));   /* item i + 3 */
+        int code = item(min(RG_SLOTS, n - 1));                  /* item i + 4 */
         for (int i = 0; i < n; i++) {
-            wait_copies_behind(min(2, n - 1 - i));
-            /* a loader writes no LDS itself: its barrier leaves the scalar
+            wait_copies_behind(min(RG_SLOTS - 2, n - 1 - i));
+            /* a copy wave writes no LDS itself: its barrier leaves the scalar
              * reads of the next items' info in flight */
             asm volatile("s_barrier" ::: "memory");
-            if (i + 3 < n) issue_copies(i + 3, fc);
+            if (i + RG_SLOTS - 1 < n) issue_copies(i + RG_SLOTS - 1, fc);
+            fc = info_code(code);
+            code = item(min(i + RG_SLOTS + 1, n - 1));
+        }
+        asm volatile("s_barrier" ::: "memory");
+        wait_copies();   /* no copy outlives the workgroup */
+        return;
+    }
+    if (loader) {
+        Fin ff = fin_head(item(0));                /* item i - 1, biases too */
+        fin_bias(ff);
+        Fin fh = fin_head(item(min(1, n - 1)));    /* item i */
+        int code = item(min(2, n - 1));            /* item i + 1 */
+        for (int i = 0; i < n; i++) {
+            asm volatile("s_barrier" ::: "memory");   /* a finishing wave writes no LDS */
             if (i > 0) {
                 finish(i - 1, ff);
-                ff = info_of(i);
+                ff = fh;
+                fin_bias(ff);
+                fh = fin_head(code);
+                code = item(min(i + 2, n - 1));
             }
-            fc = info_of(i + 4);
         }
         asm volatile("s_barrier" ::: "memory");   /* item n - 1's sums are in LDS */
         finish(n - 1, ff);
-        wait_copies();   /* no copy outlives the workgroup */
         return;
     }
     /* A run's operands are loaded into a staging set while the run before is
