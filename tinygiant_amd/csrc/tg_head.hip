@@ -391,7 +391,7 @@ __device__ inline u32x4 lds16(const uint8_t *base, uint32_t a, uint32_t sh) {
 __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict__ W, int nrows, Q8Rows x, int k,
                                                      float *logits, unsigned long long *best, int32_t *idx,
                                                      float *val) {
-    __shared__ __attribute__((aligned(16))) float red[MW][4][64];
+    __shared__ __attribute__((aligned(16))) float red[2][MW][4][64];   /* the waves' block terms, by item parity */
     __shared__ unsigned long long wb_best[16][16];
     __shared__ int last_wg;
     extern __shared__ __attribute__((aligned(16))) uint8_t hl[];   /* [HNB][HITEM] */
@@ -448,14 +448,33 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
     const int G = (int)gridDim.x;
 #pragma unroll
     for (int i = 0; i < HNB - 1; i++) issue_item(q + i * G, i);
-    for (int bi = 0; q < nq; bi = bi == HNB - 1 ? 0 : bi + 1) {
-        /* the item HNB - 1 ahead into the buffer the previous item used
-         * (every wave passed the barrier after its compute) */
-        issue_item(q + (HNB - 1) * G, bi == 0 ? HNB - 1 : bi - 1);
+    /* the epilogue of an item: its 16 rows' logits and argmax keys from the
+     * waves' block terms, added in block order (tid < 256) */
+    auto epilogue = [&](int qe, const float (&rb)[MW][4][64]) {
+        if (tid < 256) {
+            const uint32_t row = 16u * (uint32_t)qe + 4u * (uint32_t)(el >> 4) + (uint32_t)ev;
+            float s = 0.f;
+#pragma unroll
+            for (int b = 0; b < MW; b++) s = __fadd_rn(s, rb[b][ev][el]);
+            if (ej < k && row < (uint32_t)nrows) {
+                if (logits) logits[(size_t)ej * nrows + row] = s;
+                const uint64_t key = argmax_key(s, row);
+                mybest = key > mybest ? key : mybest;
+            }
+        }
+    };
+    /* One barrier an item.  Past it, item q's copies have landed (each wave
+     * waited for its own) and every wave has computed the item before: its
+     * buffer takes the copies of the item HNB - 1 ahead, and its block terms
+     * (in the other half of red) are added up while item q computes. */
+    int it = 0;
+    for (int bi = 0; q < nq; bi = bi == HNB - 1 ? 0 : bi + 1, it++) {
         /* this item's copies: the later items' (ncw each) stay in flight */
-        if (ncw == 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (HNB - 1)) : "memory");
-        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (HNB - 1)) : "memory");
+        if (ncw == 4) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (HNB - 2)) : "memory");
+        else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * (HNB - 2)) : "memory");
         bar_lds();
+        issue_item(q + (HNB - 1) * G, bi == 0 ? HNB - 1 : bi - 1);
+        if (it > 0) epilogue(q - G, red[(it - 1) & 1]);
         const uint8_t *ib = hl + bi * HITEM;
         const uint32_t odd = 2u * (uint32_t)(w & 1);   /* byte shift of block w's fields */
         const uint32_t mb = (uint32_t)c16 * HRB + 210u * (uint32_t)w;   /* this lane's row of block w */
@@ -504,23 +523,13 @@ __global__ __launch_bounds__(MT) void k_head_q6k_mfma(const uint8_t *__restrict_
             for (int v = 0; v < 4; v++) isum[v] += ai[v] - 32 * (int)cf[v];
         }
         /* the block's term d * d_x * sum, as the reference forms it */
-        float (&rb)[MW][4][64] = red;   /* rewritten only after the next item's first barrier */
+        float (&rb)[MW][4][64] = red[it & 1];   /* added up after the next item's barrier */
 #pragma unroll
         for (int v = 0; v < 4; v++) rb[w][v][lane] = __fmul_rn(__fmul_rn(dv[v], xd), (float)isum[v]);
-        bar_lds();   /* LDS only: the items in flight stay in flight */
-        if (tid < 256) {
-            const uint32_t row = 16u * (uint32_t)q + 4u * (uint32_t)(el >> 4) + (uint32_t)ev;
-            float s = 0.f;
-#pragma unroll
-            for (int b = 0; b < MW; b++) s = __fadd_rn(s, rb[b][ev][el]);
-            if (ej < k && row < (uint32_t)nrows) {
-                if (logits) logits[(size_t)ej * nrows + row] = s;
-                const uint64_t key = argmax_key(s, row);
-                mybest = key > mybest ? key : mybest;
-            }
-        }
         q += G;
     }
+    bar_lds();   /* LDS only: the last item's block terms are in */
+    if (it > 0) epilogue(q - G, red[(it - 1) & 1]);
     /* the copies of the items past the end land before the wave ends */
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     /* workgroup best per input row (16 epilogue threads each), then one
