@@ -1033,6 +1033,7 @@ def main():
                          "round (kernel traces and counter passes)")
     ap.add_argument("--attn-probe", action="store_true",
                     help="only the decode-attention probe (kernel traces and counter passes)")
+    ap.add_argument("--attn-kv", default="512,4096", help="cached positions of --attn-probe")
     ap.add_argument("--rows-probe", action="store_true",
                     help="only the 48-layer k-row passes on the persistent multi-row kernel (kernel traces)")
     ap.add_argument("--rows-k", default="5,9,8", help="row counts of --rows-probe")
@@ -1054,7 +1055,7 @@ def main():
         print(json.dumps(out), flush=True)
         return 0
     if args.attn_probe:
-        out = {"attention_layer": attention_probe(tg)}
+        out = {"attention_layer": attention_probe(tg, tuple(int(v) for v in args.attn_kv.split(",")))}
         lib.tg_hip_shutdown()
         print(json.dumps(out), flush=True)
         return 0
