@@ -441,9 +441,9 @@ Layout plan_layout(const HostPlan &h) {
     t += (size_t)4 * (n + 1) * 4 + 16;      /* active expert lists and their cost prefixes */
     t += (size_t)n * sizeof(ExpDesc) + 16;  /* active expert descriptors */
     if (qa_ring_shape(h.gate_fmt, h.D, h.I))  /* the persistent gate/up phase's items and ranges */
-        t += (size_t)(h.I / 16) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 16;
+        t += 2 * (size_t)(h.I / 16) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 32;
     if (qb_ring_shape(h.I, h.D))  /* the persistent down phase's */
-        t += (size_t)(h.D / 32) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 16;
+        t += 2 * (size_t)(h.D / 32) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 32;
     L.tables_len = t + 64;
     b.take(L.tables_len);
     L.xin = b.take((size_t)k * h.D * 4);
@@ -557,16 +557,18 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     std::stable_sort(ed.begin(), ed.end(), [](const ExpDesc &x, const ExpDesc &y) { return x.np > y.np; });
     a.ed = (const ExpDesc *)put(ed.data(), ed.size() * sizeof(ExpDesc));
     if (qa_ring_shape(h.gate_fmt, h.D, h.I) && a.n_act_a > 0) {
-        std::vector<int> items, off;
-        ring_items(ed.data(), a.n_act_a, h.I / 16, cu_count(), items, off);
+        std::vector<int> items, off, rend;
+        ring_items(ed.data(), a.n_act_a, h.I / 16, cu_count(), items, off, rend);
         a.rg_items = (const int *)put(items.data(), items.size() * 4);
+        a.rg_rend = (const int *)put(rend.data(), rend.size() * 4);
         a.rg_off = (const int *)put(off.data(), off.size() * 4);
         a.rg_n = (int)off.size() - 1;
     }
     if (qb_ring_shape(h.I, h.D) && a.n_act_a > 0) {
-        std::vector<int> items, off;
-        ring_items(ed.data(), a.n_act_a, h.D / 32, cu_count(), items, off);
+        std::vector<int> items, off, rend;
+        ring_items(ed.data(), a.n_act_a, h.D / 32, cu_count(), items, off, rend);
         a.rb_items = (const int *)put(items.data(), items.size() * 4);
+        a.rb_rend = (const int *)put(rend.data(), rend.size() * 4);
         a.rb_off = (const int *)put(off.data(), off.size() * 4);
         a.rb_n = (int)off.size() - 1;
     }

@@ -478,12 +478,7 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
         }
     };
     /* a run: items of one expert and pass */
-    auto run_end = [&](int s) {
-        const int key = item(s) & ~0xFF00;   /* expert and pass */
-        int e = s + 1;
-        while (e < n && (item(e) & ~0xFF00) == key) e++;
-        return e;
-    };
+    auto run_end = [&](int s) { return min(ldc(a.rg_rend, (size_t)(i0 + s)), i0 + n) - i0; };
 
     /* The three roles run loops of their own (so the compiler's waits for
      * the compute waves' operand loads never land in the others' code),
@@ -929,12 +924,7 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
             }
         }
     };
-    auto run_end = [&](int s0) {
-        const int key = item(s0) & ~0xFF00;   /* expert and pass */
-        int e = s0 + 1;
-        while (e < n && (item(e) & ~0xFF00) == key) e++;
-        return e;
-    };
+    auto run_end = [&](int s0) { return min(ldc(a.rb_rend, (size_t)(i0 + s0)), i0 + n) - i0; };
 
     /* as in the gate/up ring: between the barriers of items i and i + 1 the
      * compute waves compute item i (slot i % DR_SLOTS, red[i % 2]) while the
@@ -1026,12 +1016,18 @@ bool qa_ring_shape(int gate_fmt, int D, int I) { return gate_fmt == TG_FMT_Q4K &
  * contiguous stretches of equal length: each workgroup's stretch is a few
  * runs of one (expert, pass), and the passes of an expert run at about the
  * same time on neighbouring workgroups, so their slabs' second reads come
- * from the caches. */
-void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off) {
+ * from the caches.  rend[i] is the end of item i's run (the items of its
+ * expert and pass): a workgroup finds where its run ends with one load, not
+ * by scanning the items that follow. */
+void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off,
+                std::vector<int> &rend) {
     items.clear();
+    rend.clear();
     for (int ei = 0; ei < n_act; ei++)
-        for (int t = 0; t < std::max(1, (ed[ei].np + 15) / 16); t++)
+        for (int t = 0; t < std::max(1, (ed[ei].np + 15) / 16); t++) {
             for (int s = 0; s < slabs; s++) items.push_back(ei << 16 | s << 8 | t);
+            rend.resize(items.size(), (int)items.size());
+        }
     off.resize(G + 1);
     for (int w = 0; w <= G; w++) off[w] = (int)((int64_t)items.size() * w / G);
 }

@@ -58,8 +58,9 @@ struct MoeArgs {
     int ctr_n;
     int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */
     const int *rg_items, *rg_off;           /* the persistent gate/up phase's items and each workgroup's range, or null */
+    const int *rg_rend;                     /* for each item, the end of its run (items of one expert and pass) */
     int rg_n;                               /* its workgroups */
-    const int *rb_items, *rb_off;           /* the persistent down phase's, or null */
+    const int *rb_items, *rb_off, *rb_rend; /* the persistent down phase's, or null */
     int rb_n;
 };
 
@@ -130,8 +131,9 @@ bool qk_grouped_fits(const MoeArgs &a);
 bool qa_ring_shape(int gate_fmt, int D, int I);
 bool qb_ring_shape(int I, int D);
 /* the persistent phases' items (expert, pass, slab of `slabs`) cut into G
- * workgroup ranges */
-void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off);
+ * workgroup ranges, and the end of each item's run (expert and pass) */
+void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off,
+                std::vector<int> &rend);
 constexpr int QA_RING_MAX_G = 1024;
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st);
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st);
