@@ -160,7 +160,7 @@ def test_head_ties_take_the_first_row(tg, orc):
     assert am[0] == 317
 
 
-@pytest.mark.parametrize("k", [1, 9])
+@pytest.mark.parametrize("k", [1, 5, 9, 16])
 def test_head_q6k_full_vocabulary(tg, orc, k):
     """The Qwen3-30B-A3B output head at its full size, 151936 x 2048 q6_K
     (255,252,480 bytes; engine.py:347-354 with tg_matmul, csrc/libtinygiant.c:

@@ -222,13 +222,14 @@ def test_moe_qwen_layer_one_token(tg, orc):
                False, rw, x)
 
 
-@pytest.mark.parametrize("k", [2, 5, 9])
-def test_moe_grouped_verify_rows(tg, orc, k):
-    """Self-speculative verify batch: K+1 rows, Zipf-skewed top-8, 1..k rows per expert."""
-    say("moe grouped", k)
+@pytest.mark.parametrize("k,pool", [(2, 32), (5, 32), (9, 32), (5, 128), (9, 128)])
+def test_moe_grouped_verify_rows(tg, orc, k, pool):
+    """Self-speculative verify batch: K+1 rows, Zipf-skewed top-8 over a pool
+    of 32 experts (many rows per expert) or all 128 of a Qwen3 layer."""
+    say("moe grouped", k, pool)
     import tinygiant_amd.synth as S
-    rng = np.random.default_rng(100 + k)
-    experts, rw = S.routing_rows(rng, k, 32, 8)
+    rng = np.random.default_rng(100 + k + pool)
+    experts, rw = S.routing_rows(rng, k, pool, 8)
     x = rng.standard_normal((k, 2048)).astype(np.float32)
     base = rng.standard_normal((k, 2048)).astype(np.float32)
     _check_moe(tg, orc, len(experts), k, 2048, 768, O.FMT_Q4K, [O.FMT_Q6K] * len(experts), O.ACT_SILU,
