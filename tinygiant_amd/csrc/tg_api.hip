@@ -441,9 +441,11 @@ Layout plan_layout(const HostPlan &h) {
     t += (size_t)4 * (n + 1) * 4 + 16;      /* active expert lists and their cost prefixes */
     t += (size_t)n * sizeof(ExpDesc) + 16;  /* active expert descriptors */
     if (qa_ring_shape(h.gate_fmt, h.D, h.I))  /* the persistent gate/up phase's items and ranges */
-        t += 2 * (size_t)(h.I / 16) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 32;
+        t += 2 * (size_t)(h.I / 16) * (P / 16 + n + 1) * 4 + (size_t)RING_REC * (P / 16 + n + 1) * 4 +
+             2 * (QA_RING_MAX_G + 1) * 4 + 64;
     if (qb_ring_shape(h.I, h.D))  /* the persistent down phase's */
-        t += 2 * (size_t)(h.D / 32) * (P / 16 + n + 1) * 4 + (QA_RING_MAX_G + 1) * 4 + 32;
+        t += 2 * (size_t)(h.D / 32) * (P / 16 + n + 1) * 4 + (size_t)RING_REC * (P / 16 + n + 1) * 4 +
+             2 * (QA_RING_MAX_G + 1) * 4 + 64;
     L.tables_len = t + 64;
     b.take(L.tables_len);
     L.xin = b.take((size_t)k * h.D * 4);
@@ -557,20 +559,24 @@ MoeArgs plan_args(const HostPlan &h, const Layout &L, uint8_t *dev, uint8_t *img
     std::stable_sort(ed.begin(), ed.end(), [](const ExpDesc &x, const ExpDesc &y) { return x.np > y.np; });
     a.ed = (const ExpDesc *)put(ed.data(), ed.size() * sizeof(ExpDesc));
     if (qa_ring_shape(h.gate_fmt, h.D, h.I) && a.n_act_a > 0) {
-        std::vector<int> items, off, rend;
-        ring_items(ed.data(), a.n_act_a, h.I / 16, cu_count(), items, off, rend);
-        a.rg_items = (const int *)put(items.data(), items.size() * 4);
-        a.rg_rend = (const int *)put(rend.data(), rend.size() * 4);
-        a.rg_off = (const int *)put(off.data(), off.size() * 4);
-        a.rg_n = (int)off.size() - 1;
+        RingLists r;
+        ring_items(ed.data(), a.n_act_a, h.I / 16, cu_count(), h.p_row.data(), P, r);
+        a.rg_items = (const int *)put(r.items.data(), r.items.size() * 4);
+        a.rg_rend = (const int *)put(r.rend.data(), r.rend.size() * 4);
+        a.rg_runs = (const int *)put(r.runs.data(), r.runs.size() * 4);
+        a.rg_run0 = (const int *)put(r.run0.data(), r.run0.size() * 4);
+        a.rg_off = (const int *)put(r.off.data(), r.off.size() * 4);
+        a.rg_n = (int)r.off.size() - 1;
     }
     if (qb_ring_shape(h.I, h.D) && a.n_act_a > 0) {
-        std::vector<int> items, off, rend;
-        ring_items(ed.data(), a.n_act_a, h.D / 32, cu_count(), items, off, rend);
-        a.rb_items = (const int *)put(items.data(), items.size() * 4);
-        a.rb_rend = (const int *)put(rend.data(), rend.size() * 4);
-        a.rb_off = (const int *)put(off.data(), off.size() * 4);
-        a.rb_n = (int)off.size() - 1;
+        RingLists r;
+        ring_items(ed.data(), a.n_act_a, h.D / 32, cu_count(), h.p_row.data(), P, r);
+        a.rb_items = (const int *)put(r.items.data(), r.items.size() * 4);
+        a.rb_rend = (const int *)put(r.rend.data(), r.rend.size() * 4);
+        a.rb_runs = (const int *)put(r.runs.data(), r.runs.size() * 4);
+        a.rb_run0 = (const int *)put(r.run0.data(), r.run0.size() * 4);
+        a.rb_off = (const int *)put(r.off.data(), r.off.size() * 4);
+        a.rb_n = (int)r.off.size() - 1;
     }
     act_a.insert(act_a.end(), act_b.begin(), act_b.end());
     a.mx_act = (const int *)put(act_a.data(), act_a.size() * 4);

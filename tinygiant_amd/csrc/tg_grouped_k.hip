@@ -396,17 +396,18 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
         else wait_copies_but<0>();
     };
     static_assert(RG_SLOTS - 2 == 2, "wait_copies_behind covers the items in flight");
-    /* the compute lane's operands of item j's run: pair t + c16 of the expert */
-    auto load_x = [&](int j, RgX &x) __attribute__((always_inline)) {
-        const int it = item(j), ei = it >> 16, tp = 16 * (it & 255);
-        const int p0 = ldc(&a.ed[ei].p0, 0), np = ldc(&a.ed[ei].np, 0);
+    /* the compute lane's operands of run r: its pair c16, whose input row the
+     * run's record holds (one round trip of scalar loads) */
+    auto load_x = [&](int r, RgX &x) __attribute__((always_inline)) {
+        const int *rc = a.rg_runs + (size_t)RING_REC * r;
+        const int nv = ldc(rc, 1);
         uint32_t rj[16];
 #pragma unroll
-        for (int jj = 0; jj < 16; jj++) rj[jj] = (uint32_t)ldc(a.p_row, (size_t)min(p0 + tp + jj, a.P - 1));
+        for (int jj = 0; jj < 16; jj++) rj[jj] = (uint32_t)ldc(rc, 2 + jj);
         uint32_t prow = 0u;
 #pragma unroll
         for (int jj = 0; jj < 16; jj++) prow = c16 == jj ? rj[jj] : prow;
-        const bool pv = tp + c16 < np;
+        const bool pv = c16 < nv;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint32_t qb = prow * RG_NB + (uint32_t)(bw + 4 * h);
@@ -538,13 +539,14 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
                            "+v"(x.xd[h]));
     };
     RgX cur, stage;
-    load_x(0, cur);
+    int run = ldc(a.rg_run0, blockIdx.x);   /* the run of item 0; the runs follow in order */
+    load_x(run, cur);
     settle(cur);
     int re = run_end(0);
     for (int i = 0; i < n;) {
         const int pf = max(i, re - 3);
         for (; i < re; i++) {
-            if (i == pf && re < n) load_x(re, stage);
+            if (i == pf && re < n) load_x(run + 1, stage);
             bar_lds();   /* item i's slab has landed, item i - 1's sums are read */
             compute(i, cur);
         }
@@ -552,6 +554,7 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
             re = run_end(i);
             settle(stage);
             cur = stage;
+            run++;
         }
     }
     bar_lds();   /* item n - 1's sums are in LDS */
@@ -847,12 +850,13 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
         else wait_copies_but<0>();
     };
     static_assert(DR_SLOTS - 2 == 4, "wait_copies_behind covers the items in flight");
-    /* the compute lane's operands of item j's run: pair tp + c16 of the expert */
-    auto load_x = [&](int j, DrX &x) __attribute__((always_inline)) {
-        const int it = item(j), ei = it >> 16, tp = 16 * (it & 255);
-        const int p0 = ldc(&a.ed[ei].p0, 0), np = ldc(&a.ed[ei].np, 0);
-        const bool pv = tp + c16 < np;
-        const uint32_t qb = (uint32_t)(p0 + tp + c16) * DR_NB + (uint32_t)bi;
+    /* the compute lane's operands of run r: its pair c16 (the run's first
+     * pair and count from its record, one round trip of scalar loads) */
+    auto load_x = [&](int r, DrX &x) __attribute__((always_inline)) {
+        const int *rc = a.rb_runs + (size_t)RING_REC * r;
+        const int pf = ldc(rc, 0), nv = ldc(rc, 1);
+        const bool pv = c16 < nv;
+        const uint32_t qb = (uint32_t)(pf + c16) * DR_NB + (uint32_t)bi;
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const long xb = as_long(ld8(qs_b, pv ? qb * 256u + 128u * h + 32u * m + 8u * g : OOB));
@@ -970,13 +974,14 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
                        "+v"(x.x1[2]), "+v"(x.x1[3]), "+v"(x.s16a), "+v"(x.s16b), "+v"(x.xd));
     };
     DrX cur, stage;
-    load_x(0, cur);
+    int run = ldc(a.rb_run0, blockIdx.x);   /* the run of item 0; the runs follow in order */
+    load_x(run, cur);
     settle(cur);
     int re = run_end(0);
     for (int i = 0; i < n;) {
         const int pf = max(i, re - (DR_SLOTS - 1));
         for (; i < re; i++) {
-            if (i == pf && re < n) load_x(re, stage);
+            if (i == pf && re < n) load_x(run + 1, stage);
             bar_lds();   /* item i's slab has landed, item i - 1's terms are read */
             compute(i, cur);
         }
@@ -984,6 +989,7 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
             re = run_end(i);
             settle(stage);
             cur = stage;
+            run++;
         }
     }
     bar_lds();   /* item n - 1's terms are in LDS */
@@ -1019,17 +1025,28 @@ bool qa_ring_shape(int gate_fmt, int D, int I) { return gate_fmt == TG_FMT_Q4K &
  * from the caches.  rend[i] is the end of item i's run (the items of its
  * expert and pass): a workgroup finds where its run ends with one load, not
  * by scanning the items that follow. */
-void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off,
-                std::vector<int> &rend) {
-    items.clear();
-    rend.clear();
+void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, const int *p_row, int P, RingLists &r) {
+    r.items.clear();
+    r.rend.clear();
+    r.runs.clear();
+    std::vector<int> run_of;
     for (int ei = 0; ei < n_act; ei++)
         for (int t = 0; t < std::max(1, (ed[ei].np + 15) / 16); t++) {
-            for (int s = 0; s < slabs; s++) items.push_back(ei << 16 | s << 8 | t);
-            rend.resize(items.size(), (int)items.size());
+            const int run = (int)(r.runs.size() / RING_REC), pf = ed[ei].p0 + 16 * t;
+            r.runs.push_back(pf);
+            r.runs.push_back(ed[ei].np - 16 * t);
+            for (int j = 0; j < 16; j++) r.runs.push_back(p_row[std::min(pf + j, P - 1)]);
+            r.runs.resize((size_t)(run + 1) * RING_REC, 0);
+            for (int s = 0; s < slabs; s++) r.items.push_back(ei << 16 | s << 8 | t);
+            r.rend.resize(r.items.size(), (int)r.items.size());
+            run_of.resize(r.items.size(), run);
         }
-    off.resize(G + 1);
-    for (int w = 0; w <= G; w++) off[w] = (int)((int64_t)items.size() * w / G);
+    r.off.resize(G + 1);
+    r.run0.resize(G + 1);
+    for (int w = 0; w <= G; w++) {
+        r.off[w] = (int)((int64_t)r.items.size() * w / G);
+        r.run0[w] = r.off[w] < (int)run_of.size() ? run_of[r.off[w]] : 0;
+    }
 }
 
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st) {

@@ -59,8 +59,10 @@ struct MoeArgs {
     int xin_remote;                         /* xin lies in host memory: quantize it once, in its own launch */
     const int *rg_items, *rg_off;           /* the persistent gate/up phase's items and each workgroup's range, or null */
     const int *rg_rend;                     /* for each item, the end of its run (items of one expert and pass) */
+    const int *rg_runs, *rg_run0;           /* each run's record (RING_REC ints) and each workgroup's first run */
     int rg_n;                               /* its workgroups */
     const int *rb_items, *rb_off, *rb_rend; /* the persistent down phase's, or null */
+    const int *rb_runs, *rb_run0;
     int rb_n;
 };
 
@@ -130,10 +132,17 @@ bool qk_grouped_fits(const MoeArgs &a);
  * workgroups.  False when the shape is not the phase's. */
 bool qa_ring_shape(int gate_fmt, int D, int I);
 bool qb_ring_shape(int I, int D);
-/* the persistent phases' items (expert, pass, slab of `slabs`) cut into G
- * workgroup ranges, and the end of each item's run (expert and pass) */
-void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, std::vector<int> &items, std::vector<int> &off,
-                std::vector<int> &rend);
+/* The persistent phases' items (expert, pass, slab of `slabs`) cut into G
+ * workgroup ranges (off), the end of each item's run (rend: the items of one
+ * expert and pass), the runs' records (RING_REC ints each: the run's first
+ * pair p0 + 16 t, the pairs from there on, np - 16 t, possibly more than 16,
+ * and the input rows of its first 16 pairs, the last pair's row past the
+ * end) and the run of each workgroup's first item (run0). */
+constexpr int RING_REC = 20;
+struct RingLists {
+    std::vector<int> items, off, rend, runs, run0;
+};
+void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, const int *p_row, int P, RingLists &r);
 constexpr int QA_RING_MAX_G = 1024;
 void launch_moe_a_qk(const MoeArgs &a, hipStream_t st);
 void launch_moe_b_qk(const MoeArgs &a, hipStream_t st);
