@@ -607,7 +607,8 @@ def qwen_prefill_probe(tg, base, tokens=(64, 128), iters=20):
         lib.tg_hip_set_moe_qk_min_rows(0)
         us_dot4 = _time_calls(lib, lambda: lib.tg_hip_moe_plan_run(plan, x.ptr, y.ptr, None), iters)
         lib.tg_hip_set_moe_qk_min_rows(prev)
-        mfma = 0 < prev <= most   # the path the default threshold takes
+        thr = prev if prev >= 0 else 17   # the default for this shape (both persistent rings)
+        mfma = 0 < thr <= most            # the path the default threshold takes
         us = us_mfma if mfma else us_dot4
         nbytes = n * EXPERT_B
         pairs = int((rw != 0).sum())

@@ -331,8 +331,11 @@ int tg_hip_set_moe_grouped_min_rows(int rows);
  * least `rows` pairs run both phases on int8 MFMA (each weight byte read
  * once per 16 pairs; the integer sums of dot_q4k_q8 / dot_q6k_q8,
  * csrc/libtinygiant.c:223-272, :384-443, with the f32 additions grouped
- * differently); 0 keeps every such layer on the v_dot4 phases.  Default 40.
- * Returns the previous setting.  No counterpart in the reference. */
+ * differently); 0 keeps every such layer on the v_dot4 phases.  A negative
+ * value (the default) picks by shape: 17 where both persistent ring phases
+ * run (D = 2048 gate/up rows, I = 768 down rows, no down bias), 40 for the
+ * other shapes.  Returns the previous setting.  No counterpart in the
+ * reference. */
 int tg_hip_set_moe_qk_min_rows(int rows);
 /* The fused q6_K head (tg_hip_head_argmax_dev) reads the head on int8 MFMA
  * from `k` input rows on: each block's integer sum is exact and its term

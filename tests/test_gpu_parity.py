@@ -337,6 +337,7 @@ def test_moe_expert_major_equals_per_pair(tg, orc, k, pool, top, mixed):
     lib = tg.lib()
     outs = []
     prev = lib.tg_hip_set_moe_expert_major(7)
+    prev_qk = lib.tg_hip_set_moe_qk_min_rows(0)   # the v_dot4 phases, whose bits these modes share
     try:
         for on in (7, 0, 1, 5, 3, 15):
             lib.tg_hip_set_moe_expert_major(on)
@@ -346,6 +347,7 @@ def test_moe_expert_major_equals_per_pair(tg, orc, k, pool, top, mixed):
             outs.append((h, o))
     finally:
         lib.tg_hip_set_moe_expert_major(prev)
+        lib.tg_hip_set_moe_qk_min_rows(prev_qk)
     say("  pairs", P, "most per expert", int(np.count_nonzero(rw, axis=1).max()))
     for h, o in outs[1:]:
         assert h.tobytes() == outs[0][0].tobytes()

@@ -2244,7 +2244,8 @@ TG_API int tg_hip_set_moe_grouped_min_rows(int rows) {
 }
 
 /* Pairs per expert from which Q4_K gate/up + Q6_K down expert layers take
- * the int8 MFMA phases (0: never); returns the previous setting. */
+ * the int8 MFMA phases (0: never; negative: the default by shape); returns
+ * the previous setting. */
 TG_API int tg_hip_set_moe_qk_min_rows(int rows) {
     std::lock_guard<std::recursive_mutex> lk(g_mu);
     const int prev = qk_min_rows();

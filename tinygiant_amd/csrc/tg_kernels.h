@@ -124,7 +124,8 @@ void set_grouped_min_rows(int rows);
 int grouped_min_rows();
 /* Q4_K gate/up and Q6_K down phases on int8 MFMA with LDS-resident weight
  * slabs (tg_grouped_k.hip), taken by launch_moe for layers whose experts
- * hold at least qk_min_rows() pairs (0: never) */
+ * hold at least qk_min_rows() pairs (0: never; negative: the default by
+ * shape, 17 where both persistent rings run, 40 elsewhere) */
 bool qk_grouped_fits(const MoeArgs &a);
 /* The persistent int8 MFMA gate/up phase (Q4_K, D = 2048): its items, (index
  * ei into the busiest-first active experts, 16-row slab s, pass t of 16

@@ -840,8 +840,15 @@ static int g_grouped_min_rows = 4;
 
 void set_grouped_min_rows(int rows) { g_grouped_min_rows = rows < 0 ? 0 : rows; }
 int grouped_min_rows() { return g_grouped_min_rows; }
-static int g_qk_min_rows = 40;
-void set_qk_min_rows(int rows) { g_qk_min_rows = rows < 0 ? 0 : rows; }
+/* Negative: the default, by shape.  Where both persistent rings run (the
+ * Qwen3 expert shape) they beat the v_dot4 phases from ~20 pairs on the
+ * busiest expert (128 experts, Zipf top-8: 22 pairs 66 against 74 us, 29
+ * pairs 81 against 95 us, 10-15 pairs even); the grid forms of other shapes
+ * from ~40.  17 keeps every batch of up to 16 rows (a verify batch) on the
+ * v_dot4 phases, whose bits the persistent multi-row step shares. */
+constexpr int QK_RING_MIN_ROWS = 17, QK_GRID_MIN_ROWS = 40;
+static int g_qk_min_rows = -1;
+void set_qk_min_rows(int rows) { g_qk_min_rows = rows < 0 ? -1 : rows; }
 int qk_min_rows() { return g_qk_min_rows; }
 
 static int g_expert_major = EM_DEFAULT;
@@ -922,7 +929,9 @@ static void launch_bx(const MoeArgs &a, int fmt, uint32_t rb, int nitems, int T,
 void launch_moe(const MoeArgs &a, const int *down_fmts_present, int n_down_fmts, hipStream_t st,
                 const std::function<void(int)> *mark, bool quantize_x) {
     /* Q4_K / Q6_K experts with many pairs: the int8 MFMA phases */
-    if (g_qk_min_rows > 0 && a.max_rows >= g_qk_min_rows && n_down_fmts == 1 && down_fmts_present[0] == TG_FMT_Q6K &&
+    const bool rings = a.rg_items && a.rb_items && !a.dbias;
+    const int qk_min = g_qk_min_rows >= 0 ? g_qk_min_rows : rings ? QK_RING_MIN_ROWS : QK_GRID_MIN_ROWS;
+    if (qk_min > 0 && a.max_rows >= qk_min && n_down_fmts == 1 && down_fmts_present[0] == TG_FMT_Q6K &&
         qk_grouped_fits(a)) {
         if (quantize_x) {
             launch_quantize(a.xin, a.D, a.k, a.D, a.xq, st);
