@@ -327,6 +327,7 @@ __device__ inline uint32_t rg_unit(int r, int u) { return (uint32_t)(RG_UNITS * 
 struct RgX {   /* a compute lane's q8 operands of one run, blocks c % 4 and c % 4 + 4 */
     long xb[2][8];
     uint32_t bs0[2], bs1[2], xd[2];
+    float xdv[2][4];   /* the scales of pairs 4 g .. 4 g + 3, set once the run starts */
 };
 
 __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
@@ -427,9 +428,7 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int b = bw + 4 * h;
-            float xdv[4];
-#pragma unroll
-            for (int v = 0; v < 4; v++) xdv[v] = __uint_as_float(__shfl(x.xd[h], 4 * g + v, 64));
+            const float *xdv = x.xdv[h];
             const Q4Hdr hr = q4_hdr(*(const u32x4 *)(sb + 16 * rg_unit(c16, 9 * b)));
             v4f im = {0.f, 0.f, 0.f, 0.f};
             im = __builtin_amdgcn_mfma_f32_16x16x4f32((float)(int)x.bs0[h], (float)byte_of(hr.mnl, g), im, 0, 0, 0);
@@ -538,10 +537,18 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
                            "+v"(x.xb[h][5]), "+v"(x.xb[h][6]), "+v"(x.xb[h][7]), "+v"(x.bs0[h]), "+v"(x.bs1[h]),
                            "+v"(x.xd[h]));
     };
+    /* the scale of each of the lane's four result pairs, shuffled once a run */
+    auto prep = [&](RgX &x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) x.xdv[h][v] = __uint_as_float(__shfl(x.xd[h], 4 * g + v, 64));
+    };
     RgX cur, stage;
     int run = ldc(a.rg_run0, blockIdx.x);   /* the run of item 0; the runs follow in order */
     load_x(run, cur);
     settle(cur);
+    prep(cur);
     int re = run_end(0);
     for (int i = 0; i < n;) {
         const int pf = max(i, re - 3);
@@ -554,6 +561,7 @@ __global__ __launch_bounds__(RG_NT) void k_moe_qa_ring(MoeArgs a) {
             re = run_end(i);
             settle(stage);
             cur = stage;
+            prep(cur);
             run++;
         }
     }
@@ -780,6 +788,7 @@ __device__ inline u32x2 dr_ld8(const uint8_t *base, uint32_t o) {
 struct DrX {   /* a compute lane's q8 operands of one run: pair c16, its wave's half-block */
     long x0[4], x1[4];   /* K slice 8 g of chunk m, zero in the half of K the other sub-block takes */
     float s16a, s16b, xd;
+    float xdv[4];        /* the scales of pairs 4 g .. 4 g + 3, set once the run starts */
 };
 
 __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
@@ -870,9 +879,7 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
     /* compute item j from its slot: the wave's half-block of its tile */
     auto compute = [&](int j, const DrX &x) __attribute__((always_inline)) {
         const uint8_t *sb = &ring[j % DR_SLOTS][0];
-        float xdv[4];
-#pragma unroll
-        for (int v = 0; v < 4; v++) xdv[v] = __shfl(x.xd, 4 * g + v, 64);
+        const float *xdv = x.xdv;
         {
             const int tq = tw;
             const uint32_t rb = (uint32_t)(16 * tq + c16) * DR_RB + (uint32_t)bi * Q6B;   /* row c16's block */
@@ -973,10 +980,15 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
                      : "+v"(x.x0[0]), "+v"(x.x0[1]), "+v"(x.x0[2]), "+v"(x.x0[3]), "+v"(x.x1[0]), "+v"(x.x1[1]),
                        "+v"(x.x1[2]), "+v"(x.x1[3]), "+v"(x.s16a), "+v"(x.s16b), "+v"(x.xd));
     };
+    auto prep = [&](DrX &x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 4; v++) x.xdv[v] = __shfl(x.xd, 4 * g + v, 64);
+    };
     DrX cur, stage;
     int run = ldc(a.rb_run0, blockIdx.x);   /* the run of item 0; the runs follow in order */
     load_x(run, cur);
     settle(cur);
+    prep(cur);
     int re = run_end(0);
     for (int i = 0; i < n;) {
         const int pf = max(i, re - (DR_SLOTS - 1));
@@ -989,6 +1001,7 @@ __global__ __launch_bounds__(DR_NT) void k_moe_qb_ring(MoeArgs a) {
             re = run_end(i);
             settle(stage);
             cur = stage;
+            prep(cur);
             run++;
         }
     }
