@@ -1037,7 +1037,10 @@ bool qa_ring_shape(int gate_fmt, int D, int I) { return gate_fmt == TG_FMT_Q4K &
  * same time on neighbouring workgroups, so their slabs' second reads come
  * from the caches.  rend[i] is the end of item i's run (the items of its
  * expert and pass): a workgroup finds where its run ends with one load, not
- * by scanning the items that follow. */
+ * by scanning the items that follow.  runs holds each run's record (first
+ * pair, pair count, the input rows of its first 16 pairs) in list order and
+ * run0[w] the run of workgroup w's first item, so a compute wave reaches a
+ * run's operands with one round trip of scalar loads. */
 void ring_items(const ExpDesc *ed, int n_act, int slabs, int G, const int *p_row, int P, RingLists &r) {
     r.items.clear();
     r.rend.clear();
